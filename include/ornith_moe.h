@@ -1,0 +1,61 @@
+/* Router and whole-layer C ABI of the MI355X (gfx950) Ornith library.
+ *
+ * The reference computes router logits with a Triton row-dot
+ * (plugin-site/ornith_g256/iu4_correctness/gates_projection.py:18-26,36-42,
+ * bound via gates.py:112-121), selects experts in vLLM's topk_softmax
+ * (contract plugin-site/ornith_g256/moe_base.py:53-64) and gates the shared
+ * expert with rocm_unquantized_gemm + torch.sigmoid (moe_shared.py:65,
+ * shared_kernel.py:101-103).  None of these has a C ABI in the reference;
+ * these entries replace them with HIP kernels in a declared, fixed order:
+ *   logit[t,e] = bias[e] + xor-butterfly over 64 lanes of lane partials; lane l
+ *     accumulates fma(x[k], w[k], acc) for k = 8c..8c+7, c = l, l+64, l+128, l+192;
+ *   p = pexp(l - max) / butterfly-sum; the 8 largest p (ties -> lower id) in
+ *     descending order; weight_j = p_j / (slot-order sum of the 8 p).
+ *   shared logit: the same reduction over expert_gate, rounded to bf16.
+ */
+#ifndef ORNITH_MI355X_MOE_H
+#define ORNITH_MI355X_MOE_H
+#include <stddef.h>
+#include <stdint.h>
+#include <hip/hip_runtime_api.h>
+#include "ornith_routed.h"
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Replaces gates_projection.router (+ vLLM select_experts/topk_softmax, and the
+ * shared-expert gate logit of moe_shared.py:65).
+ *   x_bf16 [T, 2048] with row stride x_stride (elements, multiple of 8);
+ *   router_w_bf16 [256, 2048]; bias_f32 [256] or NULL (a benchmark-harness
+ *   additive logit term; NULL = the reference contract, moe_base.py:61);
+ *   shared_gate_w_bf16 [2048] or NULL; logits_f32 [T, 257] scratch/output
+ *   (column 256 = shared gate logit); topk outputs weights f32 [T,8],
+ *   ids int32 [T,8]; shared_logit_bf16 [T] (written iff shared_gate_w_bf16). */
+ORNITH_EXPORT hipError_t ornith_router_topk_launch(
+    const void* x_bf16, int64_t x_stride, const void* router_w_bf16, const void* bias_f32,
+    const void* shared_gate_w_bf16, void* logits_f32, void* topk_weights_f32, void* topk_ids_i32,
+    void* shared_logit_bf16, int T, hipStream_t stream);
+
+/* Whole quantized MoE layer: router + top-8, permutation, routed experts (A8),
+ * shared expert as ninth slot (routed_storage_n32_consumer.cpp:385-401 arithmetic)
+ * and the routed + shared bf16 sum done by the MoE runner.
+ *   output_bf16 [T,2048] = bf16(f32(routed) + f32(shared)).
+ *   topk_weights_f32 [T,8], topk_ids_i32 [T,8], shared_logit_bf16 [T] are outputs.
+ * Workspace: ornith_moe_layer_get_layout(Tcap). */
+ORNITH_EXPORT hipError_t ornith_moe_layer_get_layout(int Tcap, OrnithRoutedDirectLayout* out);
+ORNITH_EXPORT hipError_t ornith_moe_layer_launch(
+    const void* input_bf16, const void* router_w_bf16, const void* bias_f32, const void* shared_gate_w_bf16,
+    const void* gate_codes, const void* gate_meta, const void* down_codes, const void* down_meta,
+    const void* shared_gate_codes, const void* shared_gate_meta,
+    const void* shared_down_codes, const void* shared_down_meta,
+    const void* silu_f32, const void* sigmoid_bf16,
+    void* workspace, size_t bytes, void* topk_weights_f32, void* topk_ids_i32, void* shared_logit_bf16,
+    void* output_bf16, void* flags_u32, int T, int Tcap, hipStream_t stream);
+
+/* Build identification (no reference counterpart): returns 1. */
+ORNITH_EXPORT int ornith_mi355x_abi_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

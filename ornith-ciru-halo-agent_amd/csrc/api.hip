@@ -1,0 +1,443 @@
+// extern "C" entry points.  Argument validation is host-only and runs before
+// any launch; every entry enqueues on the caller's stream and allocates
+// nothing.  The references for each entry are in include/ornith_*.h.
+#include <limits>
+#include "kernels.hpp"
+#include "../../include/ornith_routed.h"
+#include "../../include/ornith_dense.h"
+#include "../../include/ornith_moe.h"
+
+using namespace ornith;
+
+namespace {
+
+#define TRY(expr) do { hipError_t _s = (expr); if (_s != hipSuccess) return _s; } while (0)
+
+constexpr int kMaxTokens = 8192;
+constexpr int kGateN = 2 * kInter, kDownN = kHidden;
+constexpr int64_t kGateBankWords = int64_t(kGateN) * kHidden / 8, kGateBankMeta = int64_t(kGateN) * (kHidden / kGroup);
+constexpr int64_t kDownBankWords = int64_t(kDownN) * kInter / 8, kDownBankMeta = int64_t(kDownN) * (kInter / kGroup);
+constexpr int kLogitStride = kExperts + 1;
+
+bool aligned(const void* p, size_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
+
+// Workspace plan shared by the routed, shared-slot and whole-layer entries.
+struct RoutedPlan {
+    OrnithRoutedDirectLayout l;
+    size_t permute, logits;
+};
+
+RoutedPlan routed_plan(int Tcap, bool shared_slot, bool layer) {
+    RoutedPlan p{};
+    size_t cursor = 0;
+    const size_t t = size_t(Tcap), rs = t * kTop + (shared_slot ? t : 0);
+    auto add = [&](size_t& field, size_t bytes) { field = cursor; cursor = align256(cursor + bytes); };
+    add(p.l.gate_x, 0);
+    add(p.l.gate_low, t * kHidden);                       // int8 activation words
+    add(p.l.gate_high, 0);
+    add(p.l.gate_scales, t * (kHidden / kGroup) * 2);
+    add(p.l.gate_sums, t * (kHidden / kGroup) * 4);
+    add(p.l.gate_y, rs * kGateN * 4);
+    add(p.l.middle, 0);
+    add(p.l.down_x, 0);
+    add(p.l.down_low, rs * kInter);                       // int8 activation words
+    add(p.l.down_high, 0);
+    add(p.l.down_scales, rs * (kInter / kGroup) * 2);
+    add(p.l.down_sums, rs * (kInter / kGroup) * 4);
+    add(p.l.route_out, rs * kHidden * 4);
+    add(p.l.final_f32, t * kHidden * 4);
+    add(p.permute, permute_scratch_bytes(int(t * kTop), shared_slot ? int(t) : 0));
+    if (layer) add(p.logits, t * kLogitStride * 4);
+    p.l.workspace_bytes = cursor;
+    return p;
+}
+
+// The routed pipeline after routing is known.
+hipError_t run_routed(const RoutedPlan& p, void* ws, const void* input, const float* weights, const int32_t* ids,
+                      const void* gate_codes, const void* gate_meta, const void* down_codes, const void* down_meta,
+                      const void* sg_codes, const void* sg_meta, const void* sd_codes, const void* sd_meta,
+                      const uint16_t* shared_logit, const float* silu, const uint16_t* sigmoid, int qmax,
+                      uint16_t* out, uint16_t* shared_out, uint16_t* layer_out, uint32_t* sticky, int T, int Tcap,
+                      hipStream_t s) {
+    const bool shared = sg_codes != nullptr;
+    const int R = T * kTop, RS = R + (shared ? T : 0);
+    const PermuteScratch ps = carve_permute(at<void>(ws, p.permute), Tcap * kTop, shared ? Tcap : 0);
+    TRY(launch_permute(ids, R, T, shared, ps, sticky, 64, s));
+    auto gw = at<uint32_t>(ws, p.l.gate_low);
+    auto gs = at<uint16_t>(ws, p.l.gate_scales);
+    auto gsum = at<int32_t>(ws, p.l.gate_sums);
+    TRY(launch_act_bf16(static_cast<const uint16_t*>(input), kHidden, T, kHidden, qmax, shared ? nullptr : ids, gw, gs,
+                        gsum, sticky, kFlagNonfiniteInput, kFlagInvalidActivation, s));
+    const int max_segments = (R < kExperts ? R : kExperts) + (shared ? 1 : 0);
+    ProjArgs a{};
+    a.codes = static_cast<const uint32_t*>(gate_codes);
+    a.meta = static_cast<const uint32_t*>(gate_meta);
+    a.shared_codes = static_cast<const uint32_t*>(sg_codes);
+    a.shared_meta = static_cast<const uint32_t*>(sg_meta);
+    a.bank_words = kGateBankWords;
+    a.bank_meta_words = kGateBankMeta;
+    a.segments = ps.segments;
+    a.nseg = ps.meta;
+    a.routes = ps.routes;
+    a.row_mode = 1;
+    a.R = R;
+    a.act_words = gw; a.act_scales = gs; a.act_sums = gsum;
+    a.out = at<float>(ws, p.l.gate_y);
+    a.N = kGateN; a.K = kHidden; a.tile = 32;
+    a.sticky = sticky; a.flag_projection = kFlagNonfiniteProjection;
+    TRY(launch_project_gemv(a, max_segments, Out::Routed, s));
+    auto dw = at<uint32_t>(ws, p.l.down_low);
+    auto dsc = at<uint16_t>(ws, p.l.down_scales);
+    auto dsum = at<int32_t>(ws, p.l.down_sums);
+    TRY(launch_act_middle(at<float>(ws, p.l.gate_y), RS, R, ids, qmax, silu, dw, dsc, dsum, sticky, s));
+    a.codes = static_cast<const uint32_t*>(down_codes);
+    a.meta = static_cast<const uint32_t*>(down_meta);
+    a.shared_codes = static_cast<const uint32_t*>(sd_codes);
+    a.shared_meta = static_cast<const uint32_t*>(sd_meta);
+    a.bank_words = kDownBankWords;
+    a.bank_meta_words = kDownBankMeta;
+    a.row_mode = 0;
+    a.act_words = dw; a.act_scales = dsc; a.act_sums = dsum;
+    a.out = at<float>(ws, p.l.route_out);
+    a.N = kDownN; a.K = kInter;
+    TRY(launch_project_gemv(a, max_segments, Out::Routed, s));
+    return launch_reduce(at<float>(ws, p.l.route_out), weights, ids, T, out ? at<float>(ws, p.l.final_f32) : nullptr,
+                         out, shared_logit, shared ? sigmoid : nullptr, shared_out, layer_out, sticky, s);
+}
+
+template <int QMAX>
+hipError_t routed_launch(const void* input, const void* weights, const void* ids, const void* gate_codes,
+                         const void* gate_meta, const void* down_codes, const void* down_meta, void* workspace,
+                         size_t bytes, void* output, void* flags, int T, int Tcap, hipStream_t stream) {
+    if (Tcap < 0 || Tcap > kMaxTokens || T < 0 || T > Tcap) return hipErrorInvalidValue;
+    const RoutedPlan p = routed_plan(Tcap, false, false);
+    if (bytes < p.l.workspace_bytes) return hipErrorInvalidValue;
+    if (!T) return hipSuccess;
+    if (!input || !weights || !ids || !gate_codes || !gate_meta || !down_codes || !down_meta || !workspace || !output ||
+        !flags)
+        return hipErrorInvalidValue;
+    if (!aligned(input, 8) || !aligned(weights, 4) || !aligned(ids, 4) || !aligned(gate_codes, 16) ||
+        !aligned(down_codes, 16) || !aligned(gate_meta, 4) || !aligned(down_meta, 4) || !aligned(workspace, 256) ||
+        !aligned(output, 8) || !aligned(flags, 4))
+        return hipErrorInvalidValue;
+    return run_routed(p, workspace, input, static_cast<const float*>(weights), static_cast<const int32_t*>(ids),
+                      gate_codes, gate_meta, down_codes, down_meta, nullptr, nullptr, nullptr, nullptr, nullptr,
+                      nullptr, nullptr, QMAX, static_cast<uint16_t*>(output), nullptr, nullptr,
+                      static_cast<uint32_t*>(flags), T, Tcap, stream);
+}
+
+// ---- dense helpers --------------------------------------------------------------
+bool dense_shape(int N, int K) {
+    return N > 0 && (N <= 12288 || N == 248320) && N % 16 == 0 && K > 0 && K <= 8192 && K % kGroup == 0;
+}
+
+OrnithDenseG256Layout dense_layout(int Mcap, int N, int K) {
+    OrnithDenseG256Layout l{};
+    size_t cursor = 0;
+    const size_t m = size_t(Mcap);
+    auto add = [&](size_t& field, size_t bytes) { field = cursor; cursor = align256(cursor + bytes); };
+    add(l.transformed, 0);
+    add(l.low, m * K);                       // int8 activation words
+    add(l.high, 0);
+    add(l.scales, m * (K / kGroup) * 2);
+    add(l.sums, m * (K / kGroup) * 4);
+    add(l.projection, m * N * 4);
+    l.workspace_bytes = cursor;
+    return l;
+}
+
+struct Range { uintptr_t lo, hi; };
+bool to_range(const void* p, size_t n, Range& r) {
+    const uintptr_t lo = reinterpret_cast<uintptr_t>(p);
+    if (!p || n > std::numeric_limits<uintptr_t>::max() - lo) return false;
+    r = {lo, lo + n};
+    return true;
+}
+// Pointer, alignment and overlap checks of dense_g256_consumer.cpp:240-245:
+// entries [first_mutable, n) must not overlap any other range.
+bool check_ranges(const void* const* ptr, const size_t* sizes, const size_t* align, int n, int first_mutable) {
+    Range r[8];
+    for (int i = 0; i < n; ++i)
+        if (!aligned(ptr[i], align[i]) || !to_range(ptr[i], sizes[i], r[i])) return false;
+    for (int i = first_mutable; i < n; ++i)
+        for (int j = 0; j < n; ++j)
+            if (i != j && r[i].lo < r[j].hi && r[j].lo < r[i].hi) return false;
+    return true;
+}
+
+hipError_t dense_run(const void* input, const void* codes, const void* meta, void* ws, const OrnithDenseG256Layout& l,
+                     float* projection, uint16_t* out, uint32_t* sticky, int M, int N, int K, int tile, hipStream_t s) {
+    auto w = at<uint32_t>(ws, l.low);
+    auto sc = at<uint16_t>(ws, l.scales);
+    auto su = at<int32_t>(ws, l.sums);
+    TRY(launch_act_bf16(static_cast<const uint16_t*>(input), K, M, K, 127, nullptr, w, sc, su, sticky,
+                        kDenseNonfiniteInput, kDenseInvalidActivation, s));
+    ProjArgs a{};
+    a.codes = static_cast<const uint32_t*>(codes);
+    a.meta = static_cast<const uint32_t*>(meta);
+    a.dense_rows = M;
+    a.act_words = w; a.act_scales = sc; a.act_sums = su;
+    a.out = projection; a.out_bf16 = out;
+    a.N = N; a.K = K; a.tile = tile;
+    a.sticky = sticky; a.flag_projection = kDenseNonfiniteProjection; a.flag_bf16 = kDenseNonfiniteBf16;
+    return launch_project_gemv(a, 1, Out::Dense, s);
+}
+
+// Top-1 over fp32 rows with numpy's rule: the first NaN if any, else the first maximum.
+__device__ __forceinline__ bool better(float a, int ia, float b, int ib) {
+    const bool na = isnan(a), nb = isnan(b);
+    if (na != nb) return na;
+    if (na) return ia < ib;
+    return a > b || (a == b && ia < ib);
+}
+__global__ __launch_bounds__(256) void argmax_kernel(const float* __restrict__ v, int N, int64_t* __restrict__ out) {
+    __shared__ float bv[256];
+    __shared__ int bi[256];
+    const float* row = v + size_t(blockIdx.x) * N;
+    float best = -__builtin_huge_valf();
+    int idx = 0x7fffffff;
+    for (int i = threadIdx.x; i < N; i += 256)
+        if (idx == 0x7fffffff || better(row[i], i, best, idx)) { best = row[i]; idx = i; }
+    bv[threadIdx.x] = best;
+    bi[threadIdx.x] = idx;
+    __syncthreads();
+    for (int m = 128; m > 0; m >>= 1) {
+        if (int(threadIdx.x) < m) {
+            const int o = threadIdx.x + m;
+            if (bi[o] != 0x7fffffff && (bi[threadIdx.x] == 0x7fffffff || better(bv[o], bi[o], bv[threadIdx.x], bi[threadIdx.x]))) {
+                bv[threadIdx.x] = bv[o];
+                bi[threadIdx.x] = bi[o];
+            }
+        }
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) out[blockIdx.x] = bi[0];
+}
+
+}  // namespace
+
+// =============================================================================
+// Routed
+// =============================================================================
+extern "C" hipError_t ornith_routed_direct_get_layout(int Tcap, OrnithRoutedDirectLayout* out) {
+    if (!out || Tcap < 0 || Tcap > kMaxTokens) return hipErrorInvalidValue;
+    *out = routed_plan(Tcap, false, false).l;
+    return hipSuccess;
+}
+
+extern "C" hipError_t ornith_routed_direct_launch(const void* input, const void* weights, const void* ids,
+                                                  const void* gate_codes, const void* gate_meta, const void* down_codes,
+                                                  const void* down_meta, void* workspace, size_t bytes, void* output,
+                                                  void* flags, int T, int Tcap, hipStream_t stream) {
+    return routed_launch<127>(input, weights, ids, gate_codes, gate_meta, down_codes, down_meta, workspace, bytes,
+                              output, flags, T, Tcap, stream);
+}
+
+extern "C" hipError_t ornith_routed_direct_launch_a4(const void* input, const void* weights, const void* ids,
+                                                     const void* gate_codes, const void* gate_meta,
+                                                     const void* down_codes, const void* down_meta, void* workspace,
+                                                     size_t bytes, void* output, void* flags, int T, int Tcap,
+                                                     hipStream_t stream) {
+    return routed_launch<7>(input, weights, ids, gate_codes, gate_meta, down_codes, down_meta, workspace, bytes, output,
+                            flags, T, Tcap, stream);
+}
+
+extern "C" hipError_t ornith_routed_direct_launch_a4_prefill(const void* input, const void* weights, const void* ids,
+                                                             const void* gate_codes, const void* gate_meta,
+                                                             const void* down_codes, const void* down_meta,
+                                                             void* workspace, size_t bytes, void* output, void* flags,
+                                                             int T, int Tcap, hipStream_t stream) {
+    if (T > 64)
+        return routed_launch<7>(input, weights, ids, gate_codes, gate_meta, down_codes, down_meta, workspace, bytes,
+                                output, flags, T, Tcap, stream);
+    return routed_launch<127>(input, weights, ids, gate_codes, gate_meta, down_codes, down_meta, workspace, bytes,
+                              output, flags, T, Tcap, stream);
+}
+
+extern "C" int ornith_routed_storage_n32(void) { return 32; }
+extern "C" int ornith_routed_prefill_output_tile(void) { return 32; }
+
+extern "C" hipError_t ornith_routed_shared_get_layout(int Tcap, OrnithRoutedDirectLayout* out) {
+    if (!out || Tcap < 0 || Tcap > 16) return hipErrorInvalidValue;
+    *out = routed_plan(Tcap, true, false).l;
+    return hipSuccess;
+}
+
+extern "C" hipError_t ornith_routed_direct_launch_shared_tables(
+    const void* input, const void* weights, const void* ids, const void* gate_codes, const void* gate_meta,
+    const void* down_codes, const void* down_meta, const void* shared_gate_codes, const void* shared_gate_meta,
+    const void* shared_down_codes, const void* shared_down_meta, const void* shared_logit, const void* shared_silu,
+    const void* shared_sigmoid, void* workspace, size_t bytes, void* output, void* shared_output, void* flags, int T,
+    int Tcap, hipStream_t stream) {
+    if (Tcap < 0 || Tcap > 16 || T < 0 || T > Tcap) return hipErrorInvalidValue;
+    const RoutedPlan p = routed_plan(Tcap, true, false);
+    if (bytes < p.l.workspace_bytes) return hipErrorInvalidValue;
+    if (!T) return hipSuccess;
+    const void* req[] = {input, weights, ids, gate_codes, gate_meta, down_codes, down_meta, shared_gate_codes,
+                         shared_gate_meta, shared_down_codes, shared_down_meta, shared_logit, shared_silu,
+                         shared_sigmoid, workspace, output, shared_output, flags};
+    for (const void* q : req) if (!q) return hipErrorInvalidValue;
+    if (!aligned(input, 8) || !aligned(gate_codes, 16) || !aligned(down_codes, 16) || !aligned(shared_gate_codes, 16) ||
+        !aligned(shared_down_codes, 16) || !aligned(workspace, 256) || !aligned(output, 8) ||
+        !aligned(shared_output, 8) || !aligned(flags, 4))
+        return hipErrorInvalidValue;
+    return run_routed(p, workspace, input, static_cast<const float*>(weights), static_cast<const int32_t*>(ids),
+                      gate_codes, gate_meta, down_codes, down_meta, shared_gate_codes, shared_gate_meta,
+                      shared_down_codes, shared_down_meta, static_cast<const uint16_t*>(shared_logit),
+                      static_cast<const float*>(shared_silu), static_cast<const uint16_t*>(shared_sigmoid), 127,
+                      static_cast<uint16_t*>(output), static_cast<uint16_t*>(shared_output), nullptr,
+                      static_cast<uint32_t*>(flags), T, Tcap, stream);
+}
+
+// =============================================================================
+// Router and whole layer
+// =============================================================================
+extern "C" hipError_t ornith_router_topk_launch(const void* x, int64_t x_stride, const void* router_w,
+                                                const void* bias, const void* shared_gate_w, void* logits,
+                                                void* topk_weights, void* topk_ids, void* shared_logit, int T,
+                                                hipStream_t stream) {
+    if (T < 0 || T > kMaxTokens || x_stride < kHidden || x_stride % 8) return hipErrorInvalidValue;
+    if (!T) return hipSuccess;
+    if (!x || !router_w || !logits || !topk_weights || !topk_ids || (shared_gate_w && !shared_logit))
+        return hipErrorInvalidValue;
+    if (!aligned(x, 16) || !aligned(router_w, 16) || (shared_gate_w && !aligned(shared_gate_w, 16)) ||
+        !aligned(logits, 4) || !aligned(topk_weights, 4) || !aligned(topk_ids, 4))
+        return hipErrorInvalidValue;
+    auto lg = static_cast<float*>(logits);
+    TRY(launch_router(static_cast<const uint16_t*>(x), x_stride, T, static_cast<const uint16_t*>(router_w), kExperts,
+                      static_cast<const float*>(bias), lg, kLogitStride, stream));
+    if (shared_gate_w)
+        TRY(launch_router(static_cast<const uint16_t*>(x), x_stride, T, static_cast<const uint16_t*>(shared_gate_w), 1,
+                          nullptr, lg + kExperts, kLogitStride, stream));
+    return launch_topk(lg, kLogitStride, T, static_cast<float*>(topk_weights), static_cast<int32_t*>(topk_ids),
+                       shared_gate_w ? lg + kExperts : nullptr, kLogitStride,
+                       shared_gate_w ? static_cast<uint16_t*>(shared_logit) : nullptr, stream);
+}
+
+extern "C" hipError_t ornith_moe_layer_get_layout(int Tcap, OrnithRoutedDirectLayout* out) {
+    if (!out || Tcap < 0 || Tcap > kMaxTokens) return hipErrorInvalidValue;
+    *out = routed_plan(Tcap, true, true).l;
+    return hipSuccess;
+}
+
+extern "C" hipError_t ornith_moe_layer_launch(
+    const void* input, const void* router_w, const void* bias, const void* shared_gate_w, const void* gate_codes,
+    const void* gate_meta, const void* down_codes, const void* down_meta, const void* shared_gate_codes,
+    const void* shared_gate_meta, const void* shared_down_codes, const void* shared_down_meta, const void* silu,
+    const void* sigmoid, void* workspace, size_t bytes, void* topk_weights, void* topk_ids, void* shared_logit,
+    void* output, void* flags, int T, int Tcap, hipStream_t stream) {
+    if (Tcap < 0 || Tcap > kMaxTokens || T < 0 || T > Tcap) return hipErrorInvalidValue;
+    const RoutedPlan p = routed_plan(Tcap, true, true);
+    if (bytes < p.l.workspace_bytes) return hipErrorInvalidValue;
+    if (!T) return hipSuccess;
+    const void* req[] = {input, router_w, shared_gate_w, gate_codes, gate_meta, down_codes, down_meta,
+                         shared_gate_codes, shared_gate_meta, shared_down_codes, shared_down_meta, silu, sigmoid,
+                         workspace, topk_weights, topk_ids, shared_logit, output, flags};
+    for (const void* q : req) if (!q) return hipErrorInvalidValue;
+    if (!aligned(input, 16) || !aligned(router_w, 16) || !aligned(shared_gate_w, 16) || !aligned(gate_codes, 16) ||
+        !aligned(down_codes, 16) || !aligned(shared_gate_codes, 16) || !aligned(shared_down_codes, 16) ||
+        !aligned(workspace, 256) || !aligned(output, 8) || !aligned(flags, 4))
+        return hipErrorInvalidValue;
+    TRY(ornith_router_topk_launch(input, kHidden, router_w, bias, shared_gate_w, at<float>(workspace, p.logits),
+                                  topk_weights, topk_ids, shared_logit, T, stream));
+    return run_routed(p, workspace, input, static_cast<const float*>(topk_weights),
+                      static_cast<const int32_t*>(topk_ids), gate_codes, gate_meta, down_codes, down_meta,
+                      shared_gate_codes, shared_gate_meta, shared_down_codes, shared_down_meta,
+                      static_cast<const uint16_t*>(shared_logit), static_cast<const float*>(silu),
+                      static_cast<const uint16_t*>(sigmoid), 127, nullptr, nullptr, static_cast<uint16_t*>(output),
+                      static_cast<uint32_t*>(flags), T, Tcap, stream);
+}
+
+extern "C" int ornith_mi355x_abi_version(void) { return 1; }
+
+// =============================================================================
+// Dense
+// =============================================================================
+extern "C" uint32_t ornith_dense_g256_abi_version(void) { return 1; }
+
+extern "C" hipError_t ornith_dense_g256_get_layout(int Mcap, int N, int K, int bits, OrnithDenseG256Layout* out) {
+    if (!out || Mcap < 0 || Mcap > kMaxTokens || !dense_shape(N, K) || bits != 8) return hipErrorInvalidValue;
+    *out = dense_layout(Mcap, N, K);
+    return hipSuccess;
+}
+
+extern "C" hipError_t ornith_dense_g256_launch(const void* input, const void* codes, const void* metadata,
+                                               void* workspace, size_t bytes, void* output, void* flags, int M, int Mcap,
+                                               int N, int K, int bits, int transform, int geometry,
+                                               hipStream_t stream) {
+    OrnithDenseG256Layout l{};
+    if (ornith_dense_g256_get_layout(Mcap, N, K, bits, &l) != hipSuccess || M < 0 || M > Mcap || transform != 128 ||
+        geometry < 0 || geometry > 2)
+        return hipErrorInvalidValue;
+    if (M == 0) return hipSuccess;
+    if (bytes < l.workspace_bytes) return hipErrorInvalidValue;
+    const void* ptr[] = {input, codes, metadata, workspace, output, flags};
+    const size_t sizes[] = {size_t(M) * K * 2, size_t(N) * K / 2, size_t(N) * (K / kGroup) * 4, bytes,
+                            size_t(M) * N * 2, 4};
+    const size_t align[] = {8, 16, 4, 256, 2, 4};
+    if (!check_ranges(ptr, sizes, align, 6, 3)) return hipErrorInvalidValue;
+    return dense_run(input, codes, metadata, workspace, l, at<float>(workspace, l.projection),
+                     static_cast<uint16_t*>(output), static_cast<uint32_t*>(flags), M, N, K, 16, stream);
+}
+
+extern "C" hipError_t ornith_dense_g256_prepare_bf16(const void* input, const void* codes, const void* metadata,
+                                                     void* transformed, void* weights, void* flags, int M, int N, int K,
+                                                     hipStream_t stream) {
+    if (M < 0 || M > kMaxTokens || !dense_shape(N, K)) return hipErrorInvalidValue;
+    if (M == 0) return hipSuccess;
+    const void* ptr[] = {input, codes, metadata, transformed, weights, flags};
+    const size_t sizes[] = {size_t(M) * K * 2, size_t(N) * K / 2, size_t(N) * (K / kGroup) * 4, size_t(M) * K * 2,
+                            size_t(N) * K * 2, 4};
+    const size_t align[] = {8, 4, 4, 8, 16, 4};
+    if (!check_ranges(ptr, sizes, align, 6, 3)) return hipErrorInvalidValue;
+    auto sticky = static_cast<uint32_t*>(flags);
+    TRY(launch_transform_bf16(static_cast<const uint16_t*>(input), M, K, static_cast<uint16_t*>(transformed), sticky,
+                              stream));
+    return launch_dequantize_bf16(static_cast<const uint32_t*>(codes), static_cast<const uint32_t*>(metadata), N, K, 16,
+                                  static_cast<uint16_t*>(weights), sticky, stream);
+}
+
+extern "C" hipError_t ornith_dense_g256_launch_n32(const void* input, const void* codes, const void* metadata,
+                                                   void* workspace, size_t bytes, void* output, void* flags, int M,
+                                                   int Mcap, int N, int K, int bits, int transform, int geometry,
+                                                   hipStream_t stream) {
+    OrnithDenseG256Layout l{};
+    if (M < 1 || M > 16 || M > Mcap || N % 32 || transform != 128 || geometry != 2 ||
+        ornith_dense_g256_get_layout(Mcap, N, K, bits, &l) != hipSuccess || bytes < l.workspace_bytes)
+        return hipErrorInvalidValue;
+    if (!input || !codes || !metadata || !workspace || !output || !flags || !aligned(input, 8) || !aligned(codes, 16) ||
+        !aligned(workspace, 256))
+        return hipErrorInvalidValue;
+    return dense_run(input, codes, metadata, workspace, l, at<float>(workspace, l.projection),
+                     static_cast<uint16_t*>(output), static_cast<uint32_t*>(flags), M, N, K, 32, stream);
+}
+
+extern "C" int ornith_dense_g256_n32_rows(void) { return 16; }
+
+extern "C" size_t ornith_dense_g256_head_workspace_bytes(int Mcap, int N) {
+    (void)N;
+    if (Mcap < 0 || Mcap > 64) return 0;
+    const size_t m = size_t(Mcap);
+    return align256(m * kHidden) + align256(m * (kHidden / kGroup) * 2) + align256(m * (kHidden / kGroup) * 4);
+}
+
+extern "C" hipError_t ornith_dense_g256_head_launch(const void* input, const void* codes, const void* metadata,
+                                                    void* workspace, size_t bytes, void* logits_f32, void* logits_bf16,
+                                                    void* argmax_i64, void* flags, int M, int Mcap, int N,
+                                                    hipStream_t stream) {
+    if (Mcap < 1 || Mcap > 64 || M < 0 || M > Mcap || N <= 0 || N % 32 || N > 262144) return hipErrorInvalidValue;
+    if (bytes < ornith_dense_g256_head_workspace_bytes(Mcap, N)) return hipErrorInvalidValue;
+    if (M == 0) return hipSuccess;
+    if (!input || !codes || !metadata || !workspace || !logits_f32 || !argmax_i64 || !flags || !aligned(input, 8) ||
+        !aligned(codes, 16) || !aligned(workspace, 256) || !aligned(logits_f32, 4) || !aligned(argmax_i64, 8))
+        return hipErrorInvalidValue;
+    OrnithDenseG256Layout l{};
+    const size_t m = size_t(Mcap);
+    l.low = 0;
+    l.scales = align256(m * kHidden);
+    l.sums = l.scales + align256(m * (kHidden / kGroup) * 2);
+    TRY(dense_run(input, codes, metadata, workspace, l, static_cast<float*>(logits_f32),
+                  static_cast<uint16_t*>(logits_bf16), static_cast<uint32_t*>(flags), M, N, kHidden, 32, stream));
+    argmax_kernel<<<M, 256, 0, stream>>>(static_cast<const float*>(logits_f32), N, static_cast<int64_t*>(argmax_i64));
+    return hipGetLastError();
+}

@@ -1,0 +1,192 @@
+// Shared device helpers for the MI355X (gfx950, wave64) Ornith G256 kernels.
+//
+// Numerics contract (restated from kernels/dense/dense_g256_api.h:32-38 and
+// kernels/routed_storage/routed_storage_n32_consumer.cpp:12-21): fp32
+// arithmetic is evaluated operation by operation (the library is compiled
+// with -ffp-contract=off), fp32 division is correctly rounded, bf16 and fp16
+// conversions round to nearest even.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <hip/hip_fp16.h>
+#include <stdint.h>
+#include <stddef.h>
+
+namespace ornith {
+
+constexpr int kExperts = 256, kTop = 8, kHidden = 2048, kInter = 512, kGroup = 256;
+constexpr int kShared = kExperts;            // bank id of the always-on shared expert
+constexpr int kWave = 64;
+
+// 1/sqrt(128) with the bit pattern 0x3db504f3 (routed_storage_n32_consumer.cpp:12).
+constexpr float kInvSqrt128 = 0x1.6a09e6p-4f;
+
+// Sticky flag bits of the routed ABI (routed_storage_n32_consumer.cpp:33-183).
+enum : uint32_t {
+    kFlagNonfiniteInput = 1, kFlagInvalidActivation = 2, kFlagInvalidExpert = 4,
+    kFlagNonfiniteProjection = 8, kFlagNonfiniteMiddle = 16, kFlagNonfiniteOutput = 32,
+};
+// Dense/head flag bits (dense_g256_api.h:14-19, head_i8_tile_api.h:16-21).
+enum : uint32_t {
+    kDenseNonfiniteInput = 1, kDenseInvalidActivation = 2,
+    kDenseNonfiniteProjection = 4, kDenseNonfiniteBf16 = 8,
+};
+
+__host__ __device__ inline size_t align256(size_t n) { return (n + 255) & ~size_t(255); }
+template <class T> __host__ __device__ inline T* at(void* base, size_t offset) {
+    return reinterpret_cast<T*>(static_cast<uint8_t*>(base) + offset);
+}
+
+__device__ __forceinline__ float fdiv_rn(float a, float b) { return __fdiv_rn(a, b); }
+__device__ __forceinline__ float bf16_bits_to_f32(uint32_t bits) { return __uint_as_float(bits << 16); }
+__device__ __forceinline__ uint16_t f32_to_bf16_bits(float v) {
+    uint32_t b = __float_as_uint(v);
+    if ((b & 0x7fffffffu) > 0x7f800000u) return uint16_t((b >> 16) | 0x40u);
+    return uint16_t((b + 0x7fffu + ((b >> 16) & 1u)) >> 16);
+}
+__device__ __forceinline__ float bf16_round(float v) { return bf16_bits_to_f32(f32_to_bf16_bits(v)); }
+__device__ __forceinline__ float f16_bits_to_f32(uint32_t bits) {
+    return __half2float(__ushort_as_half(uint16_t(bits)));
+}
+__device__ __forceinline__ uint16_t f32_to_f16_bits(float v) { return __half_as_ushort(__float2half_rn(v)); }
+
+// Deterministic exp with the reference's Taylor coefficients and step order
+// (kernels/routed_storage/portable_exp.h:6-26).
+__device__ __forceinline__ float portable_exp(float x) {
+    if (isnan(x)) return x;
+    if (x <= -104.f) return 0.f;
+    if (x >= 89.f) return __builtin_huge_valf();
+    const float n_float = __builtin_rintf(x * 0x1.715476p+0f);
+    const int n = static_cast<int>(n_float);
+    const float high = n_float * 0x1.62e400p-1f;
+    const float low = n_float * 0x1.7f7d1cp-20f;
+    const float r = (x - high) - low;
+    float p = 0x1.a01a02p-16f;
+    p = p * r + 0x1.a01a02p-13f;
+    p = p * r + 0x1.6c16c2p-10f;
+    p = p * r + 0x1.111112p-7f;
+    p = p * r + 0x1.555556p-5f;
+    p = p * r + 0x1.555556p-3f;
+    p = p * r + 0x1p-1f;
+    p = p * r + 0x1p+0f;
+    p = p * r + 0x1p+0f;
+    return __builtin_ldexpf(p, n);
+}
+__device__ __forceinline__ float silu_portable(float g) { return fdiv_rn(g, 1.f + portable_exp(-g)); }
+
+// ---- wave64 cross-lane helpers --------------------------------------------
+__device__ __forceinline__ float shfl_xor_f(float v, int mask) { return __shfl_xor(v, mask, kWave); }
+__device__ __forceinline__ int shfl_xor_i(int v, int mask) { return __shfl_xor(v, mask, kWave); }
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+    for (int m = 32; m > 0; m >>= 1) v = fmaxf(v, shfl_xor_f(v, m));
+    return v;
+}
+__device__ __forceinline__ int wave_sum_i(int v) {
+#pragma unroll
+    for (int m = 32; m > 0; m >>= 1) v += shfl_xor_i(v, m);
+    return v;
+}
+// Butterfly sum over the 64 lanes: lane l adds lane l^m for m = 32..1.  Every
+// lane ends with the same bits because fp32 addition is commutative.
+__device__ __forceinline__ float wave_butterfly_sum(float v) {
+#pragma unroll
+    for (int m = 32; m > 0; m >>= 1) v = v + shfl_xor_f(v, m);
+    return v;
+}
+
+__device__ __forceinline__ void flag_or(uint32_t* sticky, uint32_t bits) {
+    if (bits) atomicOr(sticky, bits);
+}
+
+// ---- 4-bit weight unpacking -----------------------------------------------
+// A packed code word holds K values 8c..8c+7, low nibble first
+// (dense_g256_api.h:25).  Even codes (k = 8c, 8c+2, 8c+4, 8c+6) go to the
+// bytes of the first word and odd codes to the bytes of the second: this is
+// the byte order the A8 activation layout uses, so both feed v_dot4 and the
+// i8 MFMA directly.
+__device__ __forceinline__ int code_even(uint32_t w) { return int(w & 0x0f0f0f0fu); }
+__device__ __forceinline__ int code_odd(uint32_t w) { return int((w >> 4) & 0x0f0f0f0fu); }
+__device__ __forceinline__ int dot4(int a, int b, int c) { return __builtin_amdgcn_sdot4(a, b, c, false); }
+
+// ---- Layout of quantized activations (this build's own format) ------------
+// For row r and K chunk c (8 values k = 8c..8c+7) two int32 words are stored
+// at word index r*(K/4) + 2c and 2c+1: bytes (q[8c], q[8c+2], q[8c+4], q[8c+6])
+// and (q[8c+1], q[8c+3], q[8c+5], q[8c+7]).  Per 256-group: fp16 scale and
+// int32 sum of q, as in the reference (routed_storage_n32_consumer.cpp:75).
+
+// Group-256 activation quantisation on one wave.  Lane l holds the four
+// transformed values k = 4l..4l+3 of the group in v[0..3].  Implements the
+// absmax / fp16 scale / round-even / clamp recipe of
+// routed_storage_n32_consumer.cpp:44-76 with any qmax, writes this build's
+// int8 layout (64 words), the scale and the sum.
+template <int QMAX>
+__device__ __forceinline__ void quantize_group_wave(float v[4], uint32_t* words, uint16_t* scale_out,
+                                                    int32_t* sum_out, uint32_t& flags, uint32_t invalid_flag) {
+    const int lane = threadIdx.x & 63;
+    float absmax = 0.f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        if (!isfinite(v[i])) { flags |= invalid_flag; v[i] = 0.f; }
+        absmax = fmaxf(absmax, fabsf(v[i]));
+    }
+    absmax = wave_max(absmax);
+    const float raw = fdiv_rn(absmax, float(QMAX));
+    const bool valid = isfinite(raw) && raw <= 65504.f;
+    if (!valid) flags |= invalid_flag;
+    const bool zero = absmax == 0.f || !valid;
+    const uint16_t sbits = f32_to_f16_bits(zero ? 1.f : fmaxf(raw, 0x1p-14f));
+    const float scale = f16_bits_to_f32(sbits);
+    int q[4], sum = 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        int t = zero ? 0 : __float2int_rn(fdiv_rn(v[i], scale));
+        t = t < -QMAX ? -QMAX : (t > QMAX ? QMAX : t);
+        q[i] = t;
+        sum += t;
+    }
+    sum = wave_sum_i(sum);
+    // lane 2c holds q[8c..8c+3], lane 2c+1 holds q[8c+4..8c+7].
+    const uint32_t ev = (uint32_t(q[0]) & 255u) | ((uint32_t(q[2]) & 255u) << 8);
+    const uint32_t od = (uint32_t(q[1]) & 255u) | ((uint32_t(q[3]) & 255u) << 8);
+    const uint32_t pev = uint32_t(__shfl_xor(int(ev), 1, kWave));
+    const uint32_t pod = uint32_t(__shfl_xor(int(od), 1, kWave));
+    const uint32_t word = (lane & 1) ? (pod | (od << 16)) : (ev | (pev << 16));
+    words[lane] = word;
+    if (lane == 0) { *scale_out = sbits; *sum_out = sum; }
+}
+
+// 128-point Hadamard transform of two blocks held by one wave: lane l holds
+// k = 4l..4l+3 of a 256-value group (block = l/32).  Seven ascending
+// butterflies exactly as routed_storage_n32_consumer.cpp:34-41, then the
+// 0x3db504f3 scale.
+__device__ __forceinline__ void h128_wave(float v[4]) {
+    const int lane = threadIdx.x & 63;
+    // step 1 (k bit 0)
+    float a0 = v[0] + v[1], a1 = v[0] - v[1], a2 = v[2] + v[3], a3 = v[2] - v[3];
+    // step 2 (k bit 1)
+    v[0] = a0 + a2; v[2] = a0 - a2; v[1] = a1 + a3; v[3] = a1 - a3;
+    // steps 4..64 (k bits 2..6 = lane bits 0..4)
+#pragma unroll
+    for (int m = 1; m < 32; m <<= 1) {
+        const bool upper = lane & m;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const float p = shfl_xor_f(v[i], m);
+            v[i] = upper ? (p - v[i]) : (v[i] + p);
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) v[i] = v[i] * kInvSqrt128;
+}
+
+// fp32 group tree term of one (row, column, group) (dense_g256_api.h:35-37):
+// RN(sw*RN(sa*dot)) + RN(off*RN(sa*sum)), returned unrounded-sum-ready.
+__device__ __forceinline__ float tree_term(int dot, float sa, float scaled_sum, uint32_t meta) {
+    const float sw = f16_bits_to_f32(meta & 0xffffu), off = f16_bits_to_f32(meta >> 16);
+    const float scaled_dot = sa * float(dot);
+    const float product = sw * scaled_dot;
+    const float correction = off * scaled_sum;
+    return product + correction;
+}
+
+}  // namespace ornith

@@ -1,0 +1,87 @@
+// Internal launch wrappers shared by the C-ABI translation units.  Every
+// wrapper enqueues on the caller's stream and returns hipGetLastError().
+#pragma once
+#include "common.hpp"
+
+namespace ornith {
+
+// A run of consecutive entries of the permuted route list that all use one
+// weight bank (expert id 0..255, or kShared for the shared expert).
+struct Segment { int32_t bank, first, count, tile_base; };
+
+// Scratch used by the permutation step, carved out of the caller's workspace.
+struct PermuteScratch {
+    int32_t* block_counts;   // [blocks, banks]
+    int32_t* counts;         // [banks]
+    int32_t* offsets;        // [banks + 1]
+    int32_t* routes;         // [routes] permuted route ids
+    Segment* segments;       // [banks]
+    int32_t* meta;           // [4]: segment count, mfma tile count, ...
+    int32_t* tiles;          // [max tiles] segment index << 16 | tile-in-segment
+};
+
+// ---- activations -----------------------------------------------------------
+// H128 + group quantisation of bf16 rows [rows, K] (row stride in elements).
+// ids != nullptr: routed gate input, tokens without a live id are zeroed
+// (routed_storage_n32_consumer.cpp:24-29).
+hipError_t launch_act_bf16(const uint16_t* x, int64_t stride, int rows, int K, int qmax,
+                           const int32_t* ids, uint32_t* words, uint16_t* scales, int32_t* sums,
+                           uint32_t* sticky, uint32_t flag_input, uint32_t flag_act, hipStream_t s);
+// Middle (SiLU(gate) * up) + H128 + quantisation for RS route rows of
+// gate_y [RS, 1024].  Rows >= R are shared-expert rows (table SiLU, bf16
+// rounding) when silu_table != nullptr.
+hipError_t launch_act_middle(const float* gate_y, int RS, int R, const int32_t* ids, int qmax,
+                             const float* silu_table, uint32_t* words, uint16_t* scales,
+                             int32_t* sums, uint32_t* sticky, hipStream_t s);
+
+// ---- routing ---------------------------------------------------------------
+hipError_t launch_router(const uint16_t* x, int64_t stride, int T, const uint16_t* w, int nrows,
+                         const float* bias, float* logits, int64_t logit_stride, hipStream_t s);
+hipError_t launch_topk(const float* logits, int64_t logit_stride, int T, float* weights, int32_t* ids,
+                       const float* shared_logit_f32, int64_t shared_stride, uint16_t* shared_logit_bf16,
+                       hipStream_t s);
+// Stable counting sort of route ids by bank.  Routes 0..R-1 use ids[r];
+// when with_shared, routes R..R+T-1 use the shared bank.
+size_t permute_scratch_bytes(int Rcap, int Tcap);
+PermuteScratch carve_permute(void* base, int Rcap, int Tcap);
+hipError_t launch_permute(const int32_t* ids, int R, int T, bool with_shared, const PermuteScratch& p,
+                          uint32_t* sticky, int mfma_rows, hipStream_t s);
+
+// ---- projections -----------------------------------------------------------
+enum class Out { Routed, Dense };
+struct ProjArgs {
+    const uint32_t* codes; const uint32_t* meta;             // routed or dense bank
+    const uint32_t* shared_codes; const uint32_t* shared_meta;
+    int64_t bank_words, bank_meta_words;                       // per-expert strides
+    const Segment* segments; const int32_t* nseg;             // device segment table
+    const int32_t* routes;                                      // permuted route ids
+    int row_mode;                                               // 0: row = route, 1: gate row (route/8 or route-R)
+    int R;
+    int dense_rows;            // rows when segments == nullptr (dense: one bank, rows 0..M-1)
+    const uint32_t* act_words; const uint16_t* act_scales; const int32_t* act_sums;
+    float* out;               // f32 [rows, N]
+    uint16_t* out_bf16;       // dense: bf16 [rows, N]
+    int N, K, tile;           // tile: 16 or 32 (bank layout)
+    uint32_t* sticky;
+    uint32_t flag_projection, flag_bf16;
+};
+hipError_t launch_project_gemv(const ProjArgs& a, int max_segments, Out mode, hipStream_t s);
+hipError_t launch_project_mfma(const ProjArgs& a, const int32_t* tiles, int max_tiles, hipStream_t s);
+
+// ---- combination -------------------------------------------------------------
+// out[t] = bf16(sum over valid slots of route_out[8t+s] * w[8t+s]); optional
+// fp32 diagnostic; optional shared output and layer sum.
+hipError_t launch_reduce(const float* route_out, const float* weights, const int32_t* ids, int T,
+                         float* final_f32, uint16_t* out, const uint16_t* shared_logit,
+                         const uint16_t* sigmoid_table, uint16_t* shared_out, uint16_t* layer_out,
+                         uint32_t* sticky, hipStream_t s);
+
+// ---- dense bf16 preparation (dense_g256_consumer.cpp:192-246) ---------------
+hipError_t launch_transform_bf16(const uint16_t* x, int M, int K, uint16_t* y, uint32_t* sticky, hipStream_t s);
+hipError_t launch_dequantize_bf16(const uint32_t* codes, const uint32_t* meta, int N, int K, int tile,
+                                  uint16_t* w, uint32_t* sticky, hipStream_t s);
+
+// ---- fill (graph-capture safe replacement for hipMemsetAsync) -------------------
+hipError_t launch_fill_u32(uint32_t* p, size_t n, uint32_t v, hipStream_t s);
+
+}  // namespace ornith

@@ -1,0 +1,346 @@
+// Router logits, softmax/top-8/renormalise, token permutation and the
+// slot-order unpermute.
+//
+// Router and top-k replace the reference's Triton row-dot
+// (iu4_correctness/gates_projection.py:18-26,36-42) and vLLM's topk_softmax
+// (contract moe_base.py:57-64, dtypes :53-54).  Both reduction orders are
+// declared by this build (the reference's are compiler/library chosen):
+//   logit[t,e] = bias[e] + butterfly over 64 lanes of lane partials, lane l
+//   accumulating fma(x[k], w[k], acc) over k = 8c..8c+7 for
+//   c = l, l+64, l+128, l+192 (bf16*bf16 products are exact in fp32, so the
+//   fma equals a separate multiply and add).
+// Permute replaces histogram/scan_routes/scatter/partition
+// (routed_storage_n32_prefill.h:19-42) with a deterministic stable order.
+#include "kernels.hpp"
+
+namespace ornith {
+
+// ---------------------------------------------------------------------------
+// Router logits.  Block = 4 waves; wave w owns router row blockIdx.x*4+w and
+// keeps it in registers; the block walks a slice of tokens staged in LDS.
+// ---------------------------------------------------------------------------
+constexpr int kRouterTokens = 16;
+
+__global__ __launch_bounds__(256) void router_kernel(const uint16_t* __restrict__ x, int64_t stride, int T,
+                                                     const uint16_t* __restrict__ w, int nrows,
+                                                     const float* __restrict__ bias, float* __restrict__ logits,
+                                                     int64_t logit_stride) {
+    __shared__ uint4 xs[kRouterTokens][256];     // 16 tokens x 2048 bf16
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    const int row = blockIdx.x * 4 + wv;
+    const int t0 = blockIdx.y * kRouterTokens;
+    const int nt = min(kRouterTokens, T - t0);
+    for (int i = threadIdx.x; i < nt * 256; i += 256) {
+        const int t = i >> 8, c = i & 255;
+        xs[t][c] = *reinterpret_cast<const uint4*>(x + (t0 + t) * stride + c * 8);
+    }
+    uint4 wr[4];
+    if (row < nrows) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) wr[i] = *reinterpret_cast<const uint4*>(w + size_t(row) * kHidden + (i * 64 + lane) * 8);
+    }
+    __syncthreads();
+    if (row >= nrows) return;
+    const float b = bias && row < kExperts ? bias[row] : 0.f;
+    for (int t = 0; t < nt; ++t) {
+        float acc = 0.f;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const uint4 xv = xs[t][i * 64 + lane];
+            const uint32_t xw[4] = {xv.x, xv.y, xv.z, xv.w};
+            const uint32_t ww[4] = {wr[i].x, wr[i].y, wr[i].z, wr[i].w};
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                acc = __builtin_fmaf(bf16_bits_to_f32(xw[j] & 0xffffu), bf16_bits_to_f32(ww[j] & 0xffffu), acc);
+                acc = __builtin_fmaf(bf16_bits_to_f32(xw[j] >> 16), bf16_bits_to_f32(ww[j] >> 16), acc);
+            }
+        }
+        acc = wave_butterfly_sum(acc);
+        if (bias && row < kExperts) acc = acc + b;
+        if (lane == 0) logits[size_t(t0 + t) * logit_stride + row] = acc;
+    }
+}
+
+hipError_t launch_router(const uint16_t* x, int64_t stride, int T, const uint16_t* w, int nrows, const float* bias,
+                         float* logits, int64_t logit_stride, hipStream_t s) {
+    if (T <= 0) return hipSuccess;
+    const dim3 grid((nrows + 3) / 4, (T + kRouterTokens - 1) / kRouterTokens);
+    router_kernel<<<grid, 256, 0, s>>>(x, stride, T, w, nrows, bias, logits, logit_stride);
+    return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
+// Softmax / top-8 / renormalise, one wave per token.  Declared order:
+// m = max; e = pexp(l - m); s = butterfly over lanes of ((e[l] + e[l+64]) +
+// e[l+128]) + e[l+192]; p = e / s; pick the largest p eight times (ties to
+// the lower id); weights p / (slot-order sum of the picked p).
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void topk_kernel(const float* __restrict__ logits, int64_t logit_stride, int T,
+                                                   float* __restrict__ weights, int32_t* __restrict__ ids,
+                                                   const float* __restrict__ shared_logit, int64_t shared_stride,
+                                                   uint16_t* __restrict__ shared_bf16) {
+    const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (t >= T) return;
+    const int lane = threadIdx.x & 63;
+    float v[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) v[i] = logits[size_t(t) * logit_stride + lane + 64 * i];
+    float m = fmaxf(fmaxf(v[0], v[1]), fmaxf(v[2], v[3]));
+    m = wave_max(m);
+    float e[4], p[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) e[i] = portable_exp(v[i] - m);
+    float part = e[0];
+#pragma unroll
+    for (int i = 1; i < 4; ++i) part = part + e[i];
+    const float sum = wave_butterfly_sum(part);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) p[i] = fdiv_rn(e[i], sum);
+    bool taken[4] = {false, false, false, false};
+    float pick_p[kTop];
+    int pick_id[kTop];
+#pragma unroll
+    for (int j = 0; j < kTop; ++j) {
+        float bp = -1.f;
+        int bi = 0x7fffffff;
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            if (!taken[i] && p[i] > bp) { bp = p[i]; bi = lane + 64 * i; }
+#pragma unroll
+        for (int msk = 32; msk > 0; msk >>= 1) {
+            const float op = shfl_xor_f(bp, msk);
+            const int oi = shfl_xor_i(bi, msk);
+            if (op > bp || (op == bp && oi < bi)) { bp = op; bi = oi; }
+        }
+        pick_p[j] = bp;
+        pick_id[j] = bi;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) if (bi == lane + 64 * i) taken[i] = true;
+    }
+    if (lane == 0) {
+        float tot = 0.f;
+#pragma unroll
+        for (int j = 0; j < kTop; ++j) tot = tot + pick_p[j];
+#pragma unroll
+        for (int j = 0; j < kTop; ++j) {
+            weights[size_t(t) * kTop + j] = fdiv_rn(pick_p[j], tot);
+            ids[size_t(t) * kTop + j] = pick_id[j];
+        }
+        if (shared_bf16) shared_bf16[t] = f32_to_bf16_bits(shared_logit[size_t(t) * shared_stride]);
+    }
+}
+
+hipError_t launch_topk(const float* logits, int64_t logit_stride, int T, float* weights, int32_t* ids,
+                       const float* shared_logit, int64_t shared_stride, uint16_t* shared_bf16, hipStream_t s) {
+    if (T <= 0) return hipSuccess;
+    topk_kernel<<<(T + 3) / 4, 256, 0, s>>>(logits, logit_stride, T, weights, ids, shared_logit, shared_stride,
+                                           shared_bf16);
+    return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
+// Permutation: stable counting sort of routes by bank.
+// banks: 0..255 routed experts, 256 = shared expert (routes R..R+T-1).
+// Produces counts, exclusive offsets, the permuted route list, one Segment
+// per non-empty bank (ascending bank order) and the MFMA tile list.
+// ---------------------------------------------------------------------------
+constexpr int kBanks = kExperts + 1;
+constexpr int kPermBlock = 256;
+
+__device__ __forceinline__ int route_bank(const int32_t* ids, int r, int R, uint32_t& flags) {
+    if (r >= R) return kShared;
+    const int id = ids[r];
+    if (id >= 0 && id < kExperts) return id;
+    if (id != -1) flags |= kFlagInvalidExpert;
+    return -1;
+}
+
+size_t permute_scratch_bytes(int Rcap, int Tcap) {
+    const size_t rall = size_t(Rcap) + size_t(Tcap);
+    const size_t blocks = (rall + kPermBlock - 1) / kPermBlock;
+    size_t bytes = 0;
+    bytes += align256(blocks * kBanks * 4);
+    bytes += align256(kBanks * 4);
+    bytes += align256((kBanks + 1) * 4);
+    bytes += align256(rall * 4);
+    bytes += align256(kBanks * sizeof(Segment));
+    bytes += align256(4 * 4);
+    bytes += align256((rall + kBanks) * 4);
+    return bytes;
+}
+
+PermuteScratch carve_permute(void* base, int Rcap, int Tcap) {
+    const size_t rall = size_t(Rcap) + size_t(Tcap);
+    const size_t blocks = (rall + kPermBlock - 1) / kPermBlock;
+    PermuteScratch p{};
+    size_t off = 0;
+    auto take = [&](size_t bytes) { void* q = at<void>(base, off); off += align256(bytes); return q; };
+    p.block_counts = static_cast<int32_t*>(take(blocks * kBanks * 4));
+    p.counts = static_cast<int32_t*>(take(kBanks * 4));
+    p.offsets = static_cast<int32_t*>(take((kBanks + 1) * 4));
+    p.routes = static_cast<int32_t*>(take(rall * 4));
+    p.segments = static_cast<Segment*>(take(kBanks * sizeof(Segment)));
+    p.meta = static_cast<int32_t*>(take(4 * 4));
+    p.tiles = static_cast<int32_t*>(take((rall + kBanks) * 4));
+    return p;
+}
+
+__global__ __launch_bounds__(kPermBlock) void permute_count_kernel(const int32_t* __restrict__ ids, int R, int Rall,
+                                                                   int32_t* __restrict__ block_counts,
+                                                                   uint32_t* sticky) {
+    __shared__ int cnt[kBanks];
+    for (int i = threadIdx.x; i < kBanks; i += kPermBlock) cnt[i] = 0;
+    __syncthreads();
+    const int r = blockIdx.x * kPermBlock + threadIdx.x;
+    uint32_t flags = 0;
+    if (r < Rall) {
+        const int b = route_bank(ids, r, R, flags);
+        if (b >= 0) atomicAdd(&cnt[b], 1);
+    }
+    flag_or(sticky, flags);
+    __syncthreads();
+    for (int i = threadIdx.x; i < kBanks; i += kPermBlock) block_counts[size_t(blockIdx.x) * kBanks + i] = cnt[i];
+}
+
+// Single block of 512 threads: per-bank exclusive running sums over blocks,
+// offsets, segments and the MFMA tile list.
+__global__ __launch_bounds__(512) void permute_scan_kernel(int nblocks, int32_t* __restrict__ block_counts,
+                                                           int32_t* __restrict__ counts, int32_t* __restrict__ offsets,
+                                                           Segment* __restrict__ segments, int32_t* __restrict__ meta,
+                                                           int32_t* __restrict__ tiles, int mfma_rows) {
+    __shared__ int a[512], b[512], c[512];
+    const int e = threadIdx.x;
+    int total = 0;
+    if (e < kBanks) {
+        for (int blk = 0; blk < nblocks; ++blk) {
+            const int v = block_counts[size_t(blk) * kBanks + e];
+            block_counts[size_t(blk) * kBanks + e] = total;
+            total += v;
+        }
+        counts[e] = total;
+    }
+    const int ntile = (e < kBanks && total > 0) ? (total + mfma_rows - 1) / mfma_rows : 0;
+    a[e] = e < kBanks ? total : 0;
+    b[e] = (e < kBanks && total > 0) ? 1 : 0;
+    c[e] = ntile;
+    __syncthreads();
+    // inclusive Hillis-Steele scans of counts, non-empty flags and tile counts
+    for (int d = 1; d < 512; d <<= 1) {
+        const int va = e >= d ? a[e - d] : 0, vb = e >= d ? b[e - d] : 0, vc = e >= d ? c[e - d] : 0;
+        __syncthreads();
+        a[e] += va; b[e] += vb; c[e] += vc;
+        __syncthreads();
+    }
+    if (e < kBanks) {
+        const int off = a[e] - total;
+        offsets[e] = off;
+        if (e == kBanks - 1) offsets[kBanks] = a[e];
+        if (total > 0) {
+            const int seg = b[e] - 1;
+            const int tile_base = c[e] - ntile;
+            segments[seg] = Segment{e, off, total, tile_base};
+            for (int k = 0; k < ntile; ++k) tiles[tile_base + k] = (seg << 16) | k;
+        }
+    }
+    if (e == 0) { meta[0] = b[kBanks - 1]; meta[1] = c[kBanks - 1]; }
+}
+
+__global__ __launch_bounds__(kPermBlock) void permute_scatter_kernel(const int32_t* __restrict__ ids, int R, int Rall,
+                                                                     const int32_t* __restrict__ block_counts,
+                                                                     const int32_t* __restrict__ offsets,
+                                                                     int32_t* __restrict__ routes) {
+    __shared__ int bank_of[kPermBlock];
+    const int r = blockIdx.x * kPermBlock + threadIdx.x;
+    uint32_t dummy = 0;
+    const int b = r < Rall ? route_bank(ids, r, R, dummy) : -1;
+    bank_of[threadIdx.x] = b;
+    __syncthreads();
+    if (b < 0) return;
+    int rank = 0;
+    for (int j = 0; j < int(threadIdx.x); ++j) rank += bank_of[j] == b;
+    routes[offsets[b] + block_counts[size_t(blockIdx.x) * kBanks + b] + rank] = r;
+}
+
+hipError_t launch_permute(const int32_t* ids, int R, int T, bool with_shared, const PermuteScratch& p,
+                          uint32_t* sticky, int mfma_rows, hipStream_t s) {
+    const int Rall = R + (with_shared ? T : 0);
+    const int nblocks = (Rall + kPermBlock - 1) / kPermBlock;
+    permute_count_kernel<<<nblocks, kPermBlock, 0, s>>>(ids, R, Rall, p.block_counts, sticky);
+    hipError_t st = hipGetLastError();
+    if (st != hipSuccess) return st;
+    permute_scan_kernel<<<1, 512, 0, s>>>(nblocks, p.block_counts, p.counts, p.offsets, p.segments, p.meta, p.tiles,
+                                          mfma_rows);
+    st = hipGetLastError();
+    if (st != hipSuccess) return st;
+    permute_scatter_kernel<<<nblocks, kPermBlock, 0, s>>>(ids, R, Rall, p.block_counts, p.offsets, p.routes);
+    return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
+// Unpermute: slot-order reduction (routed_storage_n32_consumer.cpp:176-184,
+// 296-307).  Four columns per thread.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void reduce_kernel(const float* __restrict__ route_out,
+                                                     const float* __restrict__ weights,
+                                                     const int32_t* __restrict__ ids, int T,
+                                                     float* __restrict__ final_f32, uint16_t* __restrict__ out,
+                                                     const uint16_t* __restrict__ shared_logit,
+                                                     const uint16_t* __restrict__ sigmoid_table,
+                                                     uint16_t* __restrict__ shared_out, uint16_t* __restrict__ layer_out,
+                                                     uint32_t* sticky) {
+    const size_t idx = size_t(blockIdx.x) * 256 + threadIdx.x;   // over T * H/4
+    if (idx >= size_t(T) * (kHidden / 4)) return;
+    const int t = int(idx / (kHidden / 4));
+    const int c = int(idx % (kHidden / 4)) * 4;
+    float sum[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int s = 0; s < kTop; ++s) {
+        const int r = t * kTop + s;
+        const int id = ids[r];
+        if (id >= 0 && id < kExperts) {
+            const float w = weights[r];
+            const float4 v = *reinterpret_cast<const float4*>(route_out + size_t(r) * kHidden + c);
+            sum[0] = sum[0] + v.x * w; sum[1] = sum[1] + v.y * w;
+            sum[2] = sum[2] + v.z * w; sum[3] = sum[3] + v.w * w;
+        }
+    }
+    uint32_t flags = 0;
+    uint16_t o[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        o[i] = f32_to_bf16_bits(sum[i]);
+        if (!isfinite(sum[i]) || (o[i] & 0x7f80u) == 0x7f80u) flags |= kFlagNonfiniteOutput;
+    }
+    const size_t base = size_t(t) * kHidden + c;
+    if (final_f32) *reinterpret_cast<float4*>(final_f32 + base) = make_float4(sum[0], sum[1], sum[2], sum[3]);
+    if (out) *reinterpret_cast<uint2*>(out + base) = make_uint2(o[0] | (uint32_t(o[1]) << 16), o[2] | (uint32_t(o[3]) << 16));
+    if (sigmoid_table) {
+        const int R = T * kTop;
+        const float gate = bf16_bits_to_f32(sigmoid_table[shared_logit[t]]);
+        const float4 v = *reinterpret_cast<const float4*>(route_out + size_t(R + t) * kHidden + c);
+        const float sv[4] = {v.x * gate, v.y * gate, v.z * gate, v.w * gate};
+        uint16_t so[4], lo[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            if (!isfinite(sv[i])) flags |= kFlagNonfiniteOutput;
+            so[i] = f32_to_bf16_bits(sv[i]);
+            lo[i] = f32_to_bf16_bits(bf16_bits_to_f32(o[i]) + bf16_bits_to_f32(so[i]));
+        }
+        if (shared_out)
+            *reinterpret_cast<uint2*>(shared_out + base) = make_uint2(so[0] | (uint32_t(so[1]) << 16), so[2] | (uint32_t(so[3]) << 16));
+        if (layer_out)
+            *reinterpret_cast<uint2*>(layer_out + base) = make_uint2(lo[0] | (uint32_t(lo[1]) << 16), lo[2] | (uint32_t(lo[3]) << 16));
+    }
+    flag_or(sticky, flags);
+}
+
+hipError_t launch_reduce(const float* route_out, const float* weights, const int32_t* ids, int T, float* final_f32,
+                         uint16_t* out, const uint16_t* shared_logit, const uint16_t* sigmoid_table,
+                         uint16_t* shared_out, uint16_t* layer_out, uint32_t* sticky, hipStream_t s) {
+    const size_t n = size_t(T) * (kHidden / 4);
+    reduce_kernel<<<(n + 255) / 256, 256, 0, s>>>(route_out, weights, ids, T, final_f32, out, shared_logit,
+                                                  sigmoid_table, shared_out, layer_out, sticky);
+    return hipGetLastError();
+}
+
+}  // namespace ornith

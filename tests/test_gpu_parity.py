@@ -1,0 +1,349 @@
+"""GPU parity: every C-ABI entry against the CPU oracle, bit-exact.
+
+All calls go through the C ABI (ctypes) of the built HIP library on torch's
+current stream; the oracle only checks.  Shapes are the reference's real
+shapes (E=256, H=2048, I=512, G=256) at token counts the oracle finishes in
+seconds; larger token counts are covered by size-independent properties in
+test_gpu_properties.py.
+"""
+import ctypes as C
+
+import numpy as np
+import pytest
+
+from _ornith import (Bank, LazyExperts, bf16_normal, from_dev, moe_weights, oracle_routed, random_routing,
+                     to_dev)
+from oracle import ornith_oracle as O
+
+pytestmark = pytest.mark.gpu
+
+
+def _native():
+    from ornith_g256 import native
+    return native
+
+
+def _sync():
+    import torch
+    torch.cuda.synchronize()
+
+
+def _flags(device):
+    import torch
+    return torch.zeros(1, dtype=torch.int32, device=device)
+
+
+@pytest.fixture(scope='module')
+def moe(device):
+    w = moe_weights(1234)
+    d = {k: (to_dev(v.codes, device), to_dev(v.meta, device)) for k, v in w.items() if isinstance(v, Bank)}
+    return w, d
+
+
+# ---------------------------------------------------------------------------
+# Dense G256 (dense_g256_consumer.cpp:172-189; dense_n32 :360-378)
+# ---------------------------------------------------------------------------
+@pytest.mark.parametrize('M,N,K,tile', [(1, 6144, 2048, 16), (1, 6144, 2048, 32), (5, 1024, 2048, 16),
+                                        (16, 2048, 512, 32), (3, 48, 768, 16), (64, 1024, 4096, 16)])
+def test_dense_a8_bit_exact(device, M, N, K, tile):
+    import torch
+    native = _native()
+    print(f'dense M={M} N={N} K={K} tile={tile}', flush=True)
+    rng = np.random.default_rng(7 + M + N + K)
+    bank = Bank(rng, 0, N, K, tile=tile)
+    x = bf16_normal(rng, (M, K))
+    ref_out, ref_diag, ref_flags = O.dense_a8(x, *bank.expert())
+    layout = native.dense_layout(max(M, 16), N, K)
+    ws = torch.empty(layout.workspace_bytes, dtype=torch.uint8, device=device)
+    out = torch.empty((M, N), dtype=torch.bfloat16, device=device)
+    flags = _flags(device)
+    xd, cd, md = to_dev(x, device), to_dev(bank.codes, device), to_dev(bank.meta, device)
+    h = native.lib()
+    fn = h.ornith_dense_g256_launch if tile == 16 else h.ornith_dense_g256_launch_n32
+    st = fn(native.ptr(xd), native.ptr(cd), native.ptr(md), native.ptr(ws), ws.numel(), native.ptr(out),
+            native.ptr(flags), M, max(M, 16), N, K, 8, 128, 2, native.stream(xd))
+    assert st == 0
+    _sync()
+    np.testing.assert_array_equal(from_dev(out), ref_out)
+    diag = from_dev(ws[layout.projection:layout.projection + M * N * 4].view(torch.float32)).reshape(M, N)
+    np.testing.assert_array_equal(diag.view(np.uint32), ref_diag.view(np.uint32))
+    assert int(flags.item()) == ref_flags
+
+
+def test_dense_prepare_bf16_bit_exact(device):
+    import torch
+    native = _native()
+    rng = np.random.default_rng(99)
+    M, N, K = 7, 96, 512
+    bank = Bank(rng, 0, N, K, tile=16)
+    x = bf16_normal(rng, (M, K))
+    codes, sb, ob = bank.expert()
+    xd, cd, md = to_dev(x, device), to_dev(bank.codes, device), to_dev(bank.meta, device)
+    tx = torch.empty((M, K), dtype=torch.bfloat16, device=device)
+    wt = torch.empty((N, K), dtype=torch.bfloat16, device=device)
+    flags = _flags(device)
+    st = native.lib().ornith_dense_g256_prepare_bf16(native.ptr(xd), native.ptr(cd), native.ptr(md),
+                                                     native.ptr(tx), native.ptr(wt), native.ptr(flags), M, N, K,
+                                                     native.stream(xd))
+    assert st == 0
+    _sync()
+    np.testing.assert_array_equal(from_dev(tx), O.transform_bf16(x))
+    np.testing.assert_array_equal(from_dev(wt), O.dequantize_bf16(codes, sb, ob))
+    assert int(flags.item()) == 0
+
+
+def test_dense_nonfinite_flags(device):
+    import torch
+    native = _native()
+    rng = np.random.default_rng(5)
+    M, N, K = 2, 64, 256
+    bank = Bank(rng, 0, N, K, tile=32)
+    x = bf16_normal(rng, (M, K))
+    x[1, 17] = 0x7FC0   # NaN
+    ref_out, ref_diag, ref_flags = O.dense_a8(x, *bank.expert())
+    layout = native.dense_layout(16, N, K)
+    ws = torch.empty(layout.workspace_bytes, dtype=torch.uint8, device=device)
+    out = torch.empty((M, N), dtype=torch.bfloat16, device=device)
+    flags = _flags(device)
+    xd, cd, md = to_dev(x, device), to_dev(bank.codes, device), to_dev(bank.meta, device)
+    st = native.lib().ornith_dense_g256_launch_n32(native.ptr(xd), native.ptr(cd), native.ptr(md), native.ptr(ws),
+                                                   ws.numel(), native.ptr(out), native.ptr(flags), M, 16, N, K, 8,
+                                                   128, 2, native.stream(xd))
+    assert st == 0
+    _sync()
+    assert ref_flags & 1 and int(flags.item()) == ref_flags
+    np.testing.assert_array_equal(from_dev(out)[0], ref_out[0])
+
+
+# ---------------------------------------------------------------------------
+# Routed A8 / A4 (routed_storage_n32_consumer.cpp:319-370)
+# ---------------------------------------------------------------------------
+def _run_routed(native, device, d, x, w, ids, entry, Tcap=None):
+    import torch
+    T = x.shape[0]
+    Tcap = Tcap or max(T, 1)
+    layout = native.routed_layout(Tcap)
+    ws = torch.empty(layout.workspace_bytes, dtype=torch.uint8, device=device)
+    out = torch.empty((T, 2048), dtype=torch.bfloat16, device=device)
+    flags = _flags(device)
+    xd, wd, idd = to_dev(x, device), to_dev(w, device), to_dev(ids, device)
+    fn = getattr(native.lib(), entry)
+    st = fn(*[native.ptr(t) for t in (xd, wd, idd, d['w13'][0], d['w13'][1], d['w2'][0], d['w2'][1], ws)],
+            ws.numel(), native.ptr(out), native.ptr(flags), T, Tcap, native.stream(xd))
+    assert st == 0
+    _sync()
+    final = from_dev(ws[layout.final_f32:layout.final_f32 + T * 2048 * 4].view(torch.float32)).reshape(T, 2048)
+    return from_dev(out), final, int(flags.item())
+
+
+@pytest.mark.parametrize('T,entry,qmax', [(1, 'ornith_routed_direct_launch', 127),
+                                          (4, 'ornith_routed_direct_launch', 127),
+                                          (32, 'ornith_routed_direct_launch', 127),
+                                          (3, 'ornith_routed_direct_launch_a4', 7),
+                                          (70, 'ornith_routed_direct_launch_a4_prefill', 7),
+                                          (20, 'ornith_routed_direct_launch_a4_prefill', 127)])
+def test_routed_bit_exact(device, moe, T, entry, qmax):
+    native = _native()
+    print(f'routed T={T} {entry}', flush=True)
+    w, d = moe
+    rng = np.random.default_rng(1000 + T)
+    x = bf16_normal(rng, (T, 2048))
+    rw, ids = random_routing(rng, T)
+    ref = oracle_routed(x, rw, ids, w['w13'], w['w2'], qmax=qmax)
+    out, final, flags = _run_routed(native, device, d, x, rw, ids, entry)
+    np.testing.assert_array_equal(final.view(np.uint32), ref['final'].view(np.uint32))
+    np.testing.assert_array_equal(out, ref['out'])
+    assert flags == ref['flags']
+
+
+def test_routed_padding_and_invalid_ids(device, moe):
+    """-1 padding slots are skipped silently; out-of-range ids raise flag 4
+    and contribute nothing; a token with no live slot outputs zeros."""
+    native = _native()
+    w, d = moe
+    rng = np.random.default_rng(77)
+    T = 5
+    x = bf16_normal(rng, (T, 2048))
+    rw, ids = random_routing(rng, T)
+    ids[0, 3] = -1
+    ids[1, :] = -1
+    ids[2, 7] = 300
+    ids[4, 0] = -5
+    ref = oracle_routed(x, rw, ids, w['w13'], w['w2'])
+    out, final, flags = _run_routed(native, device, d, x, rw, ids, 'ornith_routed_direct_launch', Tcap=8)
+    np.testing.assert_array_equal(final.view(np.uint32), ref['final'].view(np.uint32))
+    np.testing.assert_array_equal(out, ref['out'])
+    assert flags == ref['flags'] == 4
+    assert not out[1].any()
+
+
+def test_routed_skewed_expert(device, moe):
+    """Many routes on one expert (more than one route batch of a block)."""
+    native = _native()
+    w, d = moe
+    rng = np.random.default_rng(78)
+    T = 40
+    x = bf16_normal(rng, (T, 2048))
+    rw, ids = random_routing(rng, T)
+    ids[:, 0] = 17          # duplicates inside a token are legal: two routes to one expert
+    ref = oracle_routed(x, rw, ids, w['w13'], w['w2'])
+    out, final, flags = _run_routed(native, device, d, x, rw, ids, 'ornith_routed_direct_launch')
+    np.testing.assert_array_equal(final.view(np.uint32), ref['final'].view(np.uint32))
+    np.testing.assert_array_equal(out, ref['out'])
+
+
+# ---------------------------------------------------------------------------
+# Shared expert as ninth slot (routed_storage_n32_consumer.cpp:385-401)
+# ---------------------------------------------------------------------------
+@pytest.mark.parametrize('T', [1, 16])
+def test_shared_tables_bit_exact(device, moe, shared_tables, T):
+    import torch
+    native = _native()
+    w, d = moe
+    silu, sigmoid = shared_tables
+    rng = np.random.default_rng(2000 + T)
+    x = bf16_normal(rng, (T, 2048))
+    rw, ids = random_routing(rng, T)
+    logit = bf16_normal(rng, (T,), 0.5)
+    s13, s2 = w['s13'], w['s2']
+    ref = O.routed_layer_shared(x, rw, ids, LazyExperts(w['w13']), w['w13'].sbits, w['w13'].obits,
+                                LazyExperts(w['w2']), w['w2'].sbits, w['w2'].obits,
+                                *s13.expert(), *s2.expert(), logit, silu, sigmoid)
+    layout = native.routed_layout(16, 'shared')
+    ws = torch.empty(layout.workspace_bytes, dtype=torch.uint8, device=device)
+    out = torch.empty((T, 2048), dtype=torch.bfloat16, device=device)
+    sh = torch.empty((T, 2048), dtype=torch.bfloat16, device=device)
+    flags = _flags(device)
+    xd = to_dev(x, device)
+    native.routed_shared_tables(xd, to_dev(rw, device), to_dev(ids, device), d['w13'][0], d['w13'][1],
+                                d['w2'][0], d['w2'][1], d['s13'][0], d['s13'][1], d['s2'][0], d['s2'][1],
+                                to_dev(logit, device), to_dev(silu, device), to_dev(sigmoid, device), ws, out, sh,
+                                flags, 16)
+    _sync()
+    np.testing.assert_array_equal(from_dev(out), ref['out'])
+    np.testing.assert_array_equal(from_dev(sh), ref['shared_out'])
+    assert int(flags.item()) == ref['flags']
+
+
+# ---------------------------------------------------------------------------
+# Router + softmax/top-8 and the whole layer
+# ---------------------------------------------------------------------------
+@pytest.mark.parametrize('T,biased', [(1, False), (33, False), (64, True)])
+def test_router_topk_bit_exact(device, moe, T, biased):
+    import torch
+    native = _native()
+    w, _ = moe
+    rng = np.random.default_rng(3000 + T)
+    x = bf16_normal(rng, (T, 2048))
+    bias = (-1.1 * np.log(1 + rng.permutation(256))).astype(np.float32) if biased else None
+    logits_ref = O.router_logits(x, np.concatenate([w['router'], w['gate']]), None)
+    if biased:
+        logits_ref[:, :256] = (logits_ref[:, :256] + bias[None, :]).astype(np.float32)
+    wref, iref, _ = O.softmax_topk(logits_ref[:, :256])
+    xd = to_dev(x, device)
+    logits = torch.empty((T, 257), dtype=torch.float32, device=device)
+    tw = torch.empty((T, 8), dtype=torch.float32, device=device)
+    ti = torch.empty((T, 8), dtype=torch.int32, device=device)
+    sl = torch.empty((T,), dtype=torch.bfloat16, device=device)
+    native.router_topk(xd, to_dev(w['router'], device), to_dev(bias, device) if biased else None,
+                       to_dev(w['gate'][0], device), logits, tw, ti, sl)
+    _sync()
+    np.testing.assert_array_equal(from_dev(logits).view(np.uint32), logits_ref.view(np.uint32))
+    np.testing.assert_array_equal(from_dev(ti), iref)
+    np.testing.assert_array_equal(from_dev(tw).view(np.uint32), wref.view(np.uint32))
+    np.testing.assert_array_equal(from_dev(sl), O.f32_to_bf16(logits_ref[:, 256]))
+
+
+@pytest.mark.parametrize('T', [1, 32])
+def test_moe_layer_bit_exact(device, moe, shared_tables, T):
+    import torch
+    native = _native()
+    w, d = moe
+    silu, sigmoid = shared_tables
+    rng = np.random.default_rng(4000 + T)
+    x = bf16_normal(rng, (T, 2048))
+    logits = O.router_logits(x, np.concatenate([w['router'], w['gate']]))
+    rw, ids, _ = O.softmax_topk(logits[:, :256])
+    logit_bf16 = O.f32_to_bf16(logits[:, 256])
+    ref = O.routed_layer_shared(x, rw, ids, LazyExperts(w['w13']), w['w13'].sbits, w['w13'].obits,
+                                LazyExperts(w['w2']), w['w2'].sbits, w['w2'].obits,
+                                *w['s13'].expert(), *w['s2'].expert(), logit_bf16, silu, sigmoid)
+    expected = O.add_bf16(ref['out'], ref['shared_out'])
+    layout = native.routed_layout(T, 'layer')
+    ws = torch.empty(layout.workspace_bytes, dtype=torch.uint8, device=device)
+    out = torch.empty((T, 2048), dtype=torch.bfloat16, device=device)
+    tw = torch.empty((T, 8), dtype=torch.float32, device=device)
+    ti = torch.empty((T, 8), dtype=torch.int32, device=device)
+    sl = torch.empty((T,), dtype=torch.bfloat16, device=device)
+    flags = _flags(device)
+    xd = to_dev(x, device)
+    native.moe_layer(xd, to_dev(w['router'], device), None, to_dev(w['gate'][0], device), d['w13'][0], d['w13'][1],
+                     d['w2'][0], d['w2'][1], d['s13'][0], d['s13'][1], d['s2'][0], d['s2'][1],
+                     to_dev(silu, device), to_dev(sigmoid, device), ws, tw, ti, sl, out, flags, T)
+    _sync()
+    np.testing.assert_array_equal(from_dev(ti), ids)
+    np.testing.assert_array_equal(from_dev(tw).view(np.uint32), rw.view(np.uint32))
+    np.testing.assert_array_equal(from_dev(out), expected)
+    assert int(flags.item()) == ref['flags']
+
+
+# ---------------------------------------------------------------------------
+# Heads
+# ---------------------------------------------------------------------------
+@pytest.mark.parametrize('M,N,dots', [(1, 256, False), (3, 1024, True), (40, 4096, False)])
+def test_head_w8_bit_exact(device, M, N, dots):
+    import torch
+    native = _native()
+    rng = np.random.default_rng(500 + M)
+    w8 = rng.integers(-127, 128, size=(N, 2048), dtype=np.int64).astype(np.int8)
+    sbits = O.f32_to_f16_bits(rng.uniform(0.0005, 0.002, size=(N, 16)).astype(np.float32))
+    x = bf16_normal(rng, (M, 2048))
+    ref_out, ref_diag, ref_flags = O.head_w8(x, w8, sbits)
+    layout = native.HeadLayout()
+    h = native.lib()
+    assert h.ornith_head_i8_tile_get_layout(64, N, C.byref(layout)) == 0
+    ws = torch.empty(layout.workspace_bytes, dtype=torch.uint8, device=device)
+    out = torch.empty((M, N), dtype=torch.bfloat16, device=device)
+    gd = torch.empty((M, N, 16), dtype=torch.int32, device=device) if dots else None
+    flags = _flags(device)
+    xd = to_dev(x, device)
+    wd = to_dev(O.head_w8_tile_layout(w8), device)
+    sd = torch.from_numpy(sbits.view(np.int16)).to(device)
+    st = h.ornith_head_i8_tile_launch(native.ptr(xd), native.ptr(wd), native.ptr(sd), native.ptr(ws), ws.numel(),
+                                      native.ptr(out), native.ptr(gd), gd.numel() * 4 if dots else 0,
+                                      native.ptr(flags), M, 64, N, 2, native.stream(xd))
+    assert st == 0
+    _sync()
+    np.testing.assert_array_equal(from_dev(out), ref_out)
+    diag = from_dev(ws[layout.projection:layout.projection + M * N * 4].view(torch.float32)).reshape(M, N)
+    np.testing.assert_array_equal(diag.view(np.uint32), ref_diag.view(np.uint32))
+    if dots:
+        tx = O.h128(O.bf16_to_f32(x))
+        q, _, _, _ = O.quantize(tx, 127, group=128)
+        ref_dots = np.einsum('mgk,ngk->mng', q.reshape(M, 16, 128).astype(np.int64),
+                             w8.reshape(N, 16, 128).astype(np.int64))
+        np.testing.assert_array_equal(from_dev(gd), ref_dots)
+    assert int(flags.item()) == ref_flags
+
+
+@pytest.mark.parametrize('M,N', [(1, 4096), (32, 151936)])
+def test_head_g256_logits_and_argmax(device, M, N):
+    import torch
+    native = _native()
+    print(f'g256 head M={M} N={N}', flush=True)
+    rng = np.random.default_rng(600 + M)
+    bank = Bank(rng, 0, N, 2048, tile=32)
+    x = bf16_normal(rng, (M, 2048))
+    ref_out, ref_diag, ref_flags = O.dense_a8(x, *bank.expert())
+    xd, cd, md = to_dev(x, device), to_dev(bank.codes, device), to_dev(bank.meta, device)
+    ws = torch.empty(native.lib().ornith_dense_g256_head_workspace_bytes(64, N), dtype=torch.uint8, device=device)
+    logits = torch.empty((M, N), dtype=torch.float32, device=device)
+    lb = torch.empty((M, N), dtype=torch.bfloat16, device=device)
+    am = torch.empty((M,), dtype=torch.int64, device=device)
+    flags = _flags(device)
+    native.dense_head(xd, cd, md, ws, logits, lb, am, flags, 64)
+    _sync()
+    np.testing.assert_array_equal(from_dev(logits).view(np.uint32), ref_diag.view(np.uint32))
+    np.testing.assert_array_equal(from_dev(lb), ref_out)
+    np.testing.assert_array_equal(from_dev(am), O.argmax_first(ref_diag))
+    assert int(flags.item()) == ref_flags
