@@ -1,0 +1,177 @@
+"""The C ABI library: loads, exports every symbol include/*.h declares, and
+validates arguments on the host exactly like the reference (no GPU calls:
+every case here returns before any launch)."""
+import ctypes as C
+import re
+from pathlib import Path
+
+import pytest
+
+ROOT = Path(__file__).resolve().parents[1]
+INVALID = 1   # hipErrorInvalidValue
+
+
+def _declared_symbols():
+    names = set()
+    for h in sorted((ROOT / 'include').glob('*.h')):
+        text = h.read_text()
+        names |= set(re.findall(r'ORNITH_EXPORT\s+[\w\s\*]+?\b(ornith_\w+)\s*\(', text))
+    return names
+
+
+@pytest.fixture(scope='module')
+def lib():
+    from ornith_g256 import native
+    return native.lib()
+
+
+def test_every_declared_symbol_is_exported(lib):
+    names = _declared_symbols()
+    assert len(names) >= 23
+    for n in sorted(names):
+        assert hasattr(lib, n), n
+    # and nothing undeclared is exported
+    import subprocess
+    from ornith_g256 import native
+    nm = subprocess.run(['nm', '-D', '--defined-only', str(native.library_path())], capture_output=True, text=True)
+    if nm.returncode == 0:
+        exported = {l.split()[-1] for l in nm.stdout.splitlines() if ' T ' in l and 'ornith_' in l}
+        assert exported == names
+
+
+def test_markers(lib):
+    assert lib.ornith_routed_storage_n32() == 32
+    assert lib.ornith_routed_prefill_output_tile() == 32
+    assert lib.ornith_dense_g256_abi_version() == 1
+    assert lib.ornith_dense_g256_n32_rows() == 16
+    assert lib.ornith_head_i8_tile_abi_version() == 1
+    assert lib.ornith_mi355x_abi_version() == 1
+
+
+def test_routed_layout_contract(lib):
+    from ornith_g256 import native
+    for tcap in (0, 1, 16, 1120, 8192):
+        l = native.routed_layout(tcap)
+        offs = [getattr(l, f) for f in native._ROUTED_FIELDS[1:]]
+        assert all(o % 256 == 0 for o in offs) and offs == sorted(offs)
+        assert l.workspace_bytes >= offs[-1] + tcap * 2048 * 4
+    layout = native.RoutedLayout()
+    assert lib.ornith_routed_direct_get_layout(8193, C.byref(layout)) == INVALID
+    assert lib.ornith_routed_direct_get_layout(-1, C.byref(layout)) == INVALID
+    assert lib.ornith_routed_direct_get_layout(4, None) == INVALID
+    assert lib.ornith_routed_shared_get_layout(17, C.byref(layout)) == INVALID
+    assert lib.ornith_routed_shared_get_layout(16, C.byref(layout)) == 0
+
+
+def _routed_args(T, Tcap, ws_bytes, ptrs=1):
+    p = C.c_void_p(0x1000) if ptrs else None
+    return [p] * 8 + [ws_bytes, p, p, T, Tcap, None]
+
+
+def test_routed_launch_validation(lib):
+    from ornith_g256 import native
+    need = native.routed_layout(8).workspace_bytes
+    for name in ('ornith_routed_direct_launch', 'ornith_routed_direct_launch_a4',
+                 'ornith_routed_direct_launch_a4_prefill'):
+        fn = getattr(lib, name)
+        assert fn(*_routed_args(0, 8, need)) == 0                 # T == 0: success, no pointer touched
+        assert fn(*_routed_args(0, 8, need, ptrs=0)) == 0
+        assert fn(*_routed_args(9, 8, need)) == INVALID           # T > Tcap
+        assert fn(*_routed_args(-1, 8, need)) == INVALID
+        assert fn(*_routed_args(1, 8, need - 1)) == INVALID       # short workspace
+        assert fn(*_routed_args(1, 8193, 1 << 40)) == INVALID     # Tcap > 8192
+        assert fn(*_routed_args(1, 8, need, ptrs=0)) == INVALID   # null pointers
+        args = _routed_args(1, 8, need)
+        args[0] = C.c_void_p(0x1001)                              # misaligned input
+        assert fn(*args) == INVALID
+
+
+def test_dense_validation(lib):
+    from ornith_g256 import native
+    l = native.DenseLayout()
+    assert lib.ornith_dense_g256_get_layout(16, 6144, 2048, 8, C.byref(l)) == 0
+    assert lib.ornith_dense_g256_get_layout(16, 6144, 2048, 4, C.byref(l)) == INVALID
+    assert lib.ornith_dense_g256_get_layout(16, 6152, 2048, 8, C.byref(l)) == INVALID   # N > 12288? no: N%16
+    assert lib.ornith_dense_g256_get_layout(16, 12304, 2048, 8, C.byref(l)) == INVALID
+    assert lib.ornith_dense_g256_get_layout(16, 248320, 2048, 8, C.byref(l)) == 0
+    assert lib.ornith_dense_g256_get_layout(16, 1024, 2000, 8, C.byref(l)) == INVALID
+    assert lib.ornith_dense_g256_get_layout(8193, 1024, 2048, 8, C.byref(l)) == INVALID
+    assert lib.ornith_dense_g256_get_layout(16, 1024, 2048, 8, C.byref(l)) == 0
+    ws = l.workspace_bytes
+    p = C.c_void_p
+    base = [p(0x10000), p(0x20000), p(0x30000), p(0x100000), ws, p(0x4000000), p(0x5000000)]
+    # M == 0 succeeds without touching pointers, even null ones
+    assert lib.ornith_dense_g256_launch(*([None] * 4 + [0] + [None] * 2), 0, 16, 1024, 2048, 8, 128, 2, None) == 0
+    assert lib.ornith_dense_g256_launch(*base, 1, 16, 1024, 2048, 8, 64, 2, None) == INVALID   # transform
+    assert lib.ornith_dense_g256_launch(*base, 1, 16, 1024, 2048, 8, 128, 3, None) == INVALID  # geometry
+    assert lib.ornith_dense_g256_launch(*base, 17, 16, 1024, 2048, 8, 128, 2, None) == INVALID  # M > Mcap
+    bad = list(base)
+    bad[5] = p(0x100000 + 64)          # output overlaps the workspace
+    assert lib.ornith_dense_g256_launch(*bad, 1, 16, 1024, 2048, 8, 128, 2, None) == INVALID
+    bad = list(base)
+    bad[4] = ws - 1
+    assert lib.ornith_dense_g256_launch(*bad, 1, 16, 1024, 2048, 8, 128, 2, None) == INVALID
+    # N32 entry: M in 1..16, N % 32, geometry 2
+    assert lib.ornith_dense_g256_launch_n32(*base, 0, 16, 1024, 2048, 8, 128, 2, None) == INVALID
+    assert lib.ornith_dense_g256_launch_n32(*base, 17, 32, 1024, 2048, 8, 128, 2, None) == INVALID
+    assert lib.ornith_dense_g256_launch_n32(*base, 1, 16, 1040, 2048, 8, 128, 2, None) == INVALID
+    assert lib.ornith_dense_g256_launch_n32(*base, 1, 16, 1024, 2048, 8, 128, 1, None) == INVALID
+    # prepare_bf16
+    assert lib.ornith_dense_g256_prepare_bf16(*([None] * 6), 0, 1024, 2048, None) == 0
+    assert lib.ornith_dense_g256_prepare_bf16(*([None] * 6), 1, 1024, 2048, None) == INVALID
+
+
+def test_head_validation(lib):
+    from ornith_g256 import native
+    l = native.HeadLayout()
+    assert lib.ornith_head_i8_tile_get_layout(64, 248320, C.byref(l)) == 0
+    assert lib.ornith_head_i8_tile_get_layout(65, 248320, C.byref(l)) == INVALID
+    assert lib.ornith_head_i8_tile_get_layout(64, 151936, C.byref(l)) == INVALID
+    ws = l.workspace_bytes
+    p = C.c_void_p
+    args = [p(0x10000), p(0x200000), p(0x30000), p(0x10000000), ws, p(0x80000000)]
+    # group_dots null iff bytes == 0
+    assert lib.ornith_head_i8_tile_launch(*args, None, 4, p(0x90000000), 1, 64, 248320, 2, None) == INVALID
+    assert lib.ornith_head_i8_tile_launch(*args, p(0xA0000000), 0, p(0x90000000), 1, 64, 248320, 2, None) == INVALID
+    assert lib.ornith_head_i8_tile_launch(*args, None, 0, p(0x90000000), 0, 64, 248320, 2, None) == 0
+    assert lib.ornith_head_i8_tile_launch(*args, None, 0, p(0x90000000), 65, 64, 248320, 2, None) == INVALID
+    # G256 head: M <= 64, N % 32
+    assert lib.ornith_dense_g256_head_workspace_bytes(65, 151936) == 0
+    need = lib.ornith_dense_g256_head_workspace_bytes(64, 151936)
+    hp = [p(0x10000), p(0x200000), p(0x30000), p(0x10000000), need, p(0x20000000), None, p(0x30000000),
+          p(0x40000000)]
+    assert lib.ornith_dense_g256_head_launch(*hp, 0, 64, 151936, None) == 0
+    assert lib.ornith_dense_g256_head_launch(*hp, 1, 64, 151920, None) == INVALID
+
+
+def test_router_and_layer_validation(lib):
+    from ornith_g256 import native
+    p = C.c_void_p(0x10000)
+    assert lib.ornith_router_topk_launch(p, 2048, p, None, None, p, p, p, None, 0, None) == 0
+    assert lib.ornith_router_topk_launch(p, 2047, p, None, None, p, p, p, None, 1, None) == INVALID
+    assert lib.ornith_router_topk_launch(p, 2048, p, None, p, p, p, p, None, 1, None) == INVALID  # no shared out
+    need = native.routed_layout(4, 'layer').workspace_bytes
+    args = [p] * 15 + [need] + [p] * 5
+    assert lib.ornith_moe_layer_launch(*args, 0, 4, None) == 0
+    assert lib.ornith_moe_layer_launch(*args, 5, 4, None) == INVALID
+    args[15] = need - 256
+    assert lib.ornith_moe_layer_launch(*args, 1, 4, None) == INVALID
+
+
+def test_configure_sizes_arena():
+    from ornith_g256 import native
+    size = native.configure({'routed_storage_n32': True}, 64, [(12288, 2048), (1024, 2048)])
+    assert size >= native.routed_layout(64).workspace_bytes
+    assert size >= (64 * 2048 + 12288 * 2048) * 2
+    with pytest.raises(ValueError):
+        native.configure({'routed_activation_bits': 4, 'routed_prefill_activation_bits': 4}, 64, [])
+    with pytest.raises(ValueError):
+        native.configure({'routed_activation_bits': 5}, 64, [])
+
+
+def test_missing_library_fails_loudly(monkeypatch, tmp_path):
+    from ornith_g256 import native
+    monkeypatch.setattr(native, '_LIB', None)
+    monkeypatch.setattr(native, 'library_path', lambda: tmp_path / 'missing.so')
+    with pytest.raises(RuntimeError, match='missing'):
+        native.lib()
