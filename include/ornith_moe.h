@@ -7,7 +7,7 @@
  * expert with rocm_unquantized_gemm + torch.sigmoid (moe_shared.py:65,
  * shared_kernel.py:101-103).  None of these has a C ABI in the reference;
  * these entries replace them with HIP kernels in a declared, fixed order:
- *   logit[t,e] = bias[e] + xor-butterfly over 64 lanes of lane partials; lane l
+ *   logit[t,e] = bias[e] + xor-butterfly (masks 1,2,4,8,16,32) over 64 lanes of lane partials; lane l
  *     accumulates fma(x[k], w[k], acc) for k = 8c..8c+7, c = l, l+64, l+128, l+192;
  *   p = pexp(l - max) / butterfly-sum; the 8 largest p (ties -> lower id) in
  *     descending order; weight_j = p_j / (slot-order sum of the 8 p).

@@ -516,9 +516,9 @@ def add_bf16(a_bits, b_bits):
 # ----------------------------------------------------------------------------
 def _butterfly64(acc):
     """xor-butterfly over the last axis (64 lanes): acc[l] + acc[l^off] for
-    off = 32,16,8,4,2,1.  Returns lane 0 (all lanes agree)."""
+    off = 1,2,4,8,16,32.  Returns lane 0 (all lanes agree)."""
     lanes = np.arange(64)
-    for off in (32, 16, 8, 4, 2, 1):
+    for off in (1, 2, 4, 8, 16, 32):
         acc = (acc + acc[..., lanes ^ off]).astype(np.float32)
     return acc[..., 0]
 

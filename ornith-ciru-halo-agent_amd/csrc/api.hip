@@ -3,6 +3,7 @@
 // nothing.  The references for each entry are in include/ornith_*.h.
 #include <limits>
 #include "kernels.hpp"
+#include "decode.hpp"
 #include "../../include/ornith_routed.h"
 #include "../../include/ornith_dense.h"
 #include "../../include/ornith_moe.h"
@@ -15,16 +16,13 @@ namespace {
 
 constexpr int kMaxTokens = 8192;
 constexpr int kGateN = 2 * kInter, kDownN = kHidden;
-constexpr int64_t kGateBankWords = int64_t(kGateN) * kHidden / 8, kGateBankMeta = int64_t(kGateN) * (kHidden / kGroup);
-constexpr int64_t kDownBankWords = int64_t(kDownN) * kInter / 8, kDownBankMeta = int64_t(kDownN) * (kInter / kGroup);
-constexpr int kLogitStride = kExperts + 1;
 
 bool aligned(const void* p, size_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
 
 // Workspace plan shared by the routed, shared-slot and whole-layer entries.
 struct RoutedPlan {
     OrnithRoutedDirectLayout l;
-    size_t permute, logits;
+    size_t permute, logits, decode;
 };
 
 RoutedPlan routed_plan(int Tcap, bool shared_slot, bool layer) {
@@ -38,7 +36,7 @@ RoutedPlan routed_plan(int Tcap, bool shared_slot, bool layer) {
     add(p.l.gate_scales, t * (kHidden / kGroup) * 2);
     add(p.l.gate_sums, t * (kHidden / kGroup) * 4);
     add(p.l.gate_y, rs * kGateN * 4);
-    add(p.l.middle, 0);
+    add(p.l.middle, rs * kInter * 4);
     add(p.l.down_x, 0);
     add(p.l.down_low, rs * kInter);                       // int8 activation words
     add(p.l.down_high, 0);
@@ -48,6 +46,7 @@ RoutedPlan routed_plan(int Tcap, bool shared_slot, bool layer) {
     add(p.l.final_f32, t * kHidden * 4);
     add(p.permute, permute_scratch_bytes(int(t * kTop), shared_slot ? int(t) : 0));
     if (layer) add(p.logits, t * kLogitStride * 4);
+    add(p.decode, decode_scratch_bytes());
     p.l.workspace_bytes = cursor;
     return p;
 }
@@ -105,6 +104,50 @@ hipError_t run_routed(const RoutedPlan& p, void* ws, const void* input, const fl
                          out, shared_logit, shared ? sigmoid : nullptr, shared_out, layer_out, sticky, s);
 }
 
+// Decode path (T <= 32): three kernels, see decode.hip.
+hipError_t run_decode(const RoutedPlan& p, void* ws, const void* input, const float* weights, const int32_t* ids,
+                      const void* gate_codes, const void* gate_meta, const void* down_codes, const void* down_meta,
+                      const void* sg_codes, const void* sg_meta, const void* sd_codes, const void* sd_meta,
+                      uint16_t* shared_logit, const float* silu, const uint16_t* sigmoid, int qmax, uint16_t* out,
+                      uint16_t* shared_out, uint16_t* layer_out, uint32_t* sticky, int T, hipStream_t s,
+                      const void* router_w = nullptr, const void* bias = nullptr, const void* shared_gate_w = nullptr,
+                      float* topk_w = nullptr, int32_t* topk_ids = nullptr) {
+    DecodeArgs a{};
+    a.T = T;
+    a.x = static_cast<const uint16_t*>(input);
+    a.router_w = static_cast<const uint16_t*>(router_w);
+    a.bias = static_cast<const float*>(bias);
+    a.shared_gate_w = static_cast<const uint16_t*>(shared_gate_w);
+    a.topk_w = topk_w;
+    a.topk_ids = topk_ids;
+    a.ids_in = ids;
+    a.reduce_w = router_w ? topk_w : weights;
+    a.reduce_ids = router_w ? topk_ids : ids;
+    a.w13_codes = static_cast<const uint32_t*>(gate_codes);
+    a.w13_meta = static_cast<const uint32_t*>(gate_meta);
+    a.w2_codes = static_cast<const uint32_t*>(down_codes);
+    a.w2_meta = static_cast<const uint32_t*>(down_meta);
+    a.s13_codes = static_cast<const uint32_t*>(sg_codes);
+    a.s13_meta = static_cast<const uint32_t*>(sg_meta);
+    a.s2_codes = static_cast<const uint32_t*>(sd_codes);
+    a.s2_meta = static_cast<const uint32_t*>(sd_meta);
+    a.silu_table = silu;
+    a.sigmoid_table = sigmoid;
+    a.shared_logit = shared_logit;
+    a.x_words = at<uint32_t>(ws, p.l.gate_low);
+    a.x_scales = at<uint16_t>(ws, p.l.gate_scales);
+    a.x_sums = at<int32_t>(ws, p.l.gate_sums);
+    a.middle = at<float>(ws, p.l.middle);
+    a.route_out = at<float>(ws, p.l.route_out);
+    carve_decode(at<void>(ws, p.decode), a);
+    a.final_f32 = out ? at<float>(ws, p.l.final_f32) : nullptr;
+    a.out = out;
+    a.shared_out = shared_out;
+    a.layer_out = layer_out;
+    a.sticky = sticky;
+    return launch_decode(a, router_w != nullptr, sg_codes != nullptr, qmax, s);
+}
+
 template <int QMAX>
 hipError_t routed_launch(const void* input, const void* weights, const void* ids, const void* gate_codes,
                          const void* gate_meta, const void* down_codes, const void* down_meta, void* workspace,
@@ -120,6 +163,11 @@ hipError_t routed_launch(const void* input, const void* weights, const void* ids
         !aligned(down_codes, 16) || !aligned(gate_meta, 4) || !aligned(down_meta, 4) || !aligned(workspace, 256) ||
         !aligned(output, 8) || !aligned(flags, 4))
         return hipErrorInvalidValue;
+    if (T <= kDecodeMaxTokens)
+        return run_decode(p, workspace, input, static_cast<const float*>(weights), static_cast<const int32_t*>(ids),
+                          gate_codes, gate_meta, down_codes, down_meta, nullptr, nullptr, nullptr, nullptr, nullptr,
+                          nullptr, nullptr, QMAX, static_cast<uint16_t*>(output), nullptr, nullptr,
+                          static_cast<uint32_t*>(flags), T, stream);
     return run_routed(p, workspace, input, static_cast<const float*>(weights), static_cast<const int32_t*>(ids),
                       gate_codes, gate_meta, down_codes, down_meta, nullptr, nullptr, nullptr, nullptr, nullptr,
                       nullptr, nullptr, QMAX, static_cast<uint16_t*>(output), nullptr, nullptr,
@@ -281,6 +329,12 @@ extern "C" hipError_t ornith_routed_direct_launch_shared_tables(
         !aligned(shared_down_codes, 16) || !aligned(workspace, 256) || !aligned(output, 8) ||
         !aligned(shared_output, 8) || !aligned(flags, 4))
         return hipErrorInvalidValue;
+    return run_decode(p, workspace, input, static_cast<const float*>(weights), static_cast<const int32_t*>(ids),
+                      gate_codes, gate_meta, down_codes, down_meta, shared_gate_codes, shared_gate_meta,
+                      shared_down_codes, shared_down_meta, static_cast<uint16_t*>(const_cast<void*>(shared_logit)),
+                      static_cast<const float*>(shared_silu), static_cast<const uint16_t*>(shared_sigmoid), 127,
+                      static_cast<uint16_t*>(output), static_cast<uint16_t*>(shared_output), nullptr,
+                      static_cast<uint32_t*>(flags), T, stream);
     return run_routed(p, workspace, input, static_cast<const float*>(weights), static_cast<const int32_t*>(ids),
                       gate_codes, gate_meta, down_codes, down_meta, shared_gate_codes, shared_gate_meta,
                       shared_down_codes, shared_down_meta, static_cast<const uint16_t*>(shared_logit),
@@ -338,6 +392,13 @@ extern "C" hipError_t ornith_moe_layer_launch(
         !aligned(down_codes, 16) || !aligned(shared_gate_codes, 16) || !aligned(shared_down_codes, 16) ||
         !aligned(workspace, 256) || !aligned(output, 8) || !aligned(flags, 4))
         return hipErrorInvalidValue;
+    if (T <= kDecodeMaxTokens)
+        return run_decode(p, workspace, input, nullptr, nullptr, gate_codes, gate_meta, down_codes, down_meta,
+                          shared_gate_codes, shared_gate_meta, shared_down_codes, shared_down_meta,
+                          static_cast<uint16_t*>(shared_logit), static_cast<const float*>(silu),
+                          static_cast<const uint16_t*>(sigmoid), 127, nullptr, nullptr, static_cast<uint16_t*>(output),
+                          static_cast<uint32_t*>(flags), T, stream, router_w, bias, shared_gate_w,
+                          static_cast<float*>(topk_weights), static_cast<int32_t*>(topk_ids));
     TRY(ornith_router_topk_launch(input, kHidden, router_w, bias, shared_gate_w, at<float>(workspace, p.logits),
                                   topk_weights, topk_ids, shared_logit, T, stream));
     return run_routed(p, workspace, input, static_cast<const float*>(topk_weights),

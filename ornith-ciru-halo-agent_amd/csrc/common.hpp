@@ -74,24 +74,65 @@ __device__ __forceinline__ float portable_exp(float x) {
 __device__ __forceinline__ float silu_portable(float g) { return fdiv_rn(g, 1.f + portable_exp(-g)); }
 
 // ---- wave64 cross-lane helpers --------------------------------------------
-__device__ __forceinline__ float shfl_xor_f(float v, int mask) { return __shfl_xor(v, mask, kWave); }
-__device__ __forceinline__ int shfl_xor_i(int v, int mask) { return __shfl_xor(v, mask, kWave); }
+// Exact lane permutation l -> l ^ M inside 32-lane halves, M in {1,2,4,8,16}:
+// DPP quad_perm for 1 and 2, DPP row_ror:8 (== xor 8 within a 16-lane row)
+// for 8, ds_swizzle in bit-mask mode for 4 and 16.  None touches LDS memory.
+template <int M> __device__ __forceinline__ int xor_perm_i(int v) {
+    if constexpr (M == 1) return __builtin_amdgcn_update_dpp(0, v, 0xB1, 0xF, 0xF, false);
+    else if constexpr (M == 2) return __builtin_amdgcn_update_dpp(0, v, 0x4E, 0xF, 0xF, false);
+    else if constexpr (M == 8) return __builtin_amdgcn_update_dpp(0, v, 0x128, 0xF, 0xF, false);
+    else return __builtin_amdgcn_ds_swizzle(v, (M << 10) | 0x1F);
+}
+template <int M> __device__ __forceinline__ float xor_perm_f(float v) {
+    if constexpr (M == 32) return __shfl_xor(v, 32, kWave);
+    else return __int_as_float(xor_perm_i<M>(__float_as_int(v)));
+}
+__device__ __forceinline__ float readlane_f(float v, int lane) {
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), lane));
+}
 __device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-    for (int m = 32; m > 0; m >>= 1) v = fmaxf(v, shfl_xor_f(v, m));
-    return v;
+    v = fmaxf(v, xor_perm_f<1>(v));
+    v = fmaxf(v, xor_perm_f<2>(v));
+    v = fmaxf(v, xor_perm_f<4>(v));
+    v = fmaxf(v, xor_perm_f<8>(v));
+    v = fmaxf(v, xor_perm_f<16>(v));
+    return fmaxf(readlane_f(v, 0), readlane_f(v, 32));
+}
+__device__ __forceinline__ uint32_t wave_max_u(uint32_t v) {
+    v = max(v, uint32_t(xor_perm_i<1>(int(v))));
+    v = max(v, uint32_t(xor_perm_i<2>(int(v))));
+    v = max(v, uint32_t(xor_perm_i<4>(int(v))));
+    v = max(v, uint32_t(xor_perm_i<8>(int(v))));
+    v = max(v, uint32_t(xor_perm_i<16>(int(v))));
+    return max(uint32_t(__builtin_amdgcn_readlane(int(v), 0)), uint32_t(__builtin_amdgcn_readlane(int(v), 32)));
+}
+__device__ __forceinline__ int wave_min_i(int v) {
+    v = min(v, xor_perm_i<1>(v));
+    v = min(v, xor_perm_i<2>(v));
+    v = min(v, xor_perm_i<4>(v));
+    v = min(v, xor_perm_i<8>(v));
+    v = min(v, xor_perm_i<16>(v));
+    return min(__builtin_amdgcn_readlane(v, 0), __builtin_amdgcn_readlane(v, 32));
 }
 __device__ __forceinline__ int wave_sum_i(int v) {
-#pragma unroll
-    for (int m = 32; m > 0; m >>= 1) v += shfl_xor_i(v, m);
-    return v;
+    v += xor_perm_i<1>(v);
+    v += xor_perm_i<2>(v);
+    v += xor_perm_i<4>(v);
+    v += xor_perm_i<8>(v);
+    v += xor_perm_i<16>(v);
+    return __builtin_amdgcn_readlane(v, 0) + __builtin_amdgcn_readlane(v, 32);
 }
-// Butterfly sum over the 64 lanes: lane l adds lane l^m for m = 32..1.  Every
-// lane ends with the same bits because fp32 addition is commutative.
+// Butterfly sum over the 64 lanes: lane l adds lane l^m for m = 1, 2, 4, 8,
+// 16, 32.  fp32 addition is commutative, so after each step the partner lanes
+// hold identical bits and the last step (m = 32) is the sum of the two
+// uniform halves; the result is the same in every lane.
 __device__ __forceinline__ float wave_butterfly_sum(float v) {
-#pragma unroll
-    for (int m = 32; m > 0; m >>= 1) v = v + shfl_xor_f(v, m);
-    return v;
+    v = v + xor_perm_f<1>(v);
+    v = v + xor_perm_f<2>(v);
+    v = v + xor_perm_f<4>(v);
+    v = v + xor_perm_f<8>(v);
+    v = v + xor_perm_f<16>(v);
+    return readlane_f(v, 0) + readlane_f(v, 32);
 }
 
 __device__ __forceinline__ void flag_or(uint32_t* sticky, uint32_t bits) {
@@ -148,11 +189,22 @@ __device__ __forceinline__ void quantize_group_wave(float v[4], uint32_t* words,
     // lane 2c holds q[8c..8c+3], lane 2c+1 holds q[8c+4..8c+7].
     const uint32_t ev = (uint32_t(q[0]) & 255u) | ((uint32_t(q[2]) & 255u) << 8);
     const uint32_t od = (uint32_t(q[1]) & 255u) | ((uint32_t(q[3]) & 255u) << 8);
-    const uint32_t pev = uint32_t(__shfl_xor(int(ev), 1, kWave));
-    const uint32_t pod = uint32_t(__shfl_xor(int(od), 1, kWave));
+    const uint32_t pev = uint32_t(xor_perm_i<1>(int(ev)));
+    const uint32_t pod = uint32_t(xor_perm_i<1>(int(od)));
     const uint32_t word = (lane & 1) ? (pod | (od << 16)) : (ev | (pev << 16));
     words[lane] = word;
     if (lane == 0) { *scale_out = sbits; *sum_out = sum; }
+}
+
+// One cross-lane butterfly step: pairs lanes l and l^M; the lane with the
+// bit set keeps partner - own (src[lo] - src[hi]), the other own + partner.
+template <int M> __device__ __forceinline__ void h128_lane_step(float v[4], int lane) {
+    const bool upper = lane & M;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const float p = xor_perm_f<M>(v[i]);
+        v[i] = upper ? (p - v[i]) : (v[i] + p);
+    }
 }
 
 // 128-point Hadamard transform of two blocks held by one wave: lane l holds
@@ -166,15 +218,11 @@ __device__ __forceinline__ void h128_wave(float v[4]) {
     // step 2 (k bit 1)
     v[0] = a0 + a2; v[2] = a0 - a2; v[1] = a1 + a3; v[3] = a1 - a3;
     // steps 4..64 (k bits 2..6 = lane bits 0..4)
-#pragma unroll
-    for (int m = 1; m < 32; m <<= 1) {
-        const bool upper = lane & m;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const float p = shfl_xor_f(v[i], m);
-            v[i] = upper ? (p - v[i]) : (v[i] + p);
-        }
-    }
+    h128_lane_step<1>(v, lane);
+    h128_lane_step<2>(v, lane);
+    h128_lane_step<4>(v, lane);
+    h128_lane_step<8>(v, lane);
+    h128_lane_step<16>(v, lane);
 #pragma unroll
     for (int i = 0; i < 4; ++i) v[i] = v[i] * kInvSqrt128;
 }

@@ -14,6 +14,13 @@ namespace {
 
 constexpr int kHeadK = 2048, kHeadGroups = 16;
 
+template <int M> __device__ __forceinline__ void head_step(float& v0, float& v1, int lane) {
+    const bool upper = lane & M;
+    const float p0 = xor_perm_f<M>(v0), p1 = xor_perm_f<M>(v1);
+    v0 = upper ? (p0 - v0) : (v0 + p0);
+    v1 = upper ? (p1 - v1) : (v1 + p1);
+}
+
 // One wave per (row, 128-group): lane l holds k = 2l, 2l+1.
 __global__ __launch_bounds__(256) void head_encode_kernel(const uint16_t* __restrict__ x, int M,
                                                           uint32_t* __restrict__ words, uint16_t* __restrict__ scales,
@@ -26,13 +33,12 @@ __global__ __launch_bounds__(256) void head_encode_kernel(const uint16_t* __rest
     uint32_t flags = 0;
     if (!isfinite(a) || !isfinite(b)) flags |= kDenseNonfiniteInput;
     float v0 = a + b, v1 = a - b;                 // butterfly step 1
-#pragma unroll
-    for (int m = 1; m < 64; m <<= 1) {            // steps 2..64 = lane bits 0..5
-        const bool upper = lane & m;
-        const float p0 = shfl_xor_f(v0, m), p1 = shfl_xor_f(v1, m);
-        v0 = upper ? (p0 - v0) : (v0 + p0);
-        v1 = upper ? (p1 - v1) : (v1 + p1);
-    }
+    head_step<1>(v0, v1, lane);                   // steps 2..64 = lane bits 0..5
+    head_step<2>(v0, v1, lane);
+    head_step<4>(v0, v1, lane);
+    head_step<8>(v0, v1, lane);
+    head_step<16>(v0, v1, lane);
+    head_step<32>(v0, v1, lane);
     v0 = v0 * kInvSqrt128;
     v1 = v1 * kInvSqrt128;
     if (!isfinite(v0) || !isfinite(v1)) flags |= kDenseNonfiniteInput;
@@ -50,7 +56,7 @@ __global__ __launch_bounds__(256) void head_encode_kernel(const uint16_t* __rest
     q0 = q0 < -127 ? -127 : (q0 > 127 ? 127 : q0);
     q1 = q1 < -127 ? -127 : (q1 > 127 ? 127 : q1);
     const uint32_t half = (uint32_t(q0) & 255u) | ((uint32_t(q1) & 255u) << 8);
-    const uint32_t other = uint32_t(__shfl_xor(int(half), 1, kWave));
+    const uint32_t other = uint32_t(xor_perm_i<1>(int(half)));
     if (!(lane & 1)) words[size_t(wave) * 32 + lane / 2] = half | (other << 16);
     if (lane == 0) scales[wave] = sbits;
     flag_or(sticky, flags);

@@ -5,13 +5,14 @@
 // (iu4_correctness/gates_projection.py:18-26,36-42) and vLLM's topk_softmax
 // (contract moe_base.py:57-64, dtypes :53-54).  Both reduction orders are
 // declared by this build (the reference's are compiler/library chosen):
-//   logit[t,e] = bias[e] + butterfly over 64 lanes of lane partials, lane l
+//   logit[t,e] = bias[e] + butterfly (masks 1,2,...,32) over 64 lanes of lane partials, lane l
 //   accumulating fma(x[k], w[k], acc) over k = 8c..8c+7 for
 //   c = l, l+64, l+128, l+192 (bf16*bf16 products are exact in fp32, so the
 //   fma equals a separate multiply and add).
 // Permute replaces histogram/scan_routes/scatter/partition
 // (routed_storage_n32_prefill.h:19-42) with a deterministic stable order.
 #include "kernels.hpp"
+#include "topk.hpp"
 
 namespace ornith {
 
@@ -70,10 +71,11 @@ hipError_t launch_router(const uint16_t* x, int64_t stride, int T, const uint16_
 }
 
 // ---------------------------------------------------------------------------
-// Softmax / top-8 / renormalise, one wave per token.  Declared order:
-// m = max; e = pexp(l - m); s = butterfly over lanes of ((e[l] + e[l+64]) +
-// e[l+128]) + e[l+192]; p = e / s; pick the largest p eight times (ties to
-// the lower id); weights p / (slot-order sum of the picked p).
+// Softmax / top-8 / renormalise, one wave per token (topk.hpp).  Declared
+// order: m = max; e = pexp(l - m); s = butterfly (masks 1..32) over lanes of
+// ((e[l] + e[l+64]) + e[l+128]) + e[l+192]; p = e / s; the eight largest p
+// (ties to the lower id) in descending order; weights p / (slot-order sum of
+// the picked p).
 // ---------------------------------------------------------------------------
 __global__ __launch_bounds__(256) void topk_kernel(const float* __restrict__ logits, int64_t logit_stride, int T,
                                                    float* __restrict__ weights, int32_t* __restrict__ ids,
@@ -85,49 +87,18 @@ __global__ __launch_bounds__(256) void topk_kernel(const float* __restrict__ log
     float v[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) v[i] = logits[size_t(t) * logit_stride + lane + 64 * i];
-    float m = fmaxf(fmaxf(v[0], v[1]), fmaxf(v[2], v[3]));
-    m = wave_max(m);
-    float e[4], p[4];
+    float w8[kTop];
+    int i8[kTop];
+    softmax_top8(v, w8, i8);
+    if (lane < kTop) {
+        float wv = w8[0];
+        int iv = i8[0];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) e[i] = portable_exp(v[i] - m);
-    float part = e[0];
-#pragma unroll
-    for (int i = 1; i < 4; ++i) part = part + e[i];
-    const float sum = wave_butterfly_sum(part);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) p[i] = fdiv_rn(e[i], sum);
-    bool taken[4] = {false, false, false, false};
-    float pick_p[kTop];
-    int pick_id[kTop];
-#pragma unroll
-    for (int j = 0; j < kTop; ++j) {
-        float bp = -1.f;
-        int bi = 0x7fffffff;
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-            if (!taken[i] && p[i] > bp) { bp = p[i]; bi = lane + 64 * i; }
-#pragma unroll
-        for (int msk = 32; msk > 0; msk >>= 1) {
-            const float op = shfl_xor_f(bp, msk);
-            const int oi = shfl_xor_i(bi, msk);
-            if (op > bp || (op == bp && oi < bi)) { bp = op; bi = oi; }
-        }
-        pick_p[j] = bp;
-        pick_id[j] = bi;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) if (bi == lane + 64 * i) taken[i] = true;
+        for (int j = 1; j < kTop; ++j) if (lane == j) { wv = w8[j]; iv = i8[j]; }
+        weights[size_t(t) * kTop + lane] = wv;
+        ids[size_t(t) * kTop + lane] = iv;
     }
-    if (lane == 0) {
-        float tot = 0.f;
-#pragma unroll
-        for (int j = 0; j < kTop; ++j) tot = tot + pick_p[j];
-#pragma unroll
-        for (int j = 0; j < kTop; ++j) {
-            weights[size_t(t) * kTop + j] = fdiv_rn(pick_p[j], tot);
-            ids[size_t(t) * kTop + j] = pick_id[j];
-        }
-        if (shared_bf16) shared_bf16[t] = f32_to_bf16_bits(shared_logit[size_t(t) * shared_stride]);
-    }
+    if (lane == 0 && shared_bf16) shared_bf16[t] = f32_to_bf16_bits(shared_logit[size_t(t) * shared_stride]);
 }
 
 hipError_t launch_topk(const float* logits, int64_t logit_stride, int T, float* weights, int32_t* ids,

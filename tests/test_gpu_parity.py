@@ -177,6 +177,28 @@ def test_routed_padding_and_invalid_ids(device, moe):
     assert not out[1].any()
 
 
+@pytest.mark.parametrize('case', ['dup', 'pad', 'none'])
+def test_routed_single_token_edge_ids(device, moe, case):
+    """T == 1 runs the per-tile kernel: duplicate experts (two routes on one
+    bank), -1 padding, and a token with no live slot."""
+    native = _native()
+    w, d = moe
+    rng = np.random.default_rng(79)
+    x = bf16_normal(rng, (1, 2048))
+    rw, ids = random_routing(rng, 1)
+    if case == 'dup':
+        ids[0, 5] = ids[0, 2]
+    elif case == 'pad':
+        ids[0, [1, 6]] = -1
+    else:
+        ids[0, :] = -1
+    ref = oracle_routed(x, rw, ids, w['w13'], w['w2'])
+    out, final, flags = _run_routed(native, device, d, x, rw, ids, 'ornith_routed_direct_launch', Tcap=4)
+    np.testing.assert_array_equal(final.view(np.uint32), ref['final'].view(np.uint32))
+    np.testing.assert_array_equal(out, ref['out'])
+    assert flags == ref['flags']
+
+
 def test_routed_skewed_expert(device, moe):
     """Many routes on one expert (more than one route batch of a block)."""
     native = _native()

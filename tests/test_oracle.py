@@ -289,7 +289,7 @@ def test_router_logits_declared_order_vs_fp64():
                 acc = np.float32(np.float64(acc) + np.float64(xf[k]) * np.float64(wf[k]))
         lanes.append(acc)
     lanes = np.array(lanes, np.float32)
-    for off in (32, 16, 8, 4, 2, 1):
+    for off in (1, 2, 4, 8, 16, 32):
         lanes = (lanes + lanes[np.arange(64) ^ off]).astype(np.float32)
     assert lanes[0].view(np.uint32) == got.astype(np.float32)[2, 100].view(np.uint32)
 
