@@ -51,7 +51,8 @@ RoutedPlan routed_plan(int Tcap, bool shared_slot, bool layer) {
     return p;
 }
 
-// The routed pipeline after routing is known.
+// Prefill path (T > 32): permutation into expert segments and 64-route
+// tiles, int8-MFMA grouped projections, middle quantisation, slot reduce.
 hipError_t run_routed(const RoutedPlan& p, void* ws, const void* input, const float* weights, const int32_t* ids,
                       const void* gate_codes, const void* gate_meta, const void* down_codes, const void* down_meta,
                       const void* sg_codes, const void* sg_meta, const void* sd_codes, const void* sd_meta,
@@ -67,39 +68,39 @@ hipError_t run_routed(const RoutedPlan& p, void* ws, const void* input, const fl
     auto gsum = at<int32_t>(ws, p.l.gate_sums);
     TRY(launch_act_bf16(static_cast<const uint16_t*>(input), kHidden, T, kHidden, qmax, shared ? nullptr : ids, gw, gs,
                         gsum, sticky, kFlagNonfiniteInput, kFlagInvalidActivation, s));
-    const int max_segments = (R < kExperts ? R : kExperts) + (shared ? 1 : 0);
-    ProjArgs a{};
+    const int max_tiles = (RS + 63) / 64 + (R < kExperts ? R : kExperts) + (shared ? 1 : 0);
+    MfmaArgs a{};
+    a.segments = ps.segments;
+    a.tiles = ps.tiles;
+    a.ntiles = ps.meta + 1;
+    a.routes = ps.routes;
+    a.R = R;
     a.codes = static_cast<const uint32_t*>(gate_codes);
     a.meta = static_cast<const uint32_t*>(gate_meta);
     a.shared_codes = static_cast<const uint32_t*>(sg_codes);
     a.shared_meta = static_cast<const uint32_t*>(sg_meta);
     a.bank_words = kGateBankWords;
     a.bank_meta_words = kGateBankMeta;
-    a.segments = ps.segments;
-    a.nseg = ps.meta;
-    a.routes = ps.routes;
-    a.row_mode = 1;
-    a.R = R;
     a.act_words = gw; a.act_scales = gs; a.act_sums = gsum;
-    a.out = at<float>(ws, p.l.gate_y);
-    a.N = kGateN; a.K = kHidden; a.tile = 32;
-    a.sticky = sticky; a.flag_projection = kFlagNonfiniteProjection;
-    TRY(launch_project_gemv(a, max_segments, Out::Routed, s));
+    a.K = kHidden;
+    a.out = at<float>(ws, p.l.middle);
+    a.silu_table = silu;
+    a.sticky = sticky;
+    TRY(launch_grouped_mfma(a, true, max_tiles, s));
     auto dw = at<uint32_t>(ws, p.l.down_low);
     auto dsc = at<uint16_t>(ws, p.l.down_scales);
     auto dsum = at<int32_t>(ws, p.l.down_sums);
-    TRY(launch_act_middle(at<float>(ws, p.l.gate_y), RS, R, ids, qmax, silu, dw, dsc, dsum, sticky, s));
+    TRY(launch_quant_middle(at<float>(ws, p.l.middle), RS, R, ids, qmax, dw, dsc, dsum, sticky, s));
     a.codes = static_cast<const uint32_t*>(down_codes);
     a.meta = static_cast<const uint32_t*>(down_meta);
     a.shared_codes = static_cast<const uint32_t*>(sd_codes);
     a.shared_meta = static_cast<const uint32_t*>(sd_meta);
     a.bank_words = kDownBankWords;
     a.bank_meta_words = kDownBankMeta;
-    a.row_mode = 0;
     a.act_words = dw; a.act_scales = dsc; a.act_sums = dsum;
+    a.K = kInter;
     a.out = at<float>(ws, p.l.route_out);
-    a.N = kDownN; a.K = kInter;
-    TRY(launch_project_gemv(a, max_segments, Out::Routed, s));
+    TRY(launch_grouped_mfma(a, false, max_tiles, s));
     return launch_reduce(at<float>(ws, p.l.route_out), weights, ids, T, out ? at<float>(ws, p.l.final_f32) : nullptr,
                          out, shared_logit, shared ? sigmoid : nullptr, shared_out, layer_out, sticky, s);
 }

@@ -90,49 +90,62 @@ template <int M> __device__ __forceinline__ float xor_perm_f(float v) {
 __device__ __forceinline__ float readlane_f(float v, int lane) {
     return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), lane));
 }
+// Row-uniform reductions with DPP only: after xor 1 and xor 2 (quad_perm)
+// each quad is uniform, so row_half_mirror pairs whole quads (== xor 4) and
+// row_mirror pairs whole half-rows (== xor 8).  The four 16-lane rows are then
+// combined through readlane in the xor-16 / xor-32 pairing.  For the fp32
+// butterfly this gives exactly the bits of the xor butterfly with masks
+// 1, 2, 4, 8, 16, 32 (each step adds two identical-per-lane operands, and
+// fp32 addition is commutative).
+template <int CTRL> __device__ __forceinline__ int dpp_i(int v) {
+    return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xF, 0xF, false);
+}
+template <int CTRL> __device__ __forceinline__ float dpp_f(float v) {
+    return __int_as_float(dpp_i<CTRL>(__float_as_int(v)));
+}
+constexpr int kDppXor1 = 0xB1, kDppXor2 = 0x4E, kDppHalfMirror = 0x141, kDppMirror = 0x140;
+
 __device__ __forceinline__ float wave_max(float v) {
-    v = fmaxf(v, xor_perm_f<1>(v));
-    v = fmaxf(v, xor_perm_f<2>(v));
-    v = fmaxf(v, xor_perm_f<4>(v));
-    v = fmaxf(v, xor_perm_f<8>(v));
-    v = fmaxf(v, xor_perm_f<16>(v));
-    return fmaxf(readlane_f(v, 0), readlane_f(v, 32));
+    v = fmaxf(v, dpp_f<kDppXor1>(v));
+    v = fmaxf(v, dpp_f<kDppXor2>(v));
+    v = fmaxf(v, dpp_f<kDppHalfMirror>(v));
+    v = fmaxf(v, dpp_f<kDppMirror>(v));
+    return fmaxf(fmaxf(readlane_f(v, 0), readlane_f(v, 16)), fmaxf(readlane_f(v, 32), readlane_f(v, 48)));
 }
 __device__ __forceinline__ uint32_t wave_max_u(uint32_t v) {
-    v = max(v, uint32_t(xor_perm_i<1>(int(v))));
-    v = max(v, uint32_t(xor_perm_i<2>(int(v))));
-    v = max(v, uint32_t(xor_perm_i<4>(int(v))));
-    v = max(v, uint32_t(xor_perm_i<8>(int(v))));
-    v = max(v, uint32_t(xor_perm_i<16>(int(v))));
-    return max(uint32_t(__builtin_amdgcn_readlane(int(v), 0)), uint32_t(__builtin_amdgcn_readlane(int(v), 32)));
+    v = max(v, uint32_t(dpp_i<kDppXor1>(int(v))));
+    v = max(v, uint32_t(dpp_i<kDppXor2>(int(v))));
+    v = max(v, uint32_t(dpp_i<kDppHalfMirror>(int(v))));
+    v = max(v, uint32_t(dpp_i<kDppMirror>(int(v))));
+    const uint32_t r0 = uint32_t(__builtin_amdgcn_readlane(int(v), 0)), r1 = uint32_t(__builtin_amdgcn_readlane(int(v), 16));
+    const uint32_t r2 = uint32_t(__builtin_amdgcn_readlane(int(v), 32)), r3 = uint32_t(__builtin_amdgcn_readlane(int(v), 48));
+    return max(max(r0, r1), max(r2, r3));
 }
 __device__ __forceinline__ int wave_min_i(int v) {
-    v = min(v, xor_perm_i<1>(v));
-    v = min(v, xor_perm_i<2>(v));
-    v = min(v, xor_perm_i<4>(v));
-    v = min(v, xor_perm_i<8>(v));
-    v = min(v, xor_perm_i<16>(v));
-    return min(__builtin_amdgcn_readlane(v, 0), __builtin_amdgcn_readlane(v, 32));
+    v = min(v, dpp_i<kDppXor1>(v));
+    v = min(v, dpp_i<kDppXor2>(v));
+    v = min(v, dpp_i<kDppHalfMirror>(v));
+    v = min(v, dpp_i<kDppMirror>(v));
+    return min(min(__builtin_amdgcn_readlane(v, 0), __builtin_amdgcn_readlane(v, 16)),
+               min(__builtin_amdgcn_readlane(v, 32), __builtin_amdgcn_readlane(v, 48)));
 }
 __device__ __forceinline__ int wave_sum_i(int v) {
-    v += xor_perm_i<1>(v);
-    v += xor_perm_i<2>(v);
-    v += xor_perm_i<4>(v);
-    v += xor_perm_i<8>(v);
-    v += xor_perm_i<16>(v);
-    return __builtin_amdgcn_readlane(v, 0) + __builtin_amdgcn_readlane(v, 32);
+    v += dpp_i<kDppXor1>(v);
+    v += dpp_i<kDppXor2>(v);
+    v += dpp_i<kDppHalfMirror>(v);
+    v += dpp_i<kDppMirror>(v);
+    return (__builtin_amdgcn_readlane(v, 0) + __builtin_amdgcn_readlane(v, 16)) +
+           (__builtin_amdgcn_readlane(v, 32) + __builtin_amdgcn_readlane(v, 48));
 }
 // Butterfly sum over the 64 lanes: lane l adds lane l^m for m = 1, 2, 4, 8,
-// 16, 32.  fp32 addition is commutative, so after each step the partner lanes
-// hold identical bits and the last step (m = 32) is the sum of the two
-// uniform halves; the result is the same in every lane.
+// 16, 32 (see above); the result is the same in every lane.
 __device__ __forceinline__ float wave_butterfly_sum(float v) {
-    v = v + xor_perm_f<1>(v);
-    v = v + xor_perm_f<2>(v);
-    v = v + xor_perm_f<4>(v);
-    v = v + xor_perm_f<8>(v);
-    v = v + xor_perm_f<16>(v);
-    return readlane_f(v, 0) + readlane_f(v, 32);
+    v = v + dpp_f<kDppXor1>(v);
+    v = v + dpp_f<kDppXor2>(v);
+    v = v + dpp_f<kDppHalfMirror>(v);
+    v = v + dpp_f<kDppMirror>(v);
+    const float r0 = readlane_f(v, 0), r1 = readlane_f(v, 16), r2 = readlane_f(v, 32), r3 = readlane_f(v, 48);
+    return (r0 + r1) + (r2 + r3);
 }
 
 __device__ __forceinline__ void flag_or(uint32_t* sticky, uint32_t bits) {

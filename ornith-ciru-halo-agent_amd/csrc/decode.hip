@@ -575,6 +575,7 @@ static hipError_t run(const DecodeArgs& a, hipStream_t s) {
 
 hipError_t launch_decode(const DecodeArgs& a, bool router, bool shared, int qmax, hipStream_t s) {
     if (a.T <= 0 || a.T > kDecodeMaxTokens) return hipErrorInvalidValue;
+    if (a.T == 1) return launch_decode1(a, router, shared, qmax, s);
     if (router && shared) return run<true, true, 127>(a, s);
     if (router) return run<true, false, 127>(a, s);
     if (shared) return run<false, true, 127>(a, s);

@@ -42,5 +42,6 @@ struct DecodeArgs {
 size_t decode_scratch_bytes();
 void carve_decode(void* base, DecodeArgs& a);
 hipError_t launch_decode(const DecodeArgs& a, bool router, bool shared, int qmax, hipStream_t s);
+hipError_t launch_decode1(const DecodeArgs& a, bool router, bool shared, int qmax, hipStream_t s);
 
 }  // namespace ornith

@@ -66,7 +66,22 @@ struct ProjArgs {
     uint32_t flag_projection, flag_bf16;
 };
 hipError_t launch_project_gemv(const ProjArgs& a, int max_segments, Out mode, hipStream_t s);
-hipError_t launch_project_mfma(const ProjArgs& a, const int32_t* tiles, int max_tiles, hipStream_t s);
+
+// Grouped int8-MFMA projection over the permuted routes (prefill path).
+struct MfmaArgs {
+    const Segment* segments; const int32_t* tiles; const int32_t* ntiles; const int32_t* routes;
+    int R;                                       // routed routes; rows >= R are shared-expert rows
+    const uint32_t* codes; const uint32_t* meta; const uint32_t* shared_codes; const uint32_t* shared_meta;
+    int64_t bank_words, bank_meta_words;
+    const uint32_t* act_words; const uint16_t* act_scales; const int32_t* act_sums;
+    int K;
+    float* out;                                  // gate/up: middle [RS, 512]; down: route_out [RS, 2048]
+    const float* silu_table;
+    uint32_t* sticky;
+};
+hipError_t launch_grouped_mfma(const MfmaArgs& a, bool gateup, int max_tiles, hipStream_t s);
+hipError_t launch_quant_middle(const float* middle, int RS, int R, const int32_t* ids, int qmax, uint32_t* words,
+                               uint16_t* scales, int32_t* sums, uint32_t* sticky, hipStream_t s);
 
 // ---- combination -------------------------------------------------------------
 // out[t] = bf16(sum over valid slots of route_out[8t+s] * w[8t+s]); optional

@@ -1,0 +1,254 @@
+// Grouped G256 projection on the int8 matrix cores (prefill path, T > 32).
+//
+// Arithmetic is the reference's A8/A4 routed math, exactly
+// (routed_storage_n32_prefill.h:43-149 computes the same per-group integer
+// dots with WMMA-iu4, routed_storage_n32_consumer.cpp:152-157 the tree):
+// per (route, column, 256-group) the integer dot sum_k code*q is formed by
+// v_mfma_i32_16x16x64_i8 (exact: |dot| < 2^19), then the fp32 group tree
+// value = value + (RN(sw*RN(sa*dot)) + RN(off*RN(sa*sum))) runs in ascending
+// group order on the VALU.
+//
+// Tile: one block (4 waves) per (segment m-tile of 64 routes, 128 columns).
+// Per group: the 64 gathered activation rows (256 int8 each) and the codes of
+// the 128 columns, unpacked once to int8, are staged in LDS; the next group's
+// global loads are issued into registers before the current group's MFMAs.
+// MFMA operand layout (verified on gfx950): lane i+16q supplies the 16 bytes
+// of row/column i for k-group q, A and B bytes pair positionally, and output
+// register r of lane l is C[4*(l/16)+r][l%16].  Both operands use this
+// build's byte order (even codes then odd codes per 8-value chunk), so the
+// logical k pairing matches and the integer dot is exact.
+//
+// Gate/up: the block's 128 columns are 64 gate columns and the matching 64 up
+// columns, laid out so that one lane holds the gate and up accumulators of
+// the same (route, column) and writes SiLU(gate)*up directly.
+#include "kernels.hpp"
+#include "decode.hpp"
+
+namespace ornith {
+
+constexpr int kMT = 64, kNT = 128, kRowWords = 68;   // 64 words (256 int8) + 4 pad
+
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+
+template <bool GATEUP>
+__global__ __launch_bounds__(256, 2) void grouped_mfma_kernel(MfmaArgs a) {
+    __shared__ uint32_t sA[kMT * kRowWords];
+    __shared__ uint32_t sB[kNT * kRowWords];
+    __shared__ float s_sa[kMT], s_ss[kMT], s_sw[kNT], s_off[kNT];
+    __shared__ int s_route[kMT], s_row[kMT];
+
+    if (int(blockIdx.x) >= a.ntiles[0]) return;
+    const int tile = a.tiles[blockIdx.x];
+    const Segment sg = a.segments[tile >> 16];
+    const int r0 = (tile & 0xffff) * kMT;
+    const int nrows = min(kMT, sg.count - r0);
+    const int nt = blockIdx.y;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int wm = wave & 1, wn = wave >> 1;
+    const int GS = a.K / kGroup;
+    const bool shared = sg.bank == kShared;
+    const uint32_t* codes = shared ? a.shared_codes : a.codes + size_t(sg.bank) * a.bank_words;
+    const uint32_t* meta = shared ? a.shared_meta : a.meta + size_t(sg.bank) * a.bank_meta_words;
+
+    if (tid < kMT) {
+        int route = -1, row = 0;
+        if (tid < nrows) {
+            route = a.routes[sg.first + r0 + tid];
+            row = GATEUP ? (route < a.R ? route / kTop : route - a.R) : route;
+        }
+        s_route[tid] = route;
+        s_row[tid] = row;
+    }
+    // block column bc (0..127) -> n32 tile and column inside it
+    auto ntile_of = [&](int blk) {      // blk: 32-column block 0..3 of this block
+        if (GATEUP) return (blk < 2 ? 2 * nt + blk : 16 + 2 * nt + (blk - 2));
+        return 4 * nt + blk;
+    };
+    __syncthreads();
+
+    // ---- staging loads of one group into registers ----
+    uint4 ra[4], rb[4];
+    uint32_t rmeta = 0;
+    float rsa = 0.f, rss = 0.f;
+    const int a_row = tid >> 2, a_part = tid & 3;
+    const int b_blk = tid >> 6, b_sub = tid & 63;         // 16 packed words: chunk b_sub/2, cols (b_sub&1)*16..+15
+    auto load_group = [&](int g) {
+        const bool live = a_row < nrows;
+        const uint32_t* src = a.act_words + size_t(s_row[a_row]) * (a.K / 4) + g * 64 + a_part * 16;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) ra[i] = live ? *reinterpret_cast<const uint4*>(src + 4 * i) : make_uint4(0, 0, 0, 0);
+        const uint32_t* bsrc = codes + (size_t(ntile_of(b_blk)) * GS + g) * 1024 + b_sub * 16;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) rb[i] = *reinterpret_cast<const uint4*>(bsrc + 4 * i);
+        if (tid < kNT) rmeta = meta[(size_t(ntile_of(tid >> 5)) * GS + g) * 32 + (tid & 31)];
+        if (tid < kMT) {
+            rsa = 0.f; rss = 0.f;
+            if (tid < nrows) {
+                rsa = f16_bits_to_f32(a.act_scales[size_t(s_row[tid]) * GS + g]);
+                rss = rsa * float(a.act_sums[size_t(s_row[tid]) * GS + g]);
+            }
+        }
+    };
+    auto store_group = [&]() {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) *reinterpret_cast<uint4*>(&sA[a_row * kRowWords + a_part * 16 + 4 * i]) = ra[i];
+        // unpack: packed word (chunk j, column n) -> int8 words 2j (even k) and 2j+1 (odd k) of column n
+        const int j = b_sub >> 1, c0 = b_blk * 32 + (b_sub & 1) * 16;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const uint32_t w[4] = {rb[i].x, rb[i].y, rb[i].z, rb[i].w};
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int col = c0 + 4 * i + e;
+                *reinterpret_cast<uint2*>(&sB[col * kRowWords + 2 * j]) =
+                    make_uint2(uint32_t(code_even(w[e])), uint32_t(code_odd(w[e])));
+            }
+        }
+        if (tid < kNT) {
+            s_sw[tid] = f16_bits_to_f32(rmeta & 0xffffu);
+            s_off[tid] = f16_bits_to_f32(rmeta >> 16);
+        }
+        if (tid < kMT) { s_sa[tid] = rsa; s_ss[tid] = rss; }
+    };
+
+    // wave tiles: 2 row tiles (16 rows) x 4 column tiles (16 columns)
+    int colbase[4];
+#pragma unroll
+    for (int ct = 0; ct < 4; ++ct)
+        colbase[ct] = GATEUP ? ((ct < 2 ? 0 : 64) + 32 * wn + 16 * (ct & 1)) : (64 * wn + 16 * ct);
+    const int q = lane >> 4, li = lane & 15;
+    float val[2][4][4];
+#pragma unroll
+    for (int rt = 0; rt < 2; ++rt)
+#pragma unroll
+        for (int ct = 0; ct < 4; ++ct)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) val[rt][ct][r] = 0.f;
+
+    load_group(0);
+    for (int g = 0; g < GS; ++g) {
+        __syncthreads();                    // previous group's readers are done
+        store_group();
+        __syncthreads();
+        if (g + 1 < GS) load_group(g + 1);  // in flight during this group's math
+        i32x4 acc[2][4];
+#pragma unroll
+        for (int rt = 0; rt < 2; ++rt)
+#pragma unroll
+            for (int ct = 0; ct < 4; ++ct) acc[rt][ct] = i32x4{0, 0, 0, 0};
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+            i32x4 fa[2], fb[4];
+#pragma unroll
+            for (int rt = 0; rt < 2; ++rt) {
+                const uint4 v = *reinterpret_cast<const uint4*>(&sA[(32 * wm + 16 * rt + li) * kRowWords + 16 * s + 4 * q]);
+                fa[rt] = i32x4{int(v.x), int(v.y), int(v.z), int(v.w)};
+            }
+#pragma unroll
+            for (int ct = 0; ct < 4; ++ct) {
+                const uint4 v = *reinterpret_cast<const uint4*>(&sB[(colbase[ct] + li) * kRowWords + 16 * s + 4 * q]);
+                fb[ct] = i32x4{int(v.x), int(v.y), int(v.z), int(v.w)};
+            }
+#pragma unroll
+            for (int rt = 0; rt < 2; ++rt)
+#pragma unroll
+                for (int ct = 0; ct < 4; ++ct)
+                    acc[rt][ct] = __builtin_amdgcn_mfma_i32_16x16x64_i8(fa[rt], fb[ct], acc[rt][ct], 0, 0, 0);
+        }
+        // fp32 group tree (dense_g256_api.h:35-37)
+#pragma unroll
+        for (int rt = 0; rt < 2; ++rt) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int row = 32 * wm + 16 * rt + 4 * q + r;
+                const float sa = s_sa[row], ss = s_ss[row];
+#pragma unroll
+                for (int ct = 0; ct < 4; ++ct) {
+                    const int col = colbase[ct] + li;
+                    const float scaled_dot = sa * float(acc[rt][ct][r]);
+                    const float product = s_sw[col] * scaled_dot;
+                    const float correction = s_off[col] * ss;
+                    val[rt][ct][r] = val[rt][ct][r] + (product + correction);
+                }
+            }
+        }
+    }
+
+    // ---- epilogue ----
+    uint32_t flags = 0;
+#pragma unroll
+    for (int rt = 0; rt < 2; ++rt) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int row = 32 * wm + 16 * rt + 4 * q + r;
+            if (row >= nrows) continue;
+            const int route = s_route[row];
+            if (GATEUP) {
+#pragma unroll
+                for (int ct = 0; ct < 2; ++ct) {
+                    float vg = val[rt][ct][r], vu = val[rt][ct + 2][r];
+                    float mid;
+                    if (shared) {
+                        vg = bf16_round(vg);
+                        vu = bf16_round(vu);
+                        if (!isfinite(vg) || !isfinite(vu)) flags |= kFlagNonfiniteProjection;
+                        mid = bf16_round(a.silu_table[__float_as_uint(vg) >> 16] * vu);
+                    } else {
+                        if (!isfinite(vg) || !isfinite(vu)) flags |= kFlagNonfiniteProjection;
+                        mid = silu_portable(vg) * vu;
+                    }
+                    if (!isfinite(mid)) flags |= kFlagNonfiniteMiddle | kFlagNonfiniteInput;
+                    a.out[size_t(route) * kInter + 64 * nt + colbase[ct] + li] = mid;
+                }
+            } else {
+#pragma unroll
+                for (int ct = 0; ct < 4; ++ct) {
+                    float v = val[rt][ct][r];
+                    if (shared) v = bf16_round(v);
+                    if (!isfinite(v)) flags |= kFlagNonfiniteProjection;
+                    a.out[size_t(route) * kHidden + kNT * nt + colbase[ct] + li] = v;
+                }
+            }
+        }
+    }
+    flag_or(a.sticky, flags);
+}
+
+hipError_t launch_grouped_mfma(const MfmaArgs& a, bool gateup, int max_tiles, hipStream_t s) {
+    if (max_tiles <= 0) return hipSuccess;
+    if (gateup) grouped_mfma_kernel<true><<<dim3(max_tiles, (2 * kInter) / kNT), 256, 0, s>>>(a);
+    else grouped_mfma_kernel<false><<<dim3(max_tiles, kHidden / kNT), 256, 0, s>>>(a);
+    return hipGetLastError();
+}
+
+// H128 + quantisation of the middle rows [RS, 512] of every valid route.
+template <int QMAX>
+__global__ __launch_bounds__(256) void quant_middle_kernel(const float* __restrict__ middle, int RS, int R,
+                                                           const int32_t* __restrict__ ids, uint32_t* __restrict__ words,
+                                                           uint16_t* __restrict__ scales, int32_t* __restrict__ sums,
+                                                           uint32_t* sticky) {
+    const int wave = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (wave >= RS * 2) return;
+    const int lane = threadIdx.x & 63, route = wave >> 1, group = wave & 1;
+    if (route < R && (ids[route] < 0 || ids[route] >= kExperts)) return;
+    const float4 m4 = *reinterpret_cast<const float4*>(middle + size_t(route) * kInter + group * kGroup + lane * 4);
+    float v[4] = {m4.x, m4.y, m4.z, m4.w};
+    uint32_t flags = 0;
+    h128_wave(v);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) if (!isfinite(v[i])) flags |= kFlagNonfiniteInput;
+    quantize_group_wave<QMAX>(v, words + size_t(wave) * 64, scales + wave, sums + wave, flags, kFlagInvalidActivation);
+    flag_or(sticky, flags);
+}
+
+hipError_t launch_quant_middle(const float* middle, int RS, int R, const int32_t* ids, int qmax, uint32_t* words,
+                               uint16_t* scales, int32_t* sums, uint32_t* sticky, hipStream_t s) {
+    const int waves = RS * 2;
+    if (qmax == 127)
+        quant_middle_kernel<127><<<(waves + 3) / 4, 256, 0, s>>>(middle, RS, R, ids, words, scales, sums, sticky);
+    else
+        quant_middle_kernel<7><<<(waves + 3) / 4, 256, 0, s>>>(middle, RS, R, ids, words, scales, sums, sticky);
+    return hipGetLastError();
+}
+
+}  // namespace ornith

@@ -141,7 +141,8 @@ def _run_routed(native, device, d, x, w, ids, entry, Tcap=None):
                                           (32, 'ornith_routed_direct_launch', 127),
                                           (3, 'ornith_routed_direct_launch_a4', 7),
                                           (70, 'ornith_routed_direct_launch_a4_prefill', 7),
-                                          (20, 'ornith_routed_direct_launch_a4_prefill', 127)])
+                                          (20, 'ornith_routed_direct_launch_a4_prefill', 127),
+                                          (150, 'ornith_routed_direct_launch', 127)])
 def test_routed_bit_exact(device, moe, T, entry, qmax):
     native = _native()
     print(f'routed T={T} {entry}', flush=True)
@@ -204,7 +205,7 @@ def test_routed_skewed_expert(device, moe):
     native = _native()
     w, d = moe
     rng = np.random.default_rng(78)
-    T = 40
+    T = 140                 # 140 routes on expert 17: three 64-route tiles
     x = bf16_normal(rng, (T, 2048))
     rw, ids = random_routing(rng, T)
     ids[:, 0] = 17          # duplicates inside a token are legal: two routes to one expert
@@ -276,7 +277,7 @@ def test_router_topk_bit_exact(device, moe, T, biased):
     np.testing.assert_array_equal(from_dev(sl), O.f32_to_bf16(logits_ref[:, 256]))
 
 
-@pytest.mark.parametrize('T', [1, 32])
+@pytest.mark.parametrize('T', [1, 32, 96])
 def test_moe_layer_bit_exact(device, moe, shared_tables, T):
     import torch
     native = _native()
