@@ -359,11 +359,9 @@ extern "C" hipError_t ornith_router_topk_launch(const void* x, int64_t x_stride,
         !aligned(logits, 4) || !aligned(topk_weights, 4) || !aligned(topk_ids, 4))
         return hipErrorInvalidValue;
     auto lg = static_cast<float*>(logits);
-    TRY(launch_router(static_cast<const uint16_t*>(x), x_stride, T, static_cast<const uint16_t*>(router_w), kExperts,
-                      static_cast<const float*>(bias), lg, kLogitStride, stream));
-    if (shared_gate_w)
-        TRY(launch_router(static_cast<const uint16_t*>(x), x_stride, T, static_cast<const uint16_t*>(shared_gate_w), 1,
-                          nullptr, lg + kExperts, kLogitStride, stream));
+    TRY(launch_router(static_cast<const uint16_t*>(x), x_stride, T, static_cast<const uint16_t*>(router_w),
+                      static_cast<const uint16_t*>(shared_gate_w), static_cast<const float*>(bias), lg, kLogitStride,
+                      stream));
     return launch_topk(lg, kLogitStride, T, static_cast<float*>(topk_weights), static_cast<int32_t*>(topk_ids),
                        shared_gate_w ? lg + kExperts : nullptr, kLogitStride,
                        shared_gate_w ? static_cast<uint16_t*>(shared_logit) : nullptr, stream);

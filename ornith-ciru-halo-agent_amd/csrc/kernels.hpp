@@ -35,7 +35,9 @@ hipError_t launch_act_middle(const float* gate_y, int RS, int R, const int32_t* 
                              int32_t* sums, uint32_t* sticky, hipStream_t s);
 
 // ---- routing ---------------------------------------------------------------
-hipError_t launch_router(const uint16_t* x, int64_t stride, int T, const uint16_t* w, int nrows,
+// Router logits [T, 256 (+1)] in the declared order; shared_w (nullable) adds
+// column 256, the shared-expert gate logit.
+hipError_t launch_router(const uint16_t* x, int64_t stride, int T, const uint16_t* w, const uint16_t* shared_w,
                          const float* bias, float* logits, int64_t logit_stride, hipStream_t s);
 hipError_t launch_topk(const float* logits, int64_t logit_stride, int T, float* weights, int32_t* ids,
                        const float* shared_logit_f32, int64_t shared_stride, uint16_t* shared_logit_bf16,

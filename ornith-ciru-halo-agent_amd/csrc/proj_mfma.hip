@@ -23,14 +23,16 @@
 // the same (route, column) and writes SiLU(gate)*up directly.
 #include "kernels.hpp"
 #include "decode.hpp"
+#include <utility>
 
 namespace ornith {
 
 constexpr int kMT = 64, kNT = 128, kRowWords = 68;   // 64 words (256 int8) + 4 pad
 
 typedef int i32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
-template <bool GATEUP>
+template <bool GATEUP, int GS, int DEPTH>
 __global__ __launch_bounds__(256, 2) void grouped_mfma_kernel(MfmaArgs a) {
     __shared__ uint32_t sA[kMT * kRowWords];
     __shared__ uint32_t sB[kNT * kRowWords];
@@ -45,7 +47,6 @@ __global__ __launch_bounds__(256, 2) void grouped_mfma_kernel(MfmaArgs a) {
     const int nt = blockIdx.y;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int wm = wave & 1, wn = wave >> 1;
-    const int GS = a.K / kGroup;
     const bool shared = sg.bank == kShared;
     const uint32_t* codes = shared ? a.shared_codes : a.codes + size_t(sg.bank) * a.bank_words;
     const uint32_t* meta = shared ? a.shared_meta : a.meta + size_t(sg.bank) * a.bank_meta_words;
@@ -66,37 +67,39 @@ __global__ __launch_bounds__(256, 2) void grouped_mfma_kernel(MfmaArgs a) {
     };
     __syncthreads();
 
-    // ---- staging loads of one group into registers ----
-    uint4 ra[4], rb[4];
-    uint32_t rmeta = 0;
-    float rsa = 0.f, rss = 0.f;
+    // ---- staging loads of one group into a register slot ----
+    u32x4 ra[DEPTH][4], rb[DEPTH][4];
+    uint32_t rmeta[DEPTH];
+    uint32_t rsa[DEPTH];                // raw fp16 scale bits; converted at store time so that
+    int rsum[DEPTH];                    // no use of a load result sits behind the prefetch
     const int a_row = tid >> 2, a_part = tid & 3;
     const int b_blk = tid >> 6, b_sub = tid & 63;         // 16 packed words: chunk b_sub/2, cols (b_sub&1)*16..+15
-    auto load_group = [&](int g) {
-        const bool live = a_row < nrows;
-        const uint32_t* src = a.act_words + size_t(s_row[a_row]) * (a.K / 4) + g * 64 + a_part * 16;
+    // Every lane issues every load (dead rows read activation row s_row = 0 of
+    // a live tile and are dropped by the epilogue), so the in-order load
+    // counter stays exact and the waits leave the prefetched groups in flight.
+    const size_t a_base = size_t(s_row[a_row]) * (GS * 64) + a_part * 16;
+    const size_t m_base = size_t(ntile_of((tid & 127) >> 5)) * GS * 32 + (tid & 31);
+    const size_t s_base = size_t(s_row[tid & 63]) * GS;
+    auto load_group = [&](int g, int slot) {
+        const uint32_t* src = a.act_words + a_base + g * 64;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) ra[i] = live ? *reinterpret_cast<const uint4*>(src + 4 * i) : make_uint4(0, 0, 0, 0);
+        for (int i = 0; i < 4; ++i) ra[slot][i] = *reinterpret_cast<const u32x4*>(src + 4 * i);
         const uint32_t* bsrc = codes + (size_t(ntile_of(b_blk)) * GS + g) * 1024 + b_sub * 16;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) rb[i] = *reinterpret_cast<const uint4*>(bsrc + 4 * i);
-        if (tid < kNT) rmeta = meta[(size_t(ntile_of(tid >> 5)) * GS + g) * 32 + (tid & 31)];
-        if (tid < kMT) {
-            rsa = 0.f; rss = 0.f;
-            if (tid < nrows) {
-                rsa = f16_bits_to_f32(a.act_scales[size_t(s_row[tid]) * GS + g]);
-                rss = rsa * float(a.act_sums[size_t(s_row[tid]) * GS + g]);
-            }
-        }
+        for (int i = 0; i < 4; ++i) rb[slot][i] = *reinterpret_cast<const u32x4*>(bsrc + 4 * i);
+        rmeta[slot] = meta[m_base + g * 32];
+        rsa[slot] = a.act_scales[s_base + g];
+        rsum[slot] = a.act_sums[s_base + g];
     };
-    auto store_group = [&]() {
+    auto store_group = [&](int slot) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) *reinterpret_cast<uint4*>(&sA[a_row * kRowWords + a_part * 16 + 4 * i]) = ra[i];
+        for (int i = 0; i < 4; ++i)
+            *reinterpret_cast<u32x4*>(&sA[a_row * kRowWords + a_part * 16 + 4 * i]) = ra[slot][i];
         // unpack: packed word (chunk j, column n) -> int8 words 2j (even k) and 2j+1 (odd k) of column n
         const int j = b_sub >> 1, c0 = b_blk * 32 + (b_sub & 1) * 16;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            const uint32_t w[4] = {rb[i].x, rb[i].y, rb[i].z, rb[i].w};
+            const uint32_t w[4] = {rb[slot][i].x, rb[slot][i].y, rb[slot][i].z, rb[slot][i].w};
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
                 const int col = c0 + 4 * i + e;
@@ -105,10 +108,14 @@ __global__ __launch_bounds__(256, 2) void grouped_mfma_kernel(MfmaArgs a) {
             }
         }
         if (tid < kNT) {
-            s_sw[tid] = f16_bits_to_f32(rmeta & 0xffffu);
-            s_off[tid] = f16_bits_to_f32(rmeta >> 16);
+            s_sw[tid] = f16_bits_to_f32(rmeta[slot] & 0xffffu);
+            s_off[tid] = f16_bits_to_f32(rmeta[slot] >> 16);
         }
-        if (tid < kMT) { s_sa[tid] = rsa; s_ss[tid] = rss; }
+        if (tid < kMT) {
+            const float sa = f16_bits_to_f32(uint16_t(rsa[slot]));
+            s_sa[tid] = sa;
+            s_ss[tid] = sa * float(rsum[slot]);
+        }
     };
 
     // wave tiles: 2 row tiles (16 rows) x 4 column tiles (16 columns)
@@ -125,12 +132,17 @@ __global__ __launch_bounds__(256, 2) void grouped_mfma_kernel(MfmaArgs a) {
 #pragma unroll
             for (int r = 0; r < 4; ++r) val[rt][ct][r] = 0.f;
 
-    load_group(0);
-    for (int g = 0; g < GS; ++g) {
+#pragma unroll
+    for (int g = 0; g < DEPTH; ++g) load_group(g, g);
+    static_assert(GS % DEPTH == 0, "group ring must divide the group count");
+    // one group step; the ring slot D is a compile-time constant so the
+    // register ring never becomes an indexed private array
+    auto step = [&]<int D, bool PREFETCH>(int g) {
         __syncthreads();                    // previous group's readers are done
-        store_group();
+        constexpr int d = D;
+        store_group(d);
         __syncthreads();
-        if (g + 1 < GS) load_group(g + 1);  // in flight during this group's math
+        if constexpr (PREFETCH) load_group(g + DEPTH, d);   // DEPTH groups stay in flight
         i32x4 acc[2][4];
 #pragma unroll
         for (int rt = 0; rt < 2; ++rt)
@@ -172,7 +184,17 @@ __global__ __launch_bounds__(256, 2) void grouped_mfma_kernel(MfmaArgs a) {
                 }
             }
         }
-    }
+    };
+    // body with prefetch, then the last DEPTH groups without (straight-line
+    // code, so every wait count is exact)
+#pragma unroll 1
+    for (int g0 = 0; g0 < GS - DEPTH; g0 += DEPTH)
+        [&]<int... D>(std::integer_sequence<int, D...>) {
+            (step.template operator()<D, true>(g0 + D), ...);
+        }(std::make_integer_sequence<int, DEPTH>{});
+    [&]<int... D>(std::integer_sequence<int, D...>) {
+        (step.template operator()<D, false>(GS - DEPTH + D), ...);
+    }(std::make_integer_sequence<int, DEPTH>{});
 
     // ---- epilogue ----
     uint32_t flags = 0;
@@ -216,8 +238,8 @@ __global__ __launch_bounds__(256, 2) void grouped_mfma_kernel(MfmaArgs a) {
 
 hipError_t launch_grouped_mfma(const MfmaArgs& a, bool gateup, int max_tiles, hipStream_t s) {
     if (max_tiles <= 0) return hipSuccess;
-    if (gateup) grouped_mfma_kernel<true><<<dim3(max_tiles, (2 * kInter) / kNT), 256, 0, s>>>(a);
-    else grouped_mfma_kernel<false><<<dim3(max_tiles, kHidden / kNT), 256, 0, s>>>(a);
+    if (gateup) grouped_mfma_kernel<true, kHidden / kGroup, 2><<<dim3(max_tiles, (2 * kInter) / kNT), 256, 0, s>>>(a);
+    else grouped_mfma_kernel<false, kInter / kGroup, 2><<<dim3(max_tiles, kHidden / kNT), 256, 0, s>>>(a);
     return hipGetLastError();
 }
 

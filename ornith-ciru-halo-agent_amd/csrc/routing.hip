@@ -17,56 +17,168 @@
 namespace ornith {
 
 // ---------------------------------------------------------------------------
-// Router logits.  Block = 4 waves; wave w owns router row blockIdx.x*4+w and
-// keeps it in registers; the block walks a slice of tokens staged in LDS.
+// Router logits.  The declared butterfly is a balanced tree over the 64 lane
+// partials (every pair sum is formed once and fp32 addition commutes), so
+//   logit = ((S0 + S1) + (S2 + S3)) + bias,
+// Sq = balanced-tree sum of partials 16q..16q+15, and partial l is the fma
+// chain over chunks l, l+64, l+128, l+192.
+// Block = 4 waves on a tile of 32 router rows x 32 tokens; wave q forms Sq.
+// A thread owns 4 rows x 4 tokens.  At step s every wave accumulates partial
+// 16q+s of its 16 outputs from fp32 operands staged in LDS (the block stages
+// the 16 chunks of the step; the next step's global loads are in flight
+// meanwhile).  Two steps make a pair sum, which is folded into a
+// binary-counter stack of quad / octet sums.  Sq meet in LDS at the end.
+// Blocks with blockIdx.x == 8 form the shared-expert gate row (row 256), one
+// token per wave at a time, with the lane-partial butterfly itself.
 // ---------------------------------------------------------------------------
-constexpr int kRouterTokens = 16;
+constexpr int kRouterTile = 32;
+constexpr int kRouterIStride = 8 * kRouterTile + 4;       // [i][j][row] with a 4-float pad per i
+constexpr int kRouterWaveStride = 4 * kRouterIStride;
 
-__global__ __launch_bounds__(256) void router_kernel(const uint16_t* __restrict__ x, int64_t stride, int T,
-                                                     const uint16_t* __restrict__ w, int nrows,
-                                                     const float* __restrict__ bias, float* __restrict__ logits,
-                                                     int64_t logit_stride) {
-    __shared__ uint4 xs[kRouterTokens][256];     // 16 tokens x 2048 bf16
-    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
-    const int row = blockIdx.x * 4 + wv;
-    const int t0 = blockIdx.y * kRouterTokens;
-    const int nt = min(kRouterTokens, T - t0);
-    for (int i = threadIdx.x; i < nt * 256; i += 256) {
-        const int t = i >> 8, c = i & 255;
-        xs[t][c] = *reinterpret_cast<const uint4*>(x + (t0 + t) * stride + c * 8);
-    }
-    uint4 wr[4];
-    if (row < nrows) {
+__device__ __forceinline__ void bf16x8_to_f32(const uint4 v, float f[8]) {
+    const uint32_t u[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
-        for (int i = 0; i < 4; ++i) wr[i] = *reinterpret_cast<const uint4*>(w + size_t(row) * kHidden + (i * 64 + lane) * 8);
-    }
-    __syncthreads();
-    if (row >= nrows) return;
-    const float b = bias && row < kExperts ? bias[row] : 0.f;
-    for (int t = 0; t < nt; ++t) {
-        float acc = 0.f;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const uint4 xv = xs[t][i * 64 + lane];
-            const uint32_t xw[4] = {xv.x, xv.y, xv.z, xv.w};
-            const uint32_t ww[4] = {wr[i].x, wr[i].y, wr[i].z, wr[i].w};
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                acc = __builtin_fmaf(bf16_bits_to_f32(xw[j] & 0xffffu), bf16_bits_to_f32(ww[j] & 0xffffu), acc);
-                acc = __builtin_fmaf(bf16_bits_to_f32(xw[j] >> 16), bf16_bits_to_f32(ww[j] >> 16), acc);
-            }
-        }
-        acc = wave_butterfly_sum(acc);
-        if (bias && row < kExperts) acc = acc + b;
-        if (lane == 0) logits[size_t(t0 + t) * logit_stride + row] = acc;
+    for (int e = 0; e < 4; ++e) {
+        f[2 * e] = __uint_as_float(u[e] << 16);
+        f[2 * e + 1] = __uint_as_float(u[e] & 0xffff0000u);
     }
 }
 
-hipError_t launch_router(const uint16_t* x, int64_t stride, int T, const uint16_t* w, int nrows, const float* bias,
-                         float* logits, int64_t logit_stride, hipStream_t s) {
+__global__ __launch_bounds__(256) void router_kernel(const uint16_t* __restrict__ x, int64_t stride, int T,
+                                                     const uint16_t* __restrict__ w,
+                                                     const uint16_t* __restrict__ shared_w,
+                                                     const float* __restrict__ bias, float* __restrict__ logits,
+                                                     int64_t logit_stride) {
+    __shared__ __align__(16) float Wl[4 * kRouterWaveStride];
+    __shared__ __align__(16) float Xl[4 * kRouterWaveStride];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int t0 = blockIdx.y * kRouterTile;
+
+    if (blockIdx.x == kExperts / kRouterTile) {
+        for (int t = t0 + wave; t < min(T, t0 + kRouterTile); t += 4) {
+            float acc = 0.f;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                float xf[8], wf[8];
+                bf16x8_to_f32(*reinterpret_cast<const uint4*>(x + t * stride + (lane + 64 * i) * 8), xf);
+                bf16x8_to_f32(*reinterpret_cast<const uint4*>(shared_w + (lane + 64 * i) * 8), wf);
+#pragma unroll
+                for (int j = 0; j < 8; ++j) acc = __builtin_fmaf(xf[j], wf[j], acc);
+            }
+            const float v = wave_butterfly_sum(acc);
+            if (lane == 0) logits[size_t(t) * logit_stride + kExperts] = v;
+        }
+        return;
+    }
+
+    const int r0 = blockIdx.x * kRouterTile;
+    // staging: (row-or-token m, wave q, chunk i) for p = tid + 256e
+    uint4 pw[2], px[2];
+    const uint16_t* wp[2];
+    const uint16_t* xp[2];
+    int soff[2];
+#pragma unroll
+    for (int e = 0; e < 2; ++e) {
+        const int p = tid + 256 * e, m = p & 31, qi = p >> 5, q = qi >> 2, i = qi & 3;
+        const int k0 = (16 * q + 64 * i) * 8;               // chunk 16q + s + 64i starts at k0 + 8s
+        wp[e] = w + size_t(r0 + m) * kHidden + k0;
+        xp[e] = x + min(t0 + m, T - 1) * stride + k0;
+        soff[e] = q * kRouterWaveStride + i * kRouterIStride + m;
+    }
+    auto load_step = [&](int s) {
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+            pw[e] = *reinterpret_cast<const uint4*>(wp[e] + 8 * s);
+            px[e] = *reinterpret_cast<const uint4*>(xp[e] + 8 * s);
+        }
+    };
+    auto store_step = [&]() {
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+            float fw[8], fx[8];
+            bf16x8_to_f32(pw[e], fw);
+            bf16x8_to_f32(px[e], fx);
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                Wl[soff[e] + j * kRouterTile] = fw[j];
+                Xl[soff[e] + j * kRouterTile] = fx[j];
+            }
+        }
+    };
+
+    const int rg = lane & 7, tg = lane >> 3;
+    const float* wbase = Wl + wave * kRouterWaveStride + 4 * rg;
+    const float* xbase = Xl + wave * kRouterWaveStride + 4 * tg;
+    float quad[16], octet[16], half16[16];
+    // one partial (32 fma per output, chunk-major) of all 16 outputs
+    auto partial = [&](float acc[16]) {
+#pragma unroll
+        for (int o = 0; o < 16; ++o) acc[o] = 0.f;
+#pragma unroll 1
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const float4 wv = *reinterpret_cast<const float4*>(wbase + i * kRouterIStride + j * kRouterTile);
+                const float4 xv = *reinterpret_cast<const float4*>(xbase + i * kRouterIStride + j * kRouterTile);
+                const float wr[4] = {wv.x, wv.y, wv.z, wv.w}, xr[4] = {xv.x, xv.y, xv.z, xv.w};
+#pragma unroll
+                for (int a = 0; a < 4; ++a)
+#pragma unroll
+                    for (int b = 0; b < 4; ++b) acc[4 * a + b] = __builtin_fmaf(xr[b], wr[a], acc[4 * a + b]);
+            }
+    };
+
+    // -0 + v == v exactly for every v, so the 16-sum can start from -0
+#pragma unroll
+    for (int o = 0; o < 16; ++o) { quad[o] = 0.f; octet[o] = 0.f; half16[o] = -0.f; }
+    load_step(0);
+#pragma unroll 1
+    for (int sp = 0; sp < 8; ++sp) {
+        float acc0[16], acc1[16];
+        __syncthreads();
+        store_step();
+        __syncthreads();
+        load_step(2 * sp + 1);
+        partial(acc0);
+        __syncthreads();
+        store_step();
+        __syncthreads();
+        if (sp < 7) load_step(2 * sp + 2);
+        partial(acc1);
+        // pair sum of partials 2sp, 2sp+1 folded into the quad / octet / 16 stack
+        // (sp is uniform: the selects pick whole stack levels)
+        const bool odd = sp & 1, odd2 = sp & 2;
+#pragma unroll
+        for (int o = 0; o < 16; ++o) {
+            const float pair = acc0[o] + acc1[o];
+            const float q4 = quad[o] + pair;            // used when sp is odd
+            const float o8 = octet[o] + q4;             // used when sp % 4 == 3
+            quad[o] = odd ? quad[o] : pair;
+            octet[o] = (odd && !odd2) ? q4 : octet[o];
+            half16[o] = (odd && odd2) ? half16[o] + o8 : half16[o];
+        }
+    }
+    // Sq of this wave -> LDS, then ((S0 + S1) + (S2 + S3)) + bias
+    __syncthreads();
+    float* Sl = Wl;                                     // [q][token][row], 4 x 32 x 32
+#pragma unroll
+    for (int a = 0; a < 4; ++a)
+#pragma unroll
+        for (int b = 0; b < 4; ++b) Sl[wave * 1024 + (4 * tg + b) * 32 + 4 * rg + a] = half16[4 * a + b];
+    __syncthreads();
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {
+        const int o = tid + 256 * m, row = o & 31, tok = o >> 5;
+        const float v = (Sl[o] + Sl[1024 + o]) + (Sl[2048 + o] + Sl[3072 + o]);
+        if (t0 + tok < T) logits[size_t(t0 + tok) * logit_stride + r0 + row] = bias ? v + bias[r0 + row] : v;
+    }
+}
+
+hipError_t launch_router(const uint16_t* x, int64_t stride, int T, const uint16_t* w, const uint16_t* shared_w,
+                         const float* bias, float* logits, int64_t logit_stride, hipStream_t s) {
     if (T <= 0) return hipSuccess;
-    const dim3 grid((nrows + 3) / 4, (T + kRouterTokens - 1) / kRouterTokens);
-    router_kernel<<<grid, 256, 0, s>>>(x, stride, T, w, nrows, bias, logits, logit_stride);
+    const dim3 grid(kExperts / kRouterTile + (shared_w ? 1 : 0), (T + kRouterTile - 1) / kRouterTile);
+    router_kernel<<<grid, 256, 0, s>>>(x, stride, T, w, shared_w, bias, logits, logit_stride);
     return hipGetLastError();
 }
 
@@ -183,10 +295,16 @@ __global__ __launch_bounds__(512) void permute_scan_kernel(int nblocks, int32_t*
     const int e = threadIdx.x;
     int total = 0;
     if (e < kBanks) {
-        for (int blk = 0; blk < nblocks; ++blk) {
-            const int v = block_counts[size_t(blk) * kBanks + e];
-            block_counts[size_t(blk) * kBanks + e] = total;
-            total += v;
+        // 16 independent loads in flight, then the running exclusive sums
+        for (int b0 = 0; b0 < nblocks; b0 += 16) {
+            int v[16];
+#pragma unroll
+            for (int i = 0; i < 16; ++i) v[i] = b0 + i < nblocks ? block_counts[size_t(b0 + i) * kBanks + e] : 0;
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                if (b0 + i < nblocks) block_counts[size_t(b0 + i) * kBanks + e] = total;
+                total += v[i];
+            }
         }
         counts[e] = total;
     }
