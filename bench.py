@@ -10,7 +10,16 @@ in a HIP graph and replayed; K steps are timed with HIP events on the replay
 stream.
 
 Default workload: N=1 decode (the metric's headline).  The same JSON line also
-reports N=32 and N=1120 under "per_tokens".
+reports, under "per_tokens", N=32, the 1120-token prefill (router bias with
+Zipf(1.1) expert popularity, plus the dense G256 linear [6144, 2048] on the
+same rows) and the 8192-token prefill (Zipf(1.3), plus the G256 LM head
+[151936, 2048] on 32 rows).
+
+"roofline" is that of the kernel with the largest total time: after the timed
+graph replays, K more steps run eagerly with every library kernel launch
+bracketed by a HIP event pair on the launch's own stream (the library's
+timing hook, include/ornith_timing.h); its average interval is the
+denominator of the kernel's algorithmic bytes (or ops) per launch.
 """
 from __future__ import annotations
 
@@ -25,9 +34,46 @@ ROOT = Path(__file__).resolve().parent
 sys.path.insert(0, str(ROOT / 'ornith-ciru-halo-agent_amd'))
 
 HBM_PEAK_GBS = 8000.0
+INT8_PEAK_TOPS = 5000.0          # MI355X dense int8 MFMA
+FP32_PEAK_TFLOPS = 157.3         # MI355X vector fp32
 BF16_PEAK_TFLOPS = 2500.0
-EXPERT_BYTES = 1024 * 2048 // 2 + 4 * 1024 * 8 + 2048 * 512 // 2 + 4 * 2048 * 2   # 1,622,016
+GATEUP_BYTES = 1024 * 2048 // 2 + 4 * 1024 * 8       # one gate-up bank: u4 codes + fp16 scale|offset words
+DOWN_BYTES = 2048 * 512 // 2 + 4 * 2048 * 2          # one down bank
+EXPERT_BYTES = GATEUP_BYTES + DOWN_BYTES              # 1,622,016
 ROUTER_BYTES = 256 * 2048 * 2 + 2048 * 2
+HEAD_N, HEAD_ROWS = 151936, 32
+DENSE_N = 6144
+
+# HBM bytes per launch from rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE runs, scaled
+# by the factor a plain copy of known size reads (bench.py --copy-calibration);
+# keyed by (kernel, tokens).  Commands and raw figures:
+# profiles/decode_n1_n32_hbm_traffic_pmc.md.
+MEASURED_TRAFFIC = {
+    ('route1', 1): 1146865, ('gateup1', 1): 9974418, ('down1', 1): 5194676,
+    ('route', 32): 2442863, ('gateup', 32): 179054858, ('down', 32): 99312378,
+}
+
+
+def kernel_cost(name, T, unique):
+    """Algorithmic work of one launch of `name` for a T-token layer that touches
+    `unique` routed experts: (bound, amount, peak, unit).  hbm amounts are the
+    compulsory bytes (weights of the touched banks + activations in and out);
+    mfma amounts are the int8 ops of the exact integer dots (2 per MAC)."""
+    banks = unique + 1
+    routes = 9 * T
+    if name in ('route1', 'route'):
+        return 'hbm', ROUTER_BYTES + T * 2048 * 2, HBM_PEAK_GBS, 'GB/s'
+    if name in ('gateup1', 'gateup'):
+        return 'hbm', banks * GATEUP_BYTES + T * 2048 + routes * 512 * 4, HBM_PEAK_GBS, 'GB/s'
+    if name in ('down1', 'down'):
+        return 'hbm', banks * DOWN_BYTES + routes * 512 * 4 + T * 2048 * 2, HBM_PEAK_GBS, 'GB/s'
+    if name == 'gateup_mfma':
+        return 'mfma', 2 * routes * 1024 * 2048, INT8_PEAK_TOPS, 'TFLOP/s'
+    if name == 'down_mfma':
+        return 'mfma', 2 * routes * 2048 * 512, INT8_PEAK_TOPS, 'TFLOP/s'
+    if name == 'router':
+        return 'valu', 2 * T * 257 * 2048, FP32_PEAK_TFLOPS, 'TFLOP/s'
+    return 'hbm', T * 2048 * 2, HBM_PEAK_GBS, 'GB/s'
 
 
 def parse():
@@ -37,7 +83,9 @@ def parse():
     p.add_argument('--warmup', type=int, default=40)
     p.add_argument('--tokens', type=int, default=1)
     p.add_argument('--layers', type=int, default=40)
-    p.add_argument('--extra-tokens', default='32,1120')
+    p.add_argument('--extra-tokens', default='32,1120,8192')
+    p.add_argument('--copy-calibration', action='store_true',
+                   help='only run a plain 256 MiB device copy (PMC scale factor for FETCH_SIZE/WRITE_SIZE)')
     p.add_argument('--cpu-seconds', type=float, default=15.0)
     p.add_argument('--no-cpu-baseline', action='store_true')
     return p.parse_args()
@@ -108,8 +156,23 @@ class LayerRunner:
         return start.elapsed_time(end) / steps
 
     def routed_experts_touched(self):
-        ids = self.ti.cpu()
-        return int(ids.unique().numel())
+        """Average number of distinct routed experts per layer."""
+        counts = []
+        for i in range(len(self.layers)):
+            self.step(i)
+            counts.append(int(self.ti.unique().numel()))
+        return sum(counts) / len(counts)
+
+    def kernel_times(self, steps):
+        """Eager pass of `steps` layers with every library kernel launch
+        bracketed by a HIP event pair on its stream: {kernel: (launches, ms)}."""
+        torch, native = self.torch, self.native
+        torch.cuda.synchronize()
+        with native.KernelTimer('*') as kt:
+            for i in range(steps):
+                self.step(i)
+            torch.cuda.synchronize()
+            return {n: kt.read(n) for n in kt.names()}
 
 
 def algorithmic(T, unique):
@@ -117,6 +180,87 @@ def algorithmic(T, unique):
     bytes_ = (unique + 1) * EXPERT_BYTES + ROUTER_BYTES + T * 2048 * 2 * 2
     flops = 2 * (T * 9 * (1024 * 2048 + 2048 * 512) + T * 257 * 2048)
     return bytes_, flops
+
+
+def roofline(times, T, unique):
+    """Roofline of the kernel with the largest total time in `times`."""
+    name = max(times, key=lambda n: times[n][0] * times[n][1])
+    launches, ms = times[name]
+    bound, amount, peak, unit = kernel_cost(name, T, unique)
+    scale = 1e9 if unit == 'GB/s' else 1e12
+    achieved = amount / (ms * 1e-3) / scale
+    traffic = MEASURED_TRAFFIC.get((name, T))
+    return {'bound': bound, 'achieved': achieved, 'peak': peak, 'unit': unit, 'frac': achieved / peak,
+            'traffic': traffic, 'kernel': name, 'avg_us': ms * 1e3, 'launches': launches,
+            'algorithmic_per_launch': amount}
+
+
+def dense_prefill_ms(T, device, steps=20):
+    """Dense G256 linear [6144, 2048] on T rows through ornith_g256::dense_out."""
+    import torch
+    from ornith_g256 import native
+    gen = torch.Generator(device=device)
+    gen.manual_seed(77)
+    x = torch.randn((T, 2048), generator=gen, device=device).to(torch.bfloat16)
+    codes = torch.randint(0, 2 ** 31 - 1, (DENSE_N * 2048 // 8,), generator=gen, device=device,
+                          dtype=torch.int32)
+    meta = (torch.rand((DENSE_N * 2048 // 256,), generator=gen, device=device) * 0.015 + 0.005).half()
+    meta = meta.view(torch.int16).to(torch.int32) & 0xffff
+    layout = native.dense_layout(T, DENSE_N, 2048)
+    ws = torch.empty(max(layout.workspace_bytes, T * 2048 * 2 + DENSE_N * 2048 * 2), dtype=torch.uint8,
+                     device=device)
+    out = torch.empty((T, DENSE_N), dtype=torch.bfloat16, device=device)
+    flags = torch.zeros(1, dtype=torch.int32, device=device)
+    call = lambda: native.dense_out(x, codes, meta, ws, out, flags, T, DENSE_N, 2048, 2, 128)
+    for _ in range(3):
+        call()
+    torch.cuda.synchronize()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record()
+    for _ in range(steps):
+        call()
+    b.record()
+    torch.cuda.synchronize()
+    return a.elapsed_time(b) / steps
+
+
+def head_ms(device, steps=20):
+    """G256 LM head [151936, 2048] on 32 rows: fp32 logits, bf16 logits, argmax."""
+    import torch
+    from ornith_g256 import native, synthetic
+    gen = torch.Generator(device=device)
+    gen.manual_seed(78)
+    codes, meta = synthetic.bank(gen, HEAD_N, 2048, device)
+    x = torch.randn((HEAD_ROWS, 2048), generator=gen, device=device).to(torch.bfloat16)
+    ws = torch.empty(native.lib().ornith_dense_g256_head_workspace_bytes(64, HEAD_N), dtype=torch.uint8,
+                     device=device)
+    logits = torch.empty((HEAD_ROWS, HEAD_N), dtype=torch.float32, device=device)
+    lb = torch.empty((HEAD_ROWS, HEAD_N), dtype=torch.bfloat16, device=device)
+    am = torch.empty((HEAD_ROWS,), dtype=torch.int64, device=device)
+    flags = torch.zeros(1, dtype=torch.int32, device=device)
+    call = lambda: native.dense_head(x, codes, meta, ws, logits, lb, am, flags, 64)
+    for _ in range(3):
+        call()
+    torch.cuda.synchronize()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record()
+    for _ in range(steps):
+        call()
+    b.record()
+    torch.cuda.synchronize()
+    return a.elapsed_time(b) / steps
+
+
+def copy_calibration(device):
+    """A plain 256 MiB device-to-device copy, ten times (PMC scale factor)."""
+    import torch
+    n = 256 << 20
+    src = torch.ones(n, dtype=torch.uint8, device=device)
+    dst = torch.empty_like(src)
+    for _ in range(10):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({'copy_bytes': n, 'copies': 10}))
 
 
 def cpu_baseline(seconds):
@@ -163,31 +307,46 @@ def main():
     import torch
     from ornith_g256 import native, synthetic, tables
     dev = torch.device('cuda:0')
+    if args.copy_calibration:
+        copy_calibration(dev)
+        return
     native.lib()
     silu, sigmoid = tables.load(dev)
     layers = [synthetic.moe_layer(10_000 + i, dev) for i in range(args.layers)]
     torch.cuda.synchronize()
 
-    runner = LayerRunner(layers, args.tokens, dev, silu, sigmoid)
+    zipf = {1120: 1.1, 8192: 1.3}      # router-bias skew of the prefill workloads
+    bias_of = lambda T: synthetic.zipf_bias(zipf[T], 31, dev) if T in zipf else None
+    runner = LayerRunner(layers, args.tokens, dev, silu, sigmoid, bias_of(args.tokens))
     ms = runner.time_steps(args.steps, args.warmup)
     if int(runner.flags.item()) != 0:
         raise RuntimeError(f'native flags raised: {int(runner.flags.item())}')
     unique = runner.routed_experts_touched()
+    times = runner.kernel_times(args.steps)
     bytes_, flops = algorithmic(args.tokens, unique)
     layer_gbs = bytes_ / (ms * 1e-3) / 1e9
 
     per_tokens = {}
     for t in [int(v) for v in args.extra_tokens.split(',') if v]:
-        r = LayerRunner(layers, t, dev, silu, sigmoid)
+        if t == args.tokens:
+            continue
+        r = LayerRunner(layers, t, dev, silu, sigmoid, bias_of(t))
         tms = r.time_steps(max(args.layers, 40), 0)
         u = r.routed_experts_touched()
         b, f = algorithmic(t, u)
-        per_tokens[str(t)] = dict(tokens_per_s=t / (tms * 1e-3), us_per_layer=tms * 1e3, unique_experts=u,
-                                  hbm_frac=b / (tms * 1e-3) / 1e9 / HBM_PEAK_GBS,
-                                  mfma_bf16_frac=f / (tms * 1e-3) / 1e12 / BF16_PEAK_TFLOPS)
+        kt = r.kernel_times(len(layers))
+        entry = dict(tokens_per_s=t / (tms * 1e-3), us_per_layer=tms * 1e3, unique_experts=u,
+                     router_zipf_s=zipf.get(t), hbm_frac=b / (tms * 1e-3) / 1e9 / HBM_PEAK_GBS,
+                     roofline=roofline(kt, t, u), kernels_us={n: v[1] * 1e3 for n, v in kt.items()})
+        if t == 1120:
+            entry['dense_6144x2048_us'] = dense_prefill_ms(t, dev) * 1e3
+        if t == 8192:
+            entry['lm_head_32x151936_us'] = head_ms(dev) * 1e3
+        per_tokens[str(t)] = entry
         del r
     per_tokens[str(args.tokens)] = dict(tokens_per_s=args.tokens / (ms * 1e-3), us_per_layer=ms * 1e3,
-                                        unique_experts=unique, hbm_frac=layer_gbs / HBM_PEAK_GBS)
+                                        unique_experts=unique, hbm_frac=layer_gbs / HBM_PEAK_GBS,
+                                        kernels_us={n: v[1] * 1e3 for n, v in times.items()})
 
     result = {
         'metric': 'MoE layer tokens/s',
@@ -205,8 +364,8 @@ def main():
         'config': {'workload': f'routed MoE layer decode N={args.tokens}: E256 top-8 H2048 I512, G256 4-bit '
                                f'gate-up/down + always-on shared expert, router softmax/top-8',
                    'tokens': args.tokens, 'layers_cycled': args.layers},
-        'roofline': {'bound': 'hbm', 'achieved': layer_gbs, 'peak': HBM_PEAK_GBS, 'unit': 'GB/s',
-                     'frac': layer_gbs / HBM_PEAK_GBS, 'traffic': None, 'kernel': 'whole layer'},
+        'roofline': roofline(times, args.tokens, unique),
+        'layer_hbm_frac': layer_gbs / HBM_PEAK_GBS,
         'per_tokens': per_tokens,
     }
     if not args.no_cpu_baseline:

@@ -25,7 +25,9 @@
 extern "C" {
 #endif
 #ifndef ORNITH_EXPORT
+#ifndef ORNITH_EXPORT
 #define ORNITH_EXPORT __attribute__((visibility("default")))
+#endif
 #endif
 
 /* dense_g256_api.h:11-13 */

@@ -24,7 +24,9 @@
 extern "C" {
 #endif
 #ifndef ORNITH_EXPORT
+#ifndef ORNITH_EXPORT
 #define ORNITH_EXPORT __attribute__((visibility("default")))
+#endif
 #endif
 
 /* head_i8_tile_api.h:13-15 */

@@ -38,7 +38,9 @@
 #ifdef __cplusplus
 extern "C" {
 #endif
+#ifndef ORNITH_EXPORT
 #define ORNITH_EXPORT __attribute__((visibility("default")))
+#endif
 
 /* kernels/routed_storage/routed_direct_api.h:13-16 */
 typedef struct OrnithRoutedDirectLayout {

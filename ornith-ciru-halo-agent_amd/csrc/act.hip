@@ -6,6 +6,7 @@
 //                (routed_storage_n32_consumer.cpp:168-175, 231-295)
 // One wave owns one (row, 256-group); four waves per block.
 #include "kernels.hpp"
+#include "timing.hpp"
 
 namespace ornith {
 
@@ -98,10 +99,10 @@ hipError_t launch_act_bf16(const uint16_t* x, int64_t stride, int rows, int K, i
     const int waves = rows * groups;
     const dim3 grid((waves + 3) / 4), block(256);
     if (qmax == 127)
-        act_bf16_kernel<127><<<grid, block, 0, s>>>(x, stride, rows, groups, ids, words, scales, sums, sticky,
+        timed_launch("act", act_bf16_kernel<127>, dim3(grid), dim3(block), 0, s, x, stride, rows, groups, ids, words, scales, sums, sticky,
                                                      flag_input, flag_act);
     else
-        act_bf16_kernel<7><<<grid, block, 0, s>>>(x, stride, rows, groups, ids, words, scales, sums, sticky,
+        timed_launch("act", act_bf16_kernel<7>, dim3(grid), dim3(block), 0, s, x, stride, rows, groups, ids, words, scales, sums, sticky,
                                                    flag_input, flag_act);
     return hipGetLastError();
 }
@@ -112,9 +113,9 @@ hipError_t launch_act_middle(const float* gate_y, int RS, int R, const int32_t* 
     const int waves = RS * (kInter / kGroup);
     const dim3 grid((waves + 3) / 4), block(256);
     if (qmax == 127)
-        act_middle_kernel<127><<<grid, block, 0, s>>>(gate_y, RS, R, ids, silu_table, words, scales, sums, sticky);
+        timed_launch("act_middle", act_middle_kernel<127>, dim3(grid), dim3(block), 0, s, gate_y, RS, R, ids, silu_table, words, scales, sums, sticky);
     else
-        act_middle_kernel<7><<<grid, block, 0, s>>>(gate_y, RS, R, ids, silu_table, words, scales, sums, sticky);
+        timed_launch("act_middle", act_middle_kernel<7>, dim3(grid), dim3(block), 0, s, gate_y, RS, R, ids, silu_table, words, scales, sums, sticky);
     return hipGetLastError();
 }
 
@@ -173,14 +174,14 @@ __global__ __launch_bounds__(256) void dequantize_bf16_kernel(const uint32_t* __
 
 hipError_t launch_transform_bf16(const uint16_t* x, int M, int K, uint16_t* y, uint32_t* sticky, hipStream_t s) {
     const int waves = M * (K / kGroup);
-    transform_bf16_kernel<<<(waves + 3) / 4, 256, 0, s>>>(x, M, K / kGroup, y, sticky);
+    timed_launch("transform", transform_bf16_kernel, dim3((waves + 3) / 4), dim3(256), 0, s, x, M, K / kGroup, y, sticky);
     return hipGetLastError();
 }
 
 hipError_t launch_dequantize_bf16(const uint32_t* codes, const uint32_t* meta, int N, int K, int tile, uint16_t* w,
                                   uint32_t* sticky, hipStream_t s) {
     const size_t total = size_t(N) * (K / 8);
-    dequantize_bf16_kernel<<<(total + 255) / 256, 256, 0, s>>>(codes, meta, N, K, tile, w, sticky);
+    timed_launch("dequantize", dequantize_bf16_kernel, dim3((total + 255) / 256), dim3(256), 0, s, codes, meta, N, K, tile, w, sticky);
     return hipGetLastError();
 }
 
@@ -191,7 +192,7 @@ __global__ void fill_u32_kernel(uint32_t* p, size_t n, uint32_t v) {
 
 hipError_t launch_fill_u32(uint32_t* p, size_t n, uint32_t v, hipStream_t s) {
     if (!n) return hipSuccess;
-    fill_u32_kernel<<<(n + 255) / 256, 256, 0, s>>>(p, n, v);
+    timed_launch("fill", fill_u32_kernel, dim3((n + 255) / 256), dim3(256), 0, s, p, n, v);
     return hipGetLastError();
 }
 

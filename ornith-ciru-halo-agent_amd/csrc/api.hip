@@ -3,6 +3,7 @@
 // nothing.  The references for each entry are in include/ornith_*.h.
 #include <limits>
 #include "kernels.hpp"
+#include "timing.hpp"
 #include "decode.hpp"
 #include "../../include/ornith_routed.h"
 #include "../../include/ornith_dense.h"
@@ -498,6 +499,6 @@ extern "C" hipError_t ornith_dense_g256_head_launch(const void* input, const voi
     l.sums = l.scales + align256(m * (kHidden / kGroup) * 2);
     TRY(dense_run(input, codes, metadata, workspace, l, static_cast<float*>(logits_f32),
                   static_cast<uint16_t*>(logits_bf16), static_cast<uint32_t*>(flags), M, N, kHidden, 32, stream));
-    argmax_kernel<<<M, 256, 0, stream>>>(static_cast<const float*>(logits_f32), N, static_cast<int64_t*>(argmax_i64));
+    timed_launch("argmax", argmax_kernel, dim3(M), dim3(256), 0, stream, static_cast<const float*>(logits_f32), N, static_cast<int64_t*>(argmax_i64));
     return hipGetLastError();
 }

@@ -19,6 +19,7 @@
 // one acquire); kernel boundaries carry everything else.  Nothing waits on
 // another block, so no launch can dead-lock.
 #include "kernels.hpp"
+#include "timing.hpp"
 #include "topk.hpp"
 #include "decode.hpp"
 
@@ -555,18 +556,18 @@ template <bool ROUTER, bool SHARED, int QMAX>
 static hipError_t run(const DecodeArgs& a, hipStream_t s) {
     const int T = a.T, R = T * kTop;
     const int k1_blocks = ROUTER ? (SHARED ? 17 : 16) : max(1, (T * 8 + 15) / 16);
-    decode_route_kernel<ROUTER, SHARED, QMAX><<<k1_blocks, 1024, 0, s>>>(a);
+    timed_launch("route", decode_route_kernel<ROUTER, SHARED, QMAX>, dim3(k1_blocks), dim3(1024), 0, s, a);
     hipError_t st = hipGetLastError();
     if (st != hipSuccess) return st;
     const int maxseg = min(R, kExperts) + (SHARED ? 1 : 0);
-    decode_gateup_kernel<SHARED><<<dim3(maxseg, 16), 256, 0, s>>>(a);
+    timed_launch("gateup", decode_gateup_kernel<SHARED>, dim3(maxseg, 16), dim3(256), 0, s, a);
     st = hipGetLastError();
     if (st != hipSuccess) return st;
     if (T == 1) {
-        decode_down_tile_kernel<SHARED, QMAX><<<kHidden / 32, 256, 0, s>>>(a);
+        timed_launch("down", decode_down_tile_kernel<SHARED, QMAX>, dim3(kHidden / 32), dim3(256), 0, s, a);
         return hipGetLastError();
     }
-    decode_down_kernel<SHARED, QMAX><<<dim3(maxseg, kDownGroups), 256, 0, s>>>(a);
+    timed_launch("down", decode_down_kernel<SHARED, QMAX>, dim3(maxseg, kDownGroups), dim3(256), 0, s, a);
     st = hipGetLastError();
     if (st != hipSuccess) return st;
     return launch_reduce(a.route_out, a.reduce_w, a.reduce_ids, T, a.final_f32, a.out, a.shared_logit,

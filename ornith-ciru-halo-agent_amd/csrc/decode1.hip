@@ -17,6 +17,7 @@
 // permutation); a slot repeated by the caller simply loads its weights twice.
 // Arithmetic: routed_storage_n32_consumer.cpp:22-307.
 #include "kernels.hpp"
+#include "timing.hpp"
 #include "topk.hpp"
 #include "decode.hpp"
 
@@ -329,13 +330,13 @@ template <bool ROUTER, bool SHARED, int QMAX>
 static hipError_t run1(const DecodeArgs& a, hipStream_t s) {
     const int rows = ROUTER ? (SHARED ? kExperts + 1 : kExperts) : 0;
     const int waves = rows + kHidden / kGroup;
-    decode1_route_kernel<ROUTER, SHARED, QMAX><<<(waves + 15) / 16, 1024, 0, s>>>(a);
+    timed_launch("route1", decode1_route_kernel<ROUTER, SHARED, QMAX>, dim3((waves + 15) / 16), dim3(1024), 0, s, a);
     hipError_t st = hipGetLastError();
     if (st != hipSuccess) return st;
-    decode1_gateup_kernel<ROUTER, SHARED><<<dim3(SHARED ? kSlots : kTop, 16), 256, 0, s>>>(a);
+    timed_launch("gateup1", decode1_gateup_kernel<ROUTER, SHARED>, dim3(SHARED ? kSlots : kTop, 16), dim3(256), 0, s, a);
     st = hipGetLastError();
     if (st != hipSuccess) return st;
-    decode1_down_kernel<SHARED, QMAX><<<kHidden / 32, 512, 0, s>>>(a);
+    timed_launch("down1", decode1_down_kernel<SHARED, QMAX>, dim3(kHidden / 32), dim3(512), 0, s, a);
     return hipGetLastError();
 }
 

@@ -7,6 +7,7 @@
 // (n16 tile, group) block of 512 words (2 KiB) is contiguous.
 #include <limits>
 #include "kernels.hpp"
+#include "timing.hpp"
 #include "../../include/ornith_head.h"
 
 namespace ornith {
@@ -177,17 +178,17 @@ extern "C" hipError_t ornith_head_i8_tile_launch(const void* input, const void* 
     auto words = at<uint32_t>(workspace, l.activation_words);
     auto ascale = at<uint16_t>(workspace, l.activation_scales);
     const int waves = M * kHeadGroups;
-    head_encode_kernel<<<(waves + 3) / 4, 256, 0, stream>>>(static_cast<const uint16_t*>(input), M, words, ascale,
+    timed_launch("head_encode", head_encode_kernel, dim3((waves + 3) / 4), dim3(256), 0, stream, static_cast<const uint16_t*>(input), M, words, ascale,
                                                             sticky);
     hipError_t st = hipGetLastError();
     if (st != hipSuccess) return st;
     auto diag = at<float>(workspace, l.projection);
     if (group_dots)
-        head_project_kernel<true><<<N / 16, 256, 0, stream>>>(
+        timed_launch("head_project", head_project_kernel<true>, dim3(N / 16), dim3(256), 0, stream,
             static_cast<const uint32_t*>(weights), static_cast<const uint16_t*>(scales), words, ascale, M, N, diag,
             static_cast<uint16_t*>(output), static_cast<int32_t*>(group_dots), sticky);
     else
-        head_project_kernel<false><<<N / 16, 256, 0, stream>>>(
+        timed_launch("head_project", head_project_kernel<false>, dim3(N / 16), dim3(256), 0, stream,
             static_cast<const uint32_t*>(weights), static_cast<const uint16_t*>(scales), words, ascale, M, N, diag,
             static_cast<uint16_t*>(output), nullptr, sticky);
     return hipGetLastError();

@@ -12,6 +12,7 @@
 // coalesced loads, then every thread computes one (tile, group, column)
 // integer dot for each route; the group tree runs in a second pass.
 #include "kernels.hpp"
+#include "timing.hpp"
 
 namespace ornith {
 
@@ -144,11 +145,11 @@ hipError_t launch_project_gemv(const ProjArgs& a, int max_segments, Out mode, hi
     const dim3 grid(max_segments, (ntiles + NT - 1) / NT);
     if (max_segments <= 0) return hipSuccess;
     if (a.tile == 32) {
-        if (mode == Out::Routed) project_gemv_kernel<32, Out::Routed><<<grid, 256, 0, s>>>(a, NT, GC);
-        else project_gemv_kernel<32, Out::Dense><<<grid, 256, 0, s>>>(a, NT, GC);
+        if (mode == Out::Routed) timed_launch("dense_gemv", project_gemv_kernel<32, Out::Routed>, dim3(grid), dim3(256), 0, s, a, NT, GC);
+        else timed_launch("dense_gemv", project_gemv_kernel<32, Out::Dense>, dim3(grid), dim3(256), 0, s, a, NT, GC);
     } else {
-        if (mode == Out::Routed) project_gemv_kernel<16, Out::Routed><<<grid, 256, 0, s>>>(a, NT, GC);
-        else project_gemv_kernel<16, Out::Dense><<<grid, 256, 0, s>>>(a, NT, GC);
+        if (mode == Out::Routed) timed_launch("dense_gemv", project_gemv_kernel<16, Out::Routed>, dim3(grid), dim3(256), 0, s, a, NT, GC);
+        else timed_launch("dense_gemv", project_gemv_kernel<16, Out::Dense>, dim3(grid), dim3(256), 0, s, a, NT, GC);
     }
     return hipGetLastError();
 }

@@ -22,6 +22,7 @@
 // columns, laid out so that one lane holds the gate and up accumulators of
 // the same (route, column) and writes SiLU(gate)*up directly.
 #include "kernels.hpp"
+#include "timing.hpp"
 #include "decode.hpp"
 #include <utility>
 
@@ -238,8 +239,8 @@ __global__ __launch_bounds__(256, 2) void grouped_mfma_kernel(MfmaArgs a) {
 
 hipError_t launch_grouped_mfma(const MfmaArgs& a, bool gateup, int max_tiles, hipStream_t s) {
     if (max_tiles <= 0) return hipSuccess;
-    if (gateup) grouped_mfma_kernel<true, kHidden / kGroup, 2><<<dim3(max_tiles, (2 * kInter) / kNT), 256, 0, s>>>(a);
-    else grouped_mfma_kernel<false, kInter / kGroup, 2><<<dim3(max_tiles, kHidden / kNT), 256, 0, s>>>(a);
+    if (gateup) timed_launch("gateup_mfma", grouped_mfma_kernel<true, kHidden / kGroup, 2>, dim3(dim3(max_tiles, (2 * kInter) / kNT)), dim3(256), 0, s, a);
+    else timed_launch("down_mfma", grouped_mfma_kernel<false, kInter / kGroup, 2>, dim3(max_tiles, kHidden / kNT), dim3(256), 0, s, a);
     return hipGetLastError();
 }
 
@@ -267,9 +268,9 @@ hipError_t launch_quant_middle(const float* middle, int RS, int R, const int32_t
                                uint16_t* scales, int32_t* sums, uint32_t* sticky, hipStream_t s) {
     const int waves = RS * 2;
     if (qmax == 127)
-        quant_middle_kernel<127><<<(waves + 3) / 4, 256, 0, s>>>(middle, RS, R, ids, words, scales, sums, sticky);
+        timed_launch("quant_middle", quant_middle_kernel<127>, dim3((waves + 3) / 4), dim3(256), 0, s, middle, RS, R, ids, words, scales, sums, sticky);
     else
-        quant_middle_kernel<7><<<(waves + 3) / 4, 256, 0, s>>>(middle, RS, R, ids, words, scales, sums, sticky);
+        timed_launch("quant_middle", quant_middle_kernel<7>, dim3((waves + 3) / 4), dim3(256), 0, s, middle, RS, R, ids, words, scales, sums, sticky);
     return hipGetLastError();
 }
 

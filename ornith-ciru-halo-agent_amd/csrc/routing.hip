@@ -12,6 +12,7 @@
 // Permute replaces histogram/scan_routes/scatter/partition
 // (routed_storage_n32_prefill.h:19-42) with a deterministic stable order.
 #include "kernels.hpp"
+#include "timing.hpp"
 #include "topk.hpp"
 
 namespace ornith {
@@ -178,7 +179,7 @@ hipError_t launch_router(const uint16_t* x, int64_t stride, int T, const uint16_
                          const float* bias, float* logits, int64_t logit_stride, hipStream_t s) {
     if (T <= 0) return hipSuccess;
     const dim3 grid(kExperts / kRouterTile + (shared_w ? 1 : 0), (T + kRouterTile - 1) / kRouterTile);
-    router_kernel<<<grid, 256, 0, s>>>(x, stride, T, w, shared_w, bias, logits, logit_stride);
+    timed_launch("router", router_kernel, dim3(grid), dim3(256), 0, s, x, stride, T, w, shared_w, bias, logits, logit_stride);
     return hipGetLastError();
 }
 
@@ -216,7 +217,7 @@ __global__ __launch_bounds__(256) void topk_kernel(const float* __restrict__ log
 hipError_t launch_topk(const float* logits, int64_t logit_stride, int T, float* weights, int32_t* ids,
                        const float* shared_logit, int64_t shared_stride, uint16_t* shared_bf16, hipStream_t s) {
     if (T <= 0) return hipSuccess;
-    topk_kernel<<<(T + 3) / 4, 256, 0, s>>>(logits, logit_stride, T, weights, ids, shared_logit, shared_stride,
+    timed_launch("topk", topk_kernel, dim3((T + 3) / 4), dim3(256), 0, s, logits, logit_stride, T, weights, ids, shared_logit, shared_stride,
                                            shared_bf16);
     return hipGetLastError();
 }
@@ -354,14 +355,14 @@ hipError_t launch_permute(const int32_t* ids, int R, int T, bool with_shared, co
                           uint32_t* sticky, int mfma_rows, hipStream_t s) {
     const int Rall = R + (with_shared ? T : 0);
     const int nblocks = (Rall + kPermBlock - 1) / kPermBlock;
-    permute_count_kernel<<<nblocks, kPermBlock, 0, s>>>(ids, R, Rall, p.block_counts, sticky);
+    timed_launch("permute_count", permute_count_kernel, dim3(nblocks), dim3(kPermBlock), 0, s, ids, R, Rall, p.block_counts, sticky);
     hipError_t st = hipGetLastError();
     if (st != hipSuccess) return st;
-    permute_scan_kernel<<<1, 512, 0, s>>>(nblocks, p.block_counts, p.counts, p.offsets, p.segments, p.meta, p.tiles,
+    timed_launch("permute_scan", permute_scan_kernel, dim3(1), dim3(512), 0, s, nblocks, p.block_counts, p.counts, p.offsets, p.segments, p.meta, p.tiles,
                                           mfma_rows);
     st = hipGetLastError();
     if (st != hipSuccess) return st;
-    permute_scatter_kernel<<<nblocks, kPermBlock, 0, s>>>(ids, R, Rall, p.block_counts, p.offsets, p.routes);
+    timed_launch("permute_scatter", permute_scatter_kernel, dim3(nblocks), dim3(kPermBlock), 0, s, ids, R, Rall, p.block_counts, p.offsets, p.routes);
     return hipGetLastError();
 }
 
@@ -427,7 +428,7 @@ hipError_t launch_reduce(const float* route_out, const float* weights, const int
                          uint16_t* out, const uint16_t* shared_logit, const uint16_t* sigmoid_table,
                          uint16_t* shared_out, uint16_t* layer_out, uint32_t* sticky, hipStream_t s) {
     const size_t n = size_t(T) * (kHidden / 4);
-    reduce_kernel<<<(n + 255) / 256, 256, 0, s>>>(route_out, weights, ids, T, final_f32, out, shared_logit,
+    timed_launch("reduce", reduce_kernel, dim3((n + 255) / 256), dim3(256), 0, s, route_out, weights, ids, T, final_f32, out, shared_logit,
                                                   sigmoid_table, shared_out, layer_out, sticky);
     return hipGetLastError();
 }

@@ -16,7 +16,8 @@ PKG = Path(__file__).resolve().parent
 CSRC = PKG.parent / 'csrc'
 LIBDIR = PKG / 'lib'
 LIBNAME = 'libornith_g256_mi355x.so'
-SOURCES = ['act.hip', 'routing.hip', 'proj_gemv.hip', 'proj_mfma.hip', 'decode.hip', 'decode1.hip', 'head.hip', 'api.hip']
+SOURCES = ['act.hip', 'routing.hip', 'proj_gemv.hip', 'proj_mfma.hip', 'decode.hip', 'decode1.hip', 'head.hip', 'timing.hip',
+           'api.hip']
 HIPCC = os.environ.get('HIPCC', '/opt/rocm/bin/hipcc')
 FLAGS = ['--offload-arch=gfx950', '-O3', '-std=c++20', '-fPIC', '-ffp-contract=off',
          '-fhip-fp32-correctly-rounded-divide-sqrt', '-fvisibility=hidden',

@@ -66,6 +66,9 @@ _SIGNATURES = {
     'ornith_head_i8_tile_abi_version': ([], C.c_uint32),
     'ornith_head_i8_tile_get_layout': ([I, I, C.POINTER(HeadLayout)], I),
     'ornith_head_i8_tile_launch': ([P] * 4 + [S] + [P] * 2 + [S] + [P] + [I] * 4 + [P], I),
+    'ornith_mi355x_timing_arm': ([C.c_char_p, I], I),
+    'ornith_mi355x_timing_read': ([C.c_char_p, C.POINTER(I), C.POINTER(C.c_double)], I),
+    'ornith_mi355x_timing_names': ([C.c_char_p, I], I),
 }
 
 
@@ -328,3 +331,32 @@ def dense_head(x, codes, meta, workspace, logits, logits_bf16, argmax, flags, ca
     check(lib().ornith_dense_g256_head_launch(ptr(x), ptr(codes), ptr(meta), ptr(workspace), workspace.numel(),
                                               ptr(logits), ptr(logits_bf16), ptr(argmax), ptr(flags), x.shape[0],
                                               capacity, codes.shape[0] * 32, stream(x)), 'G256 head')
+
+
+class KernelTimer:
+    """Times launches of one library kernel ("*" = all) with HIP event pairs
+    recorded on each launch's own stream (include/ornith_timing.h).  The
+    launches themselves are unchanged."""
+
+    def __init__(self, kernel: str = '*', capacity: int = 100_000):
+        self.kernel, self.capacity = kernel, capacity
+
+    def __enter__(self):
+        check(lib().ornith_mi355x_timing_arm(self.kernel.encode(), self.capacity), "timing_arm")
+        return self
+
+    def __exit__(self, *exc):
+        lib().ornith_mi355x_timing_arm(None, 0)
+        return False
+
+    def names(self):
+        n = lib().ornith_mi355x_timing_names(None, 0)
+        buf = C.create_string_buffer(n + 1)
+        lib().ornith_mi355x_timing_names(buf, n + 1)
+        return [v for v in buf.value.decode().split(',') if v]
+
+    def read(self, kernel: str):
+        """(launches, average milliseconds per launch) for `kernel`."""
+        count, total = C.c_int(0), C.c_double(0.0)
+        check(lib().ornith_mi355x_timing_read(kernel.encode(), C.byref(count), C.byref(total)), "timing_read")
+        return count.value, (total.value / count.value if count.value else 0.0)
