@@ -14,7 +14,7 @@ Integer dot products are computed with float64 matrix products of small
 integers: every partial sum is an integer below 2**53, so the result is
 exact whatever order BLAS chooses.
 
-Pinning (what checks each function, see tests/test_oracle_*.py):
+Pinning (what checks each function, tests/test_oracle.py):
   * bf16/fp16 helpers      - exhaustive over all 65536 bit patterns against
                              torch's own conversions.
   * h128                   - closed form H @ v with the Sylvester matrix in
@@ -30,10 +30,13 @@ Pinning (what checks each function, see tests/test_oracle_*.py):
   * shared silu / sigmoid  - golden table shipped in the reference
                              (native/shared_math_reference.safetensors).
   * router / top-k         - the reduction order is this build's own
-                             declared order (the reference's Triton order is
-                             compiler-chosen): pinned by float64 agreement,
-                             permutation invariance of the selected set, and
-                             brute-force top-k on small inputs.
+                             declared order (the reference's Triton row-dot
+                             and vLLM topk_softmax orders are compiler- or
+                             library-chosen and not importable here): the
+                             declared order is pinned by brute force and
+                             float64 agreement, top-k by brute force on
+                             small inputs.  Against the reference itself:
+                             parity unpinned.
   * permute                - counts against numpy bincount, stable order
                              against argsort(kind='stable').
 """
