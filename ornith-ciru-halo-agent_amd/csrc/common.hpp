@@ -51,12 +51,13 @@ __device__ __forceinline__ uint16_t f32_to_f16_bits(float v) { return __half_as_
 
 // Deterministic exp with the reference's Taylor coefficients and step order
 // (kernels/routed_storage/portable_exp.h:6-26).
+// The special cases are applied by selects after the polynomial (the GPU's
+// float ops do not trap and the conversion saturates), so no lane branches.
 __device__ __forceinline__ float portable_exp(float x) {
-    if (isnan(x)) return x;
-    if (x <= -104.f) return 0.f;
-    if (x >= 89.f) return __builtin_huge_valf();
     const float n_float = __builtin_rintf(x * 0x1.715476p+0f);
-    const int n = static_cast<int>(n_float);
+    // in range for every x the result keeps (-104 < x < 89); the clamp keeps the
+    // conversion defined for the special cases, whose results are discarded
+    const int n = static_cast<int>(fminf(fmaxf(n_float, -200.f), 200.f));
     const float high = n_float * 0x1.62e400p-1f;
     const float low = n_float * 0x1.7f7d1cp-20f;
     const float r = (x - high) - low;
@@ -69,23 +70,39 @@ __device__ __forceinline__ float portable_exp(float x) {
     p = p * r + 0x1p-1f;
     p = p * r + 0x1p+0f;
     p = p * r + 0x1p+0f;
-    return __builtin_ldexpf(p, n);
+    float y = __builtin_ldexpf(p, n);
+    asm volatile("" : "+v"(y));               // keep the polynomial unconditional (no per-lane branch)
+    return isnan(x) ? x : (x <= -104.f ? 0.f : (x >= 89.f ? __builtin_huge_valf() : y));
 }
 __device__ __forceinline__ float silu_portable(float g) { return fdiv_rn(g, 1.f + portable_exp(-g)); }
 
 // ---- wave64 cross-lane helpers --------------------------------------------
-// Exact lane permutation l -> l ^ M inside 32-lane halves, M in {1,2,4,8,16}:
-// DPP quad_perm for 1 and 2, DPP row_ror:8 (== xor 8 within a 16-lane row)
-// for 8, ds_swizzle in bit-mask mode for 4 and 16.  None touches LDS memory.
+// Exact lane permutation l -> l ^ M, M in {1,2,4,8,16,32}, with no LDS-pipe
+// instruction: DPP quad_perm for 1 and 2; DPP row_ror for 4 and 8 (row_ror:n
+// gives lane i the value of lane (i - n) mod 16, so xor 8 is row_ror:8 and
+// xor 4 is row_ror:4 on lanes with bit 2 set, row_ror:12 on the others);
+// v_permlane16_swap / v_permlane32_swap for 16 and 32 (swapping a value with
+// itself returns rows (0,0,2,2) and (1,1,3,3), resp. halves (lo,lo) and
+// (hi,hi)).  Lanes are threadIdx.x & 63 of a one-dimensional block.
 template <int M> __device__ __forceinline__ int xor_perm_i(int v) {
     if constexpr (M == 1) return __builtin_amdgcn_update_dpp(0, v, 0xB1, 0xF, 0xF, false);
     else if constexpr (M == 2) return __builtin_amdgcn_update_dpp(0, v, 0x4E, 0xF, 0xF, false);
-    else if constexpr (M == 8) return __builtin_amdgcn_update_dpp(0, v, 0x128, 0xF, 0xF, false);
-    else return __builtin_amdgcn_ds_swizzle(v, (M << 10) | 0x1F);
+    else if constexpr (M == 4) {
+        const int down = __builtin_amdgcn_update_dpp(0, v, 0x124, 0xF, 0xF, false);
+        const int up = __builtin_amdgcn_update_dpp(0, v, 0x12C, 0xF, 0xF, false);
+        return (threadIdx.x & 4) ? down : up;
+    } else if constexpr (M == 8) return __builtin_amdgcn_update_dpp(0, v, 0x128, 0xF, 0xF, false);
+    else if constexpr (M == 16) {
+        const auto s = __builtin_amdgcn_permlane16_swap(uint32_t(v), uint32_t(v), false, false);
+        return int((threadIdx.x & 16) ? s[0] : s[1]);
+    } else {
+        static_assert(M == 32, "xor_perm: M must be a power of two up to 32");
+        const auto s = __builtin_amdgcn_permlane32_swap(uint32_t(v), uint32_t(v), false, false);
+        return int((threadIdx.x & 32) ? s[0] : s[1]);
+    }
 }
 template <int M> __device__ __forceinline__ float xor_perm_f(float v) {
-    if constexpr (M == 32) return __shfl_xor(v, 32, kWave);
-    else return __int_as_float(xor_perm_i<M>(__float_as_int(v)));
+    return __int_as_float(xor_perm_i<M>(__float_as_int(v)));
 }
 __device__ __forceinline__ float readlane_f(float v, int lane) {
     return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), lane));
@@ -191,10 +208,13 @@ __device__ __forceinline__ void quantize_group_wave(float v[4], uint32_t* words,
     const uint16_t sbits = f32_to_f16_bits(zero ? 1.f : fmaxf(raw, 0x1p-14f));
     const float scale = f16_bits_to_f32(sbits);
     int q[4], sum = 0;
+    const int keep = zero ? 0 : -1;            // scale is 1 when zero: the division is harmless
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-        int t = zero ? 0 : __float2int_rn(fdiv_rn(v[i], scale));
-        t = t < -QMAX ? -QMAX : (t > QMAX ? QMAX : t);
+        // v is finite and |v / scale| <= QMAX + 1/2 unless the group is zero (scale 1):
+        // round, clamp in float, then convert (always in range)
+        const float qf = fminf(fmaxf(__builtin_rintf(fdiv_rn(v[i], scale)), -float(QMAX)), float(QMAX));
+        const int t = int(qf) & keep;
         q[i] = t;
         sum += t;
     }
@@ -238,6 +258,86 @@ __device__ __forceinline__ void h128_wave(float v[4]) {
     h128_lane_step<16>(v, lane);
 #pragma unroll
     for (int i = 0; i < 4; ++i) v[i] = v[i] * kInvSqrt128;
+}
+
+// ---- half-wave group layout ------------------------------------------------
+// One 256-value group on 32 lanes: lane l' = lane & 31 holds k = 8l'..8l'+7,
+// so a wave holds two groups (lanes 0-31 and 32-63).  Every cross-lane step
+// of the H128 stays inside a 16-lane row (DPP only).
+
+// 128-point Hadamard of the two 128-blocks of a group (k bit 7 = lane bit 4):
+// seven ascending butterflies exactly as routed_storage_n32_consumer.cpp:34-41
+// (k bits 0..2 in registers, 3..6 = lane bits 0..3), then 0x3db504f3.
+__device__ __forceinline__ void h128_half(float v[8]) {
+    const int lane = threadIdx.x & 63;
+#pragma unroll
+    for (int b = 1; b < 8; b <<= 1) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            if (i & b) continue;
+            const float lo = v[i], hi = v[i + b];
+            v[i] = lo + hi;
+            v[i + b] = lo - hi;
+        }
+    }
+    h128_lane_step<1>(v, lane);
+    h128_lane_step<1>(v + 4, lane);
+    h128_lane_step<2>(v, lane);
+    h128_lane_step<2>(v + 4, lane);
+    h128_lane_step<4>(v, lane);
+    h128_lane_step<4>(v + 4, lane);
+    h128_lane_step<8>(v, lane);
+    h128_lane_step<8>(v + 4, lane);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) v[i] = v[i] * kInvSqrt128;
+}
+
+// Group quantisation of the half-wave layout (same arithmetic as
+// quantize_group_wave).  Every lane of the half gets the group's fp16 scale
+// bits and Σq; lane l' gets its two activation words 2l' = (q0,q2,q4,q6) and
+// 2l'+1 = (q1,q3,q5,q7) of its chunk.
+template <int QMAX>
+__device__ __forceinline__ void quantize_half(float v[8], uint32_t words[2], uint16_t& sbits_out, int& sum_out,
+                                              uint32_t& flags, uint32_t invalid_flag) {
+    float absmax = 0.f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        if (!isfinite(v[i])) { flags |= invalid_flag; v[i] = 0.f; }
+        absmax = fmaxf(absmax, fabsf(v[i]));
+    }
+    absmax = fmaxf(absmax, xor_perm_f<1>(absmax));
+    absmax = fmaxf(absmax, xor_perm_f<2>(absmax));
+    absmax = fmaxf(absmax, xor_perm_f<4>(absmax));
+    absmax = fmaxf(absmax, xor_perm_f<8>(absmax));
+    absmax = fmaxf(absmax, xor_perm_f<16>(absmax));
+    const float raw = fdiv_rn(absmax, float(QMAX));
+    const bool valid = isfinite(raw) && raw <= 65504.f;
+    if (!valid) flags |= invalid_flag;
+    const bool zero = absmax == 0.f || !valid;
+    const uint16_t sbits = f32_to_f16_bits(zero ? 1.f : fmaxf(raw, 0x1p-14f));
+    const float scale = f16_bits_to_f32(sbits);
+    int q[8], sum = 0;
+    const int keep = zero ? 0 : -1;            // scale is 1 when zero: the division is harmless
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        // v is finite and |v / scale| <= QMAX + 1/2 unless the group is zero (scale 1):
+        // round, clamp in float, then convert (always in range)
+        const float qf = fminf(fmaxf(__builtin_rintf(fdiv_rn(v[i], scale)), -float(QMAX)), float(QMAX));
+        const int t = int(qf) & keep;
+        q[i] = t;
+        sum += t;
+    }
+    sum += xor_perm_i<1>(sum);
+    sum += xor_perm_i<2>(sum);
+    sum += xor_perm_i<4>(sum);
+    sum += xor_perm_i<8>(sum);
+    sum += xor_perm_i<16>(sum);
+    words[0] = (uint32_t(q[0]) & 255u) | ((uint32_t(q[2]) & 255u) << 8) | ((uint32_t(q[4]) & 255u) << 16) |
+               ((uint32_t(q[6]) & 255u) << 24);
+    words[1] = (uint32_t(q[1]) & 255u) | ((uint32_t(q[3]) & 255u) << 8) | ((uint32_t(q[5]) & 255u) << 16) |
+               ((uint32_t(q[7]) & 255u) << 24);
+    sbits_out = sbits;
+    sum_out = sum;
 }
 
 // fp32 group tree term of one (row, column, group) (dense_g256_api.h:35-37):

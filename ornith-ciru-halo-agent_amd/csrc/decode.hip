@@ -155,14 +155,10 @@ __global__ __launch_bounds__(1024) void decode_route_kernel(DecodeArgs a) {
             float v[4];
 #pragma unroll
             for (int i = 0; i < 4; ++i) v[i] = a.logits[size_t(t) * kLogitStride + lane + 64 * i];
-            float w8[kTop];
-            int i8[kTop];
-            softmax_top8(v, w8, i8);
+            float wv;
+            int iv, i8[kTop];
+            softmax_top8(v, wv, iv, i8);
             if (lane < kTop) {
-                float wv = w8[0];
-                int iv = i8[0];
-#pragma unroll
-                for (int j = 1; j < kTop; ++j) if (lane == j) { wv = w8[j]; iv = i8[j]; }
                 a.topk_w[t * kTop + lane] = wv;
                 a.topk_ids[t * kTop + lane] = iv;
                 s_ids[t * kTop + lane] = iv;

@@ -3,14 +3,16 @@
 //
 //   D1 decode1_route_kernel    router logits (257 waves, one row each) and
 //                              the quantised gate input (8 more waves).
-//   D2 decode1_gateup_kernel   block (slot s, tile pair p): slots 0..7 are
-//                              the routed slots, slot 8 the shared expert.
-//                              The activation loads (and, for the shared
-//                              slot, the weights) start at once; routed
-//                              blocks derive their expert with an in-block
-//                              softmax/top-8 of the 257 logits.
-//   D3 decode1_down_kernel     block = 32-column tile over all slots: H128 +
-//                              A8 of the middles, exact dots, fp32 tree and
+//   D2 decode1_gateup_kernel   block (slot s, p): 16 gate + 16 up columns of
+//                              slot s (slots 0..7 routed, 8 the shared
+//                              expert), 288 blocks.  The activation loads
+//                              (and, for the shared slot, the weights) start
+//                              at once; routed blocks derive their expert
+//                              with an in-block softmax/top-8 of the 257
+//                              logits.  Codes go straight to registers.
+//   D3 decode1_down_kernel     block = 16 output columns over all slots (128
+//                              blocks, one wave per slot): H128 + A8 of the
+//                              slot's middle row, exact dots, fp32 tree and
 //                              the slot-order reduction.
 //
 // One token has no expert reuse, so slots are processed as they come (no
@@ -23,25 +25,28 @@
 
 namespace ornith {
 
-constexpr int kPad1 = 1056;
 constexpr int kSlots = kTop + 1;
 
 // ---------------------------------------------------------------------------
 template <bool ROUTER, bool SHARED, int QMAX>
-__global__ __launch_bounds__(1024) void decode1_route_kernel(DecodeArgs a) {
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int gw = blockIdx.x * 16 + wave;
+__global__ __launch_bounds__(64) void decode1_route_kernel(DecodeArgs a) {
+    const int lane = threadIdx.x;
+    const int gw = blockIdx.x;                       // one wave per block
     uint32_t flags = 0;
     const int nrows = ROUTER ? (SHARED ? kExperts + 1 : kExperts) : 0;
     if (gw < nrows) {
         const uint16_t* wrow = gw < kExperts ? a.router_w + size_t(gw) * kHidden : a.shared_gate_w;
+        uint4 wv[4], xv[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            wv[i] = *reinterpret_cast<const uint4*>(wrow + (i * 64 + lane) * 8);
+            xv[i] = *reinterpret_cast<const uint4*>(a.x + (i * 64 + lane) * 8);
+        }
         float acc = 0.f;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            const uint4 wv = *reinterpret_cast<const uint4*>(wrow + (i * 64 + lane) * 8);
-            const uint4 xv = *reinterpret_cast<const uint4*>(a.x + (i * 64 + lane) * 8);
-            const uint32_t xw[4] = {xv.x, xv.y, xv.z, xv.w};
-            const uint32_t ww[4] = {wv.x, wv.y, wv.z, wv.w};
+            const uint32_t xw[4] = {xv[i].x, xv[i].y, xv[i].z, xv[i].w};
+            const uint32_t ww[4] = {wv[i].x, wv[i].y, wv[i].z, wv[i].w};
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
                 acc = __builtin_fmaf(bf16_bits_to_f32(xw[j] & 0xffffu), bf16_bits_to_f32(ww[j] & 0xffffu), acc);
@@ -51,56 +56,67 @@ __global__ __launch_bounds__(1024) void decode1_route_kernel(DecodeArgs a) {
         float v = wave_butterfly_sum(acc);
         if (a.bias && gw < kExperts) v = v + a.bias[gw];
         if (lane == 0) a.logits[gw] = v;
+        return;
     }
-    // quantised gate input on the waves after the router rows
-    const int job = gw - (ROUTER ? kExperts + 1 : 0);
-    if (job >= 0 && job < kHidden / kGroup) {
-        bool live = true;
-        if (!ROUTER && !SHARED) {
-            live = false;
+    // quantised gate input: two groups per wave (half-wave layout)
+    const int job = 2 * (gw - nrows) + (lane >> 5), lp = lane & 31;
+    bool live = true;
+    if (!ROUTER && !SHARED) {
+        live = false;
 #pragma unroll
-            for (int s = 0; s < kTop; ++s) {
-                const int id = a.ids_in[s];
-                live |= id >= 0 && id < kExperts;
-            }
+        for (int s = 0; s < kTop; ++s) {
+            const int id = a.ids_in[s];
+            live |= id >= 0 && id < kExperts;
         }
-        const uint2 raw = *reinterpret_cast<const uint2*>(a.x + job * kGroup + lane * 4);
-        float v[4] = {bf16_bits_to_f32(raw.x & 0xffffu), bf16_bits_to_f32(raw.x >> 16),
-                      bf16_bits_to_f32(raw.y & 0xffffu), bf16_bits_to_f32(raw.y >> 16)};
-        if (live) {
+    }
+    const uint4 raw = *reinterpret_cast<const uint4*>(a.x + job * kGroup + lp * 8);
+    const uint32_t rw[4] = {raw.x, raw.y, raw.z, raw.w};
+    float v[8];
 #pragma unroll
-            for (int i = 0; i < 4; ++i) if (!isfinite(v[i])) flags |= kFlagNonfiniteInput;
-            h128_wave(v);
+    for (int e = 0; e < 4; ++e) {
+        v[2 * e] = bf16_bits_to_f32(rw[e] & 0xffffu);
+        v[2 * e + 1] = bf16_bits_to_f32(rw[e] >> 16);
+    }
+    if (live) {
 #pragma unroll
-            for (int i = 0; i < 4; ++i) if (!isfinite(v[i])) flags |= kFlagNonfiniteInput;
-        } else {
-            v[0] = v[1] = v[2] = v[3] = 0.f;
-        }
-        quantize_group_wave<QMAX>(v, a.x_words + job * 64, a.x_scales + job, a.x_sums + job, flags,
-                                  kFlagInvalidActivation);
+        for (int e = 0; e < 8; ++e) if (!isfinite(v[e])) flags |= kFlagNonfiniteInput;
+        h128_half(v);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) if (!isfinite(v[e])) flags |= kFlagNonfiniteInput;
+    } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) v[e] = 0.f;
+    }
+    uint32_t w2[2];
+    uint16_t sb;
+    int sum;
+    quantize_half<QMAX>(v, w2, sb, sum, flags, kFlagInvalidActivation);
+    *reinterpret_cast<uint2*>(a.x_words + job * 64 + 2 * lp) = make_uint2(w2[0], w2[1]);
+    if (lp == 0) {
+        a.x_scales[job] = sb;
+        a.x_sums[job] = sum;
     }
     flag_or(a.sticky, flags);
 }
 
 // ---------------------------------------------------------------------------
+// D2: block (slot s, p) computes gate columns 16p..16p+15 and the matching up
+// columns 512+16p.. over all 8 groups.  Thread (n, g): local column n (0..15
+// gate, 16..31 up), group g; it loads its 32 code words (stride 32, so each
+// half-wave reads two contiguous 64-byte runs) straight into registers.
 template <bool ROUTER, bool SHARED>
 __global__ __launch_bounds__(256) void decode1_gateup_kernel(DecodeArgs a) {
-    __shared__ uint32_t lw[16 * kPad1];
-    __shared__ uint32_t lm[16 * 32];
-    __shared__ uint32_t la[8 * 64];
+    __shared__ __align__(16) uint32_t la[8 * 64];
     __shared__ float lsa[8], lss[8];
-    __shared__ float lterm[16][32];
+    __shared__ float lterm[8][32];
     __shared__ int s_bank;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int s = blockIdx.x, p = blockIdx.y;
     const bool shared = SHARED && s == kTop;
     // activations of the token: no dependency, issue first
     const uint32_t a0 = a.x_words[tid], a1 = a.x_words[256 + tid];
-    float sreg = 0.f, ssum = 0.f;
-    if (tid < 8) {
-        sreg = f16_bits_to_f32(a.x_scales[tid]);
-        ssum = sreg * float(a.x_sums[tid]);
-    }
+    const uint32_t sbits = a.x_scales[tid & 7];
+    const int sum = a.x_sums[tid & 7];
     int bank = kShared;
     if (!shared) {
         if (ROUTER) {
@@ -108,18 +124,14 @@ __global__ __launch_bounds__(256) void decode1_gateup_kernel(DecodeArgs a) {
                 float v[4];
 #pragma unroll
                 for (int i = 0; i < 4; ++i) v[i] = a.logits[lane + 64 * i];
-                float w8[kTop];
-                int i8[kTop];
-                softmax_top8(v, w8, i8);
+                float wv;
+                int iv, i8[kTop];
+                softmax_top8(v, wv, iv, i8);
                 int mine = i8[0];
 #pragma unroll
                 for (int j = 1; j < kTop; ++j) if (s == j) mine = i8[j];
                 if (lane == 0) s_bank = mine;
                 if (s == 0 && p == 0 && lane < kTop) {
-                    float wv = w8[0];
-                    int iv = i8[0];
-#pragma unroll
-                    for (int j = 1; j < kTop; ++j) if (lane == j) { wv = w8[j]; iv = i8[j]; }
                     a.topk_w[lane] = wv;
                     a.topk_ids[lane] = iv;
                 }
@@ -137,48 +149,41 @@ __global__ __launch_bounds__(256) void decode1_gateup_kernel(DecodeArgs a) {
     }
     const uint32_t* codes = shared ? a.s13_codes : a.w13_codes + size_t(bank) * kGateBankWords;
     const uint32_t* meta = shared ? a.s13_meta : a.w13_meta + size_t(bank) * kGateBankMeta;
-    uint4 stage[16];
+    const int n = lane & 31, g = 2 * wave + (lane >> 5);
+    const int col = n < 16 ? 16 * p + n : kInter + 16 * p + (n - 16);
+    const size_t blk = size_t(col >> 5) * 8 + g;
+    const uint32_t* wp = codes + blk * 1024 + (col & 31);
+    uint32_t wr[32];
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
-        const int h = i >> 3, g = i & 7;
-        stage[i] = *reinterpret_cast<const uint4*>(codes + (size_t(p + 16 * h) * 8 + g) * 1024 + tid * 4);
-    }
-    uint32_t mreg[2];
-#pragma unroll
-    for (int k = 0; k < 2; ++k) {
-        const int q = tid + 256 * k, blk = q >> 5, n = q & 31, h = blk >> 3, g = blk & 7;
-        mreg[k] = meta[(size_t(p + 16 * h) * 8 + g) * 32 + n];
-    }
+    for (int j = 0; j < 32; ++j) wr[j] = wp[j * 32];
+    const uint32_t mw = meta[blk * 32 + (col & 31)];
     la[tid] = a0;
     la[tid + 256] = a1;
-    if (tid < 8) { lsa[tid] = sreg; lss[tid] = ssum; }
-#pragma unroll
-    for (int i = 0; i < 16; ++i) *reinterpret_cast<uint4*>(&lw[i * kPad1 + tid * 4]) = stage[i];
-    lm[tid] = mreg[0];
-    lm[tid + 256] = mreg[1];
-    __syncthreads();
-#pragma unroll
-    for (int k = 0; k < 2; ++k) {
-        const int blk = (tid >> 5) + 8 * k, n = tid & 31, g = blk & 7;
-        const uint32_t* wb = &lw[blk * kPad1 + n];
-        const uint32_t* ab = &la[g * 64];
-        int dot = 0;
-#pragma unroll 8
-        for (int c = 0; c < 32; ++c) {
-            const uint32_t w = wb[c * 32];
-            dot = dot4(code_even(w), int(ab[2 * c]), dot);
-            dot = dot4(code_odd(w), int(ab[2 * c + 1]), dot);
-        }
-        lterm[blk][n] = tree_term(dot, lsa[g], lss[g], lm[blk * 32 + n]);
+    if (tid < 8) {
+        const float sc = f16_bits_to_f32(uint16_t(sbits));
+        lsa[tid] = sc;
+        lss[tid] = sc * float(sum);
     }
     __syncthreads();
-    if (tid < 32) {
+    const uint4* ab = reinterpret_cast<const uint4*>(&la[g * 64]);
+    int dot = 0;
+#pragma unroll
+    for (int c4 = 0; c4 < 16; ++c4) {
+        const uint4 av = ab[c4];
+        dot = dot4(code_even(wr[2 * c4]), int(av.x), dot);
+        dot = dot4(code_odd(wr[2 * c4]), int(av.y), dot);
+        dot = dot4(code_even(wr[2 * c4 + 1]), int(av.z), dot);
+        dot = dot4(code_odd(wr[2 * c4 + 1]), int(av.w), dot);
+    }
+    lterm[g][n] = tree_term(dot, lsa[g], lss[g], mw);
+    __syncthreads();
+    if (tid < 16) {
         uint32_t flags = 0;
         float vg = 0.f, vu = 0.f;
 #pragma unroll
-        for (int g = 0; g < 8; ++g) vg = vg + lterm[g][tid];
+        for (int gg = 0; gg < 8; ++gg) vg = vg + lterm[gg][tid];
 #pragma unroll
-        for (int g = 0; g < 8; ++g) vu = vu + lterm[8 + g][tid];
+        for (int gg = 0; gg < 8; ++gg) vu = vu + lterm[gg][16 + tid];
         float mid;
         if (shared) {
             vg = bf16_round(vg);
@@ -190,132 +195,118 @@ __global__ __launch_bounds__(256) void decode1_gateup_kernel(DecodeArgs a) {
             mid = silu_portable(vg) * vu;
         }
         if (!isfinite(mid)) flags |= kFlagNonfiniteMiddle | kFlagNonfiniteInput;
-        a.middle[size_t(s) * kInter + p * 32 + tid] = mid;
+        a.middle[size_t(s) * kInter + p * 16 + tid] = mid;
         flag_or(a.sticky, flags);
     }
 }
 
 // ---------------------------------------------------------------------------
+// D3: block = 16 output columns over all slots (9 waves).  Wave w quantises
+// slot w's middle row (H128 + A8/A4 of both groups, half-wave layout) while
+// every thread's down-code loads are in flight.  Thread: (slot i, group g) =
+// tid / 64 and lane / 32, chunk half h = (lane / 16) & 1, column n = lane & 15,
+// 16 code words in registers; the two halves' integer dots are added exactly,
+// the two groups' terms meet through xor 32, and the slots are reduced in
+// slot order (routed_storage_n32_consumer.cpp:176-184, 296-307).
 template <bool SHARED, int QMAX>
-__global__ __launch_bounds__(512) void decode1_down_kernel(DecodeArgs a) {
-    __shared__ uint32_t lw[kSlots * 2 * kPad1];
-    __shared__ uint32_t lm[kSlots * 2 * 32];
-    __shared__ uint32_t la[kSlots * 2 * 64];
+__global__ __launch_bounds__(576) void decode1_down_kernel(DecodeArgs a) {
+    __shared__ __align__(16) uint32_t la[kSlots * 2 * 64];
     __shared__ float lsa[kSlots * 2], lss[kSlots * 2];
-    __shared__ float lterm[kSlots * 2][32];
-    __shared__ float lro[kSlots][32];
+    __shared__ float lro[kSlots][16];
     __shared__ int lbank[kSlots];
     __shared__ float lw8[kTop];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, c = blockIdx.x;
     const int nslots = SHARED ? kSlots : kTop;
+    // Every load below is unconditional (unused lanes read a valid address and
+    // drop the value), so the in-order load counter stays exact and each wait
+    // leaves the younger loads in flight.
+    // Load order = wait order: routing first, then the middle row of slot
+    // `wave` (lanes 0-31 group 0, 32-63 group 1), then the shared logit.
+    const int id_in = a.reduce_ids[tid & 7];
+    const float w_in = a.reduce_w[tid & 7];
+    __builtin_amdgcn_sched_barrier(0);                 // keep the routing loads oldest
+    const int lp = lane & 31, gm = lane >> 5;
+    const float* mrow = a.middle + size_t(wave < nslots ? wave : nslots - 1) * kInter + gm * kGroup + lp * 8;
+    const float4 m0 = *reinterpret_cast<const float4*>(mrow);
+    const float4 m1 = *reinterpret_cast<const float4*>(mrow + 4);
+    const uint16_t shared_logit = SHARED ? a.shared_logit[0] : 0;
     if (tid < kTop) {
-        const int id = a.reduce_ids[tid];
-        lbank[tid] = (id >= 0 && id < kExperts) ? id : -1;
-        lw8[tid] = a.reduce_w[tid];
+        lbank[tid] = (id_in >= 0 && id_in < kExperts) ? id_in : -1;
+        lw8[tid] = w_in;
     }
     if (tid == kTop) lbank[kTop] = SHARED ? kShared : -1;
     __syncthreads();
-    // ---- middle rows: job (i, g) = 2i + g on wave job % 8 ----
+    // ---- down codes of (slot i, group g, column n, chunks 16h..16h+15) ----
+    const int i = wave, g = gm, h = (lane >> 4) & 1, n = lane & 15;
+    const int bank = i < nslots ? lbank[i] : -1;
+    const int tile = c >> 1, nn = 16 * (c & 1) + n;
+    const int lb = bank >= 0 ? bank : 0;
+    const uint32_t* base = lb == kShared ? a.s2_codes : a.w2_codes + size_t(lb) * kDownBankWords;
+    const uint32_t* mbase = lb == kShared ? a.s2_meta : a.w2_meta + size_t(lb) * kDownBankMeta;
+    const uint32_t* wp = base + (size_t(tile) * 2 + g) * 1024 + 16 * h * 32 + nn;
+    uint32_t wr[16];
+#pragma unroll
+    for (int j = 0; j < 16; ++j) wr[j] = wp[j * 32];
+    const uint32_t mw = mbase[(size_t(tile) * 2 + g) * 32 + nn];
+    // shared-expert gate: its table load goes out behind the codes, used at the end
+    const uint16_t gate_bits = SHARED ? a.sigmoid_table[shared_logit] : 0;
+    // ---- middle quantisation, one slot per wave ----
     uint32_t flags = 0;
-    float4 mid[3];
+    if (bank >= 0) {
+        float v[8] = {m0.x, m0.y, m0.z, m0.w, m1.x, m1.y, m1.z, m1.w};
+        h128_half(v);
 #pragma unroll
-    for (int k = 0; k < 3; ++k) {
-        const int job = wave + 8 * k, i = job >> 1, g = job & 1;
-        mid[k] = make_float4(0.f, 0.f, 0.f, 0.f);
-        if (i < nslots && lbank[i] >= 0)
-            mid[k] = *reinterpret_cast<const float4*>(a.middle + size_t(i) * kInter + g * kGroup + lane * 4);
-    }
-    // ---- weights: slot i, group g, tile c ----
-    uint4 stage[kSlots * 2 / 2];
-#pragma unroll
-    for (int k = 0; k < kSlots; ++k) {
-        // 18 (slot, group) blocks of 256 uint4 over 512 threads: thread half h takes blocks 2k+h
-        const int blk = 2 * k + (tid >> 8), i = blk >> 1, g = blk & 1;
-        const int bank = lbank[i];
-        stage[k] = make_uint4(0, 0, 0, 0);
-        if (i < nslots && bank >= 0) {
-            const uint32_t* base = bank == kShared ? a.s2_codes : a.w2_codes + size_t(bank) * kDownBankWords;
-            stage[k] = *reinterpret_cast<const uint4*>(base + (size_t(c) * 2 + g) * 1024 + (tid & 255) * 4);
+        for (int e = 0; e < 8; ++e) if (!isfinite(v[e])) flags |= kFlagNonfiniteInput;
+        uint32_t w2[2];
+        uint16_t sb;
+        int sum;
+        quantize_half<QMAX>(v, w2, sb, sum, flags, kFlagInvalidActivation);
+        *reinterpret_cast<uint2*>(&la[(2 * i + gm) * 64 + 2 * lp]) = make_uint2(w2[0], w2[1]);
+        if (lp == 0) {
+            const float sc = f16_bits_to_f32(sb);
+            lsa[2 * i + gm] = sc;
+            lss[2 * i + gm] = sc * float(sum);
         }
     }
-    uint32_t mreg[2];
-#pragma unroll
-    for (int k = 0; k < 2; ++k) {
-        const int q = tid + 512 * k, i = q >> 6, g = (q >> 5) & 1, n = q & 31;
-        mreg[k] = 0;
-        if (i < nslots && lbank[i] >= 0) {
-            const int bank = lbank[i];
-            const uint32_t* meta = bank == kShared ? a.s2_meta : a.w2_meta + size_t(bank) * kDownBankMeta;
-            mreg[k] = meta[(size_t(c) * 2 + g) * 32 + n];
-        }
-    }
-#pragma unroll
-    for (int k = 0; k < 3; ++k) {
-        const int job = wave + 8 * k, i = job >> 1;
-        if (i < nslots && lbank[i] >= 0) {
-            float v[4] = {mid[k].x, mid[k].y, mid[k].z, mid[k].w};
-            h128_wave(v);
-#pragma unroll
-            for (int e = 0; e < 4; ++e) if (!isfinite(v[e])) flags |= kFlagNonfiniteInput;
-            uint16_t sb;
-            int32_t sum;
-            quantize_group_wave<QMAX>(v, &la[job * 64], &sb, &sum, flags, kFlagInvalidActivation);
-            if (lane == 0) {
-                const float sc = f16_bits_to_f32(sb);
-                lsa[job] = sc;
-                lss[job] = sc * float(sum);
-            }
-        }
-    }
-#pragma unroll
-    for (int k = 0; k < kSlots; ++k) {
-        const int blk = 2 * k + (tid >> 8);
-        *reinterpret_cast<uint4*>(&lw[blk * kPad1 + (tid & 255) * 4]) = stage[k];
-    }
-#pragma unroll
-    for (int k = 0; k < 2; ++k) if (tid + 512 * k < kSlots * 64) lm[tid + 512 * k] = mreg[k];
     __syncthreads();
-    // ---- dots: term (i, g, n) ----
-    for (int q = tid; q < nslots * 64; q += 512) {
-        const int blk = q >> 5, n = q & 31;
-        if (lbank[blk >> 1] < 0) continue;
-        const uint32_t* wb = &lw[blk * kPad1 + n];
-        const uint32_t* ab = &la[blk * 64];
+    // ---- dots and the two-group tree ----
+    float term = 0.f;
+    if (bank >= 0) {
+        const uint4* ab = reinterpret_cast<const uint4*>(&la[(2 * i + g) * 64 + 32 * h]);
         int dot = 0;
-#pragma unroll 8
-        for (int cc = 0; cc < 32; ++cc) {
-            const uint32_t w = wb[cc * 32];
-            dot = dot4(code_even(w), int(ab[2 * cc]), dot);
-            dot = dot4(code_odd(w), int(ab[2 * cc + 1]), dot);
+#pragma unroll
+        for (int c4 = 0; c4 < 8; ++c4) {
+            const uint4 av = ab[c4];
+            dot = dot4(code_even(wr[2 * c4]), int(av.x), dot);
+            dot = dot4(code_odd(wr[2 * c4]), int(av.y), dot);
+            dot = dot4(code_even(wr[2 * c4 + 1]), int(av.z), dot);
+            dot = dot4(code_odd(wr[2 * c4 + 1]), int(av.w), dot);
         }
-        lterm[blk][n] = tree_term(dot, lsa[blk], lss[blk], lm[blk * 32 + n]);
+        dot += xor_perm_i<16>(dot);
+        term = tree_term(dot, lsa[2 * i + g], lss[2 * i + g], mw);
+    }
+    const float term1 = xor_perm_f<32>(term);          // group 1 of the same (slot, column)
+    if (bank >= 0 && lane < 16) {
+        float v = 0.f;
+        v = v + term;
+        v = v + term1;
+        if (i == kTop) v = bf16_round(v);
+        if (!isfinite(v)) flags |= kFlagNonfiniteProjection;
+        lro[i][n] = v;
     }
     __syncthreads();
-    if (tid < nslots * 32) {
-        const int i = tid >> 5, n = tid & 31;
-        if (lbank[i] >= 0) {
-            float v = 0.f;
-            v = v + lterm[2 * i][n];
-            v = v + lterm[2 * i + 1][n];
-            if (i == kTop) v = bf16_round(v);
-            if (!isfinite(v)) flags |= kFlagNonfiniteProjection;
-            lro[i][n] = v;
-        }
-    }
-    __syncthreads();
-    // ---- slot-order reduction (routed_storage_n32_consumer.cpp:176-184, 296-307) ----
-    if (tid < 32) {
-        const int col = c * 32 + tid;
+    if (tid < 16) {
+        const int col = c * 16 + tid;
         float sum = 0.f;
 #pragma unroll
-        for (int s = 0; s < kTop; ++s)
-            if (lbank[s] >= 0) sum = sum + lro[s][tid] * lw8[s];
+        for (int sl = 0; sl < kTop; ++sl)
+            if (lbank[sl] >= 0) sum = sum + lro[sl][tid] * lw8[sl];
         const uint16_t o = f32_to_bf16_bits(sum);
         if (!isfinite(sum) || (o & 0x7f80u) == 0x7f80u) flags |= kFlagNonfiniteOutput;
         if (a.final_f32) a.final_f32[col] = sum;
         if (a.out) a.out[col] = o;
         if (SHARED) {
-            const float gate = bf16_bits_to_f32(a.sigmoid_table[a.shared_logit[0]]);
+            const float gate = bf16_bits_to_f32(gate_bits);
             const float sv = lro[kTop][tid] * gate;
             if (!isfinite(sv)) flags |= kFlagNonfiniteOutput;
             const uint16_t so = f32_to_bf16_bits(sv);
@@ -329,14 +320,14 @@ __global__ __launch_bounds__(512) void decode1_down_kernel(DecodeArgs a) {
 template <bool ROUTER, bool SHARED, int QMAX>
 static hipError_t run1(const DecodeArgs& a, hipStream_t s) {
     const int rows = ROUTER ? (SHARED ? kExperts + 1 : kExperts) : 0;
-    const int waves = rows + kHidden / kGroup;
-    timed_launch("route1", decode1_route_kernel<ROUTER, SHARED, QMAX>, dim3((waves + 15) / 16), dim3(1024), 0, s, a);
+    const int waves = rows + kHidden / kGroup / 2;
+    timed_launch("route1", decode1_route_kernel<ROUTER, SHARED, QMAX>, dim3(waves), dim3(64), 0, s, a);
     hipError_t st = hipGetLastError();
     if (st != hipSuccess) return st;
-    timed_launch("gateup1", decode1_gateup_kernel<ROUTER, SHARED>, dim3(SHARED ? kSlots : kTop, 16), dim3(256), 0, s, a);
+    timed_launch("gateup1", decode1_gateup_kernel<ROUTER, SHARED>, dim3(SHARED ? kSlots : kTop, kInter / 16), dim3(256), 0, s, a);
     st = hipGetLastError();
     if (st != hipSuccess) return st;
-    timed_launch("down1", decode1_down_kernel<SHARED, QMAX>, dim3(kHidden / 32), dim3(512), 0, s, a);
+    timed_launch("down1", decode1_down_kernel<SHARED, QMAX>, dim3(kHidden / 16), dim3(64 * kSlots), 0, s, a);
     return hipGetLastError();
 }
 

@@ -200,14 +200,10 @@ __global__ __launch_bounds__(256) void topk_kernel(const float* __restrict__ log
     float v[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) v[i] = logits[size_t(t) * logit_stride + lane + 64 * i];
-    float w8[kTop];
-    int i8[kTop];
-    softmax_top8(v, w8, i8);
+    float wv;
+    int iv, i8[kTop];
+    softmax_top8(v, wv, iv, i8);
     if (lane < kTop) {
-        float wv = w8[0];
-        int iv = i8[0];
-#pragma unroll
-        for (int j = 1; j < kTop; ++j) if (lane == j) { wv = w8[j]; iv = i8[j]; }
         weights[size_t(t) * kTop + lane] = wv;
         ids[size_t(t) * kTop + lane] = iv;
     }

@@ -17,9 +17,10 @@ __device__ __forceinline__ void cswap(uint32_t& ka, int& ia, uint32_t& kb, int& 
     ka = tk; kb = tk2; ia = ti; ib = ti2;
 }
 
-// v: lane l holds the logits of experts l, l+64, l+128, l+192.  Writes the
-// eight weights and ids (identical on every lane).
-__device__ __forceinline__ void softmax_top8(const float v[4], float* w_out, int* id_out) {
+// v: lane l holds the logits of experts l, l+64, l+128, l+192.  Returns the
+// eight selected ids (identical on every lane) in pid, and on lane j < 8 the
+// weight and id of slot j (the renormalisation runs lane-parallel).
+__device__ __forceinline__ void softmax_top8(const float v[4], float& w_lane, int& id_lane, int pid[kTop]) {
     const int lane = threadIdx.x & 63;
     const float m = wave_max(fmaxf(fmaxf(v[0], v[1]), fmaxf(v[2], v[3])));
     float e[4];
@@ -42,28 +43,42 @@ __device__ __forceinline__ void softmax_top8(const float v[4], float* w_out, int
     cswap(k[0], id[0], k[2], id[2]);
     cswap(k[1], id[1], k[3], id[3]);
     cswap(k[1], id[1], k[2], id[2]);
-    int head = 0;
+    // Each lane's four form a queue: the head is k[0]/id[0]; a pop shifts the
+    // rest up and appends the sentinel id 0x7fffffff (a lane is exhausted
+    // when its head id is the sentinel).  All selects, no lane branches.
+    constexpr int kNone = 0x7fffffff;
     uint32_t pk[kTop];
-    int pid[kTop];
 #pragma unroll
     for (int j = 0; j < kTop; ++j) {
-        const uint32_t hk = head == 0 ? k[0] : head == 1 ? k[1] : head == 2 ? k[2] : head == 3 ? k[3] : 0u;
-        const int hid = head == 0 ? id[0] : head == 1 ? id[1] : head == 2 ? id[2] : head == 3 ? id[3] : 0x7fffffff;
-        const bool live = head < 4;
-        const uint32_t best = wave_max_u(live ? hk : 0u);
-        const uint64_t tied = __ballot(live && hk == best);
+        const bool live = id[0] != kNone;
+        const uint32_t best = wave_max_u(live ? k[0] : 0u);
+        const bool cand = live && k[0] == best;
+        const uint64_t tied = __ballot(cand);
         int win;
-        if (__popcll(tied) == 1) win = __builtin_amdgcn_readlane(hid, __ffsll((long long)tied) - 1);
-        else win = wave_min_i((live && hk == best) ? hid : 0x7fffffff);
+        if (__popcll(tied) == 1) win = __builtin_amdgcn_readlane(id[0], __ffsll((long long)tied) - 1);
+        else win = wave_min_i(cand ? id[0] : kNone);
         pk[j] = best;
         pid[j] = win;
-        if (live && hid == win) ++head;
+        const bool pop = cand && id[0] == win;
+        k[0] = pop ? k[1] : k[0];
+        k[1] = pop ? k[2] : k[1];
+        k[2] = pop ? k[3] : k[2];
+        k[3] = pop ? 0u : k[3];
+        id[0] = pop ? id[1] : id[0];
+        id[1] = pop ? id[2] : id[1];
+        id[2] = pop ? id[3] : id[2];
+        id[3] = pop ? kNone : id[3];
     }
     float tot = 0.f;
 #pragma unroll
     for (int j = 0; j < kTop; ++j) tot = tot + __uint_as_float(pk[j]);
+    uint32_t mk = pk[0];
+    int mi = pid[0];
 #pragma unroll
-    for (int j = 0; j < kTop; ++j) { w_out[j] = fdiv_rn(__uint_as_float(pk[j]), tot); id_out[j] = pid[j]; }
+    for (int j = 1; j < kTop; ++j)
+        if (lane == j) { mk = pk[j]; mi = pid[j]; }
+    w_lane = fdiv_rn(__uint_as_float(mk), tot);
+    id_lane = mi;
 }
 
 }  // namespace ornith
