@@ -1,23 +1,24 @@
-// Decode path (T <= 32 tokens): the routed MoE layer in three or four kernels.
+// Decode path for 2..32 tokens: the routed MoE layer as seven kernels, none of
+// which waits on another block (kernel boundaries carry every hand-off).
 //
-//   K1 decode_route_kernel       router logits (fp32, declared order) and the
-//                                quantised gate input; the last block to
-//                                arrive runs softmax/top-8 and the stable
-//                                permutation into per-bank segments.
-//   K2 decode_gateup_kernel      one block per (segment, gate/up tile pair):
-//                                64 KiB of codes staged in LDS, exact int8
-//                                dots, fp32 group tree, then SiLU(gate)*up.
-//   K3 decode_down_tile_kernel   T == 1: one block per 32-column tile over all
-//                                routes; H128 + A8 of the middles, exact dots,
-//                                fp32 tree and the slot reduction in-block.
-//      decode_down_kernel        T > 1: one block per (segment, 128 columns),
-//                                then reduce_kernel combines the slots.
+//   S1 decode_route_kernel     router logits, one wave per (router row, batch
+//                              of 8 tokens), and the quantised gate input
+//                              (H128 + A8/A4, half-wave layout).
+//   S2 topk                    softmax/top-8, one wave per token (routing.hip),
+//      decode_sort_kernel      then one block: stable counting sort of the
+//                              routes into per-bank segments.
+//   S3 decode_gateup_kernel    block (segment, 16 gate + 16 up columns): the
+//                              codes stay in registers while the segment's
+//                              routes stream through four at a time; exact
+//                              int8 dots, fp32 group tree, SiLU(gate)*up.
+//   S4 quant_middle            H128 + quantisation of every middle row once.
+//   S5 decode_down_kernel      block (segment, 32 output columns), same
+//                              scheme, writing route_out.
+//   S6 reduce                  slot-order combination (+ shared expert).
 //
 // Arithmetic is the reference's (routed_storage_n32_consumer.cpp:22-307); the
-// decomposition into kernels is this build's.  The only cross-block hand-off
-// inside a kernel is K1's last-block election (one release fence per block,
-// one acquire); kernel boundaries carry everything else.  Nothing waits on
-// another block, so no launch can dead-lock.
+// decomposition into kernels is this build's.  A single token takes the
+// three-kernel path of decode1.hip.
 #include "kernels.hpp"
 #include "timing.hpp"
 #include "topk.hpp"
@@ -25,163 +26,152 @@
 
 namespace ornith {
 
-// Arrival counter of K1's last-block election.  It lives in this library's
-// own device memory (not the caller's arena, which other ops overwrite
-// between calls) and is reset by the last block, so every launch starts at 0.
-// Launches on one device must therefore not overlap (the same single-stream
-// use the reference's shared arena requires).
-static __device__ uint32_t g_route_arrivals;
-
 constexpr int kDecodeBanks = kExperts + 1;
 constexpr int kMaxRoutes = kDecodeMaxTokens * (kTop + 1);
-constexpr int kPadWords = 1056;
+constexpr int kRouteChunk = 4;
+constexpr int kTokenBatch = 8;
 
 // ---------------------------------------------------------------------------
-// K1
+// S1
 // ---------------------------------------------------------------------------
 template <bool ROUTER, bool SHARED, int QMAX>
-__global__ __launch_bounds__(1024) void decode_route_kernel(DecodeArgs a) {
-    __shared__ uint4 xs[8][256];                  // 8 tokens x 2048 bf16
-    __shared__ int s_last;
-    __shared__ int s_bank[kMaxRoutes];
-    __shared__ int s_cnt[kDecodeBanks], s_off[kDecodeBanks + 1];
-    __shared__ int s_segidx[kDecodeBanks];
-    __shared__ int s_ids[kDecodeMaxTokens * kTop];
-    const int T = a.T, R = T * kTop;
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int gw = blockIdx.x * 16 + wave, nwaves = gridDim.x * 16;
+__global__ __launch_bounds__(256) void decode_route_kernel(DecodeArgs a, int router_waves) {
+    const int T = a.T, lane = threadIdx.x & 63;
+    const int gw = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (ROUTER && gw < router_waves) {
+        const int nb = (T + kTokenBatch - 1) / kTokenBatch;
+        const int row = gw / nb, t0 = (gw % nb) * kTokenBatch, nt = min(kTokenBatch, T - t0);
+        const uint16_t* wrow = row < kExperts ? a.router_w + size_t(row) * kHidden : a.shared_gate_w;
+        uint4 wv[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) wv[i] = *reinterpret_cast<const uint4*>(wrow + (i * 64 + lane) * 8);
+        // every token's row is loaded before the first fma (rows past T repeat
+        // the last token and are not written), so the loads overlap
+        u32x4 xv[kTokenBatch][4];
+#pragma unroll
+        for (int t = 0; t < kTokenBatch; ++t) {
+            const uint16_t* xrow = a.x + size_t(min(t0 + t, T - 1)) * kHidden;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) xv[t][i] = *reinterpret_cast<const u32x4*>(xrow + (i * 64 + lane) * 8);
+        }
+        float acc[kTokenBatch];
+#pragma unroll
+        for (int t = 0; t < kTokenBatch; ++t) {
+            acc[t] = 0.f;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const uint32_t ww[4] = {wv[i].x, wv[i].y, wv[i].z, wv[i].w};
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const uint32_t xw = xv[t][i][j];
+                    acc[t] = __builtin_fmaf(bf16_bits_to_f32(xw & 0xffffu), bf16_bits_to_f32(ww[j] & 0xffffu), acc[t]);
+                    acc[t] = __builtin_fmaf(bf16_bits_to_f32(xw >> 16), bf16_bits_to_f32(ww[j] >> 16), acc[t]);
+                }
+            }
+        }
+        const float b = (a.bias && row < kExperts) ? a.bias[row] : 0.f;
+#pragma unroll
+        for (int t = 0; t < kTokenBatch; ++t) {
+            if (t < nt) {
+                float v = wave_butterfly_sum(acc[t]);
+                if (a.bias && row < kExperts) v = v + b;
+                if (lane == 0) a.logits[size_t(t0 + t) * kLogitStride + row] = v;
+            }
+        }
+        return;
+    }
+    // quantised gate input: wave q handles groups 2(q%4), 2(q%4)+1 of token q/4
+    const int q = gw - (ROUTER ? router_waves : 0);
+    if (q >= T * 4) return;
+    const int tok = q >> 2, job = (q & 3) * 2 + (lane >> 5), lp = lane & 31;
     uint32_t flags = 0;
-
-    // ---- router logits: wave gw owns router row gw (256 = shared gate) ----
-    if (ROUTER) {
-        const bool has_row = gw < (SHARED ? kExperts + 1 : kExperts);
-        const uint16_t* wrow = gw < kExperts ? a.router_w + size_t(gw) * kHidden : a.shared_gate_w;
-        uint4 wr[4];
-        if (has_row) {
+    bool live = true;
+    if (!ROUTER && !SHARED) {
+        live = false;
 #pragma unroll
-            for (int i = 0; i < 4; ++i) wr[i] = *reinterpret_cast<const uint4*>(wrow + (i * 64 + lane) * 8);
-        }
-        const float b = (has_row && a.bias && gw < kExperts) ? a.bias[gw] : 0.f;
-        for (int t0 = 0; t0 < T; t0 += 8) {
-            const int nt = min(8, T - t0);
-            __syncthreads();
-            for (int q = tid; q < nt * 256; q += 1024)
-                xs[q >> 8][q & 255] = *reinterpret_cast<const uint4*>(a.x + size_t(t0 + (q >> 8)) * kHidden + (q & 255) * 8);
-            __syncthreads();
-            if (has_row) {
-                // lane partials of up to eight tokens first (independent chains), then the butterflies
-                float acc[8];
-#pragma unroll
-                for (int t = 0; t < 8; ++t) {
-                    acc[t] = 0.f;
-                    if (t < nt) {
-#pragma unroll
-                        for (int i = 0; i < 4; ++i) {
-                            const uint4 xv = xs[t][i * 64 + lane];
-                            const uint32_t xw[4] = {xv.x, xv.y, xv.z, xv.w};
-                            const uint32_t ww[4] = {wr[i].x, wr[i].y, wr[i].z, wr[i].w};
-#pragma unroll
-                            for (int j = 0; j < 4; ++j) {
-                                acc[t] = __builtin_fmaf(bf16_bits_to_f32(xw[j] & 0xffffu), bf16_bits_to_f32(ww[j] & 0xffffu), acc[t]);
-                                acc[t] = __builtin_fmaf(bf16_bits_to_f32(xw[j] >> 16), bf16_bits_to_f32(ww[j] >> 16), acc[t]);
-                            }
-                        }
-                    }
-                }
-#pragma unroll
-                for (int t = 0; t < 8; ++t) {
-                    if (t < nt) {
-                        float v = wave_butterfly_sum(acc[t]);
-                        if (a.bias && gw < kExperts) v = v + b;
-                        if (lane == 0) a.logits[size_t(t0 + t) * kLogitStride + gw] = v;
-                    }
-                }
-            }
+        for (int s = 0; s < kTop; ++s) {
+            const int id = a.ids_in[tok * kTop + s];
+            live |= id >= 0 && id < kExperts;
         }
     }
-
-    // ---- quantised gate input: one wave per (token, 256-group) ----
-    for (int job = gw; job < T * (kHidden / kGroup); job += nwaves) {
-        const int row = job >> 3, group = job & 7;
-        bool live = true;
-        if (!ROUTER && !SHARED) {
-            live = false;
+    const uint4 raw = *reinterpret_cast<const uint4*>(a.x + size_t(tok) * kHidden + job * kGroup + lp * 8);
+    const uint32_t rw[4] = {raw.x, raw.y, raw.z, raw.w};
+    float v[8];
 #pragma unroll
-            for (int s = 0; s < kTop; ++s) {
-                const int id = a.ids_in[row * kTop + s];
-                live |= id >= 0 && id < kExperts;
-            }
-        }
-        const uint2 raw = *reinterpret_cast<const uint2*>(a.x + size_t(row) * kHidden + group * kGroup + lane * 4);
-        float v[4] = {bf16_bits_to_f32(raw.x & 0xffffu), bf16_bits_to_f32(raw.x >> 16),
-                      bf16_bits_to_f32(raw.y & 0xffffu), bf16_bits_to_f32(raw.y >> 16)};
-        if (live) {
-#pragma unroll
-            for (int i = 0; i < 4; ++i) if (!isfinite(v[i])) flags |= kFlagNonfiniteInput;
-            h128_wave(v);
-#pragma unroll
-            for (int i = 0; i < 4; ++i) if (!isfinite(v[i])) flags |= kFlagNonfiniteInput;
-        } else {
-            v[0] = v[1] = v[2] = v[3] = 0.f;
-        }
-        const size_t g = size_t(row) * 8 + group;
-        quantize_group_wave<QMAX>(v, a.x_words + g * 64, a.x_scales + g, a.x_sums + g, flags,
-                                  kFlagInvalidActivation);
+    for (int e = 0; e < 4; ++e) {
+        v[2 * e] = bf16_bits_to_f32(rw[e] & 0xffffu);
+        v[2 * e + 1] = bf16_bits_to_f32(rw[e] >> 16);
     }
-
-    // ---- K3's column-group counters (stream order makes these visible) ----
-    if (blockIdx.x == 0 && tid < kDownGroups) a.counters[tid] = 0;
-
-    // ---- last-block election ----
-    // Every wave waits for its own stores, one release fence per block makes
-    // them visible device-wide, and only the last block acquires.
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
-    if (tid == 0) {
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
-        const uint32_t old = atomicAdd(&g_route_arrivals, 1u);
-        s_last = old == gridDim.x - 1;
-        if (s_last) {
-            g_route_arrivals = 0;
-            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-        }
-    }
-    __syncthreads();
-    if (!s_last) { flag_or(a.sticky, flags); return; }
-
-    // ---- top-8 (router) or the caller's ids ----
-    if (ROUTER) {
-        for (int t = wave; t < T; t += 16) {
-            float v[4];
+    if (live) {
 #pragma unroll
-            for (int i = 0; i < 4; ++i) v[i] = a.logits[size_t(t) * kLogitStride + lane + 64 * i];
-            float wv;
-            int iv, i8[kTop];
-            softmax_top8(v, wv, iv, i8);
-            if (lane < kTop) {
-                a.topk_w[t * kTop + lane] = wv;
-                a.topk_ids[t * kTop + lane] = iv;
-                s_ids[t * kTop + lane] = iv;
-            }
-            if (SHARED && lane == 0) a.shared_logit[t] = f32_to_bf16_bits(a.logits[size_t(t) * kLogitStride + kExperts]);
-        }
+        for (int e = 0; e < 8; ++e) if (!isfinite(v[e])) flags |= kFlagNonfiniteInput;
+        h128_half(v);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) if (!isfinite(v[e])) flags |= kFlagNonfiniteInput;
     } else {
-        for (int r = tid; r < R; r += 1024) s_ids[r] = a.ids_in[r];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) v[e] = 0.f;
     }
-    for (int b = tid; b < kDecodeBanks; b += 1024) s_cnt[b] = 0;
-    __syncthreads();
+    uint32_t w2[2];
+    uint16_t sb;
+    int sum;
+    quantize_half<QMAX>(v, w2, sb, sum, flags, kFlagInvalidActivation);
+    const size_t g = size_t(tok) * 8 + job;
+    *reinterpret_cast<uint2*>(a.x_words + g * 64 + 2 * lp) = make_uint2(w2[0], w2[1]);
+    if (lp == 0) {
+        a.x_scales[g] = sb;
+        a.x_sums[g] = sum;
+    }
+    flag_or(a.sticky, flags);
+}
 
-    // ---- stable counting sort of routes by bank ----
-    const int Rall = R + (SHARED ? T : 0);
-    for (int r = tid; r < Rall; r += 1024) {
-        int bank = kShared;
-        if (r < R) {
-            const int id = s_ids[r];
-            bank = (id >= 0 && id < kExperts) ? id : -1;
-            if (bank < 0 && id != -1) flags |= kFlagInvalidExpert;
+// ---------------------------------------------------------------------------
+// S2b (after the top-k kernel): one block.  Segments are the non-empty banks
+// in bank order (0..255, 256 = shared); inside a segment routes keep their
+// index order (route r = 8t + slot, shared route R + t).  Route r is thread
+// r: its stable rank = routes of its bank in earlier 64-route chunks (chunk
+// histograms, prefixed per bank) + earlier lanes of its own chunk (readlane
+// scan inside the wave).
+// ---------------------------------------------------------------------------
+constexpr int kSortChunks = (kMaxRoutes + 63) / 64;
+constexpr int kSegRoutes = 8;          // a segment longer than this is split into pieces of 8 routes
+constexpr int kMaxSegments = kDecodeBanks + kMaxRoutes / kSegRoutes;
+
+template <bool SHARED>
+__global__ __launch_bounds__(512) void decode_sort_kernel(DecodeArgs a, const int32_t* __restrict__ ids) {
+    __shared__ int s_hist[kSortChunks][kDecodeBanks];
+    __shared__ int s_total[kDecodeBanks], s_off[kDecodeBanks];
+    const int T = a.T, R = T * kTop, Rall = R + (SHARED ? T : 0);
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    for (int i = tid; i < kSortChunks * kDecodeBanks; i += 512) (&s_hist[0][0])[i] = 0;
+    uint32_t flags = 0;
+    int bank = -1;
+    const int r = tid;
+    if (r < R) {
+        const int id = ids[r];
+        bank = (id >= 0 && id < kExperts) ? id : -1;
+        if (bank < 0 && id != -1) flags |= kFlagInvalidExpert;
+    } else if (r < Rall) {
+        bank = kShared;
+    }
+    __syncthreads();
+    if (bank >= 0) atomicAdd(&s_hist[wave][bank], 1);
+    int rank_in = 0;
+#pragma unroll 8
+    for (int l = 0; l < 64; ++l) {
+        const int bl = __builtin_amdgcn_readlane(bank, l);
+        rank_in += (l < lane && bl == bank) ? 1 : 0;
+    }
+    __syncthreads();
+    if (tid < kDecodeBanks) {
+        int run = 0;
+#pragma unroll
+        for (int k = 0; k < kSortChunks; ++k) {
+            const int c = s_hist[k][tid];
+            s_hist[k][tid] = run;
+            run += c;
         }
-        s_bank[r] = bank;
-        if (bank >= 0) atomicAdd(&s_cnt[bank], 1);
+        s_total[tid] = run;
     }
     __syncthreads();
     if (wave == 0) {
@@ -191,8 +181,8 @@ __global__ __launch_bounds__(1024) void decode_route_kernel(DecodeArgs a) {
 #pragma unroll
         for (int i = 0; i < 5; ++i) {
             const int b = lane * 5 + i;
-            c[i] = b < kDecodeBanks ? s_cnt[b] : 0;
-            nz[i] = c[i] > 0;
+            c[i] = b < kDecodeBanks ? s_total[b] : 0;
+            nz[i] = (c[i] + kSegRoutes - 1) / kSegRoutes;      // pieces of this bank
             tc += c[i];
             tn += nz[i];
         }
@@ -208,110 +198,105 @@ __global__ __launch_bounds__(1024) void decode_route_kernel(DecodeArgs a) {
             const int b = lane * 5 + i;
             if (b < kDecodeBanks) {
                 s_off[b] = runc;
-                s_segidx[b] = nz[i] ? runn : -1;
-                if (nz[i]) a.segments[runn] = Segment{b, runc, c[i], 0};
+                for (int k = 0; k < nz[i]; ++k)
+                    a.segments[runn + k] = Segment{b, runc + k * kSegRoutes, min(kSegRoutes, c[i] - k * kSegRoutes), 0};
             }
             runc += c[i];
             runn += nz[i];
         }
-        if (lane == 63) { s_off[kDecodeBanks] = ic; a.nseg[0] = in; a.nseg[1] = ic; }
+        if (lane == 63) { a.nseg[0] = in; a.nseg[1] = ic; }
     }
     __syncthreads();
-    for (int r = tid; r < Rall; r += 1024) {
-        const int bank = s_bank[r];
-        if (bank < 0) continue;
-        int rank = 0;
-        for (int j = 0; j < r; ++j) rank += s_bank[j] == bank;
-        a.routes[s_off[bank] + rank] = r;
-    }
+    if (bank >= 0) a.routes[s_off[bank] + s_hist[wave][bank] + rank_in] = r;
     flag_or(a.sticky, flags);
 }
 
 // ---------------------------------------------------------------------------
-// K2: gate/up for one (segment, tile pair p): gate columns 32p..32p+31 and the
-// matching up columns 512+32p..; writes middle[route, 32p..32p+31].
-// Every global load that depends only on the segment is issued before the
-// first wait: the 64 KiB of codes, the metadata, and the first route's
-// quantised activations.
+// S3: block (segment, p): gate columns 32p..32p+31 and up columns 512+32p..
+// (one whole 32-column tile each).  Wave g = group g; lane = local column
+// (0..31 gate, 32..63 up), so every load instruction reads two whole 128-byte
+// rows.  Each thread keeps its 32 code words in registers while the
+// segment's routes stream through four at a time; the next chunk's
+// activations load while the current one computes.
 // ---------------------------------------------------------------------------
 template <bool SHARED>
-__global__ __launch_bounds__(256) void decode_gateup_kernel(DecodeArgs a) {
-    __shared__ uint32_t lw[16 * kPadWords];
-    __shared__ uint32_t lm[16 * 32];
-    __shared__ uint32_t la[8 * 64];
-    __shared__ float lsa[8], lss[8];
-    __shared__ float lterm[16][32];
-    if (int(blockIdx.x) >= a.nseg[0]) return;
-    const Segment sg = a.segments[blockIdx.x];
-    const int tid = threadIdx.x, p = blockIdx.y, R = a.T * kTop;
+__global__ __launch_bounds__(512) void decode_gateup_kernel(DecodeArgs a) {
+    __shared__ __align__(16) uint32_t la[kRouteChunk][512];
+    __shared__ float lsa[kRouteChunk][8], lss[kRouteChunk][8];
+    __shared__ float lterm[kRouteChunk][8][64];
+    __shared__ int lr[256];
+    // segments in reverse bank order: the shared expert's (longest, last)
+    // segment is dispatched first
+    const int nseg = a.nseg[0];
+    if (int(blockIdx.y) >= nseg) return;
+    const Segment sg = a.segments[nseg - 1 - int(blockIdx.y)];
+    const int tid = threadIdx.x, lane = tid & 63, g = tid >> 6, p = blockIdx.x, R = a.T * kTop;
     const bool shared = SHARED && sg.bank == kShared;
     const uint32_t* codes = shared ? a.s13_codes : a.w13_codes + size_t(sg.bank) * kGateBankWords;
     const uint32_t* meta = shared ? a.s13_meta : a.w13_meta + size_t(sg.bank) * kGateBankMeta;
-    uint4 stage[16];
+    // route list first (waiting for it must not wait for the codes)
+    const int route_in = a.routes[sg.first + min(tid, sg.count - 1)];
+    __builtin_amdgcn_sched_barrier(0);
+    const int tile = lane < 32 ? p : 16 + p;
+    const size_t blk = size_t(tile) * 8 + g;
+    const uint32_t* wp = codes + blk * 1024 + (lane & 31);
+    uint32_t wr[32];
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
-        // block i = (h, g): tile p + 16h, group g; thread tid owns words 4tid..4tid+3
-        const int h = i >> 3, g = i & 7;
-        stage[i] = *reinterpret_cast<const uint4*>(codes + (size_t(p + 16 * h) * 8 + g) * 1024 + tid * 4);
-    }
-    uint32_t mreg[2];
-#pragma unroll
-    for (int k = 0; k < 2; ++k) {
-        const int q = tid + 256 * k, blk = q >> 5, n = q & 31, h = blk >> 3, g = blk & 7;
-        mreg[k] = meta[(size_t(p + 16 * h) * 8 + g) * 32 + n];
-    }
-    int route = a.routes[sg.first];
-    int row = route < R ? route / kTop : route - R;
-    uint32_t areg[2];
-    areg[0] = a.x_words[size_t(row) * 512 + tid];
-    areg[1] = a.x_words[size_t(row) * 512 + 256 + tid];
-    float sreg = 0.f, ssum = 0.f;
-    if (tid < 8) {
-        sreg = f16_bits_to_f32(a.x_scales[row * 8 + tid]);
-        ssum = sreg * float(a.x_sums[row * 8 + tid]);
-    }
-#pragma unroll
-    for (int i = 0; i < 16; ++i) *reinterpret_cast<uint4*>(&lw[i * kPadWords + tid * 4]) = stage[i];
-    lm[tid] = mreg[0];
-    lm[tid + 256] = mreg[1];
+    for (int j = 0; j < 32; ++j) wr[j] = wp[j * 32];
+    const uint32_t mw = meta[blk * 32 + (lane & 31)];
+    if (tid < sg.count) lr[tid] = route_in;
+    __syncthreads();
+    // staging registers for one chunk: route rr = tid / 128 holds words
+    // (tid % 128) * 4 .. + 3 of its row; threads tid < 32 also hold the
+    // (route tid / 8, group tid % 8) scale and sum
+    u32x4 areg;
+    uint32_t sreg = 0;
+    int sumreg = 0;
+    auto load_chunk = [&](int r0) {
+        const int k = min(r0 + (tid >> 7), sg.count - 1);
+        const int route = lr[k];
+        const int row = route < R ? route / kTop : route - R;
+        areg = *reinterpret_cast<const u32x4*>(a.x_words + size_t(row) * 512 + (tid & 127) * 4);
+        const int k2 = min(r0 + ((tid & 31) >> 3), sg.count - 1);
+        const int route2 = lr[k2];
+        const int row2 = route2 < R ? route2 / kTop : route2 - R;
+        sreg = a.x_scales[size_t(row2) * 8 + (tid & 7)];
+        sumreg = a.x_sums[size_t(row2) * 8 + (tid & 7)];
+    };
     uint32_t flags = 0;
-    for (int r = 0; r < sg.count; ++r) {
-        if (r > 0) {
-            __syncthreads();
-            route = a.routes[sg.first + r];
-            row = route < R ? route / kTop : route - R;
-            areg[0] = a.x_words[size_t(row) * 512 + tid];
-            areg[1] = a.x_words[size_t(row) * 512 + 256 + tid];
-            if (tid < 8) {
-                sreg = f16_bits_to_f32(a.x_scales[row * 8 + tid]);
-                ssum = sreg * float(a.x_sums[row * 8 + tid]);
-            }
-        }
-        la[tid] = areg[0];
-        la[tid + 256] = areg[1];
-        if (tid < 8) { lsa[tid] = sreg; lss[tid] = ssum; }
-        __syncthreads();
-#pragma unroll
-        for (int k = 0; k < 2; ++k) {
-            const int blk = (tid >> 5) + 8 * k, n = tid & 31, g = blk & 7;
-            const uint32_t* wb = &lw[blk * kPadWords + n];
-            const uint32_t* ab = &la[g * 64];
-            int dot = 0;
-#pragma unroll 8
-            for (int c = 0; c < 32; ++c) {
-                const uint32_t w = wb[c * 32];
-                dot = dot4(code_even(w), int(ab[2 * c]), dot);
-                dot = dot4(code_odd(w), int(ab[2 * c + 1]), dot);
-            }
-            lterm[blk][n] = tree_term(dot, lsa[g], lss[g], lm[blk * 32 + n]);
-        }
-        __syncthreads();
+    load_chunk(0);
+    for (int r0 = 0; r0 < sg.count; r0 += kRouteChunk) {
+        const int nr = min(kRouteChunk, sg.count - r0);
+        __syncthreads();                                   // previous chunk's readers are done
+        *reinterpret_cast<u32x4*>(&la[tid >> 7][(tid & 127) * 4]) = areg;
         if (tid < 32) {
+            const float sc = f16_bits_to_f32(uint16_t(sreg));
+            lsa[tid >> 3][tid & 7] = sc;
+            lss[tid >> 3][tid & 7] = sc * float(sumreg);
+        }
+        __syncthreads();
+        if (r0 + kRouteChunk < sg.count) load_chunk(r0 + kRouteChunk);
+        for (int rr = 0; rr < nr; ++rr) {
+            const uint4* ab = reinterpret_cast<const uint4*>(&la[rr][g * 64]);
+            int dot = 0;
+#pragma unroll
+            for (int c4 = 0; c4 < 16; ++c4) {
+                const uint4 av = ab[c4];
+                dot = dot4(code_even(wr[2 * c4]), int(av.x), dot);
+                dot = dot4(code_odd(wr[2 * c4]), int(av.y), dot);
+                dot = dot4(code_even(wr[2 * c4 + 1]), int(av.z), dot);
+                dot = dot4(code_odd(wr[2 * c4 + 1]), int(av.w), dot);
+            }
+            lterm[rr][g][lane] = tree_term(dot, lsa[rr][g], lss[rr][g], mw);
+        }
+        __syncthreads();
+        if (tid < nr * 32) {
+            const int rr = tid >> 5, c = tid & 31;
             float vg = 0.f, vu = 0.f;
 #pragma unroll
-            for (int g = 0; g < 8; ++g) vg = vg + lterm[g][tid];
+            for (int gg = 0; gg < 8; ++gg) vg = vg + lterm[rr][gg][c];
 #pragma unroll
-            for (int g = 0; g < 8; ++g) vu = vu + lterm[8 + g][tid];
+            for (int gg = 0; gg < 8; ++gg) vu = vu + lterm[rr][gg][32 + c];
             float mid;
             if (shared) {
                 // shared linear outputs are bf16; tabulated SiLU; bf16 product
@@ -325,208 +310,93 @@ __global__ __launch_bounds__(256) void decode_gateup_kernel(DecodeArgs a) {
                 mid = silu_portable(vg) * vu;
             }
             if (!isfinite(mid)) flags |= kFlagNonfiniteMiddle | kFlagNonfiniteInput;
-            a.middle[size_t(route) * kInter + p * 32 + tid] = mid;
-        }
-    }
-    flag_or(a.sticky, flags);
-}
-
-// H128 + quantisation of one 256-group of a middle row, held as float4 per lane.
-template <int QMAX>
-__device__ __forceinline__ void quantize_middle(float4 m4, uint32_t* words, float* sa, float* ss, uint32_t& flags) {
-    float v[4] = {m4.x, m4.y, m4.z, m4.w};
-    h128_wave(v);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) if (!isfinite(v[i])) flags |= kFlagNonfiniteInput;
-    uint16_t sb;
-    int32_t sum;
-    quantize_group_wave<QMAX>(v, words, &sb, &sum, flags, kFlagInvalidActivation);
-    if ((threadIdx.x & 63) == 0) {
-        const float s = f16_bits_to_f32(sb);
-        *sa = s;
-        *ss = s * float(sum);
-    }
-}
-
-// ---------------------------------------------------------------------------
-// K3 (T == 1): one block per 32-column tile over every route (at most 8
-// routed + 1 shared), so the slot reduction needs no other block.  Each block
-// quantises the (at most 9) middle rows itself.
-// ---------------------------------------------------------------------------
-template <bool SHARED, int QMAX>
-__global__ __launch_bounds__(256) void decode_down_tile_kernel(DecodeArgs a) {
-    constexpr int MR = kTop + 1;
-    __shared__ uint32_t lw[MR * 2 * kPadWords];
-    __shared__ uint32_t lm[MR * 2 * 32];
-    __shared__ uint32_t la[MR * 2 * 64];
-    __shared__ float lsa[MR * 2], lss[MR * 2];
-    __shared__ float lterm[MR * 2][32];
-    __shared__ float lro[MR][32];
-    __shared__ int lroute[MR], lslot[kTop + 1];
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, c = blockIdx.x;
-    const int nr = a.nseg[1];                      // valid routes in permuted order
-    if (tid < MR) {
-        const int route = tid < nr ? a.routes[tid] : -1;
-        lroute[tid] = route;
-    }
-    if (tid < kTop + 1) lslot[tid] = -1;
-    __syncthreads();
-    if (tid < nr) lslot[lroute[tid] < kTop ? lroute[tid] : kTop] = tid;    // route -> row in this block
-    // ---- weights: route i, group g, tile c (2 KiB-aligned 4 KiB blocks) ----
-    uint4 stage[2 * MR];
-#pragma unroll
-    for (int k = 0; k < 2 * MR; ++k) {
-        const int i = k >> 1, g = k & 1;
-        stage[k] = make_uint4(0, 0, 0, 0);
-        if (i < nr) {
-            const int route = lroute[i];
-            const int id = route < kTop ? a.reduce_ids[route] : kShared;
-            const bool sh = SHARED && route >= kTop;
-            const uint32_t* bank = sh ? a.s2_codes : a.w2_codes + size_t(id) * kDownBankWords;
-            stage[k] = *reinterpret_cast<const uint4*>(bank + (size_t(c) * 2 + g) * 1024 + tid * 4);
-        }
-    }
-    uint32_t mreg[3];
-#pragma unroll
-    for (int k = 0; k < 3; ++k) {
-        const int q = tid + 256 * k, i = q >> 6, g = (q >> 5) & 1, n = q & 31;
-        mreg[k] = 0;
-        if (i < nr) {
-            const int route = lroute[i];
-            const int id = route < kTop ? a.reduce_ids[route] : kShared;
-            const bool sh = SHARED && route >= kTop;
-            const uint32_t* meta = sh ? a.s2_meta : a.w2_meta + size_t(id) * kDownBankMeta;
-            mreg[k] = meta[(size_t(c) * 2 + g) * 32 + n];
-        }
-    }
-    // ---- middle rows: job (i, g) on wave (2i + g) % 4 ----
-    uint32_t flags = 0;
-    float4 mid[5];
-#pragma unroll
-    for (int k = 0; k < 5; ++k) {
-        const int job = wave + 4 * k, i = job >> 1, g = job & 1;
-        mid[k] = make_float4(0.f, 0.f, 0.f, 0.f);
-        if (i < nr) mid[k] = *reinterpret_cast<const float4*>(a.middle + size_t(lroute[i]) * kInter + g * kGroup + lane * 4);
-    }
-#pragma unroll
-    for (int k = 0; k < 5; ++k) {
-        const int job = wave + 4 * k, i = job >> 1;
-        if (i < nr) quantize_middle<QMAX>(mid[k], &la[job * 64], &lsa[job], &lss[job], flags);
-    }
-#pragma unroll
-    for (int k = 0; k < 2 * MR; ++k) *reinterpret_cast<uint4*>(&lw[k * kPadWords + tid * 4]) = stage[k];
-#pragma unroll
-    for (int k = 0; k < 3; ++k) if (tid + 256 * k < MR * 64) lm[tid + 256 * k] = mreg[k];
-    __syncthreads();
-    // ---- dots: term (i, g, n) ----
-    for (int q = tid; q < nr * 64; q += 256) {
-        const int blk = q >> 5, n = q & 31;
-        const uint32_t* wb = &lw[blk * kPadWords + n];
-        const uint32_t* ab = &la[blk * 64];
-        int dot = 0;
-#pragma unroll 8
-        for (int cc = 0; cc < 32; ++cc) {
-            const uint32_t w = wb[cc * 32];
-            dot = dot4(code_even(w), int(ab[2 * cc]), dot);
-            dot = dot4(code_odd(w), int(ab[2 * cc + 1]), dot);
-        }
-        lterm[blk][n] = tree_term(dot, lsa[blk], lss[blk], lm[blk * 32 + n]);
-    }
-    __syncthreads();
-    for (int q = tid; q < nr * 32; q += 256) {
-        const int i = q >> 5, n = q & 31;
-        float v = 0.f;
-        v = v + lterm[2 * i][n];
-        v = v + lterm[2 * i + 1][n];
-        if (SHARED && lroute[i] >= kTop) v = bf16_round(v);
-        if (!isfinite(v)) flags |= kFlagNonfiniteProjection;
-        lro[i][n] = v;
-    }
-    __syncthreads();
-    // ---- slot-order reduction of token 0 (routed_storage_n32_consumer.cpp:176-184, 296-307) ----
-    if (tid < 32) {
-        const int col = c * 32 + tid;
-        float sum = 0.f;
-#pragma unroll
-        for (int s = 0; s < kTop; ++s) {
-            const int id = a.reduce_ids[s];
-            if (id >= 0 && id < kExperts) sum = sum + lro[lslot[s]][tid] * a.reduce_w[s];
-        }
-        const uint16_t o = f32_to_bf16_bits(sum);
-        if (!isfinite(sum) || (o & 0x7f80u) == 0x7f80u) flags |= kFlagNonfiniteOutput;
-        if (a.final_f32) a.final_f32[col] = sum;
-        if (a.out) a.out[col] = o;
-        if (SHARED) {
-            const float gate = bf16_bits_to_f32(a.sigmoid_table[a.shared_logit[0]]);
-            const float sv = lro[lslot[kTop]][tid] * gate;
-            if (!isfinite(sv)) flags |= kFlagNonfiniteOutput;
-            const uint16_t so = f32_to_bf16_bits(sv);
-            if (a.shared_out) a.shared_out[col] = so;
-            if (a.layer_out) a.layer_out[col] = f32_to_bf16_bits(bf16_bits_to_f32(o) + bf16_bits_to_f32(so));
+            a.middle[size_t(lr[r0 + rr]) * kInter + p * 32 + c] = mid;
         }
     }
     flag_or(a.sticky, flags);
 }
 
 // ---------------------------------------------------------------------------
-// K3 (T > 1): down projection for one (segment, 128-column group), writing
-// route_out; the slot reduction runs in its own kernel afterwards.
+// S5: block (segment, 32-column tile c).  Wave q = chunk quarter (chunks
+// 8q..8q+7); lane = (group lane / 32, column lane % 32), so every load
+// instruction reads two whole 128-byte rows.  The quarters' exact integer
+// partial dots meet in LDS; the two groups' terms follow in group order.
 // ---------------------------------------------------------------------------
-template <bool SHARED, int QMAX>
+template <bool SHARED>
 __global__ __launch_bounds__(256) void decode_down_kernel(DecodeArgs a) {
-    __shared__ uint32_t lw[8 * kPadWords];
-    __shared__ uint32_t lm[8 * 32];
-    __shared__ uint32_t la[2 * 64];
-    __shared__ float lsa[2], lss[2];
-    __shared__ float lterm[8][32];
-    if (int(blockIdx.x) >= a.nseg[0]) return;
-    const Segment sg = a.segments[blockIdx.x];
-    const int tid = threadIdx.x, cg = blockIdx.y, lane = tid & 63, wave = tid >> 6;
+    __shared__ __align__(16) uint32_t la[kRouteChunk][128];
+    __shared__ float lsa[kRouteChunk][2], lss[kRouteChunk][2];
+    __shared__ int lpart[kRouteChunk][4][64];
+    __shared__ int lr[256];
+    const int nseg = a.nseg[0];
+    if (int(blockIdx.y) >= nseg) return;
+    const Segment sg = a.segments[nseg - 1 - int(blockIdx.y)];    // shared expert's segments first
+    const int tid = threadIdx.x, lane = tid & 63, q = tid >> 6, c = blockIdx.x;
     const bool shared = SHARED && sg.bank == kShared;
     const uint32_t* codes = shared ? a.s2_codes : a.w2_codes + size_t(sg.bank) * kDownBankWords;
     const uint32_t* meta = shared ? a.s2_meta : a.w2_meta + size_t(sg.bank) * kDownBankMeta;
-    uint4 stage[8];
-    const uint32_t* src = codes + size_t(4 * cg) * 2 * 1024;
+    const int route_in = a.routes[sg.first + min(tid, sg.count - 1)];
+    __builtin_amdgcn_sched_barrier(0);
+    const int g = lane >> 5, n = lane & 31;
+    const uint32_t* wp = codes + (size_t(c) * 2 + g) * 1024 + 8 * q * 32 + n;
+    uint32_t wr[8];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) stage[i] = *reinterpret_cast<const uint4*>(src + size_t(i * 256 + tid) * 4);
-    const uint32_t mreg = meta[size_t(4 * cg) * 2 * 32 + tid];
-    int route = a.routes[sg.first];
-    float4 m4 = make_float4(0.f, 0.f, 0.f, 0.f);
-    if (wave < 2) m4 = *reinterpret_cast<const float4*>(a.middle + size_t(route) * kInter + wave * kGroup + lane * 4);
-#pragma unroll
-    for (int i = 0; i < 8; ++i) *reinterpret_cast<uint4*>(&lw[i * kPadWords + tid * 4]) = stage[i];
-    lm[tid] = mreg;
+    for (int j = 0; j < 8; ++j) wr[j] = wp[j * 32];
+    const uint32_t mw = meta[(size_t(c) * 2 + g) * 32 + n];     // used by the epilogue thread (g, n) of every wave
+    if (tid < sg.count) lr[tid] = route_in;
+    __syncthreads();
+    uint2 areg;
+    uint32_t sreg = 0;
+    int sumreg = 0;
+    auto load_chunk = [&](int r0) {
+        // route rr = tid / 64 holds words 2(tid % 64), +1 of its quantised middle row
+        const int k = min(r0 + (tid >> 6), sg.count - 1);
+        areg = *reinterpret_cast<const uint2*>(a.m_words + size_t(lr[k]) * 128 + (tid & 63) * 2);
+        const int k2 = min(r0 + ((tid & 7) >> 1), sg.count - 1);
+        sreg = a.m_scales[size_t(lr[k2]) * 2 + (tid & 1)];
+        sumreg = a.m_sums[size_t(lr[k2]) * 2 + (tid & 1)];
+    };
     uint32_t flags = 0;
-    for (int r = 0; r < sg.count; ++r) {
-        if (r > 0) {
-            __syncthreads();
-            route = a.routes[sg.first + r];
-            if (wave < 2) m4 = *reinterpret_cast<const float4*>(a.middle + size_t(route) * kInter + wave * kGroup + lane * 4);
-        }
-        if (wave < 2) quantize_middle<QMAX>(m4, &la[wave * 64], &lsa[wave], &lss[wave], flags);
+    load_chunk(0);
+    for (int r0 = 0; r0 < sg.count; r0 += kRouteChunk) {
+        const int nr = min(kRouteChunk, sg.count - r0);
         __syncthreads();
-        {
-            const int blk = tid >> 5, n = tid & 31, g = blk & 1;
-            const uint32_t* wb = &lw[blk * kPadWords + n];
-            const uint32_t* ab = &la[g * 64];
+        *reinterpret_cast<uint2*>(&la[tid >> 6][(tid & 63) * 2]) = areg;
+        if (tid < 8) {
+            const float sc = f16_bits_to_f32(uint16_t(sreg));
+            lsa[tid >> 1][tid & 1] = sc;
+            lss[tid >> 1][tid & 1] = sc * float(sumreg);
+        }
+        __syncthreads();
+        if (r0 + kRouteChunk < sg.count) load_chunk(r0 + kRouteChunk);
+        for (int rr = 0; rr < nr; ++rr) {
+            const uint4* ab = reinterpret_cast<const uint4*>(&la[rr][g * 64 + 16 * q]);
             int dot = 0;
-#pragma unroll 8
-            for (int c = 0; c < 32; ++c) {
-                const uint32_t w = wb[c * 32];
-                dot = dot4(code_even(w), int(ab[2 * c]), dot);
-                dot = dot4(code_odd(w), int(ab[2 * c + 1]), dot);
+#pragma unroll
+            for (int c4 = 0; c4 < 4; ++c4) {
+                const uint4 av = ab[c4];
+                dot = dot4(code_even(wr[2 * c4]), int(av.x), dot);
+                dot = dot4(code_odd(wr[2 * c4]), int(av.y), dot);
+                dot = dot4(code_even(wr[2 * c4 + 1]), int(av.z), dot);
+                dot = dot4(code_odd(wr[2 * c4 + 1]), int(av.w), dot);
             }
-            lterm[blk][n] = tree_term(dot, lsa[g], lss[g], lm[blk * 32 + n]);
+            lpart[rr][q][lane] = dot;
         }
         __syncthreads();
-        if (tid < 128) {
-            const int tl = tid >> 5, n = tid & 31;
-            float v = 0.f;
-            v = v + lterm[2 * tl][n];
-            v = v + lterm[2 * tl + 1][n];
-            if (shared) v = bf16_round(v);
-            if (!isfinite(v)) flags |= kFlagNonfiniteProjection;
-            a.route_out[size_t(route) * kHidden + cg * 128 + tid] = v;
+        if (tid < nr * 64) {
+            // thread (route rr, group, column): the exact dot, then the group term
+            const int rr = tid >> 6;
+            const int dot = lpart[rr][0][lane] + lpart[rr][1][lane] + lpart[rr][2][lane] + lpart[rr][3][lane];
+            const float term = tree_term(dot, lsa[rr][g], lss[rr][g], mw);
+            const float term1 = xor_perm_f<32>(term);       // group 1 of the same column
+            if (g == 0) {
+                float v = 0.f;
+                v = v + term;
+                v = v + term1;
+                if (shared) v = bf16_round(v);
+                if (!isfinite(v)) flags |= kFlagNonfiniteProjection;
+                a.route_out[size_t(lr[r0 + rr]) * kHidden + c * 32 + n] = v;
+            }
         }
     }
     flag_or(a.sticky, flags);
@@ -534,36 +404,44 @@ __global__ __launch_bounds__(256) void decode_down_kernel(DecodeArgs a) {
 
 // ---------------------------------------------------------------------------
 size_t decode_scratch_bytes() {
-    return align256(size_t(kDecodeMaxTokens) * kLogitStride * 4) + align256(kDecodeBanks * sizeof(Segment)) +
-           align256(kMaxRoutes * 4) + align256(kDownGroups * 4) + align256(8);
+    return align256(size_t(kDecodeMaxTokens) * kLogitStride * 4) + align256(kMaxSegments * sizeof(Segment)) +
+           align256(kMaxRoutes * 4) + align256(8);
 }
 
 void carve_decode(void* base, DecodeArgs& a) {
     size_t off = 0;
     auto take = [&](size_t bytes) { void* q = at<void>(base, off); off += align256(bytes); return q; };
     a.logits = static_cast<float*>(take(size_t(kDecodeMaxTokens) * kLogitStride * 4));
-    a.segments = static_cast<Segment*>(take(kDecodeBanks * sizeof(Segment)));
+    a.segments = static_cast<Segment*>(take(kMaxSegments * sizeof(Segment)));
     a.routes = static_cast<int32_t*>(take(kMaxRoutes * 4));
-    a.counters = static_cast<uint32_t*>(take(kDownGroups * 4));
     a.nseg = static_cast<int32_t*>(take(8));
 }
 
 template <bool ROUTER, bool SHARED, int QMAX>
 static hipError_t run(const DecodeArgs& a, hipStream_t s) {
-    const int T = a.T, R = T * kTop;
-    const int k1_blocks = ROUTER ? (SHARED ? 17 : 16) : max(1, (T * 8 + 15) / 16);
-    timed_launch("route", decode_route_kernel<ROUTER, SHARED, QMAX>, dim3(k1_blocks), dim3(1024), 0, s, a);
+    const int T = a.T, R = T * kTop, RS = R + (SHARED ? T : 0);
+    const int router_waves = ROUTER ? (SHARED ? kExperts + 1 : kExperts) * ((T + kTokenBatch - 1) / kTokenBatch) : 0;
+    const int s1_waves = router_waves + T * 4;
+    timed_launch("route", decode_route_kernel<ROUTER, SHARED, QMAX>, dim3((s1_waves + 3) / 4), dim3(256), 0, s, a,
+                 router_waves);
     hipError_t st = hipGetLastError();
     if (st != hipSuccess) return st;
-    const int maxseg = min(R, kExperts) + (SHARED ? 1 : 0);
-    timed_launch("gateup", decode_gateup_kernel<SHARED>, dim3(maxseg, 16), dim3(256), 0, s, a);
+    if (ROUTER) {
+        st = launch_topk(a.logits, kLogitStride, T, a.topk_w, a.topk_ids, SHARED ? a.logits + kExperts : nullptr,
+                         kLogitStride, SHARED ? a.shared_logit : nullptr, s);
+        if (st != hipSuccess) return st;
+    }
+    timed_launch("sort", decode_sort_kernel<SHARED>, dim3(1), dim3(512), 0, s, a, ROUTER ? a.topk_ids : a.ids_in);
     st = hipGetLastError();
     if (st != hipSuccess) return st;
-    if (T == 1) {
-        timed_launch("down", decode_down_tile_kernel<SHARED, QMAX>, dim3(kHidden / 32), dim3(256), 0, s, a);
-        return hipGetLastError();
-    }
-    timed_launch("down", decode_down_kernel<SHARED, QMAX>, dim3(maxseg, kDownGroups), dim3(256), 0, s, a);
+    // segments: at most one per non-empty bank plus one per extra 8 routes
+    const int maxseg = min(R, kExperts) + (SHARED ? 1 : 0) + (R + (SHARED ? T : 0)) / kSegRoutes;
+    timed_launch("gateup", decode_gateup_kernel<SHARED>, dim3(kInter / 32, maxseg), dim3(512), 0, s, a);
+    st = hipGetLastError();
+    if (st != hipSuccess) return st;
+    st = launch_quant_middle(a.middle, RS, R, a.reduce_ids, QMAX, a.m_words, a.m_scales, a.m_sums, a.sticky, s);
+    if (st != hipSuccess) return st;
+    timed_launch("down", decode_down_kernel<SHARED>, dim3(kHidden / 32, maxseg), dim3(256), 0, s, a);
     st = hipGetLastError();
     if (st != hipSuccess) return st;
     return launch_reduce(a.route_out, a.reduce_w, a.reduce_ids, T, a.final_f32, a.out, a.shared_logit,

@@ -6,7 +6,6 @@ namespace ornith {
 
 constexpr int kDecodeMaxTokens = 32;
 constexpr int kLogitStride = kExperts + 1;
-constexpr int kDownGroups = kHidden / 128;                 // K3 column groups of 128
 constexpr int64_t kGateBankWords = int64_t(2 * kInter) * kHidden / 8;
 constexpr int64_t kGateBankMeta = int64_t(2 * kInter) * (kHidden / kGroup);
 constexpr int64_t kDownBankWords = int64_t(kHidden) * kInter / 8;
@@ -32,8 +31,9 @@ struct DecodeArgs {
     // workspace
     uint32_t* x_words; uint16_t* x_scales; int32_t* x_sums;
     float* middle;                     // [RS, 512]
+    uint32_t* m_words; uint16_t* m_scales; int32_t* m_sums;   // quantised middle rows (2..32 tokens)
     float* route_out;                  // [RS, 2048]
-    float* logits; Segment* segments; int32_t* routes; uint32_t* counters; int32_t* nseg;
+    float* logits; Segment* segments; int32_t* routes; int32_t* nseg;
     // outputs
     float* final_f32; uint16_t* out; uint16_t* shared_out; uint16_t* layer_out;
     uint32_t* sticky;

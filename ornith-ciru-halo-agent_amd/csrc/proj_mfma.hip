@@ -31,7 +31,6 @@ namespace ornith {
 constexpr int kMT = 64, kNT = 128, kRowWords = 68;   // 64 words (256 int8) + 4 pad
 
 typedef int i32x4 __attribute__((ext_vector_type(4)));
-typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 template <bool GATEUP, int GS, int DEPTH>
 __global__ __launch_bounds__(256, 2) void grouped_mfma_kernel(MfmaArgs a) {
