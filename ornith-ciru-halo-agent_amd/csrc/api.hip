@@ -236,37 +236,6 @@ hipError_t dense_run(const void* input, const void* codes, const void* meta, voi
     return launch_project_gemv(a, 1, Out::Dense, s);
 }
 
-// Top-1 over fp32 rows with numpy's rule: the first NaN if any, else the first maximum.
-__device__ __forceinline__ bool better(float a, int ia, float b, int ib) {
-    const bool na = isnan(a), nb = isnan(b);
-    if (na != nb) return na;
-    if (na) return ia < ib;
-    return a > b || (a == b && ia < ib);
-}
-__global__ __launch_bounds__(256) void argmax_kernel(const float* __restrict__ v, int N, int64_t* __restrict__ out) {
-    __shared__ float bv[256];
-    __shared__ int bi[256];
-    const float* row = v + size_t(blockIdx.x) * N;
-    float best = -__builtin_huge_valf();
-    int idx = 0x7fffffff;
-    for (int i = threadIdx.x; i < N; i += 256)
-        if (idx == 0x7fffffff || better(row[i], i, best, idx)) { best = row[i]; idx = i; }
-    bv[threadIdx.x] = best;
-    bi[threadIdx.x] = idx;
-    __syncthreads();
-    for (int m = 128; m > 0; m >>= 1) {
-        if (int(threadIdx.x) < m) {
-            const int o = threadIdx.x + m;
-            if (bi[o] != 0x7fffffff && (bi[threadIdx.x] == 0x7fffffff || better(bv[o], bi[o], bv[threadIdx.x], bi[threadIdx.x]))) {
-                bv[threadIdx.x] = bv[o];
-                bi[threadIdx.x] = bi[o];
-            }
-        }
-        __syncthreads();
-    }
-    if (threadIdx.x == 0) out[blockIdx.x] = bi[0];
-}
-
 }  // namespace
 
 // =============================================================================
@@ -478,11 +447,18 @@ extern "C" hipError_t ornith_dense_g256_launch_n32(const void* input, const void
 
 extern "C" int ornith_dense_g256_n32_rows(void) { return 16; }
 
+// head workspace: A8 activation words, scales, sums, then the per-128-column
+// argmax partials (value, index) of every row
+namespace {
+constexpr int kHeadBlockCols = 128;
+size_t head_partials(int Mcap, int N) { return size_t(Mcap) * size_t((N + kHeadBlockCols - 1) / kHeadBlockCols); }
+}  // namespace
+
 extern "C" size_t ornith_dense_g256_head_workspace_bytes(int Mcap, int N) {
-    (void)N;
-    if (Mcap < 0 || Mcap > 64) return 0;
+    if (Mcap < 0 || Mcap > 64 || N < 0) return 0;
     const size_t m = size_t(Mcap);
-    return align256(m * kHidden) + align256(m * (kHidden / kGroup) * 2) + align256(m * (kHidden / kGroup) * 4);
+    return align256(m * kHidden) + align256(m * (kHidden / kGroup) * 2) + align256(m * (kHidden / kGroup) * 4) +
+           2 * align256(head_partials(Mcap, N) * 4);
 }
 
 extern "C" hipError_t ornith_dense_g256_head_launch(const void* input, const void* codes, const void* metadata,
@@ -495,13 +471,28 @@ extern "C" hipError_t ornith_dense_g256_head_launch(const void* input, const voi
     if (!input || !codes || !metadata || !workspace || !logits_f32 || !argmax_i64 || !flags || !aligned(input, 8) ||
         !aligned(codes, 16) || !aligned(workspace, 256) || !aligned(logits_f32, 4) || !aligned(argmax_i64, 8))
         return hipErrorInvalidValue;
-    OrnithDenseG256Layout l{};
     const size_t m = size_t(Mcap);
-    l.low = 0;
-    l.scales = align256(m * kHidden);
-    l.sums = l.scales + align256(m * (kHidden / kGroup) * 2);
-    TRY(dense_run(input, codes, metadata, workspace, l, static_cast<float*>(logits_f32),
-                  static_cast<uint16_t*>(logits_bf16), static_cast<uint32_t*>(flags), M, N, kHidden, 32, stream));
-    timed_launch("argmax", argmax_kernel, dim3(M), dim3(256), 0, stream, static_cast<const float*>(logits_f32), N, static_cast<int64_t*>(argmax_i64));
-    return hipGetLastError();
+    const size_t scales = align256(m * kHidden), sums = scales + align256(m * (kHidden / kGroup) * 2);
+    const size_t vals = sums + align256(m * (kHidden / kGroup) * 4);
+    const size_t idxs = vals + align256(head_partials(Mcap, N) * 4);
+    auto w = at<uint32_t>(workspace, 0);
+    auto sc = at<uint16_t>(workspace, scales);
+    auto su = at<int32_t>(workspace, sums);
+    TRY(launch_act_bf16(static_cast<const uint16_t*>(input), kHidden, M, kHidden, 127, nullptr, w, sc, su,
+                        static_cast<uint32_t*>(flags), kDenseNonfiniteInput, kDenseInvalidActivation, stream));
+    MfmaArgs a{};
+    a.R = M;
+    a.codes = static_cast<const uint32_t*>(codes);
+    a.meta = static_cast<const uint32_t*>(metadata);
+    a.act_words = w; a.act_scales = sc; a.act_sums = su;
+    a.K = kHidden;
+    a.N = N;
+    a.out = static_cast<float*>(logits_f32);
+    a.out_bf16 = static_cast<uint16_t*>(logits_bf16);
+    a.arg_val = at<float>(workspace, vals);
+    a.arg_idx = at<int32_t>(workspace, idxs);
+    a.sticky = static_cast<uint32_t*>(flags);
+    a.flag_projection = kDenseNonfiniteProjection;
+    a.flag_bf16 = kDenseNonfiniteBf16;
+    return launch_head_mfma(a, static_cast<int64_t*>(argmax_i64), stream);
 }

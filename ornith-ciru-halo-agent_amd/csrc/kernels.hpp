@@ -80,8 +80,17 @@ struct MfmaArgs {
     float* out;                                  // gate/up: middle [RS, 512]; down: route_out [RS, 2048]
     const float* silu_table;
     uint32_t* sticky;
+    // dense head (rows = R, identity; columns N): fp32 and bf16 logits [R, N],
+    // per-128-column argmax partials [R, ceil(N/128)], the dense flag bits
+    int N;
+    uint16_t* out_bf16;
+    float* arg_val; int32_t* arg_idx;
+    uint32_t flag_projection, flag_bf16;
 };
 hipError_t launch_grouped_mfma(const MfmaArgs& a, bool gateup, int max_tiles, hipStream_t s);
+// Dense G256 head on the matrix cores: M <= 64 rows of A8 activations against
+// N32 codes, then the per-row argmax (numpy rule) into argmax[M].
+hipError_t launch_head_mfma(const MfmaArgs& a, int64_t* argmax, hipStream_t s);
 hipError_t launch_quant_middle(const float* middle, int RS, int R, const int32_t* ids, int qmax, uint32_t* words,
                                uint16_t* scales, int32_t* sums, uint32_t* sticky, hipStream_t s);
 

@@ -32,37 +32,54 @@ constexpr int kMT = 64, kNT = 128, kRowWords = 68;   // 64 words (256 int8) + 4 
 
 typedef int i32x4 __attribute__((ext_vector_type(4)));
 
-template <bool GATEUP, int GS, int DEPTH>
+constexpr int kModeGateUp = 0, kModeDown = 1, kModeHead = 2;
+
+// Top-1 order of numpy's argmax: the first NaN if any, else the first maximum.
+__device__ __forceinline__ bool arg_better(float a, int ia, float b, int ib) {
+    const bool na = isnan(a), nb = isnan(b);
+    if (na != nb) return na;
+    if (na) return ia < ib;
+    return a > b || (a == b && ia < ib);
+}
+
+template <int MODE, int GS, int DEPTH>
 __global__ __launch_bounds__(256, 2) void grouped_mfma_kernel(MfmaArgs a) {
+    constexpr bool GATEUP = MODE == kModeGateUp, HEAD = MODE == kModeHead;
     __shared__ uint32_t sA[kMT * kRowWords];
     __shared__ uint32_t sB[kNT * kRowWords];
     __shared__ float s_sa[kMT], s_ss[kMT], s_sw[kNT], s_off[kNT];
     __shared__ int s_route[kMT], s_row[kMT];
 
-    if (int(blockIdx.x) >= a.ntiles[0]) return;
-    const int tile = a.tiles[blockIdx.x];
-    const Segment sg = a.segments[tile >> 16];
-    const int r0 = (tile & 0xffff) * kMT;
+    Segment sg{0, 0, a.R, 0};
+    int r0 = 0;
+    if (!HEAD) {
+        if (int(blockIdx.x) >= a.ntiles[0]) return;
+        const int tile = a.tiles[blockIdx.x];
+        sg = a.segments[tile >> 16];
+        r0 = (tile & 0xffff) * kMT;
+    }
     const int nrows = min(kMT, sg.count - r0);
     const int nt = blockIdx.y;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int wm = wave & 1, wn = wave >> 1;
-    const bool shared = sg.bank == kShared;
+    const bool shared = !HEAD && sg.bank == kShared;
     const uint32_t* codes = shared ? a.shared_codes : a.codes + size_t(sg.bank) * a.bank_words;
     const uint32_t* meta = shared ? a.shared_meta : a.meta + size_t(sg.bank) * a.bank_meta_words;
 
     if (tid < kMT) {
         int route = -1, row = 0;
         if (tid < nrows) {
-            route = a.routes[sg.first + r0 + tid];
+            route = HEAD ? tid : a.routes[sg.first + r0 + tid];
             row = GATEUP ? (route < a.R ? route / kTop : route - a.R) : route;
         }
         s_route[tid] = route;
         s_row[tid] = row;
     }
-    // block column bc (0..127) -> n32 tile and column inside it
+    // block column bc (0..127) -> n32 tile and column inside it; the head's
+    // last block clamps tiles past N to the last one (loaded, never written)
     auto ntile_of = [&](int blk) {      // blk: 32-column block 0..3 of this block
         if (GATEUP) return (blk < 2 ? 2 * nt + blk : 16 + 2 * nt + (blk - 2));
+        if (HEAD) return min(4 * nt + blk, a.N / 32 - 1);
         return 4 * nt + blk;
     };
     __syncthreads();
@@ -222,6 +239,19 @@ __global__ __launch_bounds__(256, 2) void grouped_mfma_kernel(MfmaArgs a) {
                     if (!isfinite(mid)) flags |= kFlagNonfiniteMiddle | kFlagNonfiniteInput;
                     a.out[size_t(route) * kInter + 64 * nt + colbase[ct] + li] = mid;
                 }
+            } else if (HEAD) {
+#pragma unroll
+                for (int ct = 0; ct < 4; ++ct) {
+                    const int col = kNT * nt + colbase[ct] + li;
+                    if (col >= a.N) continue;
+                    const float v = val[rt][ct][r];
+                    const size_t o = size_t(route) * a.N + col;
+                    const uint16_t b = f32_to_bf16_bits(v);
+                    if (!isfinite(v)) flags |= a.flag_projection;
+                    if ((b & 0x7f80u) == 0x7f80u) flags |= a.flag_bf16;
+                    a.out[o] = v;
+                    if (a.out_bf16) a.out_bf16[o] = b;
+                }
             } else {
 #pragma unroll
                 for (int ct = 0; ct < 4; ++ct) {
@@ -233,13 +263,102 @@ __global__ __launch_bounds__(256, 2) void grouped_mfma_kernel(MfmaArgs a) {
             }
         }
     }
+    if constexpr (HEAD) {
+        // per-row best of this block's 128 columns: lane (4 columns, ascending),
+        // then the 16 lanes of the row group (xor 1..8), then the two column
+        // halves (waves wn = 0, 1) through LDS
+        __shared__ float s_bv[2][kMT];
+        __shared__ int s_bi[2][kMT];
+#pragma unroll
+        for (int rt = 0; rt < 2; ++rt) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                float bv = 0.f;
+                int bi = 0x7fffffff;
+#pragma unroll
+                for (int ct = 0; ct < 4; ++ct) {
+                    const int col = kNT * nt + colbase[ct] + li;
+                    if (col < a.N && (bi == 0x7fffffff || arg_better(val[rt][ct][r], col, bv, bi))) {
+                        bv = val[rt][ct][r];
+                        bi = col;
+                    }
+                }
+#define ORNITH_ARG_STEP(M)                                                                       \
+                {                                                                                \
+                    const float ov = xor_perm_f<M>(bv);                                          \
+                    const int oi = xor_perm_i<M>(bi);                                            \
+                    if (oi != 0x7fffffff && (bi == 0x7fffffff || arg_better(ov, oi, bv, bi))) { \
+                        bv = ov;                                                                 \
+                        bi = oi;                                                                 \
+                    }                                                                            \
+                }
+                ORNITH_ARG_STEP(1)
+                ORNITH_ARG_STEP(2)
+                ORNITH_ARG_STEP(4)
+                ORNITH_ARG_STEP(8)
+#undef ORNITH_ARG_STEP
+                const int row = 32 * wm + 16 * rt + 4 * q + r;
+                if (li == 0) { s_bv[wn][row] = bv; s_bi[wn][row] = bi; }
+            }
+        }
+        __syncthreads();
+        if (tid < nrows) {
+            float bv = s_bv[0][tid];
+            int bi = s_bi[0][tid];
+            const float ov = s_bv[1][tid];
+            const int oi = s_bi[1][tid];
+            if (oi != 0x7fffffff && (bi == 0x7fffffff || arg_better(ov, oi, bv, bi))) { bv = ov; bi = oi; }
+            const int nblk = (a.N + kNT - 1) / kNT;
+            a.arg_val[size_t(tid) * nblk + nt] = bv;
+            a.arg_idx[size_t(tid) * nblk + nt] = bi;
+        }
+    }
     flag_or(a.sticky, flags);
+}
+
+// Per-row combination of the head's block partials (numpy argmax rule).
+__global__ __launch_bounds__(256) void head_argmax_kernel(const float* __restrict__ val, const int32_t* __restrict__ idx,
+                                                          int nblk, int64_t* __restrict__ out) {
+    __shared__ float bv[256];
+    __shared__ int bi[256];
+    const int row = blockIdx.x, t = threadIdx.x;
+    float v = 0.f;
+    int i = 0x7fffffff;
+    for (int b = t; b < nblk; b += 256) {
+        const float ov = val[size_t(row) * nblk + b];
+        const int oi = idx[size_t(row) * nblk + b];
+        if (oi != 0x7fffffff && (i == 0x7fffffff || arg_better(ov, oi, v, i))) { v = ov; i = oi; }
+    }
+    bv[t] = v;
+    bi[t] = i;
+    __syncthreads();
+    for (int m = 128; m > 0; m >>= 1) {
+        if (t < m) {
+            const int o = t + m;
+            if (bi[o] != 0x7fffffff && (bi[t] == 0x7fffffff || arg_better(bv[o], bi[o], bv[t], bi[t]))) {
+                bv[t] = bv[o];
+                bi[t] = bi[o];
+            }
+        }
+        __syncthreads();
+    }
+    if (t == 0) out[row] = bi[0];
 }
 
 hipError_t launch_grouped_mfma(const MfmaArgs& a, bool gateup, int max_tiles, hipStream_t s) {
     if (max_tiles <= 0) return hipSuccess;
-    if (gateup) timed_launch("gateup_mfma", grouped_mfma_kernel<true, kHidden / kGroup, 2>, dim3(dim3(max_tiles, (2 * kInter) / kNT)), dim3(256), 0, s, a);
-    else timed_launch("down_mfma", grouped_mfma_kernel<false, kInter / kGroup, 2>, dim3(max_tiles, kHidden / kNT), dim3(256), 0, s, a);
+    if (gateup) timed_launch("gateup_mfma", grouped_mfma_kernel<kModeGateUp, kHidden / kGroup, 2>, dim3(max_tiles, (2 * kInter) / kNT), dim3(256), 0, s, a);
+    else timed_launch("down_mfma", grouped_mfma_kernel<kModeDown, kInter / kGroup, 2>, dim3(max_tiles, kHidden / kNT), dim3(256), 0, s, a);
+    return hipGetLastError();
+}
+
+hipError_t launch_head_mfma(const MfmaArgs& a, int64_t* argmax, hipStream_t s) {
+    if (a.R <= 0 || a.R > kMT || a.N <= 0 || a.N % 32 != 0 || a.K != kHidden) return hipErrorInvalidValue;
+    const int nblk = (a.N + kNT - 1) / kNT;
+    timed_launch("head_mfma", grouped_mfma_kernel<kModeHead, kHidden / kGroup, 2>, dim3(1, nblk), dim3(256), 0, s, a);
+    hipError_t st = hipGetLastError();
+    if (st != hipSuccess) return st;
+    timed_launch("argmax", head_argmax_kernel, dim3(a.R), dim3(256), 0, s, a.arg_val, a.arg_idx, nblk, argmax);
     return hipGetLastError();
 }
 
