@@ -40,44 +40,11 @@ __global__ __launch_bounds__(256) void decode_route_kernel(DecodeArgs a, int rou
     const int gw = blockIdx.x * 4 + (threadIdx.x >> 6);
     if (ROUTER && gw < router_waves) {
         const int nb = (T + kTokenBatch - 1) / kTokenBatch;
-        const int row = gw / nb, t0 = (gw % nb) * kTokenBatch, nt = min(kTokenBatch, T - t0);
+        const int row = gw / nb, t0 = (gw % nb) * kTokenBatch;
         const uint16_t* wrow = row < kExperts ? a.router_w + size_t(row) * kHidden : a.shared_gate_w;
-        uint4 wv[4];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) wv[i] = *reinterpret_cast<const uint4*>(wrow + (i * 64 + lane) * 8);
-        // every token's row is loaded before the first fma (rows past T repeat
-        // the last token and are not written), so the loads overlap
-        u32x4 xv[kTokenBatch][4];
-#pragma unroll
-        for (int t = 0; t < kTokenBatch; ++t) {
-            const uint16_t* xrow = a.x + size_t(min(t0 + t, T - 1)) * kHidden;
-#pragma unroll
-            for (int i = 0; i < 4; ++i) xv[t][i] = *reinterpret_cast<const u32x4*>(xrow + (i * 64 + lane) * 8);
-        }
-        float acc[kTokenBatch];
-#pragma unroll
-        for (int t = 0; t < kTokenBatch; ++t) {
-            acc[t] = 0.f;
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const uint32_t ww[4] = {wv[i].x, wv[i].y, wv[i].z, wv[i].w};
-#pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    const uint32_t xw = xv[t][i][j];
-                    acc[t] = __builtin_fmaf(bf16_bits_to_f32(xw & 0xffffu), bf16_bits_to_f32(ww[j] & 0xffffu), acc[t]);
-                    acc[t] = __builtin_fmaf(bf16_bits_to_f32(xw >> 16), bf16_bits_to_f32(ww[j] >> 16), acc[t]);
-                }
-            }
-        }
-        const float b = (a.bias && row < kExperts) ? a.bias[row] : 0.f;
-#pragma unroll
-        for (int t = 0; t < kTokenBatch; ++t) {
-            if (t < nt) {
-                float v = wave_butterfly_sum(acc[t]);
-                if (a.bias && row < kExperts) v = v + b;
-                if (lane == 0) a.logits[size_t(t0 + t) * kLogitStride + row] = v;
-            }
-        }
+        const bool has_bias = a.bias && row < kExperts;
+        router_rows_wave(a.x, kHidden, T, t0, wrow, has_bias ? a.bias[row] : 0.f, has_bias, a.logits, kLogitStride,
+                         row);
         return;
     }
     // quantised gate input: wave q handles groups 2(q%4), 2(q%4)+1 of token q/4

@@ -90,7 +90,11 @@ __global__ __launch_bounds__(256, 2) void grouped_mfma_kernel(MfmaArgs a) {
     uint32_t rsa[DEPTH];                // raw fp16 scale bits; converted at store time so that
     int rsum[DEPTH];                    // no use of a load result sits behind the prefetch
     const int a_row = tid >> 2, a_part = tid & 3;
-    const int b_blk = tid >> 6, b_sub = tid & 63;         // 16 packed words: chunk b_sub/2, cols (b_sub&1)*16..+15
+    // B staging: wave b_blk takes 32-column block b_blk; lane b_sub takes chunk
+    // row j = b_sub % 32 and columns 16 * (b_sub / 32) .. +15 (16 packed
+    // words).  Consecutive lanes hold consecutive chunk rows, so the unpacked
+    // int8 stores of a wave hit distinct LDS banks.
+    const int b_blk = tid >> 6, b_sub = tid & 63, b_j = b_sub & 31, b_half = b_sub >> 5;
     // Every lane issues every load (dead rows read activation row s_row = 0 of
     // a live tile and are dropped by the epilogue), so the in-order load
     // counter stays exact and the waits leave the prefetched groups in flight.
@@ -101,7 +105,7 @@ __global__ __launch_bounds__(256, 2) void grouped_mfma_kernel(MfmaArgs a) {
         const uint32_t* src = a.act_words + a_base + g * 64;
 #pragma unroll
         for (int i = 0; i < 4; ++i) ra[slot][i] = *reinterpret_cast<const u32x4*>(src + 4 * i);
-        const uint32_t* bsrc = codes + (size_t(ntile_of(b_blk)) * GS + g) * 1024 + b_sub * 16;
+        const uint32_t* bsrc = codes + (size_t(ntile_of(b_blk)) * GS + g) * 1024 + b_j * 32 + b_half * 16;
 #pragma unroll
         for (int i = 0; i < 4; ++i) rb[slot][i] = *reinterpret_cast<const u32x4*>(bsrc + 4 * i);
         rmeta[slot] = meta[m_base + g * 32];
@@ -113,7 +117,7 @@ __global__ __launch_bounds__(256, 2) void grouped_mfma_kernel(MfmaArgs a) {
         for (int i = 0; i < 4; ++i)
             *reinterpret_cast<u32x4*>(&sA[a_row * kRowWords + a_part * 16 + 4 * i]) = ra[slot][i];
         // unpack: packed word (chunk j, column n) -> int8 words 2j (even k) and 2j+1 (odd k) of column n
-        const int j = b_sub >> 1, c0 = b_blk * 32 + (b_sub & 1) * 16;
+        const int j = b_j, c0 = b_blk * 32 + b_half * 16;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const uint32_t w[4] = {rb[slot][i].x, rb[slot][i].y, rb[slot][i].z, rb[slot][i].w};
@@ -141,6 +145,8 @@ __global__ __launch_bounds__(256, 2) void grouped_mfma_kernel(MfmaArgs a) {
     for (int ct = 0; ct < 4; ++ct)
         colbase[ct] = GATEUP ? ((ct < 2 ? 0 : 64) + 32 * wn + 16 * (ct & 1)) : (64 * wn + 16 * ct);
     const int q = lane >> 4, li = lane & 15;
+    // wave-uniform: does row tile rt (rows 32wm+16rt .. +15) hold a live row?
+    const bool live[2] = {32 * wm < nrows, 32 * wm + 16 < nrows};
     float val[2][4][4];
 #pragma unroll
     for (int rt = 0; rt < 2; ++rt)
@@ -165,6 +171,7 @@ __global__ __launch_bounds__(256, 2) void grouped_mfma_kernel(MfmaArgs a) {
         for (int rt = 0; rt < 2; ++rt)
 #pragma unroll
             for (int ct = 0; ct < 4; ++ct) acc[rt][ct] = i32x4{0, 0, 0, 0};
+        if (!live[0]) return;                           // both row tiles past the segment's rows
 #pragma unroll
         for (int s = 0; s < 4; ++s) {
             i32x4 fa[2], fb[4];
@@ -179,14 +186,18 @@ __global__ __launch_bounds__(256, 2) void grouped_mfma_kernel(MfmaArgs a) {
                 fb[ct] = i32x4{int(v.x), int(v.y), int(v.z), int(v.w)};
             }
 #pragma unroll
-            for (int rt = 0; rt < 2; ++rt)
+            for (int ct = 0; ct < 4; ++ct)
+                acc[0][ct] = __builtin_amdgcn_mfma_i32_16x16x64_i8(fa[0], fb[ct], acc[0][ct], 0, 0, 0);
+            if (live[1]) {
 #pragma unroll
                 for (int ct = 0; ct < 4; ++ct)
-                    acc[rt][ct] = __builtin_amdgcn_mfma_i32_16x16x64_i8(fa[rt], fb[ct], acc[rt][ct], 0, 0, 0);
+                    acc[1][ct] = __builtin_amdgcn_mfma_i32_16x16x64_i8(fa[1], fb[ct], acc[1][ct], 0, 0, 0);
+            }
         }
-        // fp32 group tree (dense_g256_api.h:35-37)
+        // fp32 group tree (dense_g256_api.h:35-37), row tiles with live rows only
 #pragma unroll
         for (int rt = 0; rt < 2; ++rt) {
+            if (!live[rt]) continue;
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 const int row = 32 * wm + 16 * rt + 4 * q + r;

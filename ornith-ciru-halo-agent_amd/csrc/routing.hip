@@ -33,6 +33,7 @@ namespace ornith {
 // token per wave at a time, with the lane-partial butterfly itself.
 // ---------------------------------------------------------------------------
 constexpr int kRouterTile = 32;
+constexpr int kRouterRowsMaxTokens = 256;      // wave-per-row kernel up to here, tiled kernel beyond
 constexpr int kRouterIStride = 8 * kRouterTile + 4;       // [i][j][row] with a 4-float pad per i
 constexpr int kRouterWaveStride = 4 * kRouterIStride;
 
@@ -175,9 +176,32 @@ __global__ __launch_bounds__(256) void router_kernel(const uint16_t* __restrict_
     }
 }
 
+// One wave per (router row, batch of 8 tokens): the choice for small and
+// medium T, where the tiled kernel has too few blocks to fill the chip.
+__global__ __launch_bounds__(256) void router_rows_kernel(const uint16_t* __restrict__ x, int64_t stride, int T,
+                                                          const uint16_t* __restrict__ w,
+                                                          const uint16_t* __restrict__ shared_w,
+                                                          const float* __restrict__ bias, float* __restrict__ logits,
+                                                          int64_t logit_stride, int nrows) {
+    const int gw = blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int nb = (T + 7) / 8;
+    if (gw >= nrows * nb) return;
+    const int row = gw / nb, t0 = (gw % nb) * 8;
+    const uint16_t* wrow = row < kExperts ? w + size_t(row) * kHidden : shared_w;
+    const bool has_bias = bias && row < kExperts;
+    router_rows_wave(x, stride, T, t0, wrow, has_bias ? bias[row] : 0.f, has_bias, logits, logit_stride, row);
+}
+
 hipError_t launch_router(const uint16_t* x, int64_t stride, int T, const uint16_t* w, const uint16_t* shared_w,
                          const float* bias, float* logits, int64_t logit_stride, hipStream_t s) {
     if (T <= 0) return hipSuccess;
+    if (T <= kRouterRowsMaxTokens) {
+        const int nrows = kExperts + (shared_w ? 1 : 0);
+        const int waves = nrows * ((T + 7) / 8);
+        timed_launch("router", router_rows_kernel, dim3((waves + 3) / 4), dim3(256), 0, s, x, stride, T, w, shared_w,
+                     bias, logits, logit_stride, nrows);
+        return hipGetLastError();
+    }
     const dim3 grid(kExperts / kRouterTile + (shared_w ? 1 : 0), (T + kRouterTile - 1) / kRouterTile);
     timed_launch("router", router_kernel, dim3(grid), dim3(256), 0, s, x, stride, T, w, shared_w, bias, logits, logit_stride);
     return hipGetLastError();

@@ -17,6 +17,51 @@ __device__ __forceinline__ void cswap(uint32_t& ka, int& ia, uint32_t& kb, int& 
     ka = tk; kb = tk2; ia = ti; ib = ti2;
 }
 
+// Router logits of one router row for up to 8 consecutive tokens t0.. on one
+// wave, in the declared order (routing.hip): lane l forms the fma chain over
+// chunks l, l+64, l+128, l+192, then the butterfly; + bias.  Every token row
+// is loaded before the first fma (rows past T repeat the last token and are
+// not written), so the loads overlap.
+__device__ __forceinline__ void router_rows_wave(const uint16_t* __restrict__ x, int64_t stride, int T, int t0,
+                                                 const uint16_t* __restrict__ wrow, float bias, bool has_bias,
+                                                 float* __restrict__ logits, int64_t logit_stride, int row) {
+    constexpr int kBatch = 8;
+    const int lane = threadIdx.x & 63, nt = min(kBatch, T - t0);
+    uint4 wv[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) wv[i] = *reinterpret_cast<const uint4*>(wrow + (i * 64 + lane) * 8);
+    u32x4 xv[kBatch][4];
+#pragma unroll
+    for (int t = 0; t < kBatch; ++t) {
+        const uint16_t* xrow = x + size_t(min(t0 + t, T - 1)) * stride;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) xv[t][i] = *reinterpret_cast<const u32x4*>(xrow + (i * 64 + lane) * 8);
+    }
+    float acc[kBatch];
+#pragma unroll
+    for (int t = 0; t < kBatch; ++t) {
+        acc[t] = 0.f;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const uint32_t ww[4] = {wv[i].x, wv[i].y, wv[i].z, wv[i].w};
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const uint32_t xw = xv[t][i][j];
+                acc[t] = __builtin_fmaf(bf16_bits_to_f32(xw & 0xffffu), bf16_bits_to_f32(ww[j] & 0xffffu), acc[t]);
+                acc[t] = __builtin_fmaf(bf16_bits_to_f32(xw >> 16), bf16_bits_to_f32(ww[j] >> 16), acc[t]);
+            }
+        }
+    }
+#pragma unroll
+    for (int t = 0; t < kBatch; ++t) {
+        if (t < nt) {
+            float v = wave_butterfly_sum(acc[t]);
+            if (has_bias) v = v + bias;
+            if (lane == 0) logits[size_t(t0 + t) * logit_stride + row] = v;
+        }
+    }
+}
+
 // v: lane l holds the logits of experts l, l+64, l+128, l+192.  Returns the
 // eight selected ids (identical on every lane) in pid, and on lane j < 8 the
 // weight and id of slot j (the renormalisation runs lane-parallel).
