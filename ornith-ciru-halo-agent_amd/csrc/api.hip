@@ -91,7 +91,9 @@ hipError_t run_routed(const RoutedPlan& p, void* ws, const void* input, const fl
     auto dw = at<uint32_t>(ws, p.l.down_low);
     auto dsc = at<uint16_t>(ws, p.l.down_scales);
     auto dsum = at<int32_t>(ws, p.l.down_sums);
-    TRY(launch_quant_middle(at<float>(ws, p.l.middle), RS, R, ids, qmax, dw, dsc, dsum, sticky, s));
+    // middle rows are in permuted route order; offsets[257] = routes with a valid bank
+    TRY(launch_quant_middle_permuted(at<float>(ws, p.l.middle), RS, ps.offsets + kExperts + 1, qmax, dw, dsc, dsum,
+                                     sticky, s));
     a.codes = static_cast<const uint32_t*>(down_codes);
     a.meta = static_cast<const uint32_t*>(down_meta);
     a.shared_codes = static_cast<const uint32_t*>(sd_codes);

@@ -17,7 +17,7 @@ struct PermuteScratch {
     int32_t* routes;         // [routes] permuted route ids
     Segment* segments;       // [banks]
     int32_t* meta;           // [4]: segment count, mfma tile count, ...
-    int32_t* tiles;          // [max tiles] segment index << 16 | tile-in-segment
+    Segment* tiles;          // [max tiles] per m-tile: bank, first permuted route, rows, tile-in-segment
 };
 
 // ---- activations -----------------------------------------------------------
@@ -71,7 +71,7 @@ hipError_t launch_project_gemv(const ProjArgs& a, int max_segments, Out mode, hi
 
 // Grouped int8-MFMA projection over the permuted routes (prefill path).
 struct MfmaArgs {
-    const Segment* segments; const int32_t* tiles; const int32_t* ntiles; const int32_t* routes;
+    const Segment* segments; const Segment* tiles; const int32_t* ntiles; const int32_t* routes;
     int R;                                       // routed routes; rows >= R are shared-expert rows
     const uint32_t* codes; const uint32_t* meta; const uint32_t* shared_codes; const uint32_t* shared_meta;
     int64_t bank_words, bank_meta_words;
@@ -93,6 +93,10 @@ hipError_t launch_grouped_mfma(const MfmaArgs& a, bool gateup, int max_tiles, hi
 hipError_t launch_head_mfma(const MfmaArgs& a, int64_t* argmax, hipStream_t s);
 hipError_t launch_quant_middle(const float* middle, int RS, int R, const int32_t* ids, int qmax, uint32_t* words,
                                uint16_t* scales, int32_t* sums, uint32_t* sticky, hipStream_t s);
+// Same over middle rows stored in permuted route order: rows 0 .. *nrows - 1
+// (the permuted routes, all with a valid bank), RS rows at most.
+hipError_t launch_quant_middle_permuted(const float* middle, int RS, const int32_t* nrows, int qmax, uint32_t* words,
+                                        uint16_t* scales, int32_t* sums, uint32_t* sticky, hipStream_t s);
 
 // ---- combination -------------------------------------------------------------
 // out[t] = bf16(sum over valid slots of route_out[8t+s] * w[8t+s]); optional

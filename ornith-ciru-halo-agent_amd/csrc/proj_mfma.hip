@@ -50,16 +50,20 @@ __global__ __launch_bounds__(256, 2) void grouped_mfma_kernel(MfmaArgs a) {
     __shared__ float s_sa[kMT], s_ss[kMT], s_sw[kNT], s_off[kNT];
     __shared__ int s_route[kMT], s_row[kMT];
 
+    // Linear block b -> (m-tile b / NCB, column block b % NCB).  Workgroups go
+    // to the 8 XCDs round-robin, so every XCD sees the same column blocks of
+    // all m-tiles: an expert's column slice is fetched into one L2 and reused
+    // by the expert's following m-tiles there.
+    const int ncb = HEAD ? int(gridDim.x) : (GATEUP ? (2 * kInter) / kNT : kHidden / kNT);
+    const int nt = int(blockIdx.x) % ncb, mtile = int(blockIdx.x) / ncb;
     Segment sg{0, 0, a.R, 0};
     int r0 = 0;
     if (!HEAD) {
-        if (int(blockIdx.x) >= a.ntiles[0]) return;
-        const int tile = a.tiles[blockIdx.x];
-        sg = a.segments[tile >> 16];
-        r0 = (tile & 0xffff) * kMT;
+        if (mtile >= a.ntiles[0]) return;
+        const Segment td = a.tiles[mtile];
+        sg = Segment{td.bank, td.first, td.count, 0};
     }
     const int nrows = min(kMT, sg.count - r0);
-    const int nt = blockIdx.y;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int wm = wave & 1, wn = wave >> 1;
     const bool shared = !HEAD && sg.bank == kShared;
@@ -356,17 +360,258 @@ __global__ __launch_bounds__(256) void head_argmax_kernel(const float* __restric
     if (t == 0) out[row] = bi[0];
 }
 
+// ---------------------------------------------------------------------------
+// Prefill projections with column-owning waves.
+//
+// Block = (64-route m-tile, column block).  Wave w owns two 16-column tiles
+// over all 64 rows, so every code word is fetched and unpacked once per block:
+//  - B: each lane loads its own packed code words straight into registers.
+//    Lane i+16q of column tile ct takes, for k-step s (64 k), the words
+//    j = 8s+2q and 8s+2q+1 (chunks of 8 codes) of its column; unpacked
+//    (even codes, odd codes) they are the 16 operand bytes of that lane.
+//  - A: the tile's activation rows of one 256-group per step are staged in
+//    LDS through registers; 16-byte piece p of row r sits at slot p ^ (r & 15),
+//    so the 16 rows read by one k-group of lanes hit distinct banks.  Lane
+//    i+16q reads activation words 2j..2j+3 of row i, the same chunks j.
+// Gate/up: block nt covers middle columns 64nt..64nt+63; wave w's tiles are
+// gate and up of columns 64nt+16w+i, so a lane forms SiLU(gate)*up itself and
+// writes the middle row of the route's position in the permuted order.
+// Down: a block covers NSUB x 128 output columns of its m-tile; both groups of
+// A (K = 512) stay in LDS while the column blocks are walked.
+// Steps (one 256-group of one column block each) are unrolled: the register
+// rings have compile-time slots and every load wait is exact.
+// ---------------------------------------------------------------------------
+template <bool GATEUP, int GS, int NSUB, int DB>
+__global__ __launch_bounds__(256, 2) void prefill_mfma_kernel(MfmaArgs a) {
+    constexpr int NSTEP = GS * NSUB;
+    constexpr int KW = GS * 64;                               // activation words per row
+    constexpr int NCB = GATEUP ? (2 * kInter) / kNT : kHidden / (kNT * NSUB);
+    static_assert(GS >= 2, "two A stages are filled in the prologue");
+    __shared__ __attribute__((aligned(16))) uint32_t sA[2][kMT * 64];
+    __shared__ __attribute__((aligned(16))) float s_sa[2][kMT];
+    __shared__ __attribute__((aligned(16))) float s_ss[2][kMT];
+    __shared__ int s_route[kMT];
+
+    // linear block -> (m-tile, column block); consecutive blocks share the m-tile
+    const int nt = int(blockIdx.x) % NCB, mtile = int(blockIdx.x) / NCB;
+    const int ntiles = a.ntiles[0];
+    const Segment td = a.tiles[mtile];                        // in bounds for every launched m-tile
+    if (mtile >= ntiles) return;
+    const int bank = td.bank, first = td.first, nrows = td.count;
+    const bool shared = bank == kShared;
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, li = lane & 15, q = lane >> 4;
+    const uint32_t* codes = shared ? a.shared_codes : a.codes + size_t(bank) * a.bank_words;
+    const uint32_t* meta = shared ? a.shared_meta : a.meta + size_t(bank) * a.bank_meta_words;
+
+    // ---- B: code words of step st for this lane ----
+    // column tile ct of step st: 32-column code tile and the column in it
+    auto b_tile = [&](int st, int ct, int& ntile, int& n) {
+        if (GATEUP) {
+            const int c = 64 * nt + 16 * w + li;
+            ntile = (ct ? kInter / 32 : 0) + (c >> 5);
+            n = c & 31;
+        } else {
+            const int base = kNT * (nt * NSUB + st / GS);
+            ntile = (base >> 5) + w;
+            n = 16 * ct + li;
+        }
+    };
+    // routes of this lane's A row (tid / 4) and scale row (tid % 64), first:
+    // later waits on them must not wait on the code loads
+    const int a_r = tid >> 2, a_part = tid & 3;
+    const int route_a = a.routes[first + min(a_r, nrows - 1)];
+    const int route_s = a.routes[first + min(tid & 63, nrows - 1)];
+    uint32_t bw[DB][2][8];          // [slot][ct][2s + e]
+    uint32_t bm[DB][2];             // meta word (sw | off << 16) per column tile
+    auto load_b = [&](int st, int slot) {
+        const int g = st % GS;
+#pragma unroll
+        for (int ct = 0; ct < 2; ++ct) {
+            int ntile, n;
+            b_tile(st, ct, ntile, n);
+            const uint32_t* src = codes + (size_t(ntile) * GS + g) * 1024 + (2 * q) * 32 + n;
+#pragma unroll
+            for (int s = 0; s < 4; ++s) {
+                bw[slot][ct][2 * s] = src[(8 * s) * 32];
+                bw[slot][ct][2 * s + 1] = src[(8 * s + 1) * 32];
+            }
+            bm[slot][ct] = meta[(size_t(ntile) * GS + g) * 32 + n];
+        }
+    };
+#pragma unroll
+    for (int st = 0; st < DB; ++st) load_b(st, st);
+
+    // ---- rows of the tile (dead rows repeat the last live row; never written) ----
+    // gate/up: activation row = token of the route; down: the permuted position
+    auto act_row = [&](int r, int route) {
+        return GATEUP ? (route < a.R ? route / kTop : route - a.R) : first + min(r, nrows - 1);
+    };
+
+    // ---- A: activation words of group g, 64 bytes per lane ----
+    const uint32_t* a_src = a.act_words + size_t(act_row(a_r, route_a)) * KW + 16 * a_part;
+    const size_t sa_base = size_t(act_row(tid & 63, route_s)) * GS;
+    u32x4 ra[2][4];
+    uint32_t rsa[2];
+    int rsum[2];
+    auto load_a = [&](int g, int slot) {
+#pragma unroll
+        for (int k = 0; k < 4; ++k) ra[slot][k] = *reinterpret_cast<const u32x4*>(a_src + g * 64 + 4 * k);
+        rsa[slot] = a.act_scales[sa_base + g];
+        rsum[slot] = a.act_sums[sa_base + g];
+    };
+    auto store_a = [&](int slot, int stage) {
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const int piece = (4 * a_part + k) ^ (a_r & 15);
+            *reinterpret_cast<u32x4*>(&sA[stage][a_r * 64 + 4 * piece]) = ra[slot][k];
+        }
+        if (tid < kMT) {
+            const float sa = f16_bits_to_f32(uint16_t(rsa[slot]));
+            s_sa[stage][tid] = sa;
+            s_ss[stage][tid] = sa * float(rsum[slot]);
+        }
+    };
+    load_a(0, 0);
+    load_a(1, 1);
+    store_a(0, 0);
+    if (!GATEUP && tid < kMT) s_route[tid] = tid < nrows ? route_s : -1;   // read after the first step's barrier
+    if (GS > 2) load_a(2, 0);
+
+    const bool live[4] = {true, nrows > 16, nrows > 32, nrows > 48};
+    float val[4][2][4];
+#pragma unroll
+    for (int rt = 0; rt < 4; ++rt)
+#pragma unroll
+        for (int ct = 0; ct < 2; ++ct)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) val[rt][ct][r] = 0.f;
+    uint32_t flags = 0;
+
+    auto step = [&]<int ST>() {
+        constexpr int g = ST % GS, sub = ST / GS, stage = g % 2, bslot = ST % DB;
+        __syncthreads();                    // stage g visible; the other stage's readers are done
+        if constexpr (ST + 1 < GS) {
+            store_a((ST + 1) % 2, (ST + 1) % 2);
+            if constexpr (ST + 3 < GS) load_a(ST + 3, (ST + 1) % 2);
+        }
+        // all four row tiles go through the matrix cores (dead rows hold copies
+        // of a live row); only the VALU tree skips row tiles with no live row
+        i32x4 acc[4][2];
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+            i32x4 fa[4], fb[2];
+#pragma unroll
+            for (int rt = 0; rt < 4; ++rt) {
+                const int row = 16 * rt + li;
+                const u32x4 v = *reinterpret_cast<const u32x4*>(&sA[stage][row * 64 + 4 * ((4 * s + q) ^ li)]);
+                fa[rt] = i32x4{int(v.x), int(v.y), int(v.z), int(v.w)};
+            }
+#pragma unroll
+            for (int ct = 0; ct < 2; ++ct) {
+                const uint32_t w0 = bw[bslot][ct][2 * s], w1 = bw[bslot][ct][2 * s + 1];
+                fb[ct] = i32x4{code_even(w0), code_odd(w0), code_even(w1), code_odd(w1)};
+            }
+#pragma unroll
+            for (int rt = 0; rt < 4; ++rt)
+#pragma unroll
+                for (int ct = 0; ct < 2; ++ct)
+                    acc[rt][ct] = __builtin_amdgcn_mfma_i32_16x16x64_i8(fa[rt], fb[ct], s ? acc[rt][ct] : i32x4{0, 0, 0, 0},
+                                                                       0, 0, 0);
+        }
+        float sw[2], off[2];
+#pragma unroll
+        for (int ct = 0; ct < 2; ++ct) {
+            sw[ct] = f16_bits_to_f32(uint16_t(bm[bslot][ct] & 0xffffu));
+            off[ct] = f16_bits_to_f32(uint16_t(bm[bslot][ct] >> 16));
+        }
+        if constexpr (ST + DB < NSTEP) load_b(ST + DB, bslot);
+        // fp32 group tree (dense_g256_api.h:35-37) in ascending group order
+#pragma unroll
+        for (int rt = 0; rt < 4; ++rt) {
+            if (!live[rt]) continue;
+            const float4 sa4 = *reinterpret_cast<const float4*>(&s_sa[stage][16 * rt + 4 * q]);
+            const float4 ss4 = *reinterpret_cast<const float4*>(&s_ss[stage][16 * rt + 4 * q]);
+            const float sa[4] = {sa4.x, sa4.y, sa4.z, sa4.w}, ss[4] = {ss4.x, ss4.y, ss4.z, ss4.w};
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+#pragma unroll
+                for (int ct = 0; ct < 2; ++ct) {
+                    const float scaled_dot = sa[r] * float(acc[rt][ct][r]);
+                    const float product = sw[ct] * scaled_dot;
+                    const float correction = off[ct] * ss[r];
+                    val[rt][ct][r] = val[rt][ct][r] + (product + correction);
+                }
+        }
+        // keep each step's tree in its step: sinking it would keep every
+        // step's accumulators alive at once
+#pragma unroll
+        for (int rt = 0; rt < 4; ++rt)
+#pragma unroll
+            for (int ct = 0; ct < 2; ++ct)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) asm volatile("" : "+v"(val[rt][ct][r]));
+        if constexpr (g == GS - 1) {
+            // ---- epilogue of one column block ----
+#pragma unroll
+            for (int rt = 0; rt < 4; ++rt) {
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const int row = 16 * rt + 4 * q + r;
+                    if (row < nrows) {
+                        if constexpr (GATEUP) {
+                            float vg = val[rt][0][r], vu = val[rt][1][r];
+                            float mid;
+                            if (shared) {
+                                vg = bf16_round(vg);
+                                vu = bf16_round(vu);
+                                if (!isfinite(vg) || !isfinite(vu)) flags |= kFlagNonfiniteProjection;
+                                mid = bf16_round(a.silu_table[__float_as_uint(vg) >> 16] * vu);
+                            } else {
+                                if (!isfinite(vg) || !isfinite(vu)) flags |= kFlagNonfiniteProjection;
+                                mid = silu_portable(vg) * vu;
+                            }
+                            if (!isfinite(mid)) flags |= kFlagNonfiniteMiddle | kFlagNonfiniteInput;
+                            a.out[size_t(first + row) * kInter + 64 * nt + 16 * w + li] = mid;
+                        } else {
+                            const int route = s_route[row];
+                            const int col0 = kNT * (nt * NSUB + sub) + 32 * w + li;
+#pragma unroll
+                            for (int ct = 0; ct < 2; ++ct) {
+                                float v = val[rt][ct][r];
+                                if (shared) v = bf16_round(v);
+                                if (!isfinite(v)) flags |= kFlagNonfiniteProjection;
+                                a.out[size_t(route) * kHidden + col0 + 16 * ct] = v;
+                            }
+                        }
+                    }
+#pragma unroll
+                    for (int ct = 0; ct < 2; ++ct) val[rt][ct][r] = 0.f;
+                }
+            }
+        }
+    };
+    [&]<int... S>(std::integer_sequence<int, S...>) {
+        (step.template operator()<S>(), ...);
+    }(std::make_integer_sequence<int, NSTEP>{});
+    flag_or(a.sticky, flags);
+}
+
 hipError_t launch_grouped_mfma(const MfmaArgs& a, bool gateup, int max_tiles, hipStream_t s) {
     if (max_tiles <= 0) return hipSuccess;
-    if (gateup) timed_launch("gateup_mfma", grouped_mfma_kernel<kModeGateUp, kHidden / kGroup, 2>, dim3(max_tiles, (2 * kInter) / kNT), dim3(256), 0, s, a);
-    else timed_launch("down_mfma", grouped_mfma_kernel<kModeDown, kInter / kGroup, 2>, dim3(max_tiles, kHidden / kNT), dim3(256), 0, s, a);
+    constexpr int kDownSub = 4;     // down: 4 column blocks (512 columns) per block
+    if (gateup)
+        timed_launch("gateup_mfma", prefill_mfma_kernel<true, kHidden / kGroup, 1, 2>,
+                     dim3(max_tiles * ((2 * kInter) / kNT)), dim3(256), 0, s, a);
+    else
+        timed_launch("down_mfma", prefill_mfma_kernel<false, kInter / kGroup, kDownSub, 3>,
+                     dim3(max_tiles * (kHidden / (kNT * kDownSub))), dim3(256), 0, s, a);
     return hipGetLastError();
 }
 
 hipError_t launch_head_mfma(const MfmaArgs& a, int64_t* argmax, hipStream_t s) {
     if (a.R <= 0 || a.R > kMT || a.N <= 0 || a.N % 32 != 0 || a.K != kHidden) return hipErrorInvalidValue;
     const int nblk = (a.N + kNT - 1) / kNT;
-    timed_launch("head_mfma", grouped_mfma_kernel<kModeHead, kHidden / kGroup, 2>, dim3(1, nblk), dim3(256), 0, s, a);
+    timed_launch("head_mfma", grouped_mfma_kernel<kModeHead, kHidden / kGroup, 2>, dim3(nblk), dim3(256), 0, s, a);
     hipError_t st = hipGetLastError();
     if (st != hipSuccess) return st;
     timed_launch("argmax", head_argmax_kernel, dim3(a.R), dim3(256), 0, s, a.arg_val, a.arg_idx, nblk, argmax);
@@ -391,6 +636,36 @@ __global__ __launch_bounds__(256) void quant_middle_kernel(const float* __restri
     for (int i = 0; i < 4; ++i) if (!isfinite(v[i])) flags |= kFlagNonfiniteInput;
     quantize_group_wave<QMAX>(v, words + size_t(wave) * 64, scales + wave, sums + wave, flags, kFlagInvalidActivation);
     flag_or(sticky, flags);
+}
+
+// Same over middle rows in permuted route order: rows 0 .. *nrows - 1.
+template <int QMAX>
+__global__ __launch_bounds__(256) void quant_middle_permuted_kernel(const float* __restrict__ middle, int RS,
+                                                                    const int32_t* __restrict__ nrows,
+                                                                    uint32_t* __restrict__ words,
+                                                                    uint16_t* __restrict__ scales,
+                                                                    int32_t* __restrict__ sums, uint32_t* sticky) {
+    const int wave = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (wave >= RS * 2 || (wave >> 1) >= nrows[0]) return;
+    const int lane = threadIdx.x & 63, row = wave >> 1, group = wave & 1;
+    const float4 m4 = *reinterpret_cast<const float4*>(middle + size_t(row) * kInter + group * kGroup + lane * 4);
+    float v[4] = {m4.x, m4.y, m4.z, m4.w};
+    uint32_t flags = 0;
+    h128_wave(v);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) if (!isfinite(v[i])) flags |= kFlagNonfiniteInput;
+    quantize_group_wave<QMAX>(v, words + size_t(wave) * 64, scales + wave, sums + wave, flags, kFlagInvalidActivation);
+    flag_or(sticky, flags);
+}
+
+hipError_t launch_quant_middle_permuted(const float* middle, int RS, const int32_t* nrows, int qmax, uint32_t* words,
+                                        uint16_t* scales, int32_t* sums, uint32_t* sticky, hipStream_t s) {
+    const int waves = RS * 2;
+    if (qmax == 127)
+        timed_launch("quant_middle", quant_middle_permuted_kernel<127>, dim3((waves + 3) / 4), dim3(256), 0, s, middle, RS, nrows, words, scales, sums, sticky);
+    else
+        timed_launch("quant_middle", quant_middle_permuted_kernel<7>, dim3((waves + 3) / 4), dim3(256), 0, s, middle, RS, nrows, words, scales, sums, sticky);
+    return hipGetLastError();
 }
 
 hipError_t launch_quant_middle(const float* middle, int RS, int R, const int32_t* ids, int qmax, uint32_t* words,

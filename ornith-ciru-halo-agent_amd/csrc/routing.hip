@@ -269,7 +269,7 @@ size_t permute_scratch_bytes(int Rcap, int Tcap) {
     bytes += align256(rall * 4);
     bytes += align256(kBanks * sizeof(Segment));
     bytes += align256(4 * 4);
-    bytes += align256((rall + kBanks) * 4);
+    bytes += align256((rall / 64 + kBanks + 2) * sizeof(Segment));   // one per 64-route m-tile
     return bytes;
 }
 
@@ -285,7 +285,7 @@ PermuteScratch carve_permute(void* base, int Rcap, int Tcap) {
     p.routes = static_cast<int32_t*>(take(rall * 4));
     p.segments = static_cast<Segment*>(take(kBanks * sizeof(Segment)));
     p.meta = static_cast<int32_t*>(take(4 * 4));
-    p.tiles = static_cast<int32_t*>(take((rall + kBanks) * 4));
+    p.tiles = static_cast<Segment*>(take((rall / 64 + kBanks + 2) * sizeof(Segment)));
     return p;
 }
 
@@ -311,7 +311,7 @@ __global__ __launch_bounds__(kPermBlock) void permute_count_kernel(const int32_t
 __global__ __launch_bounds__(512) void permute_scan_kernel(int nblocks, int32_t* __restrict__ block_counts,
                                                            int32_t* __restrict__ counts, int32_t* __restrict__ offsets,
                                                            Segment* __restrict__ segments, int32_t* __restrict__ meta,
-                                                           int32_t* __restrict__ tiles, int mfma_rows) {
+                                                           Segment* __restrict__ tiles, int mfma_rows) {
     __shared__ int a[512], b[512], c[512];
     const int e = threadIdx.x;
     int total = 0;
@@ -349,7 +349,8 @@ __global__ __launch_bounds__(512) void permute_scan_kernel(int nblocks, int32_t*
             const int seg = b[e] - 1;
             const int tile_base = c[e] - ntile;
             segments[seg] = Segment{e, off, total, tile_base};
-            for (int k = 0; k < ntile; ++k) tiles[tile_base + k] = (seg << 16) | k;
+            for (int k = 0; k < ntile; ++k)
+                tiles[tile_base + k] = Segment{e, off + k * mfma_rows, min(mfma_rows, total - k * mfma_rows), k};
         }
     }
     if (e == 0) { meta[0] = b[kBanks - 1]; meta[1] = c[kBanks - 1]; }

@@ -157,13 +157,15 @@ def test_routed_bit_exact(device, moe, T, entry, qmax):
     assert flags == ref['flags']
 
 
-def test_routed_padding_and_invalid_ids(device, moe):
+@pytest.mark.parametrize('T', [5, 48])
+def test_routed_padding_and_invalid_ids(device, moe, T):
     """-1 padding slots are skipped silently; out-of-range ids raise flag 4
-    and contribute nothing; a token with no live slot outputs zeros."""
+    and contribute nothing; a token with no live slot outputs zeros.  T = 48
+    runs the prefill path, whose permuted route list holds only live routes."""
     native = _native()
+    print(f'routed padding/invalid T={T}', flush=True)
     w, d = moe
     rng = np.random.default_rng(77)
-    T = 5
     x = bf16_normal(rng, (T, 2048))
     rw, ids = random_routing(rng, T)
     ids[0, 3] = -1
@@ -171,7 +173,7 @@ def test_routed_padding_and_invalid_ids(device, moe):
     ids[2, 7] = 300
     ids[4, 0] = -5
     ref = oracle_routed(x, rw, ids, w['w13'], w['w2'])
-    out, final, flags = _run_routed(native, device, d, x, rw, ids, 'ornith_routed_direct_launch', Tcap=8)
+    out, final, flags = _run_routed(native, device, d, x, rw, ids, 'ornith_routed_direct_launch', Tcap=max(8, T))
     np.testing.assert_array_equal(final.view(np.uint32), ref['final'].view(np.uint32))
     np.testing.assert_array_equal(out, ref['out'])
     assert flags == ref['flags'] == 4
