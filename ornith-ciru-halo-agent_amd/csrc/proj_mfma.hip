@@ -378,18 +378,26 @@ __global__ __launch_bounds__(256) void head_argmax_kernel(const float* __restric
 // writes the middle row of the route's position in the permuted order.
 // Down: a block covers NSUB x 128 output columns of its m-tile; both groups of
 // A (K = 512) stay in LDS while the column blocks are walked.
-// Steps (one 256-group of one column block each) are unrolled: the register
-// rings have compile-time slots and every load wait is exact.
+//
+// Steps (one 256-group of one column block each) are unrolled, so the
+// register rings have compile-time slots and every load wait is exact, and
+// software-pipelined inside the wave: step st issues the matrix-core dots of
+// step st+1 (accumulators double-buffered) and then runs the fp32 tree of
+// step st on the VALU while they execute.  A moves global -> registers
+// (loaded one step before its store) -> LDS (stored one step before its dots,
+// three stages) -> MFMA.  The step body is instantiated for 1, 2 and 4 row
+// tiles of 16 rows, so partial tiles skip dead row tiles without branches.
 // ---------------------------------------------------------------------------
 template <bool GATEUP, int GS, int NSUB, int DB>
 __global__ __launch_bounds__(256, 2) void prefill_mfma_kernel(MfmaArgs a) {
     constexpr int NSTEP = GS * NSUB;
     constexpr int KW = GS * 64;                               // activation words per row
     constexpr int NCB = GATEUP ? (2 * kInter) / kNT : kHidden / (kNT * NSUB);
+    constexpr int NSTAGE = GS < 3 ? GS : 3;                   // A stages in LDS
     static_assert(GS >= 2, "two A stages are filled in the prologue");
-    __shared__ __attribute__((aligned(16))) uint32_t sA[2][kMT * 64];
-    __shared__ __attribute__((aligned(16))) float s_sa[2][kMT];
-    __shared__ __attribute__((aligned(16))) float s_ss[2][kMT];
+    __shared__ __attribute__((aligned(16))) uint32_t sA[NSTAGE][kMT * 64];
+    __shared__ __attribute__((aligned(16))) float s_sa[NSTAGE][kMT];
+    __shared__ __attribute__((aligned(16))) float s_ss[NSTAGE][kMT];
     __shared__ int s_route[kMT];
 
     // linear block -> (m-tile, column block); consecutive blocks share the m-tile
@@ -402,6 +410,12 @@ __global__ __launch_bounds__(256, 2) void prefill_mfma_kernel(MfmaArgs a) {
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, li = lane & 15, q = lane >> 4;
     const uint32_t* codes = shared ? a.shared_codes : a.codes + size_t(bank) * a.bank_words;
     const uint32_t* meta = shared ? a.shared_meta : a.meta + size_t(bank) * a.bank_meta_words;
+
+    // routes of this lane's A row (tid / 4) and scale row (tid % 64), first:
+    // later waits on them must not wait on the code loads
+    const int a_r = tid >> 2, a_part = tid & 3;
+    const int route_a = a.routes[first + min(a_r, nrows - 1)];
+    const int route_s = a.routes[first + min(tid & 63, nrows - 1)];
 
     // ---- B: code words of step st for this lane ----
     // column tile ct of step st: 32-column code tile and the column in it
@@ -416,11 +430,6 @@ __global__ __launch_bounds__(256, 2) void prefill_mfma_kernel(MfmaArgs a) {
             n = 16 * ct + li;
         }
     };
-    // routes of this lane's A row (tid / 4) and scale row (tid % 64), first:
-    // later waits on them must not wait on the code loads
-    const int a_r = tid >> 2, a_part = tid & 3;
-    const int route_a = a.routes[first + min(a_r, nrows - 1)];
-    const int route_s = a.routes[first + min(tid & 63, nrows - 1)];
     uint32_t bw[DB][2][8];          // [slot][ct][2s + e]
     uint32_t bm[DB][2];             // meta word (sw | off << 16) per column tile
     auto load_b = [&](int st, int slot) {
@@ -450,9 +459,9 @@ __global__ __launch_bounds__(256, 2) void prefill_mfma_kernel(MfmaArgs a) {
     // ---- A: activation words of group g, 64 bytes per lane ----
     const uint32_t* a_src = a.act_words + size_t(act_row(a_r, route_a)) * KW + 16 * a_part;
     const size_t sa_base = size_t(act_row(tid & 63, route_s)) * GS;
-    u32x4 ra[2][4];
-    uint32_t rsa[2];
-    int rsum[2];
+    u32x4 ra[1][4];                 // one register slot: A(g) is loaded one step before its LDS store
+    uint32_t rsa[1];
+    int rsum[1];
     auto load_a = [&](int g, int slot) {
 #pragma unroll
         for (int k = 0; k < 4; ++k) ra[slot][k] = *reinterpret_cast<const u32x4*>(a_src + g * 64 + 4 * k);
@@ -471,128 +480,157 @@ __global__ __launch_bounds__(256, 2) void prefill_mfma_kernel(MfmaArgs a) {
             s_ss[stage][tid] = sa * float(rsum[slot]);
         }
     };
+    // A(0) and A(1) in flight together (A(1) through prologue-only registers)
+    u32x4 ra1[4];
+    uint32_t rsa1;
+    int rsum1;
     load_a(0, 0);
-    load_a(1, 1);
+#pragma unroll
+    for (int k = 0; k < 4; ++k) ra1[k] = *reinterpret_cast<const u32x4*>(a_src + 64 + 4 * k);
+    rsa1 = a.act_scales[sa_base + 1];
+    rsum1 = a.act_sums[sa_base + 1];
     store_a(0, 0);
-    if (!GATEUP && tid < kMT) s_route[tid] = tid < nrows ? route_s : -1;   // read after the first step's barrier
+#pragma unroll
+    for (int k = 0; k < 4; ++k) ra[0][k] = ra1[k];
+    rsa[0] = rsa1;
+    rsum[0] = rsum1;
+    store_a(0, 1);
+    if (!GATEUP && tid < kMT) s_route[tid] = tid < nrows ? route_s : -1;   // read after the first barrier
     if (GS > 2) load_a(2, 0);
+    __syncthreads();
 
-    const bool live[4] = {true, nrows > 16, nrows > 32, nrows > 48};
-    float val[4][2][4];
-#pragma unroll
-    for (int rt = 0; rt < 4; ++rt)
-#pragma unroll
-        for (int ct = 0; ct < 2; ++ct)
-#pragma unroll
-            for (int r = 0; r < 4; ++r) val[rt][ct][r] = 0.f;
     uint32_t flags = 0;
-
-    auto step = [&]<int ST>() {
-        constexpr int g = ST % GS, sub = ST / GS, stage = g % 2, bslot = ST % DB;
-        __syncthreads();                    // stage g visible; the other stage's readers are done
-        if constexpr (ST + 1 < GS) {
-            store_a((ST + 1) % 2, (ST + 1) % 2);
-            if constexpr (ST + 3 < GS) load_a(ST + 3, (ST + 1) % 2);
-        }
-        // all four row tiles go through the matrix cores (dead rows hold copies
-        // of a live row); only the VALU tree skips row tiles with no live row
-        i32x4 acc[4][2];
-#pragma unroll
-        for (int s = 0; s < 4; ++s) {
-            i32x4 fa[4], fb[2];
-#pragma unroll
-            for (int rt = 0; rt < 4; ++rt) {
-                const int row = 16 * rt + li;
-                const u32x4 v = *reinterpret_cast<const u32x4*>(&sA[stage][row * 64 + 4 * ((4 * s + q) ^ li)]);
-                fa[rt] = i32x4{int(v.x), int(v.y), int(v.z), int(v.w)};
-            }
-#pragma unroll
-            for (int ct = 0; ct < 2; ++ct) {
-                const uint32_t w0 = bw[bslot][ct][2 * s], w1 = bw[bslot][ct][2 * s + 1];
-                fb[ct] = i32x4{code_even(w0), code_odd(w0), code_even(w1), code_odd(w1)};
-            }
-#pragma unroll
-            for (int rt = 0; rt < 4; ++rt)
-#pragma unroll
-                for (int ct = 0; ct < 2; ++ct)
-                    acc[rt][ct] = __builtin_amdgcn_mfma_i32_16x16x64_i8(fa[rt], fb[ct], s ? acc[rt][ct] : i32x4{0, 0, 0, 0},
-                                                                       0, 0, 0);
-        }
-        float sw[2], off[2];
-#pragma unroll
-        for (int ct = 0; ct < 2; ++ct) {
-            sw[ct] = f16_bits_to_f32(uint16_t(bm[bslot][ct] & 0xffffu));
-            off[ct] = f16_bits_to_f32(uint16_t(bm[bslot][ct] >> 16));
-        }
-        if constexpr (ST + DB < NSTEP) load_b(ST + DB, bslot);
-        // fp32 group tree (dense_g256_api.h:35-37) in ascending group order
-#pragma unroll
-        for (int rt = 0; rt < 4; ++rt) {
-            if (!live[rt]) continue;
-            const float4 sa4 = *reinterpret_cast<const float4*>(&s_sa[stage][16 * rt + 4 * q]);
-            const float4 ss4 = *reinterpret_cast<const float4*>(&s_ss[stage][16 * rt + 4 * q]);
-            const float sa[4] = {sa4.x, sa4.y, sa4.z, sa4.w}, ss[4] = {ss4.x, ss4.y, ss4.z, ss4.w};
-#pragma unroll
-            for (int r = 0; r < 4; ++r)
-#pragma unroll
-                for (int ct = 0; ct < 2; ++ct) {
-                    const float scaled_dot = sa[r] * float(acc[rt][ct][r]);
-                    const float product = sw[ct] * scaled_dot;
-                    const float correction = off[ct] * ss[r];
-                    val[rt][ct][r] = val[rt][ct][r] + (product + correction);
-                }
-        }
-        // keep each step's tree in its step: sinking it would keep every
-        // step's accumulators alive at once
+    // L = row tiles with a live row (compile time, so the step body is branch-free)
+    auto run = [&]<int L>() {
+        float val[4][2][4];
 #pragma unroll
         for (int rt = 0; rt < 4; ++rt)
 #pragma unroll
             for (int ct = 0; ct < 2; ++ct)
 #pragma unroll
-                for (int r = 0; r < 4; ++r) asm volatile("" : "+v"(val[rt][ct][r]));
-        if constexpr (g == GS - 1) {
-            // ---- epilogue of one column block ----
+                for (int r = 0; r < 4; ++r) val[rt][ct][r] = 0.f;
+        i32x4 acc[2][4][2];
+        float swv[2][2], offv[2][2];
+
+        // matrix-core dots of step ST into accumulator set ST % 2 for the L
+        // live row tiles (rows past nrows in them hold copies of a live row)
+        auto mfma_step = [&]<int ST>() {
+            constexpr int g = ST % GS, stage = g % NSTAGE, bslot = ST % DB, as = ST % 2;
 #pragma unroll
-            for (int rt = 0; rt < 4; ++rt) {
+            for (int s = 0; s < 4; ++s) {
+                i32x4 fa[4], fb[2];
 #pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    const int row = 16 * rt + 4 * q + r;
-                    if (row < nrows) {
-                        if constexpr (GATEUP) {
-                            float vg = val[rt][0][r], vu = val[rt][1][r];
-                            float mid;
-                            if (shared) {
-                                vg = bf16_round(vg);
-                                vu = bf16_round(vu);
-                                if (!isfinite(vg) || !isfinite(vu)) flags |= kFlagNonfiniteProjection;
-                                mid = bf16_round(a.silu_table[__float_as_uint(vg) >> 16] * vu);
+                for (int rt = 0; rt < L; ++rt) {
+                    const int row = 16 * rt + li;
+                    const u32x4 v = *reinterpret_cast<const u32x4*>(&sA[stage][row * 64 + 4 * ((4 * s + q) ^ li)]);
+                    fa[rt] = i32x4{int(v.x), int(v.y), int(v.z), int(v.w)};
+                }
+#pragma unroll
+                for (int ct = 0; ct < 2; ++ct) {
+                    const uint32_t w0 = bw[bslot][ct][2 * s], w1 = bw[bslot][ct][2 * s + 1];
+                    fb[ct] = i32x4{code_even(w0), code_odd(w0), code_even(w1), code_odd(w1)};
+                }
+#pragma unroll
+                for (int rt = 0; rt < L; ++rt)
+#pragma unroll
+                    for (int ct = 0; ct < 2; ++ct)
+                        acc[as][rt][ct] = __builtin_amdgcn_mfma_i32_16x16x64_i8(
+                            fa[rt], fb[ct], s ? acc[as][rt][ct] : i32x4{0, 0, 0, 0}, 0, 0, 0);
+            }
+            // the slot's scales are taken before the slot is refilled
+#pragma unroll
+            for (int ct = 0; ct < 2; ++ct) {
+                swv[as][ct] = f16_bits_to_f32(uint16_t(bm[bslot][ct] & 0xffffu));
+                offv[as][ct] = f16_bits_to_f32(uint16_t(bm[bslot][ct] >> 16));
+            }
+            if constexpr (ST + DB < NSTEP) load_b(ST + DB, bslot);
+        };
+
+        // fp32 group tree of step ST (dense_g256_api.h:35-37), ascending groups
+        auto tree_step = [&]<int ST>() {
+            constexpr int g = ST % GS, sub = ST / GS, stage = g % NSTAGE, as = ST % 2;
+#pragma unroll
+            for (int rt = 0; rt < L; ++rt) {
+                const float4 sa4 = *reinterpret_cast<const float4*>(&s_sa[stage][16 * rt + 4 * q]);
+                const float4 ss4 = *reinterpret_cast<const float4*>(&s_ss[stage][16 * rt + 4 * q]);
+                const float sa[4] = {sa4.x, sa4.y, sa4.z, sa4.w}, ss[4] = {ss4.x, ss4.y, ss4.z, ss4.w};
+#pragma unroll
+                for (int r = 0; r < 4; ++r)
+#pragma unroll
+                    for (int ct = 0; ct < 2; ++ct) {
+                        const float scaled_dot = sa[r] * float(acc[as][rt][ct][r]);
+                        const float product = swv[as][ct] * scaled_dot;
+                        const float correction = offv[as][ct] * ss[r];
+                        val[rt][ct][r] = val[rt][ct][r] + (product + correction);
+                    }
+            }
+            // keep each step's tree in its step: sinking it would keep every
+            // step's accumulators alive at once
+#pragma unroll
+            for (int rt = 0; rt < L; ++rt)
+#pragma unroll
+                for (int ct = 0; ct < 2; ++ct)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) asm volatile("" : "+v"(val[rt][ct][r]));
+            if constexpr (g == GS - 1) {
+                // ---- epilogue of one column block ----
+#pragma unroll
+                for (int rt = 0; rt < L; ++rt) {
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        const int row = 16 * rt + 4 * q + r;
+                        if (row < nrows) {
+                            if constexpr (GATEUP) {
+                                float vg = val[rt][0][r], vu = val[rt][1][r];
+                                float mid;
+                                if (shared) {
+                                    vg = bf16_round(vg);
+                                    vu = bf16_round(vu);
+                                    if (!isfinite(vg) || !isfinite(vu)) flags |= kFlagNonfiniteProjection;
+                                    mid = bf16_round(a.silu_table[__float_as_uint(vg) >> 16] * vu);
+                                } else {
+                                    if (!isfinite(vg) || !isfinite(vu)) flags |= kFlagNonfiniteProjection;
+                                    mid = silu_portable(vg) * vu;
+                                }
+                                if (!isfinite(mid)) flags |= kFlagNonfiniteMiddle | kFlagNonfiniteInput;
+                                a.out[size_t(first + row) * kInter + 64 * nt + 16 * w + li] = mid;
                             } else {
-                                if (!isfinite(vg) || !isfinite(vu)) flags |= kFlagNonfiniteProjection;
-                                mid = silu_portable(vg) * vu;
-                            }
-                            if (!isfinite(mid)) flags |= kFlagNonfiniteMiddle | kFlagNonfiniteInput;
-                            a.out[size_t(first + row) * kInter + 64 * nt + 16 * w + li] = mid;
-                        } else {
-                            const int route = s_route[row];
-                            const int col0 = kNT * (nt * NSUB + sub) + 32 * w + li;
+                                const int route = s_route[row];
+                                const int col0 = kNT * (nt * NSUB + sub) + 32 * w + li;
 #pragma unroll
-                            for (int ct = 0; ct < 2; ++ct) {
-                                float v = val[rt][ct][r];
-                                if (shared) v = bf16_round(v);
-                                if (!isfinite(v)) flags |= kFlagNonfiniteProjection;
-                                a.out[size_t(route) * kHidden + col0 + 16 * ct] = v;
+                                for (int ct = 0; ct < 2; ++ct) {
+                                    float v = val[rt][ct][r];
+                                    if (shared) v = bf16_round(v);
+                                    if (!isfinite(v)) flags |= kFlagNonfiniteProjection;
+                                    a.out[size_t(route) * kHidden + col0 + 16 * ct] = v;
+                                }
                             }
                         }
-                    }
 #pragma unroll
-                    for (int ct = 0; ct < 2; ++ct) val[rt][ct][r] = 0.f;
+                        for (int ct = 0; ct < 2; ++ct) val[rt][ct][r] = 0.f;
+                    }
                 }
             }
-        }
+        };
+
+        mfma_step.template operator()<0>();
+        [&]<int... S>(std::integer_sequence<int, S...>) {
+            ([&] {
+                constexpr int ST = S;
+                __syncthreads();            // A of step ST+1 visible; stage (ST+2)%3 free
+                if constexpr (ST + 2 < GS) {
+                    store_a(0, (ST + 2) % NSTAGE);
+                    if constexpr (ST + 3 < GS) load_a(ST + 3, 0);
+                }
+                if constexpr (ST + 1 < NSTEP) mfma_step.template operator()<ST + 1>();
+                tree_step.template operator()<ST>();
+            }(), ...);
+        }(std::make_integer_sequence<int, NSTEP>{});
     };
-    [&]<int... S>(std::integer_sequence<int, S...>) {
-        (step.template operator()<S>(), ...);
-    }(std::make_integer_sequence<int, NSTEP>{});
+    // 33..48 rows run the four-tile body (a fourth instantiation costs registers)
+    if (nrows > 32) run.template operator()<4>();
+    else if (nrows > 16) run.template operator()<2>();
+    else run.template operator()<1>();
     flag_or(a.sticky, flags);
 }
 
