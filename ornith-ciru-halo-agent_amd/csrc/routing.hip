@@ -176,6 +176,112 @@ __global__ __launch_bounds__(256) void router_kernel(const uint16_t* __restrict_
     }
 }
 
+// Router logits for large T, lane = token (same declared order as above).
+// Block = 64 tokens x 8 router rows; wave q forms Sq (partials 16q..16q+15)
+// of all 512 outputs, one token per lane.  The block's 8 weight rows are
+// staged once as fp32 in LDS and read by broadcast (every lane of a wave
+// reads the same address).  A lane walks its token's chunks in memory order,
+// 16q..16q+15 then +64, +128, +192 (one full 128-byte line per 8 chunks),
+// updating the 16 partial chains at once; the 16 partials are then summed in
+// the balanced tree.  Blocks are laid out so that the row groups of one token
+// group run on one XCD (workgroups go to the 8 XCDs round-robin) and share
+// its L2.
+constexpr int kRtRows = 8, kRtTokens = 64;
+
+__global__ __launch_bounds__(256, 2) void router_tokens_kernel(const uint16_t* __restrict__ x, int64_t stride, int T,
+                                                               const uint16_t* __restrict__ w,
+                                                               const uint16_t* __restrict__ shared_w,
+                                                               const float* __restrict__ bias, float* __restrict__ logits,
+                                                               int64_t logit_stride, int nrows, int ntg) {
+    __shared__ __align__(16) float sW[kRtRows][kHidden];       // fp32 weights of the block's rows
+    __shared__ __align__(16) float sS[4][kRtRows][kRtTokens];  // Sq per wave
+    const int ngroups = (nrows + kRtRows - 1) / kRtRows;
+    const int blk = blockIdx.x, idx = blk >> 3;
+    const int tg = 8 * (idx / ngroups) + (blk & 7), rg = idx % ngroups;
+    if (tg >= ntg) return;
+    const int tid = threadIdx.x, lane = tid & 63, q = tid >> 6;
+    const int e0 = rg * kRtRows;
+
+    // this lane's token (tokens past T repeat the last one; never stored)
+    const uint16_t* xrow = x + size_t(min(tg * kRtTokens + lane, T - 1)) * stride + 8 * (16 * q);
+    // chunk s (0..15) of segment j: 16q + s + 64j; a line of 8 chunks in registers,
+    // each slot refilled with the next line's chunk once converted
+    u32x4 xv[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) xv[i] = *reinterpret_cast<const u32x4*>(xrow + 8 * i);
+
+    // stage the 8 weight rows (rows past nrows repeat the last one; never stored)
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const int p = tid + 256 * i, r = p >> 8, c = p & 255;
+        const int e = min(e0 + r, nrows - 1);
+        const uint16_t* row = e < kExperts ? w + size_t(e) * kHidden : shared_w;
+        const uint4 v = *reinterpret_cast<const uint4*>(row + 8 * c);
+        float f[8];
+        bf16x8_to_f32(v, f);
+        *reinterpret_cast<float4*>(&sW[r][8 * c]) = float4{f[0], f[1], f[2], f[3]};
+        *reinterpret_cast<float4*>(&sW[r][8 * c + 4]) = float4{f[4], f[5], f[6], f[7]};
+    }
+    __syncthreads();
+
+    // unit u = (j, s, r), u = 128j + 8s + r: row r of chunk 16q + s + 64j.  The
+    // broadcast weight reads run two units ahead through a 3-slot ring.
+    auto wread = [&](int u, float (&dst)[8]) __attribute__((always_inline)) {
+        const int j = u >> 7, sr = u & 127, s = sr >> 3, r = sr & 7, c = 16 * q + s + 64 * j;
+        const float4 w0 = *reinterpret_cast<const float4*>(&sW[r][8 * c]);
+        const float4 w1 = *reinterpret_cast<const float4*>(&sW[r][8 * c + 4]);
+        dst[0] = w0.x; dst[1] = w0.y; dst[2] = w0.z; dst[3] = w0.w;
+        dst[4] = w1.x; dst[5] = w1.y; dst[6] = w1.z; dst[7] = w1.w;
+    };
+    // acc[s][r]: partial 16q + s of row r, fma chain over chunks j = 0..3, k ascending
+    float acc[16][kRtRows];
+#pragma unroll
+    for (int s = 0; s < 16; ++s)
+#pragma unroll
+        for (int r = 0; r < kRtRows; ++r) acc[s][r] = 0.f;
+    float wr[3][8], xf[8];
+    wread(0, wr[0]);
+    wread(1, wr[1]);
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int s = 0; s < 16; ++s)
+#pragma unroll
+            for (int r = 0; r < kRtRows; ++r) {
+                const int u = 128 * j + 8 * s + r, i = s & 7;
+                if (u + 2 < 512) wread(u + 2, wr[(u + 2) % 3]);
+                if (r == 0) {
+                    bf16x8_to_f32(uint4{xv[i].x, xv[i].y, xv[i].z, xv[i].w}, xf);
+                    // next line's chunk i: same segment's second half, or the next segment's first
+                    const int nc = s < 8 ? 64 * j + 8 + i : 64 * (j + 1) + i;
+                    if (s < 8 || j < 3) xv[i] = *reinterpret_cast<const u32x4*>(xrow + 8 * nc);
+                }
+#pragma unroll
+                for (int k = 0; k < 8; ++k) acc[s][r] = __builtin_fmaf(xf[k], wr[u % 3][k], acc[s][r]);
+            }
+    // Sq = balanced tree over the 16 partials
+#pragma unroll
+    for (int r = 0; r < kRtRows; ++r) {
+        float p8[8], p4[4], p2[2];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) p8[i] = acc[2 * i][r] + acc[2 * i + 1][r];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) p4[i] = p8[2 * i] + p8[2 * i + 1];
+#pragma unroll
+        for (int i = 0; i < 2; ++i) p2[i] = p4[2 * i] + p4[2 * i + 1];
+        sS[q][r][lane] = p2[0] + p2[1];
+    }
+    __syncthreads();
+    // ((S0 + S1) + (S2 + S3)) + bias; thread -> (token, row pair)
+    const int t = tid >> 2, rp = 2 * (tid & 3), tok = tg * kRtTokens + t;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        const int r = rp + i, e = e0 + r;
+        const float v = (sS[0][r][t] + sS[1][r][t]) + (sS[2][r][t] + sS[3][r][t]);
+        if (tok < T && e < nrows) logits[size_t(tok) * logit_stride + e] = (bias && e < kExperts) ? v + bias[e] : v;
+    }
+}
+
 // One wave per (router row, batch of 8 tokens): the choice for small and
 // medium T, where the tiled kernel has too few blocks to fill the chip.
 __global__ __launch_bounds__(256) void router_rows_kernel(const uint16_t* __restrict__ x, int64_t stride, int T,
@@ -202,8 +308,12 @@ hipError_t launch_router(const uint16_t* x, int64_t stride, int T, const uint16_
                      bias, logits, logit_stride, nrows);
         return hipGetLastError();
     }
-    const dim3 grid(kExperts / kRouterTile + (shared_w ? 1 : 0), (T + kRouterTile - 1) / kRouterTile);
-    timed_launch("router", router_kernel, dim3(grid), dim3(256), 0, s, x, stride, T, w, shared_w, bias, logits, logit_stride);
+    const int nrows = kExperts + (shared_w ? 1 : 0);
+    const int ngroups = (nrows + kRtRows - 1) / kRtRows;
+    const int ntg = (T + kRtTokens - 1) / kRtTokens;
+    const int blocks = ((ntg + 7) / 8) * 8 * ngroups;     // token groups padded to a multiple of the 8 XCDs
+    timed_launch("router", router_tokens_kernel, dim3(blocks), dim3(256), 0, s, x, stride, T, w, shared_w, bias, logits,
+                 logit_stride, nrows, ntg);
     return hipGetLastError();
 }
 

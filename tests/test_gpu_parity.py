@@ -253,7 +253,7 @@ def test_shared_tables_bit_exact(device, moe, shared_tables, T):
 # ---------------------------------------------------------------------------
 # Router + softmax/top-8 and the whole layer
 # ---------------------------------------------------------------------------
-@pytest.mark.parametrize('T,biased', [(1, False), (33, False), (64, True)])
+@pytest.mark.parametrize('T,biased', [(1, False), (33, False), (64, True), (300, True), (700, False)])
 def test_router_topk_bit_exact(device, moe, T, biased):
     import torch
     native = _native()
