@@ -380,16 +380,18 @@ __global__ __launch_bounds__(256) void head_argmax_kernel(const float* __restric
 // A (K = 512) stay in LDS while the column blocks are walked.
 //
 // Steps (one 256-group of one column block each) are unrolled, so the
-// register rings have compile-time slots and every load wait is exact, and
-// software-pipelined inside the wave: step st issues the matrix-core dots of
-// step st+1 (accumulators double-buffered) and then runs the fp32 tree of
-// step st on the VALU while they execute.  A moves global -> registers
-// (loaded one step before its store) -> LDS (stored one step before its dots,
-// three stages) -> MFMA.  The step body is instantiated for 1, 2 and 4 row
-// tiles of 16 rows, so partial tiles skip dead row tiles without branches.
+// register rings have compile-time slots and every load wait is exact.  A
+// moves global -> registers (loaded one step before its store) -> LDS
+// (stored two steps before its dots, three stages) -> MFMA; codes are DB
+// steps ahead.  Matrix-core and VALU work of one SIMD do not overlap on
+// gfx950 (measured), so a step runs its dots and then its tree, and the
+// register budget goes to occupancy instead: gate/up holds two blocks per
+// CU, down (one code slot) three.  The step body is instantiated for 1, 2
+// and 4 row tiles of 16 rows, so partial tiles skip dead row tiles without
+// branches.
 // ---------------------------------------------------------------------------
 template <bool GATEUP, int GS, int NSUB, int DB>
-__global__ __launch_bounds__(256, 2) void prefill_mfma_kernel(MfmaArgs a) {
+__global__ __launch_bounds__(256, GATEUP ? 2 : 3) void prefill_mfma_kernel(MfmaArgs a) {
     constexpr int NSTEP = GS * NSUB;
     constexpr int KW = GS * 64;                               // activation words per row
     constexpr int NCB = GATEUP ? (2 * kInter) / kNT : kHidden / (kNT * NSUB);
@@ -509,13 +511,13 @@ __global__ __launch_bounds__(256, 2) void prefill_mfma_kernel(MfmaArgs a) {
             for (int ct = 0; ct < 2; ++ct)
 #pragma unroll
                 for (int r = 0; r < 4; ++r) val[rt][ct][r] = 0.f;
-        i32x4 acc[2][4][2];
-        float swv[2][2], offv[2][2];
+        i32x4 acc[4][2];
+        float swv[2], offv[2];
 
-        // matrix-core dots of step ST into accumulator set ST % 2 for the L
-        // live row tiles (rows past nrows in them hold copies of a live row)
+        // matrix-core dots of step ST for the L live row tiles (rows past
+        // nrows in them hold copies of a live row)
         auto mfma_step = [&]<int ST>() {
-            constexpr int g = ST % GS, stage = g % NSTAGE, bslot = ST % DB, as = ST % 2;
+            constexpr int g = ST % GS, stage = g % NSTAGE, bslot = ST % DB;
 #pragma unroll
             for (int s = 0; s < 4; ++s) {
                 i32x4 fa[4], fb[2];
@@ -534,21 +536,21 @@ __global__ __launch_bounds__(256, 2) void prefill_mfma_kernel(MfmaArgs a) {
                 for (int rt = 0; rt < L; ++rt)
 #pragma unroll
                     for (int ct = 0; ct < 2; ++ct)
-                        acc[as][rt][ct] = __builtin_amdgcn_mfma_i32_16x16x64_i8(
-                            fa[rt], fb[ct], s ? acc[as][rt][ct] : i32x4{0, 0, 0, 0}, 0, 0, 0);
+                        acc[rt][ct] = __builtin_amdgcn_mfma_i32_16x16x64_i8(
+                            fa[rt], fb[ct], s ? acc[rt][ct] : i32x4{0, 0, 0, 0}, 0, 0, 0);
             }
             // the slot's scales are taken before the slot is refilled
 #pragma unroll
             for (int ct = 0; ct < 2; ++ct) {
-                swv[as][ct] = f16_bits_to_f32(uint16_t(bm[bslot][ct] & 0xffffu));
-                offv[as][ct] = f16_bits_to_f32(uint16_t(bm[bslot][ct] >> 16));
+                swv[ct] = f16_bits_to_f32(uint16_t(bm[bslot][ct] & 0xffffu));
+                offv[ct] = f16_bits_to_f32(uint16_t(bm[bslot][ct] >> 16));
             }
             if constexpr (ST + DB < NSTEP) load_b(ST + DB, bslot);
         };
 
         // fp32 group tree of step ST (dense_g256_api.h:35-37), ascending groups
         auto tree_step = [&]<int ST>() {
-            constexpr int g = ST % GS, sub = ST / GS, stage = g % NSTAGE, as = ST % 2;
+            constexpr int g = ST % GS, sub = ST / GS, stage = g % NSTAGE;
 #pragma unroll
             for (int rt = 0; rt < L; ++rt) {
                 const float4 sa4 = *reinterpret_cast<const float4*>(&s_sa[stage][16 * rt + 4 * q]);
@@ -558,9 +560,9 @@ __global__ __launch_bounds__(256, 2) void prefill_mfma_kernel(MfmaArgs a) {
                 for (int r = 0; r < 4; ++r)
 #pragma unroll
                     for (int ct = 0; ct < 2; ++ct) {
-                        const float scaled_dot = sa[r] * float(acc[as][rt][ct][r]);
-                        const float product = swv[as][ct] * scaled_dot;
-                        const float correction = offv[as][ct] * ss[r];
+                        const float scaled_dot = sa[r] * float(acc[rt][ct][r]);
+                        const float product = swv[ct] * scaled_dot;
+                        const float correction = offv[ct] * ss[r];
                         val[rt][ct][r] = val[rt][ct][r] + (product + correction);
                     }
             }
@@ -613,16 +615,15 @@ __global__ __launch_bounds__(256, 2) void prefill_mfma_kernel(MfmaArgs a) {
             }
         };
 
-        mfma_step.template operator()<0>();
         [&]<int... S>(std::integer_sequence<int, S...>) {
             ([&] {
                 constexpr int ST = S;
-                __syncthreads();            // A of step ST+1 visible; stage (ST+2)%3 free
+                __syncthreads();            // A of step ST visible; stage (ST+2)%3 free
                 if constexpr (ST + 2 < GS) {
                     store_a(0, (ST + 2) % NSTAGE);
                     if constexpr (ST + 3 < GS) load_a(ST + 3, 0);
                 }
-                if constexpr (ST + 1 < NSTEP) mfma_step.template operator()<ST + 1>();
+                mfma_step.template operator()<ST>();
                 tree_step.template operator()<ST>();
             }(), ...);
         }(std::make_integer_sequence<int, NSTEP>{});
@@ -641,7 +642,7 @@ hipError_t launch_grouped_mfma(const MfmaArgs& a, bool gateup, int max_tiles, hi
         timed_launch("gateup_mfma", prefill_mfma_kernel<true, kHidden / kGroup, 1, 2>,
                      dim3(max_tiles * ((2 * kInter) / kNT)), dim3(256), 0, s, a);
     else
-        timed_launch("down_mfma", prefill_mfma_kernel<false, kInter / kGroup, kDownSub, 3>,
+        timed_launch("down_mfma", prefill_mfma_kernel<false, kInter / kGroup, kDownSub, 1>,
                      dim3(max_tiles * (kHidden / (kNT * kDownSub))), dim3(256), 0, s, a);
     return hipGetLastError();
 }
