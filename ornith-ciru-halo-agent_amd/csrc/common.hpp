@@ -295,6 +295,98 @@ __device__ __forceinline__ void h128_half(float v[8]) {
     for (int i = 0; i < 8; ++i) v[i] = v[i] * kInvSqrt128;
 }
 
+// ---- Quarter-wave groups: 16 lanes, 16 values per lane ------------------------
+// Lane l (= threadIdx.x & 15) of a 16-lane quarter (one DPP row) holds the 16
+// consecutive values k = quarter_base(l) + i of its 256-group.  Lane bits 0, 1
+// and 3 are k bits 4, 5 and 6, lane bit 2 is k bit 7: every H128 butterfly is
+// in-register (k bits 0..3) or a single DPP lane exchange (xor 1, 2, 8), and
+// the two 128-blocks (k bit 7) never exchange.
+__device__ __forceinline__ int quarter_base(int l) {
+    return 16 * ((l & 3) | (((l >> 3) & 1) << 2) | (((l >> 2) & 1) << 3));
+}
+template <int N> __device__ __forceinline__ float row_ror_f(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x120 + N, 0xF, 0xF, false));
+}
+template <int N> __device__ __forceinline__ int row_ror_i(int v) {
+    return __builtin_amdgcn_update_dpp(0, v, 0x120 + N, 0xF, 0xF, false);
+}
+// Cross-lane butterfly on lane bit M: the lane with the bit clear keeps
+// lo + hi, the other lo - hi.  partner + (+-v), the sign flipped on the upper
+// lane, is exactly both (a + (-b) == a - b in IEEE arithmetic).
+template <int M> __device__ __forceinline__ void h128_quarter_step(float v[16]) {
+    const uint32_t flip = (threadIdx.x & M) ? 0x80000000u : 0u;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) v[i] = xor_perm_f<M>(v[i]) + __uint_as_float(__float_as_uint(v[i]) ^ flip);
+}
+// H128 of both 128-blocks of the quarter's group (butterflies on k bits 0..6
+// in ascending order), then x 1/sqrt(128).
+__device__ __forceinline__ void h128_quarter(float v[16]) {
+#pragma unroll
+    for (int b = 1; b < 16; b <<= 1) {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            if (i & b) continue;
+            const float lo = v[i], hi = v[i + b];
+            v[i] = lo + hi;
+            v[i + b] = lo - hi;
+        }
+    }
+    h128_quarter_step<1>(v);
+    h128_quarter_step<2>(v);
+    h128_quarter_step<8>(v);
+#pragma unroll
+    for (int i = 0; i < 16; ++i) v[i] = v[i] * kInvSqrt128;
+}
+// Group-256 quantisation of a quarter (the recipe of quantize_group_wave).
+// Every lane gets the group's fp16 scale bits and the sum of q; words[0..3]
+// are activation words 2c..2c+3 of its chunks c = quarter_base(l) / 8 + 0, 1.
+template <int QMAX>
+__device__ __forceinline__ void quantize_quarter(float v[16], uint32_t words[4], uint16_t& sbits_out, int& sum_out,
+                                                 uint32_t& flags, uint32_t invalid_flag) {
+    float absmax = 0.f;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        if (!isfinite(v[i])) { flags |= invalid_flag; v[i] = 0.f; }
+        absmax = fmaxf(absmax, fabsf(v[i]));
+    }
+    // lanes i, i-4, i-8, i-12 of the row, then xor 1, 2: all 16 lanes
+    absmax = fmaxf(absmax, row_ror_f<4>(absmax));
+    absmax = fmaxf(absmax, row_ror_f<8>(absmax));
+    absmax = fmaxf(absmax, xor_perm_f<1>(absmax));
+    absmax = fmaxf(absmax, xor_perm_f<2>(absmax));
+    const float raw = fdiv_rn(absmax, float(QMAX));
+    const bool valid = isfinite(raw) && raw <= 65504.f;
+    if (!valid) flags |= invalid_flag;
+    const bool zero = absmax == 0.f || !valid;
+    const uint16_t sbits = f32_to_f16_bits(zero ? 1.f : fmaxf(raw, 0x1p-14f));
+    const float scale = f16_bits_to_f32(sbits);
+    int q[16], sum = 0;
+    const int keep = zero ? 0 : -1;            // scale is 1 when zero: the division is harmless
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        // v is finite and |v / scale| <= QMAX + 1/2 unless the group is zero (scale 1):
+        // round, clamp in float, then convert (always in range)
+        const float qf = fminf(fmaxf(__builtin_rintf(fdiv_rn(v[i], scale)), -float(QMAX)), float(QMAX));
+        const int t = int(qf) & keep;
+        q[i] = t;
+        sum += t;
+    }
+    sum += row_ror_i<4>(sum);
+    sum += row_ror_i<8>(sum);
+    sum += xor_perm_i<1>(sum);
+    sum += xor_perm_i<2>(sum);
+#pragma unroll
+    for (int c = 0; c < 2; ++c) {
+        const int* qc = q + 8 * c;
+        words[2 * c] = (uint32_t(qc[0]) & 255u) | ((uint32_t(qc[2]) & 255u) << 8) | ((uint32_t(qc[4]) & 255u) << 16) |
+                       ((uint32_t(qc[6]) & 255u) << 24);
+        words[2 * c + 1] = (uint32_t(qc[1]) & 255u) | ((uint32_t(qc[3]) & 255u) << 8) |
+                           ((uint32_t(qc[5]) & 255u) << 16) | ((uint32_t(qc[7]) & 255u) << 24);
+    }
+    sbits_out = sbits;
+    sum_out = sum;
+}
+
 // Group quantisation of the half-wave layout (same arithmetic as
 // quantize_group_wave).  Every lane of the half gets the group's fp16 scale
 // bits and Σq; lane l' gets its two activation words 2l' = (q0,q2,q4,q6) and

@@ -677,7 +677,8 @@ __global__ __launch_bounds__(256) void quant_middle_kernel(const float* __restri
     flag_or(sticky, flags);
 }
 
-// Same over middle rows in permuted route order: rows 0 .. *nrows - 1.
+// Same over middle rows in permuted route order: rows 0 .. *nrows - 1, on
+// quarter-wave groups (common.hpp), four groups (two rows) per wave.
 template <int QMAX>
 __global__ __launch_bounds__(256) void quant_middle_permuted_kernel(const float* __restrict__ middle, int RS,
                                                                     const int32_t* __restrict__ nrows,
@@ -685,21 +686,37 @@ __global__ __launch_bounds__(256) void quant_middle_permuted_kernel(const float*
                                                                     uint16_t* __restrict__ scales,
                                                                     int32_t* __restrict__ sums, uint32_t* sticky) {
     const int wave = blockIdx.x * 4 + (threadIdx.x >> 6);
-    if (wave >= RS * 2 || (wave >> 1) >= nrows[0]) return;
-    const int lane = threadIdx.x & 63, row = wave >> 1, group = wave & 1;
-    const float4 m4 = *reinterpret_cast<const float4*>(middle + size_t(row) * kInter + group * kGroup + lane * 4);
-    float v[4] = {m4.x, m4.y, m4.z, m4.w};
-    uint32_t flags = 0;
-    h128_wave(v);
+    const int lane = threadIdx.x & 63, l = lane & 15;
+    const int total = min(nrows[0], RS) * 2;                  // two groups per 512-wide row
+    if (4 * wave >= total) return;
+    const int g = 4 * wave + (lane >> 4), k0 = quarter_base(l);
+    const float* src = middle + size_t(min(g, total - 1)) * kGroup + k0;   // row g / 2, group g % 2
+    float v[16];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) if (!isfinite(v[i])) flags |= kFlagNonfiniteInput;
-    quantize_group_wave<QMAX>(v, words + size_t(wave) * 64, scales + wave, sums + wave, flags, kFlagInvalidActivation);
+    for (int i = 0; i < 4; ++i) {
+        const float4 m = *reinterpret_cast<const float4*>(src + 4 * i);
+        v[4 * i] = m.x; v[4 * i + 1] = m.y; v[4 * i + 2] = m.z; v[4 * i + 3] = m.w;
+    }
+    uint32_t flags = 0;
+    h128_quarter(v);
+#pragma unroll
+    for (int e = 0; e < 16; ++e) if (!isfinite(v[e])) flags |= kFlagNonfiniteInput;
+    uint32_t w4[4];
+    uint16_t sbits;
+    int sum;
+    quantize_quarter<QMAX>(v, w4, sbits, sum, flags, kFlagInvalidActivation);
+    if (g < total) {
+        *reinterpret_cast<uint4*>(words + size_t(g) * 64 + k0 / 4) = make_uint4(w4[0], w4[1], w4[2], w4[3]);
+        if (l == 0) { scales[g] = sbits; sums[g] = sum; }
+    } else {
+        flags = 0;
+    }
     flag_or(sticky, flags);
 }
 
 hipError_t launch_quant_middle_permuted(const float* middle, int RS, const int32_t* nrows, int qmax, uint32_t* words,
                                         uint16_t* scales, int32_t* sums, uint32_t* sticky, hipStream_t s) {
-    const int waves = RS * 2;
+    const int waves = (RS * 2 + 3) / 4;
     if (qmax == 127)
         timed_launch("quant_middle", quant_middle_permuted_kernel<127>, dim3((waves + 3) / 4), dim3(256), 0, s, middle, RS, nrows, words, scales, sums, sticky);
     else
