@@ -499,8 +499,11 @@ hipError_t launch_permute(const int32_t* ids, int R, int T, bool with_shared, co
 
 // ---------------------------------------------------------------------------
 // Unpermute: slot-order reduction (routed_storage_n32_consumer.cpp:176-184,
-// 296-307).  Four columns per thread.
+// 296-307).
 // ---------------------------------------------------------------------------
+// Eight columns per thread; every slot's row is loaded unconditionally (rows
+// of slots without a live id hold stale data and are dropped by the select),
+// so all 18 row loads of a thread are in flight together.
 __global__ __launch_bounds__(256) void reduce_kernel(const float* __restrict__ route_out,
                                                      const float* __restrict__ weights,
                                                      const int32_t* __restrict__ ids, int T,
@@ -509,48 +512,72 @@ __global__ __launch_bounds__(256) void reduce_kernel(const float* __restrict__ r
                                                      const uint16_t* __restrict__ sigmoid_table,
                                                      uint16_t* __restrict__ shared_out, uint16_t* __restrict__ layer_out,
                                                      uint32_t* sticky) {
-    const size_t idx = size_t(blockIdx.x) * 256 + threadIdx.x;   // over T * H/4
-    if (idx >= size_t(T) * (kHidden / 4)) return;
-    const int t = int(idx / (kHidden / 4));
-    const int c = int(idx % (kHidden / 4)) * 4;
-    float sum[4] = {0.f, 0.f, 0.f, 0.f};
+    constexpr int kCols = 8, kThreadsPerToken = kHidden / kCols;
+    const size_t idx = size_t(blockIdx.x) * 256 + threadIdx.x;   // over T * H/8
+    if (idx >= size_t(T) * kThreadsPerToken) return;
+    const int t = int(idx / kThreadsPerToken);
+    const int c = int(idx % kThreadsPerToken) * kCols;
+    int idv[kTop];
+    float wv[kTop];
+#pragma unroll
+    for (int s = 0; s < kTop; ++s) { idv[s] = ids[t * kTop + s]; wv[s] = weights[t * kTop + s]; }
+    float4 rv[kTop][2];
 #pragma unroll
     for (int s = 0; s < kTop; ++s) {
-        const int r = t * kTop + s;
-        const int id = ids[r];
-        if (id >= 0 && id < kExperts) {
-            const float w = weights[r];
-            const float4 v = *reinterpret_cast<const float4*>(route_out + size_t(r) * kHidden + c);
-            sum[0] = sum[0] + v.x * w; sum[1] = sum[1] + v.y * w;
-            sum[2] = sum[2] + v.z * w; sum[3] = sum[3] + v.w * w;
-        }
+        const float* row = route_out + size_t(t * kTop + s) * kHidden + c;
+        rv[s][0] = *reinterpret_cast<const float4*>(row);
+        rv[s][1] = *reinterpret_cast<const float4*>(row + 4);
+    }
+    const bool shared = sigmoid_table != nullptr;
+    float4 sh[2] = {};
+    float gate = 0.f;
+    if (shared) {
+        const float* row = route_out + size_t(T * kTop + t) * kHidden + c;
+        sh[0] = *reinterpret_cast<const float4*>(row);
+        sh[1] = *reinterpret_cast<const float4*>(row + 4);
+        gate = bf16_bits_to_f32(sigmoid_table[shared_logit[t]]);
+    }
+    // slot-order fp32 sum (routed_storage_n32_consumer.cpp:176-184)
+    float sum[kCols];
+#pragma unroll
+    for (int i = 0; i < kCols; ++i) sum[i] = 0.f;
+#pragma unroll
+    for (int s = 0; s < kTop; ++s) {
+        const bool live = idv[s] >= 0 && idv[s] < kExperts;
+        const float v[kCols] = {rv[s][0].x, rv[s][0].y, rv[s][0].z, rv[s][0].w,
+                                rv[s][1].x, rv[s][1].y, rv[s][1].z, rv[s][1].w};
+#pragma unroll
+        for (int i = 0; i < kCols; ++i) sum[i] = live ? sum[i] + v[i] * wv[s] : sum[i];
     }
     uint32_t flags = 0;
-    uint16_t o[4];
+    uint16_t o[kCols];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
+    for (int i = 0; i < kCols; ++i) {
         o[i] = f32_to_bf16_bits(sum[i]);
         if (!isfinite(sum[i]) || (o[i] & 0x7f80u) == 0x7f80u) flags |= kFlagNonfiniteOutput;
     }
+    auto pack = [](const uint16_t h[kCols]) {
+        return make_uint4(h[0] | (uint32_t(h[1]) << 16), h[2] | (uint32_t(h[3]) << 16), h[4] | (uint32_t(h[5]) << 16),
+                          h[6] | (uint32_t(h[7]) << 16));
+    };
     const size_t base = size_t(t) * kHidden + c;
-    if (final_f32) *reinterpret_cast<float4*>(final_f32 + base) = make_float4(sum[0], sum[1], sum[2], sum[3]);
-    if (out) *reinterpret_cast<uint2*>(out + base) = make_uint2(o[0] | (uint32_t(o[1]) << 16), o[2] | (uint32_t(o[3]) << 16));
-    if (sigmoid_table) {
-        const int R = T * kTop;
-        const float gate = bf16_bits_to_f32(sigmoid_table[shared_logit[t]]);
-        const float4 v = *reinterpret_cast<const float4*>(route_out + size_t(R + t) * kHidden + c);
-        const float sv[4] = {v.x * gate, v.y * gate, v.z * gate, v.w * gate};
-        uint16_t so[4], lo[4];
+    if (final_f32) {
+        *reinterpret_cast<float4*>(final_f32 + base) = make_float4(sum[0], sum[1], sum[2], sum[3]);
+        *reinterpret_cast<float4*>(final_f32 + base + 4) = make_float4(sum[4], sum[5], sum[6], sum[7]);
+    }
+    if (out) *reinterpret_cast<uint4*>(out + base) = pack(o);
+    if (shared) {
+        const float sv[kCols] = {sh[0].x * gate, sh[0].y * gate, sh[0].z * gate, sh[0].w * gate,
+                                 sh[1].x * gate, sh[1].y * gate, sh[1].z * gate, sh[1].w * gate};
+        uint16_t so[kCols], lo[kCols];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
+        for (int i = 0; i < kCols; ++i) {
             if (!isfinite(sv[i])) flags |= kFlagNonfiniteOutput;
             so[i] = f32_to_bf16_bits(sv[i]);
             lo[i] = f32_to_bf16_bits(bf16_bits_to_f32(o[i]) + bf16_bits_to_f32(so[i]));
         }
-        if (shared_out)
-            *reinterpret_cast<uint2*>(shared_out + base) = make_uint2(so[0] | (uint32_t(so[1]) << 16), so[2] | (uint32_t(so[3]) << 16));
-        if (layer_out)
-            *reinterpret_cast<uint2*>(layer_out + base) = make_uint2(lo[0] | (uint32_t(lo[1]) << 16), lo[2] | (uint32_t(lo[3]) << 16));
+        if (shared_out) *reinterpret_cast<uint4*>(shared_out + base) = pack(so);
+        if (layer_out) *reinterpret_cast<uint4*>(layer_out + base) = pack(lo);
     }
     flag_or(sticky, flags);
 }
@@ -558,7 +585,7 @@ __global__ __launch_bounds__(256) void reduce_kernel(const float* __restrict__ r
 hipError_t launch_reduce(const float* route_out, const float* weights, const int32_t* ids, int T, float* final_f32,
                          uint16_t* out, const uint16_t* shared_logit, const uint16_t* sigmoid_table,
                          uint16_t* shared_out, uint16_t* layer_out, uint32_t* sticky, hipStream_t s) {
-    const size_t n = size_t(T) * (kHidden / 4);
+    const size_t n = size_t(T) * (kHidden / 8);
     timed_launch("reduce", reduce_kernel, dim3((n + 255) / 256), dim3(256), 0, s, route_out, weights, ids, T, final_f32, out, shared_logit,
                                                   sigmoid_table, shared_out, layer_out, sticky);
     return hipGetLastError();
