@@ -416,41 +416,83 @@ __global__ __launch_bounds__(kPermBlock) void permute_count_kernel(const int32_t
     for (int i = threadIdx.x; i < kBanks; i += kPermBlock) block_counts[size_t(blockIdx.x) * kBanks + i] = cnt[i];
 }
 
-// Single block of 512 threads: per-bank exclusive running sums over blocks,
-// offsets, segments and the MFMA tile list.
-__global__ __launch_bounds__(512) void permute_scan_kernel(int nblocks, int32_t* __restrict__ block_counts,
-                                                           int32_t* __restrict__ counts, int32_t* __restrict__ offsets,
-                                                           Segment* __restrict__ segments, int32_t* __restrict__ meta,
-                                                           Segment* __restrict__ tiles, int mfma_rows) {
-    __shared__ int a[512], b[512], c[512];
-    const int e = threadIdx.x;
-    int total = 0;
-    if (e < kBanks) {
-        // 16 independent loads in flight, then the running exclusive sums
-        for (int b0 = 0; b0 < nblocks; b0 += 16) {
-            int v[16];
+// Single block of 256 x parts threads (2..4 parts): per-bank exclusive running
+// sums over blocks, offsets, segments and the MFMA tile list.  Thread (part,
+// bank) takes 1/parts of the blocks of banks 0..255 (its loads all in flight,
+// the part sums meet in LDS; a second pass writes the running sums).  Bank 256 (the shared
+// expert) is one count per block: thread b loads block b's, and a block-wide
+// scan in LDS gives the running sums.
+constexpr int kScanParts = 4;
+constexpr int kScanMaxPerPart = 72;          // 4 x 72 blocks x 256 routes >= 8192 tokens x 9 routes
+
+__global__ __launch_bounds__(1024) void permute_scan_kernel(int nblocks, int32_t* __restrict__ block_counts,
+                                                            int32_t* __restrict__ counts, int32_t* __restrict__ offsets,
+                                                            Segment* __restrict__ segments, int32_t* __restrict__ meta,
+                                                            Segment* __restrict__ tiles, int mfma_rows) {
+    __shared__ int part_sum[kScanParts][kExperts];
+    __shared__ int a[512], b[512], c[512], d[512];
+    __shared__ int total256;
+    const int tid = threadIdx.x, parts = int(blockDim.x) >> 8;
+    const int per = (nblocks + parts - 1) / parts;
+    const int pt = tid >> 8, bk = tid & 255, lo = pt * per;
+    const int x256 = tid < nblocks ? block_counts[size_t(tid) * kBanks + kExperts] : 0;
+    // counts of this part, 24 loads in flight per round
+    constexpr int kChunk = 24;
+    int qsum = 0;
+    for (int c0 = 0; c0 < per; c0 += kChunk) {
+        int v[kChunk];
 #pragma unroll
-            for (int i = 0; i < 16; ++i) v[i] = b0 + i < nblocks ? block_counts[size_t(b0 + i) * kBanks + e] : 0;
+        for (int i = 0; i < kChunk; ++i)
+            v[i] = (c0 + i < per && lo + c0 + i < nblocks) ? block_counts[size_t(lo + c0 + i) * kBanks + bk] : 0;
 #pragma unroll
-            for (int i = 0; i < 16; ++i) {
-                if (b0 + i < nblocks) block_counts[size_t(b0 + i) * kBanks + e] = total;
-                total += v[i];
+        for (int i = 0; i < kChunk; ++i) qsum += v[i];
+    }
+    if (tid == 0) total256 = 0;
+    __syncthreads();
+    part_sum[pt][bk] = qsum;
+    if (tid < 512) d[tid] = x256;              // scanned with a, b, c below
+    if (x256) atomicAdd(&total256, x256);
+    __syncthreads();
+    {
+        int run = 0;
+        for (int i = 0; i < pt; ++i) run += part_sum[i][bk];
+        for (int c0 = 0; c0 < per; c0 += kChunk) {
+            int v[kChunk];
+#pragma unroll
+            for (int i = 0; i < kChunk; ++i)
+                v[i] = (c0 + i < per && lo + c0 + i < nblocks) ? block_counts[size_t(lo + c0 + i) * kBanks + bk] : 0;
+#pragma unroll
+            for (int i = 0; i < kChunk; ++i) {
+                if (c0 + i < per && lo + c0 + i < nblocks) block_counts[size_t(lo + c0 + i) * kBanks + bk] = run;
+                run += v[i];
             }
         }
-        counts[e] = total;
     }
+    const int e = tid;
+    int total = 0;
+    if (e < kExperts) {
+        for (int i = 0; i < parts; ++i) total += part_sum[i][e];
+    } else if (e == kExperts) {
+        total = total256;
+    }
+    if (e < kBanks) counts[e] = total;
     const int ntile = (e < kBanks && total > 0) ? (total + mfma_rows - 1) / mfma_rows : 0;
-    a[e] = e < kBanks ? total : 0;
-    b[e] = (e < kBanks && total > 0) ? 1 : 0;
-    c[e] = ntile;
+    if (e < 512) {
+        a[e] = e < kBanks ? total : 0;
+        b[e] = (e < kBanks && total > 0) ? 1 : 0;
+        c[e] = ntile;
+    }
     __syncthreads();
-    // inclusive Hillis-Steele scans of counts, non-empty flags and tile counts
-    for (int d = 1; d < 512; d <<= 1) {
-        const int va = e >= d ? a[e - d] : 0, vb = e >= d ? b[e - d] : 0, vc = e >= d ? c[e - d] : 0;
+    // inclusive Hillis-Steele scans of counts, non-empty flags, tile counts and
+    // the shared bank's per-block counts
+    for (int dd = 1; dd < 512; dd <<= 1) {
+        int va = 0, vb = 0, vc = 0, vd = 0;
+        if (e < 512 && e >= dd) { va = a[e - dd]; vb = b[e - dd]; vc = c[e - dd]; vd = d[e - dd]; }
         __syncthreads();
-        a[e] += va; b[e] += vb; c[e] += vc;
+        if (e < 512) { a[e] += va; b[e] += vb; c[e] += vc; d[e] += vd; }
         __syncthreads();
     }
+    if (e < nblocks) block_counts[size_t(e) * kBanks + kExperts] = d[e] - x256;
     if (e < kBanks) {
         const int off = a[e] - total;
         offsets[e] = off;
@@ -486,10 +528,12 @@ hipError_t launch_permute(const int32_t* ids, int R, int T, bool with_shared, co
                           uint32_t* sticky, int mfma_rows, hipStream_t s) {
     const int Rall = R + (with_shared ? T : 0);
     const int nblocks = (Rall + kPermBlock - 1) / kPermBlock;
+    if (nblocks > kScanParts * kScanMaxPerPart) return hipErrorInvalidValue;
+    const int scan_parts = max(2, (nblocks + kScanMaxPerPart - 1) / kScanMaxPerPart);
     timed_launch("permute_count", permute_count_kernel, dim3(nblocks), dim3(kPermBlock), 0, s, ids, R, Rall, p.block_counts, sticky);
     hipError_t st = hipGetLastError();
     if (st != hipSuccess) return st;
-    timed_launch("permute_scan", permute_scan_kernel, dim3(1), dim3(512), 0, s, nblocks, p.block_counts, p.counts, p.offsets, p.segments, p.meta, p.tiles,
+    timed_launch("permute_scan", permute_scan_kernel, dim3(1), dim3(256 * scan_parts), 0, s, nblocks, p.block_counts, p.counts, p.offsets, p.segments, p.meta, p.tiles,
                                           mfma_rows);
     st = hipGetLastError();
     if (st != hipSuccess) return st;
