@@ -27,6 +27,15 @@ namespace ornith {
 
 constexpr int kSlots = kTop + 1;
 
+// Blocks 2m and 2m+1 of a kernel read the two 64-byte halves of the same
+// 128-byte code rows.  Workgroups go to the 8 XCDs round-robin, so linear
+// block L = 16q + 8h + x is mapped to pair 8q + x, half h: both halves of a
+// row then come through one XCD's L2 and each row is fetched once.
+__device__ __forceinline__ int xcd_paired_block(int L) {
+    const int x = L & 7, h = (L >> 3) & 1, q = L >> 4;
+    return 2 * (8 * q + x) + h;
+}
+
 // ---------------------------------------------------------------------------
 template <bool ROUTER, bool SHARED, int QMAX>
 __global__ __launch_bounds__(64) void decode1_route_kernel(DecodeArgs a) {
@@ -111,7 +120,8 @@ __global__ __launch_bounds__(256) void decode1_gateup_kernel(DecodeArgs a) {
     __shared__ float lterm[8][32];
     __shared__ int s_bank;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int s = blockIdx.x, p = blockIdx.y;
+    // (slot, column pair) from the XCD-paired block index: 32 blocks per slot
+    const int bi = xcd_paired_block(int(blockIdx.x)), s = bi >> 5, p = bi & 31;
     const bool shared = SHARED && s == kTop;
     // activations of the token: no dependency, issue first
     const uint32_t a0 = a.x_words[tid], a1 = a.x_words[256 + tid];
@@ -215,7 +225,7 @@ __global__ __launch_bounds__(576) void decode1_down_kernel(DecodeArgs a) {
     __shared__ float lro[kSlots][16];
     __shared__ int lbank[kSlots];
     __shared__ float lw8[kTop];
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, c = blockIdx.x;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, c = xcd_paired_block(int(blockIdx.x));
     const int nslots = SHARED ? kSlots : kTop;
     // Every load below is unconditional (unused lanes read a valid address and
     // drop the value), so the in-order load counter stays exact and each wait
@@ -324,7 +334,7 @@ static hipError_t run1(const DecodeArgs& a, hipStream_t s) {
     timed_launch("route1", decode1_route_kernel<ROUTER, SHARED, QMAX>, dim3(waves), dim3(64), 0, s, a);
     hipError_t st = hipGetLastError();
     if (st != hipSuccess) return st;
-    timed_launch("gateup1", decode1_gateup_kernel<ROUTER, SHARED>, dim3(SHARED ? kSlots : kTop, kInter / 16), dim3(256), 0, s, a);
+    timed_launch("gateup1", decode1_gateup_kernel<ROUTER, SHARED>, dim3((SHARED ? kSlots : kTop) * (kInter / 16)), dim3(256), 0, s, a);
     st = hipGetLastError();
     if (st != hipSuccess) return st;
     timed_launch("down1", decode1_down_kernel<SHARED, QMAX>, dim3(kHidden / 16), dim3(64 * kSlots), 0, s, a);
