@@ -87,6 +87,8 @@ hipError_t run_routed(const RoutedPlan& p, void* ws, const void* input, const fl
     a.out = at<float>(ws, p.l.middle);
     a.silu_table = silu;
     a.sticky = sticky;
+    // above 2048 tokens nearly every tile is full: keep each tile on one XCD
+    a.tile_xcd = T > 2048 ? 1 : 0;
     TRY(launch_grouped_mfma(a, true, max_tiles, s));
     auto dw = at<uint32_t>(ws, p.l.down_low);
     auto dsc = at<uint16_t>(ws, p.l.down_scales);
@@ -102,6 +104,7 @@ hipError_t run_routed(const RoutedPlan& p, void* ws, const void* input, const fl
     a.bank_meta_words = kDownBankMeta;
     a.act_words = dw; a.act_scales = dsc; a.act_sums = dsum;
     a.K = kInter;
+    a.tile_xcd = 0;
     a.out = at<float>(ws, p.l.route_out);
     TRY(launch_grouped_mfma(a, false, max_tiles, s));
     return launch_reduce(at<float>(ws, p.l.route_out), weights, ids, T, out ? at<float>(ws, p.l.final_f32) : nullptr,

@@ -379,7 +379,8 @@ size_t permute_scratch_bytes(int Rcap, int Tcap) {
     bytes += align256(rall * 4);
     bytes += align256(kBanks * sizeof(Segment));
     bytes += align256(4 * 4);
-    bytes += align256((rall / 64 + kBanks + 2) * sizeof(Segment));   // one per 64-route m-tile
+    // one per 64-route m-tile, plus the launch's rounding up to a multiple of 8 tiles
+    bytes += align256((rall / 64 + kBanks + 10) * sizeof(Segment));
     return bytes;
 }
 
@@ -395,7 +396,7 @@ PermuteScratch carve_permute(void* base, int Rcap, int Tcap) {
     p.routes = static_cast<int32_t*>(take(rall * 4));
     p.segments = static_cast<Segment*>(take(kBanks * sizeof(Segment)));
     p.meta = static_cast<int32_t*>(take(4 * 4));
-    p.tiles = static_cast<Segment*>(take((rall / 64 + kBanks + 2) * sizeof(Segment)));
+    p.tiles = static_cast<Segment*>(take((rall / 64 + kBanks + 10) * sizeof(Segment)));
     return p;
 }
 
