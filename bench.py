@@ -44,13 +44,20 @@ ROUTER_BYTES = 256 * 2048 * 2 + 2048 * 2
 HEAD_N, HEAD_ROWS = 151936, 32
 DENSE_N = 6144
 
-# HBM bytes per launch from rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE runs, scaled
-# by the factor a plain copy of known size reads (bench.py --copy-calibration);
-# keyed by (kernel, tokens).  Commands and raw figures:
-# profiles/decode_n1_n32_hbm_traffic_pmc.md.
+# HBM bytes per launch (L2 misses: FETCH_SIZE + WRITE_SIZE) from rocprofv3
+# --pmc runs, scaled by the factor a plain copy of known size reads (bench.py
+# --copy-calibration); keyed by (kernel, tokens).  Commands and raw figures:
+# profiles/decode_n1_n32_hbm_traffic_pmc.md, profiles/prefill_1120_8192_hbm_traffic_pmc.md.
 MEASURED_TRAFFIC = {
-    ('route1', 1): 1146865, ('gateup1', 1): 9974418, ('down1', 1): 5194676,
-    ('route', 32): 2442863, ('gateup', 32): 179054858, ('down', 32): 99312378,
+    ('route1', 1): 1162628, ('gateup1', 1): 9961807, ('down1', 1): 5125852,
+    ('route', 32): 2583516, ('topk', 32): 134473, ('sort', 32): 12783, ('gateup', 32): 176480764,
+    ('quant_middle', 32): 800766, ('down', 32): 90912586, ('reduce', 32): 2593294,
+    ('router', 1120): 14734302, ('topk', 1120): 1361783, ('act', 1120): 7040551,
+    ('gateup_mfma', 1120): 189109402, ('quant_middle', 1120): 26013078, ('down_mfma', 1120): 169427858,
+    ('reduce', 1120): 87585722,
+    ('router', 8192): 50978750, ('topk', 8192): 9338227, ('act', 8192): 50827495,
+    ('gateup_mfma', 8192): 623747520, ('quant_middle', 8192): 189703981, ('down_mfma', 8192): 844292265,
+    ('reduce', 8192): 639972559,
 }
 
 
