@@ -9,11 +9,15 @@
 //                              (and, for the shared slot, the weights) start
 //                              at once; routed blocks derive their expert
 //                              with an in-block softmax/top-8 of the 257
-//                              logits.  Codes go straight to registers.
+//                              logits (threshold + rank count, topk.hpp).
+//                              Codes go straight to registers.  The middle
+//                              row leaves with the first four H128
+//                              butterflies of the down input applied.
 //   D3 decode1_down_kernel     block = 16 output columns over all slots (128
-//                              blocks, one wave per slot): H128 + A8 of the
-//                              slot's middle row, exact dots, fp32 tree and
-//                              the slot-order reduction.
+//                              blocks, one wave per slot): the last three
+//                              H128 butterflies + A8 of the slot's middle
+//                              row, exact dots, fp32 tree and the
+//                              slot-order reduction.
 //
 // One token has no expert reuse, so slots are processed as they come (no
 // permutation); a slot repeated by the caller simply loads its weights twice.
@@ -113,12 +117,16 @@ __global__ __launch_bounds__(64) void decode1_route_kernel(DecodeArgs a) {
 // columns 512+16p.. over all 8 groups.  Thread (n, g): local column n (0..15
 // gate, 16..31 up), group g; it loads its 32 code words (stride 32, so each
 // half-wave reads two contiguous 64-byte runs) straight into registers.
+// Wave 0 finishes the 16 middle values and applies the H128 butterflies on
+// k bits 0..3 (the 16 values of a block are one run of k), so the consumer
+// only does k bits 4..6; the order of the butterflies is unchanged.
 template <bool ROUTER, bool SHARED>
 __global__ __launch_bounds__(256) void decode1_gateup_kernel(DecodeArgs a) {
     __shared__ __align__(16) uint32_t la[8 * 64];
     __shared__ float lsa[8], lss[8];
     __shared__ float lterm[8][32];
-    __shared__ int s_bank;
+    __shared__ __align__(16) uint64_t s_cand[65];
+    __shared__ uint2 s_sel[kTop];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     // (slot, column pair) from the XCD-paired block index: 32 blocks per slot
     const int bi = xcd_paired_block(int(blockIdx.x)), s = bi >> 5, p = bi & 31;
@@ -134,21 +142,24 @@ __global__ __launch_bounds__(256) void decode1_gateup_kernel(DecodeArgs a) {
                 float v[4];
 #pragma unroll
                 for (int i = 0; i < 4; ++i) v[i] = a.logits[lane + 64 * i];
-                float wv;
-                int iv, i8[kTop];
-                softmax_top8(v, wv, iv, i8);
-                int mine = i8[0];
+                uint32_t k[4];
+                softmax_keys(v, k);
+                top8_rank_lds(k, s_cand, s_sel);
+                if (s == 0 && p == 0) {
+                    // slot weights renormalised by the slot-order sum of the picks
+                    float tot = 0.f;
 #pragma unroll
-                for (int j = 1; j < kTop; ++j) if (s == j) mine = i8[j];
-                if (lane == 0) s_bank = mine;
-                if (s == 0 && p == 0 && lane < kTop) {
-                    a.topk_w[lane] = wv;
-                    a.topk_ids[lane] = iv;
+                    for (int j = 0; j < kTop; ++j) tot = tot + __uint_as_float(s_sel[j].x);
+                    if (lane < kTop) {
+                        const uint2 pick = s_sel[lane];
+                        a.topk_w[lane] = fdiv_rn(__uint_as_float(pick.x), tot);
+                        a.topk_ids[lane] = int(pick.y);
+                    }
+                    if (SHARED && lane == 0) a.shared_logit[0] = f32_to_bf16_bits(a.logits[kExperts]);
                 }
-                if (SHARED && s == 0 && p == 0 && lane == 0) a.shared_logit[0] = f32_to_bf16_bits(a.logits[kExperts]);
             }
             __syncthreads();
-            bank = s_bank;
+            bank = int(s_sel[s].y);
         } else {
             bank = a.ids_in[s];
             if (bank < 0 || bank >= kExperts) {
@@ -187,13 +198,15 @@ __global__ __launch_bounds__(256) void decode1_gateup_kernel(DecodeArgs a) {
     }
     lterm[g][n] = tree_term(dot, lsa[g], lss[g], mw);
     __syncthreads();
-    if (tid < 16) {
+    if (wave == 0) {
+        // lanes 16..63 repeat lanes 0..15 so the butterflies see a full row
+        const int c = lane & 15;
         uint32_t flags = 0;
         float vg = 0.f, vu = 0.f;
 #pragma unroll
-        for (int gg = 0; gg < 8; ++gg) vg = vg + lterm[gg][tid];
+        for (int gg = 0; gg < 8; ++gg) vg = vg + lterm[gg][c];
 #pragma unroll
-        for (int gg = 0; gg < 8; ++gg) vu = vu + lterm[gg][16 + tid];
+        for (int gg = 0; gg < 8; ++gg) vu = vu + lterm[gg][16 + c];
         float mid;
         if (shared) {
             vg = bf16_round(vg);
@@ -205,15 +218,24 @@ __global__ __launch_bounds__(256) void decode1_gateup_kernel(DecodeArgs a) {
             mid = silu_portable(vg) * vu;
         }
         if (!isfinite(mid)) flags |= kFlagNonfiniteMiddle | kFlagNonfiniteInput;
-        a.middle[size_t(s) * kInter + p * 16 + tid] = mid;
-        flag_or(a.sticky, flags);
+        // the first four H128 butterflies of the down input (k bits 0..3 =
+        // column bits 0..3 = lane bits 0..3), in ascending order
+        mid = butterfly_lane<1>(mid);
+        mid = butterfly_lane<2>(mid);
+        mid = butterfly_lane<4>(mid);
+        mid = butterfly_lane<8>(mid);
+        if (lane < 16) {
+            a.middle[size_t(s) * kInter + p * 16 + lane] = mid;
+            flag_or(a.sticky, flags);
+        }
     }
 }
 
 // ---------------------------------------------------------------------------
 // D3: block = 16 output columns over all slots (9 waves).  Wave w quantises
-// slot w's middle row (H128 + A8/A4 of both groups, half-wave layout) while
-// every thread's down-code loads are in flight.  Thread: (slot i, group g) =
+// slot w's middle row (H128 butterflies on k bits 4..6 + A8/A4 of both
+// groups, half-wave layout with chunk half_chunk(lane & 31)) while every
+// thread's down-code loads are in flight.  Thread: (slot i, group g) =
 // tid / 64 and lane / 32, chunk half h = (lane / 16) & 1, column n = lane & 15,
 // 16 code words in registers; the two halves' integer dots are added exactly,
 // the two groups' terms meet through xor 32, and the slots are reduced in
@@ -235,8 +257,8 @@ __global__ __launch_bounds__(576) void decode1_down_kernel(DecodeArgs a) {
     const int id_in = a.reduce_ids[tid & 7];
     const float w_in = a.reduce_w[tid & 7];
     __builtin_amdgcn_sched_barrier(0);                 // keep the routing loads oldest
-    const int lp = lane & 31, gm = lane >> 5;
-    const float* mrow = a.middle + size_t(wave < nslots ? wave : nslots - 1) * kInter + gm * kGroup + lp * 8;
+    const int lp = lane & 31, gm = lane >> 5, ch = half_chunk(lp);
+    const float* mrow = a.middle + size_t(wave < nslots ? wave : nslots - 1) * kInter + gm * kGroup + ch * 8;
     const float4 m0 = *reinterpret_cast<const float4*>(mrow);
     const float4 m1 = *reinterpret_cast<const float4*>(mrow + 4);
     const uint16_t shared_logit = SHARED ? a.shared_logit[0] : 0;
@@ -264,14 +286,13 @@ __global__ __launch_bounds__(576) void decode1_down_kernel(DecodeArgs a) {
     uint32_t flags = 0;
     if (bank >= 0) {
         float v[8] = {m0.x, m0.y, m0.z, m0.w, m1.x, m1.y, m1.z, m1.w};
-        h128_half(v);
-#pragma unroll
-        for (int e = 0; e < 8; ++e) if (!isfinite(v[e])) flags |= kFlagNonfiniteInput;
+        h128_tail_half(v);
         uint32_t w2[2];
         uint16_t sb;
         int sum;
-        quantize_half<QMAX>(v, w2, sb, sum, flags, kFlagInvalidActivation);
-        *reinterpret_cast<uint2*>(&la[(2 * i + gm) * 64 + 2 * lp]) = make_uint2(w2[0], w2[1]);
+        quantize_half_fast<QMAX>(v, w2, sb, sum, flags, kFlagNonfiniteInput | kFlagInvalidActivation,
+                                 kFlagInvalidActivation);
+        *reinterpret_cast<uint2*>(&la[(2 * i + gm) * 64 + 2 * ch]) = make_uint2(w2[0], w2[1]);
         if (lp == 0) {
             const float sc = f16_bits_to_f32(sb);
             lsa[2 * i + gm] = sc;
@@ -307,10 +328,21 @@ __global__ __launch_bounds__(576) void decode1_down_kernel(DecodeArgs a) {
     __syncthreads();
     if (tid < 16) {
         const int col = c * 16 + tid;
+        // every LDS read first, then the slot-order sum over live slots
+        int lb8[kTop];
+        float ro[kTop], w8[kTop];
+#pragma unroll
+        for (int sl = 0; sl < kTop; ++sl) {
+            lb8[sl] = lbank[sl];
+            ro[sl] = lro[sl][tid];
+            w8[sl] = lw8[sl];
+        }
         float sum = 0.f;
 #pragma unroll
-        for (int sl = 0; sl < kTop; ++sl)
-            if (lbank[sl] >= 0) sum = sum + lro[sl][tid] * lw8[sl];
+        for (int sl = 0; sl < kTop; ++sl) {
+            const float t = sum + ro[sl] * w8[sl];
+            sum = lb8[sl] >= 0 ? t : sum;
+        }
         const uint16_t o = f32_to_bf16_bits(sum);
         if (!isfinite(sum) || (o & 0x7f80u) == 0x7f80u) flags |= kFlagNonfiniteOutput;
         if (a.final_f32) a.final_f32[col] = sum;

@@ -318,7 +318,8 @@ hipError_t launch_router(const uint16_t* x, int64_t stride, int T, const uint16_
 }
 
 // ---------------------------------------------------------------------------
-// Softmax / top-8 / renormalise, one wave per token (topk.hpp).  Declared
+// Softmax / top-8 / renormalise, one wave per token (topk.hpp: threshold and
+// rank count, LDS scratch per wave).  Declared
 // order: m = max; e = pexp(l - m); s = butterfly (masks 1..32) over lanes of
 // ((e[l] + e[l+64]) + e[l+128]) + e[l+192]; p = e / s; the eight largest p
 // (ties to the lower id) in descending order; weights p / (slot-order sum of
@@ -328,18 +329,24 @@ __global__ __launch_bounds__(256) void topk_kernel(const float* __restrict__ log
                                                    float* __restrict__ weights, int32_t* __restrict__ ids,
                                                    const float* __restrict__ shared_logit, int64_t shared_stride,
                                                    uint16_t* __restrict__ shared_bf16) {
-    const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
+    __shared__ __align__(16) uint64_t s_cand[4][66];
+    __shared__ uint2 s_sel[4][kTop];
+    const int w = threadIdx.x >> 6, t = blockIdx.x * 4 + w;
     if (t >= T) return;
     const int lane = threadIdx.x & 63;
     float v[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) v[i] = logits[size_t(t) * logit_stride + lane + 64 * i];
-    float wv;
-    int iv, i8[kTop];
-    softmax_top8(v, wv, iv, i8);
+    uint32_t k[4];
+    softmax_keys(v, k);
+    top8_rank_lds(k, s_cand[w], s_sel[w]);
+    float tot = 0.f;
+#pragma unroll
+    for (int j = 0; j < kTop; ++j) tot = tot + __uint_as_float(s_sel[w][j].x);
     if (lane < kTop) {
-        weights[size_t(t) * kTop + lane] = wv;
-        ids[size_t(t) * kTop + lane] = iv;
+        const uint2 pick = s_sel[w][lane];
+        weights[size_t(t) * kTop + lane] = fdiv_rn(__uint_as_float(pick.x), tot);
+        ids[size_t(t) * kTop + lane] = int(pick.y);
     }
     if (lane == 0 && shared_bf16) shared_bf16[t] = f32_to_bf16_bits(shared_logit[size_t(t) * shared_stride]);
 }

@@ -4,6 +4,8 @@
 // patterns, all non-negative, so integer order is value order); exact ties
 // between lane heads go to the lowest expert id.  The picks come out in
 // descending order and are renormalised by their slot-order sum.
+// top8_rank_lds makes the same picks with a threshold and a rank count (for
+// kernels where the selection latency is on the critical path).
 #pragma once
 #include "common.hpp"
 
@@ -62,11 +64,10 @@ __device__ __forceinline__ void router_rows_wave(const uint16_t* __restrict__ x,
     }
 }
 
-// v: lane l holds the logits of experts l, l+64, l+128, l+192.  Returns the
-// eight selected ids (identical on every lane) in pid, and on lane j < 8 the
-// weight and id of slot j (the renormalisation runs lane-parallel).
-__device__ __forceinline__ void softmax_top8(const float v[4], float& w_lane, int& id_lane, int pid[kTop]) {
-    const int lane = threadIdx.x & 63;
+// Softmax probabilities of one token as order keys: lane l holds experts l,
+// l+64, l+128, l+192; k[i] is the fp32 bit pattern of the probability (all
+// non-negative, so integer order is value order).
+__device__ __forceinline__ void softmax_keys(const float v[4], uint32_t k[4]) {
     const float m = wave_max(fmaxf(fmaxf(v[0], v[1]), fmaxf(v[2], v[3])));
     float e[4];
 #pragma unroll
@@ -75,11 +76,21 @@ __device__ __forceinline__ void softmax_top8(const float v[4], float& w_lane, in
 #pragma unroll
     for (int i = 1; i < 4; ++i) part = part + e[i];
     const float sum = wave_butterfly_sum(part);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) k[i] = __float_as_uint(fdiv_rn(e[i], sum));
+}
+
+// Top-8 of the keys by eight wave-wide rounds.  Each lane sorts its four
+// (key desc, id asc); eight rounds then take the wave-wide maximum of the lane
+// heads, exact ties between lane heads going to the lowest expert id.  pk/pid
+// come out in descending order, identical on every lane.
+__device__ __forceinline__ void top8_rounds(const uint32_t keys[4], uint32_t pk[kTop], int pid[kTop]) {
+    const int lane = threadIdx.x & 63;
     uint32_t k[4];
     int id[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-        k[i] = __float_as_uint(fdiv_rn(e[i], sum));
+        k[i] = keys[i];
         id[i] = lane + 64 * i;
     }
     // sorting network for four (key desc, id asc)
@@ -92,7 +103,6 @@ __device__ __forceinline__ void softmax_top8(const float v[4], float& w_lane, in
     // rest up and appends the sentinel id 0x7fffffff (a lane is exhausted
     // when its head id is the sentinel).  All selects, no lane branches.
     constexpr int kNone = 0x7fffffff;
-    uint32_t pk[kTop];
 #pragma unroll
     for (int j = 0; j < kTop; ++j) {
         const bool live = id[0] != kNone;
@@ -114,6 +124,16 @@ __device__ __forceinline__ void softmax_top8(const float v[4], float& w_lane, in
         id[2] = pop ? id[3] : id[2];
         id[3] = pop ? kNone : id[3];
     }
+}
+
+// v: lane l holds the logits of experts l, l+64, l+128, l+192.  Returns the
+// eight selected ids (identical on every lane) in pid, and on lane j < 8 the
+// weight and id of slot j (the renormalisation runs lane-parallel).
+__device__ __forceinline__ void softmax_top8(const float v[4], float& w_lane, int& id_lane, int pid[kTop]) {
+    const int lane = threadIdx.x & 63;
+    uint32_t k[4], pk[kTop];
+    softmax_keys(v, k);
+    top8_rounds(k, pk, pid);
     float tot = 0.f;
 #pragma unroll
     for (int j = 0; j < kTop; ++j) tot = tot + __uint_as_float(pk[j]);
@@ -124,6 +144,75 @@ __device__ __forceinline__ void softmax_top8(const float v[4], float& w_lane, in
         if (lane == j) { mk = pk[j]; mi = pid[j]; }
     w_lane = fdiv_rn(__uint_as_float(mk), tot);
     id_lane = mi;
+}
+
+// Top-8 of the keys by a threshold and a rank count, on one wave:
+//  1. Threshold t: the largest quad maximum (quad = 4 lanes, 16 keys) that
+//     at least eight quad maxima reach.  Those eight belong to distinct
+//     experts, so every key below t is beaten by eight keys and the top
+//     eight lie among the candidates {key >= t} (t itself is a key; about
+//     ten candidates for router-like logits).
+//  2. The candidates are compacted into LDS as (key << 32 | ~id); candidate c
+//     (lane c) counts the candidates ahead of it in (key desc, id asc) order
+//     -- one 64-bit compare each -- and ranks 0..7 write themselves to
+//     sel[rank].
+// More than 64 candidates (many equal keys) take top8_rounds instead; both
+// give the same picks.  cand: 65 entries of LDS (the last one takes the
+// writes of non-candidates), 16-byte aligned; sel: 8.  sel[r] = {key bits,
+// id}; visible to the wave when this returns.
+__device__ __forceinline__ void top8_rank_lds(const uint32_t k[4], uint64_t* cand, uint2* sel) {
+    const int lane = threadIdx.x & 63;
+    uint32_t q = max(max(k[0], k[1]), max(k[2], k[3]));
+    q = max(q, uint32_t(dpp_i<kDppXor1>(int(q))));
+    q = max(q, uint32_t(dpp_i<kDppXor2>(int(q))));           // the quad's maximum
+    int ge = 0;                                               // quad maxima >= this quad's
+#pragma unroll
+    for (int j = 0; j < 16; ++j) ge += uint32_t(__builtin_amdgcn_readlane(int(q), 4 * j)) >= q ? 1 : 0;
+    const uint32_t t = wave_max_u(ge >= kTop ? q : 0u);
+    uint64_t b[4];
+    int base[4], C = 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        b[i] = __ballot(k[i] >= t);
+        base[i] = C;
+        C += __popcll(b[i]);
+    }
+    if (C <= 64) {
+        // zero padding (a zero entry is ahead of no candidate: every candidate
+        // has ~id > 0), then the candidates; others write entry 64
+        cand[lane] = 0;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int pos = base[i] + int(__builtin_amdgcn_mbcnt_hi(uint32_t(b[i] >> 32),
+                                                                    __builtin_amdgcn_mbcnt_lo(uint32_t(b[i]), 0u)));
+            cand[k[i] >= t ? pos : 64] = (uint64_t(k[i]) << 32) | ~uint32_t(lane + 64 * i);
+        }
+        __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        const uint64_t me = cand[lane];
+        int rank = 0;
+        for (int j = 0; j < C; j += 16) {
+            const ulonglong2* p = reinterpret_cast<const ulonglong2*>(cand + j);
+            ulonglong2 e[8];
+#pragma unroll
+            for (int r = 0; r < 8; ++r) e[r] = p[r];
+#pragma unroll
+            for (int r = 0; r < 8; ++r) rank += (e[r].x > me ? 1 : 0) + (e[r].y > me ? 1 : 0);
+        }
+        if (lane < C && rank < kTop) sel[rank] = make_uint2(uint32_t(me >> 32), ~uint32_t(me));
+    } else {
+        uint32_t pk[kTop];
+        int pid[kTop];
+        top8_rounds(k, pk, pid);
+        uint32_t mk = pk[0];
+        int mi = pid[0];
+#pragma unroll
+        for (int j = 1; j < kTop; ++j)
+            if (lane == j) { mk = pk[j]; mi = pid[j]; }
+        if (lane < kTop) sel[lane] = make_uint2(mk, uint32_t(mi));
+    }
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+    __builtin_amdgcn_wave_barrier();
 }
 
 }  // namespace ornith

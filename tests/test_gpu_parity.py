@@ -312,6 +312,83 @@ def test_moe_layer_bit_exact(device, moe, shared_tables, T):
     assert int(flags.item()) == ref['flags']
 
 
+def _tied_router(router, case):
+    """Router rows repeated so that logits (and probabilities) tie exactly:
+    'quads' -- experts 4j..4j+3 share a row (ties decided by the lower id);
+    'three' -- three distinct rows (about 85 experts per value: more than 64
+    candidates above any threshold, the selection's fallback);
+    'flat' -- one row (all 256 probabilities equal: picks 0..7)."""
+    r = router.copy()
+    e = np.arange(256)
+    if case == 'quads':
+        r[:] = router[e - e % 4]
+    elif case == 'three':
+        r[:] = router[e % 3]
+    else:
+        r[:] = router[0]
+    return r
+
+
+@pytest.mark.parametrize('case', ['quads', 'three', 'flat'])
+def test_router_topk_ties(device, moe, case):
+    """Exact probability ties between experts, one wave per token (T = 40)."""
+    import torch
+    native = _native()
+    w, _ = moe
+    T = 40
+    rng = np.random.default_rng(3500)
+    x = bf16_normal(rng, (T, 2048))
+    router = _tied_router(w['router'], case)
+    logits_ref = O.router_logits(x, np.concatenate([router, w['gate']]), None)
+    wref, iref, _ = O.softmax_topk(logits_ref[:, :256])
+    logits = torch.empty((T, 257), dtype=torch.float32, device=device)
+    tw = torch.empty((T, 8), dtype=torch.float32, device=device)
+    ti = torch.empty((T, 8), dtype=torch.int32, device=device)
+    sl = torch.empty((T,), dtype=torch.bfloat16, device=device)
+    native.router_topk(to_dev(x, device), to_dev(router, device), None, to_dev(w['gate'][0], device),
+                       logits, tw, ti, sl)
+    _sync()
+    np.testing.assert_array_equal(from_dev(logits).view(np.uint32), logits_ref.view(np.uint32))
+    np.testing.assert_array_equal(from_dev(ti), iref)
+    np.testing.assert_array_equal(from_dev(tw).view(np.uint32), wref.view(np.uint32))
+    if case == 'flat':
+        assert (iref == np.arange(8)[None, :]).all()
+
+
+@pytest.mark.parametrize('case', ['quads', 'three', 'flat'])
+def test_moe_layer_single_token_ties(device, moe, shared_tables, case):
+    """The single-token layer selects its experts inside the gate-up kernel;
+    exact probability ties must give the oracle's picks, weights and output."""
+    import torch
+    native = _native()
+    w, d = moe
+    silu, sigmoid = shared_tables
+    rng = np.random.default_rng(3600)
+    x = bf16_normal(rng, (1, 2048))
+    router = _tied_router(w['router'], case)
+    logits = O.router_logits(x, np.concatenate([router, w['gate']]))
+    rw, ids, _ = O.softmax_topk(logits[:, :256])
+    ref = O.routed_layer_shared(x, rw, ids, LazyExperts(w['w13']), w['w13'].sbits, w['w13'].obits,
+                                LazyExperts(w['w2']), w['w2'].sbits, w['w2'].obits,
+                                *w['s13'].expert(), *w['s2'].expert(), O.f32_to_bf16(logits[:, 256]), silu, sigmoid)
+    expected = O.add_bf16(ref['out'], ref['shared_out'])
+    layout = native.routed_layout(1, 'layer')
+    ws = torch.empty(layout.workspace_bytes, dtype=torch.uint8, device=device)
+    out = torch.empty((1, 2048), dtype=torch.bfloat16, device=device)
+    tw = torch.empty((1, 8), dtype=torch.float32, device=device)
+    ti = torch.empty((1, 8), dtype=torch.int32, device=device)
+    sl = torch.empty((1,), dtype=torch.bfloat16, device=device)
+    flags = _flags(device)
+    native.moe_layer(to_dev(x, device), to_dev(router, device), None, to_dev(w['gate'][0], device), d['w13'][0],
+                     d['w13'][1], d['w2'][0], d['w2'][1], d['s13'][0], d['s13'][1], d['s2'][0], d['s2'][1],
+                     to_dev(silu, device), to_dev(sigmoid, device), ws, tw, ti, sl, out, flags, 1)
+    _sync()
+    np.testing.assert_array_equal(from_dev(ti), ids)
+    np.testing.assert_array_equal(from_dev(tw).view(np.uint32), rw.view(np.uint32))
+    np.testing.assert_array_equal(from_dev(out), expected)
+    assert int(flags.item()) == ref['flags']
+
+
 # ---------------------------------------------------------------------------
 # Heads
 # ---------------------------------------------------------------------------
