@@ -78,7 +78,7 @@ def kernel_cost(name, T, unique):
         return 'mfma', 2 * routes * 1024 * 2048, INT8_PEAK_TOPS, 'TFLOP/s'
     if name == 'down_mfma':
         return 'mfma', 2 * routes * 2048 * 512, INT8_PEAK_TOPS, 'TFLOP/s'
-    if name == 'router':
+    if name in ('router', 'router_act'):
         return 'valu', 2 * T * 257 * 2048, FP32_PEAK_TFLOPS, 'TFLOP/s'
     return 'hbm', T * 2048 * 2, HBM_PEAK_GBS, 'GB/s'
 

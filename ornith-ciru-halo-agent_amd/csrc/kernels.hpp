@@ -35,10 +35,19 @@ hipError_t launch_act_middle(const float* gate_y, int RS, int R, const int32_t* 
                              int32_t* sums, uint32_t* sticky, hipStream_t s);
 
 // ---- routing ---------------------------------------------------------------
+constexpr int kRouterRowsMaxTokens = 256;      // wave-per-row router up to here, token-tiled beyond
 // Router logits [T, 256 (+1)] in the declared order; shared_w (nullable) adds
 // column 256, the shared-expert gate logit.
 hipError_t launch_router(const uint16_t* x, int64_t stride, int T, const uint16_t* w, const uint16_t* shared_w,
                          const float* bias, float* logits, int64_t logit_stride, hipStream_t s);
+// The same router logits for T > 256 tokens (contiguous x, shared row
+// present) in one launch with the A8 gate-input quantisation of x
+// (launch_act_bf16 with ids == nullptr).
+hipError_t launch_router_act(const uint16_t* x, int T, const uint16_t* w, const uint16_t* shared_w, const float* bias,
+                             float* logits, int64_t logit_stride, uint32_t* words, uint16_t* scales, int32_t* sums,
+                             uint32_t* sticky, hipStream_t s);
+// Whether the fused launch beats router + activation launches at T tokens.
+bool router_act_pays(int T);
 hipError_t launch_topk(const float* logits, int64_t logit_stride, int T, float* weights, int32_t* ids,
                        const float* shared_logit_f32, int64_t shared_stride, uint16_t* shared_logit_bf16,
                        hipStream_t s);

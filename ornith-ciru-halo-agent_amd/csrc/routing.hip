@@ -14,6 +14,7 @@
 #include "kernels.hpp"
 #include "timing.hpp"
 #include "topk.hpp"
+#include "act.hpp"
 
 namespace ornith {
 
@@ -33,7 +34,6 @@ namespace ornith {
 // token per wave at a time, with the lane-partial butterfly itself.
 // ---------------------------------------------------------------------------
 constexpr int kRouterTile = 32;
-constexpr int kRouterRowsMaxTokens = 256;      // wave-per-row kernel up to here, tiled kernel beyond
 constexpr int kRouterIStride = 8 * kRouterTile + 4;       // [i][j][row] with a 4-float pad per i
 constexpr int kRouterWaveStride = 4 * kRouterIStride;
 
@@ -188,15 +188,15 @@ __global__ __launch_bounds__(256) void router_kernel(const uint16_t* __restrict_
 // its L2.
 constexpr int kRtRows = 8, kRtTokens = 64;
 
-__global__ __launch_bounds__(256, 2) void router_tokens_kernel(const uint16_t* __restrict__ x, int64_t stride, int T,
-                                                               const uint16_t* __restrict__ w,
-                                                               const uint16_t* __restrict__ shared_w,
-                                                               const float* __restrict__ bias, float* __restrict__ logits,
-                                                               int64_t logit_stride, int nrows, int ntg) {
+__device__ __forceinline__ void router_tokens_block(int blk, const uint16_t* __restrict__ x, int64_t stride, int T,
+                                                    const uint16_t* __restrict__ w,
+                                                    const uint16_t* __restrict__ shared_w,
+                                                    const float* __restrict__ bias, float* __restrict__ logits,
+                                                    int64_t logit_stride, int nrows, int ntg) {
     __shared__ __align__(16) float sW[kRtRows][kHidden];       // fp32 weights of the block's rows
     __shared__ __align__(16) float sS[4][kRtRows][kRtTokens];  // Sq per wave
     const int ngroups = (nrows + kRtRows - 1) / kRtRows;
-    const int blk = blockIdx.x, idx = blk >> 3;
+    const int idx = blk >> 3;
     const int tg = 8 * (idx / ngroups) + (blk & 7), rg = idx % ngroups;
     if (tg >= ntg) return;
     const int tid = threadIdx.x, lane = tid & 63, q = tid >> 6;
@@ -282,6 +282,33 @@ __global__ __launch_bounds__(256, 2) void router_tokens_kernel(const uint16_t* _
     }
 }
 
+__global__ __launch_bounds__(256, 2) void router_tokens_kernel(const uint16_t* __restrict__ x, int64_t stride, int T,
+                                                               const uint16_t* __restrict__ w,
+                                                               const uint16_t* __restrict__ shared_w,
+                                                               const float* __restrict__ bias, float* __restrict__ logits,
+                                                               int64_t logit_stride, int nrows, int ntg) {
+    router_tokens_block(int(blockIdx.x), x, stride, T, w, shared_w, bias, logits, logit_stride, nrows, ntg);
+}
+
+// Router tiles followed by the activation quantisation of the same rows (the
+// layer path with the shared expert, where every token is live, so the gate
+// input does not wait for routing).  The activation blocks take the CUs the
+// last round of router tiles leaves idle.
+__global__ __launch_bounds__(256, 2) void router_act_kernel(const uint16_t* __restrict__ x, int T,
+                                                            const uint16_t* __restrict__ w,
+                                                            const uint16_t* __restrict__ shared_w,
+                                                            const float* __restrict__ bias, float* __restrict__ logits,
+                                                            int64_t logit_stride, int nrows, int ntg, int router_blocks,
+                                                            uint32_t* __restrict__ words, uint16_t* __restrict__ scales,
+                                                            int32_t* __restrict__ sums, uint32_t* sticky) {
+    const int b = int(blockIdx.x);
+    if (b < router_blocks)
+        router_tokens_block(b, x, kHidden, T, w, shared_w, bias, logits, logit_stride, nrows, ntg);
+    else
+        act_bf16_block<127>(b - router_blocks, x, kHidden, T, kHidden / kGroup, nullptr, words, scales, sums, sticky,
+                            kFlagNonfiniteInput, kFlagInvalidActivation);
+}
+
 // One wave per (router row, batch of 8 tokens): the choice for small and
 // medium T, where the tiled kernel has too few blocks to fill the chip.
 __global__ __launch_bounds__(256) void router_rows_kernel(const uint16_t* __restrict__ x, int64_t stride, int T,
@@ -314,6 +341,42 @@ hipError_t launch_router(const uint16_t* x, int64_t stride, int T, const uint16_
     const int blocks = ((ntg + 7) / 8) * 8 * ngroups;     // token groups padded to a multiple of the 8 XCDs
     timed_launch("router", router_tokens_kernel, dim3(blocks), dim3(256), 0, s, x, stride, T, w, shared_w, bias, logits,
                  logit_stride, nrows, ntg);
+    return hipGetLastError();
+}
+
+// The fused launch runs its activation blocks at the router's occupancy (two
+// blocks per CU); it pays when they fit the slots the last round of router
+// tiles leaves idle (about 4 activation blocks per router-tile time).
+bool router_act_pays(int T) {
+    if (T <= kRouterRowsMaxTokens) return false;
+    static int slots = 0;
+    if (!slots) {
+        int dev = 0, cus = 0;
+        if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) !=
+                                                    hipSuccess || cus <= 0)
+            return false;
+        slots = 2 * cus;
+    }
+    const int ngroups = (kExperts + 1 + kRtRows - 1) / kRtRows;
+    const int tiles = ((T + kRtTokens - 1) / kRtTokens) * ngroups;   // router blocks with work
+    const int tail = tiles % slots;
+    const int idle = tail ? slots - tail : 0;
+    const int act_blocks = ((T * (kHidden / kGroup) + 3) / 4 + 3) / 4;
+    return act_blocks <= 2 * idle;
+}
+
+hipError_t launch_router_act(const uint16_t* x, int T, const uint16_t* w, const uint16_t* shared_w, const float* bias,
+                             float* logits, int64_t logit_stride, uint32_t* words, uint16_t* scales, int32_t* sums,
+                             uint32_t* sticky, hipStream_t s) {
+    if (T <= kRouterRowsMaxTokens || !shared_w) return hipErrorInvalidValue;
+    const int nrows = kExperts + 1;
+    const int ngroups = (nrows + kRtRows - 1) / kRtRows;
+    const int ntg = (T + kRtTokens - 1) / kRtTokens;
+    const int router_blocks = ((ntg + 7) / 8) * 8 * ngroups;
+    const int act_waves = (T * (kHidden / kGroup) + 3) / 4;
+    const int act_blocks = (act_waves + 3) / 4;
+    timed_launch("router_act", router_act_kernel, dim3(router_blocks + act_blocks), dim3(256), 0, s, x, T, w, shared_w,
+                 bias, logits, logit_stride, nrows, ntg, router_blocks, words, scales, sums, sticky);
     return hipGetLastError();
 }
 

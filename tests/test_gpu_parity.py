@@ -279,7 +279,7 @@ def test_router_topk_bit_exact(device, moe, T, biased):
     np.testing.assert_array_equal(from_dev(sl), O.f32_to_bf16(logits_ref[:, 256]))
 
 
-@pytest.mark.parametrize('T', [1, 32, 96])
+@pytest.mark.parametrize('T', [1, 32, 96, 300])
 def test_moe_layer_bit_exact(device, moe, shared_tables, T):
     import torch
     native = _native()
