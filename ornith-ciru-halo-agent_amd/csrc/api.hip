@@ -59,11 +59,11 @@ hipError_t run_routed(const RoutedPlan& p, void* ws, const void* input, const fl
                       const void* sg_codes, const void* sg_meta, const void* sd_codes, const void* sd_meta,
                       const uint16_t* shared_logit, const float* silu, const uint16_t* sigmoid, int qmax,
                       uint16_t* out, uint16_t* shared_out, uint16_t* layer_out, uint32_t* sticky, int T, int Tcap,
-                      hipStream_t s, bool act_done = false) {
+                      hipStream_t s, bool act_done = false, bool counted = false) {
     const bool shared = sg_codes != nullptr;
     const int R = T * kTop, RS = R + (shared ? T : 0);
     const PermuteScratch ps = carve_permute(at<void>(ws, p.permute), Tcap * kTop, shared ? Tcap : 0);
-    TRY(launch_permute(ids, R, T, shared, ps, sticky, 64, s));
+    TRY(launch_permute(ids, R, T, shared, ps, sticky, 64, s, counted));
     auto gw = at<uint32_t>(ws, p.l.gate_low);
     auto gs = at<uint16_t>(ws, p.l.gate_scales);
     auto gsum = at<int32_t>(ws, p.l.gate_sums);
@@ -381,24 +381,27 @@ extern "C" hipError_t ornith_moe_layer_launch(
     // with the shared expert): same words as launch_act_bf16.
     const bool fused = router_act_pays(T);
     auto logits = at<float>(workspace, p.logits);
+    // top-8 also counts the routed banks per 16-token block (permutation step 1)
+    const PermuteScratch ps = carve_permute(at<void>(workspace, p.permute), Tcap * kTop, Tcap);
     if (fused) {
         TRY(launch_router_act(static_cast<const uint16_t*>(input), T, static_cast<const uint16_t*>(router_w),
                               static_cast<const uint16_t*>(shared_gate_w), static_cast<const float*>(bias), logits,
                               kLogitStride, at<uint32_t>(workspace, p.l.gate_low),
                               at<uint16_t>(workspace, p.l.gate_scales), at<int32_t>(workspace, p.l.gate_sums),
                               static_cast<uint32_t*>(flags), stream));
-        TRY(launch_topk(logits, kLogitStride, T, static_cast<float*>(topk_weights), static_cast<int32_t*>(topk_ids),
-                        logits + kExperts, kLogitStride, static_cast<uint16_t*>(shared_logit), stream));
     } else {
-        TRY(ornith_router_topk_launch(input, kHidden, router_w, bias, shared_gate_w, logits, topk_weights, topk_ids,
-                                      shared_logit, T, stream));
+        TRY(launch_router(static_cast<const uint16_t*>(input), kHidden, T, static_cast<const uint16_t*>(router_w),
+                          static_cast<const uint16_t*>(shared_gate_w), static_cast<const float*>(bias), logits,
+                          kLogitStride, stream));
     }
+    TRY(launch_topk(logits, kLogitStride, T, static_cast<float*>(topk_weights), static_cast<int32_t*>(topk_ids),
+                    logits + kExperts, kLogitStride, static_cast<uint16_t*>(shared_logit), stream, ps.block_counts));
     return run_routed(p, workspace, input, static_cast<const float*>(topk_weights),
                       static_cast<const int32_t*>(topk_ids), gate_codes, gate_meta, down_codes, down_meta,
                       shared_gate_codes, shared_gate_meta, shared_down_codes, shared_down_meta,
                       static_cast<const uint16_t*>(shared_logit), static_cast<const float*>(silu),
                       static_cast<const uint16_t*>(sigmoid), 127, nullptr, nullptr, static_cast<uint16_t*>(output),
-                      static_cast<uint32_t*>(flags), T, Tcap, stream, fused);
+                      static_cast<uint32_t*>(flags), T, Tcap, stream, fused, true);
 }
 
 extern "C" int ornith_mi355x_abi_version(void) { return 1; }

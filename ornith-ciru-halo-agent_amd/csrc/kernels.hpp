@@ -48,15 +48,17 @@ hipError_t launch_router_act(const uint16_t* x, int T, const uint16_t* w, const 
                              uint32_t* sticky, hipStream_t s);
 // Whether the fused launch beats router + activation launches at T tokens.
 bool router_act_pays(int T);
+// block_counts != nullptr (the layer path) also does the permutation's count
+// step: launch_permute(..., counted = true) then skips it.
 hipError_t launch_topk(const float* logits, int64_t logit_stride, int T, float* weights, int32_t* ids,
                        const float* shared_logit_f32, int64_t shared_stride, uint16_t* shared_logit_bf16,
-                       hipStream_t s);
+                       hipStream_t s, int32_t* block_counts = nullptr);
 // Stable counting sort of route ids by bank.  Routes 0..R-1 use ids[r];
 // when with_shared, routes R..R+T-1 use the shared bank.
 size_t permute_scratch_bytes(int Rcap, int Tcap);
 PermuteScratch carve_permute(void* base, int Rcap, int Tcap);
 hipError_t launch_permute(const int32_t* ids, int R, int T, bool with_shared, const PermuteScratch& p,
-                          uint32_t* sticky, int mfma_rows, hipStream_t s);
+                          uint32_t* sticky, int mfma_rows, hipStream_t s, bool counted = false);
 
 // ---- projections -----------------------------------------------------------
 enum class Out { Routed, Dense };

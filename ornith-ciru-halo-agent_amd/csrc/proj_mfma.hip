@@ -425,9 +425,12 @@ __global__ __launch_bounds__(256, GATEUP ? 2 : 3) void prefill_mfma_kernel(MfmaA
 
     // routes of this lane's A row (tid / 4) and scale row (tid % 64), first:
     // later waits on them must not wait on the code loads
+    // (clamped to the route range: a malformed list gives wrong rows, never
+    // an access outside the activation / output buffers)
     const int a_r = tid >> 2, a_part = tid & 3;
-    const int route_a = a.routes[first + min(a_r, nrows - 1)];
-    const int route_s = a.routes[first + min(tid & 63, nrows - 1)];
+    const int rmax = a.R + (a.shared_codes ? a.R / kTop : 0) - 1;
+    const int route_a = min(max(a.routes[first + min(a_r, nrows - 1)], 0), rmax);
+    const int route_s = min(max(a.routes[first + min(tid & 63, nrows - 1)], 0), rmax);
 
     // ---- B: code words of step st for this lane ----
     // column tile ct of step st: 32-column code tile and the column in it

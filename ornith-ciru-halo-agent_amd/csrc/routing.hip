@@ -187,6 +187,8 @@ __global__ __launch_bounds__(256) void router_kernel(const uint16_t* __restrict_
 // group run on one XCD (workgroups go to the 8 XCDs round-robin) and share
 // its L2.
 constexpr int kRtRows = 8, kRtTokens = 64;
+constexpr int kPermTokens = 16;                      // tokens per permutation count / scatter block
+constexpr int kPermRoutes = kPermTokens * kTop;      // routed routes per block
 
 __device__ __forceinline__ void router_tokens_block(int blk, const uint16_t* __restrict__ x, int64_t stride, int T,
                                                     const uint16_t* __restrict__ w,
@@ -388,37 +390,60 @@ hipError_t launch_router_act(const uint16_t* x, int T, const uint16_t* w, const 
 // (ties to the lower id) in descending order; weights p / (slot-order sum of
 // the picked p).
 // ---------------------------------------------------------------------------
-__global__ __launch_bounds__(256) void topk_kernel(const float* __restrict__ logits, int64_t logit_stride, int T,
-                                                   float* __restrict__ weights, int32_t* __restrict__ ids,
-                                                   const float* __restrict__ shared_logit, int64_t shared_stride,
-                                                   uint16_t* __restrict__ shared_bf16) {
-    __shared__ __align__(16) uint64_t s_cand[4][66];
-    __shared__ uint2 s_sel[4][kTop];
-    const int w = threadIdx.x >> 6, t = blockIdx.x * 4 + w;
-    if (t >= T) return;
+// WAVES tokens per block; COUNT adds the routed-bank histogram of the block's
+// tokens (block_counts[blockIdx.x][bank], the count step of the permutation;
+// WAVES is then its 16-token block).
+template <int WAVES, bool COUNT>
+__global__ __launch_bounds__(64 * WAVES) void topk_kernel(const float* __restrict__ logits, int64_t logit_stride, int T,
+                                                          float* __restrict__ weights, int32_t* __restrict__ ids,
+                                                          const float* __restrict__ shared_logit, int64_t shared_stride,
+                                                          uint16_t* __restrict__ shared_bf16,
+                                                          int32_t* __restrict__ block_counts) {
+    __shared__ __align__(16) uint64_t s_cand[WAVES][66];
+    __shared__ uint2 s_sel[WAVES][kTop];
+    __shared__ int s_hist[COUNT ? kExperts : 1];
+    const int w = threadIdx.x >> 6, t = blockIdx.x * WAVES + w;
     const int lane = threadIdx.x & 63;
-    float v[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) v[i] = logits[size_t(t) * logit_stride + lane + 64 * i];
-    uint32_t k[4];
-    softmax_keys(v, k);
-    top8_rank_lds(k, s_cand[w], s_sel[w]);
-    float tot = 0.f;
-#pragma unroll
-    for (int j = 0; j < kTop; ++j) tot = tot + __uint_as_float(s_sel[w][j].x);
-    if (lane < kTop) {
-        const uint2 pick = s_sel[w][lane];
-        weights[size_t(t) * kTop + lane] = fdiv_rn(__uint_as_float(pick.x), tot);
-        ids[size_t(t) * kTop + lane] = int(pick.y);
+    if (COUNT) {
+        for (int i = threadIdx.x; i < kExperts; i += 64 * WAVES) s_hist[i] = 0;
+        __syncthreads();
     }
-    if (lane == 0 && shared_bf16) shared_bf16[t] = f32_to_bf16_bits(shared_logit[size_t(t) * shared_stride]);
+    if (t < T) {
+        float v[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) v[i] = logits[size_t(t) * logit_stride + lane + 64 * i];
+        uint32_t k[4];
+        softmax_keys(v, k);
+        top8_rank_lds(k, s_cand[w], s_sel[w]);
+        float tot = 0.f;
+#pragma unroll
+        for (int j = 0; j < kTop; ++j) tot = tot + __uint_as_float(s_sel[w][j].x);
+        if (lane < kTop) {
+            const uint2 pick = s_sel[w][lane];
+            weights[size_t(t) * kTop + lane] = fdiv_rn(__uint_as_float(pick.x), tot);
+            ids[size_t(t) * kTop + lane] = int(pick.y);
+            if (COUNT) atomicAdd(&s_hist[pick.y], 1);
+        }
+        if (lane == 0 && shared_bf16) shared_bf16[t] = f32_to_bf16_bits(shared_logit[size_t(t) * shared_stride]);
+    }
+    if (COUNT) {
+        __syncthreads();
+        for (int i = threadIdx.x; i < kExperts; i += 64 * WAVES)
+            block_counts[size_t(blockIdx.x) * kExperts + i] = s_hist[i];
+    }
 }
 
 hipError_t launch_topk(const float* logits, int64_t logit_stride, int T, float* weights, int32_t* ids,
-                       const float* shared_logit, int64_t shared_stride, uint16_t* shared_bf16, hipStream_t s) {
+                       const float* shared_logit, int64_t shared_stride, uint16_t* shared_bf16, hipStream_t s,
+                       int32_t* block_counts) {
     if (T <= 0) return hipSuccess;
-    timed_launch("topk", topk_kernel, dim3((T + 3) / 4), dim3(256), 0, s, logits, logit_stride, T, weights, ids, shared_logit, shared_stride,
-                                           shared_bf16);
+    if (block_counts)
+        timed_launch("topk", topk_kernel<kPermTokens, true>, dim3((T + kPermTokens - 1) / kPermTokens),
+                     dim3(64 * kPermTokens), 0, s, logits, logit_stride, T, weights, ids, shared_logit, shared_stride,
+                     shared_bf16, block_counts);
+    else
+        timed_launch("topk", topk_kernel<4, false>, dim3((T + 3) / 4), dim3(256), 0, s, logits, logit_stride, T,
+                     weights, ids, shared_logit, shared_stride, shared_bf16, block_counts);
     return hipGetLastError();
 }
 
@@ -429,7 +454,6 @@ hipError_t launch_topk(const float* logits, int64_t logit_stride, int T, float* 
 // per non-empty bank (ascending bank order) and the MFMA tile list.
 // ---------------------------------------------------------------------------
 constexpr int kBanks = kExperts + 1;
-constexpr int kPermBlock = 256;
 
 __device__ __forceinline__ int route_bank(const int32_t* ids, int r, int R, uint32_t& flags) {
     if (r >= R) return kShared;
@@ -439,11 +463,21 @@ __device__ __forceinline__ int route_bank(const int32_t* ids, int r, int R, uint
     return -1;
 }
 
+__device__ __forceinline__ int wave_inclusive_scan(int v) {
+    const int lane = threadIdx.x & 63;
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+        const int u = __shfl_up(v, d, 64);
+        if (lane >= d) v += u;
+    }
+    return v;
+}
+
 size_t permute_scratch_bytes(int Rcap, int Tcap) {
     const size_t rall = size_t(Rcap) + size_t(Tcap);
-    const size_t blocks = (rall + kPermBlock - 1) / kPermBlock;
+    const size_t blocks = (size_t(Rcap / kTop) + kPermTokens - 1) / kPermTokens;
     size_t bytes = 0;
-    bytes += align256(blocks * kBanks * 4);
+    bytes += align256(blocks * kExperts * 4);
     bytes += align256(kBanks * 4);
     bytes += align256((kBanks + 1) * 4);
     bytes += align256(rall * 4);
@@ -456,11 +490,11 @@ size_t permute_scratch_bytes(int Rcap, int Tcap) {
 
 PermuteScratch carve_permute(void* base, int Rcap, int Tcap) {
     const size_t rall = size_t(Rcap) + size_t(Tcap);
-    const size_t blocks = (rall + kPermBlock - 1) / kPermBlock;
+    const size_t blocks = (size_t(Rcap / kTop) + kPermTokens - 1) / kPermTokens;
     PermuteScratch p{};
     size_t off = 0;
     auto take = [&](size_t bytes) { void* q = at<void>(base, off); off += align256(bytes); return q; };
-    p.block_counts = static_cast<int32_t*>(take(blocks * kBanks * 4));
+    p.block_counts = static_cast<int32_t*>(take(blocks * kExperts * 4));
     p.counts = static_cast<int32_t*>(take(kBanks * 4));
     p.offsets = static_cast<int32_t*>(take((kBanks + 1) * 4));
     p.routes = static_cast<int32_t*>(take(rall * 4));
@@ -470,145 +504,172 @@ PermuteScratch carve_permute(void* base, int Rcap, int Tcap) {
     return p;
 }
 
-__global__ __launch_bounds__(kPermBlock) void permute_count_kernel(const int32_t* __restrict__ ids, int R, int Rall,
-                                                                   int32_t* __restrict__ block_counts,
-                                                                   uint32_t* sticky) {
-    __shared__ int cnt[kBanks];
-    for (int i = threadIdx.x; i < kBanks; i += kPermBlock) cnt[i] = 0;
+// Stable counting sort of routes by bank (ascending route within a bank; the
+// shared expert's routes R + t are bank 256, in token order):
+//   count      per 16-token block, the routed banks' route counts (LDS
+//              histogram; fused into topk_kernel on the layer path)
+//   bank scan  one wave per routed bank: exclusive running sums over blocks
+//              (in place) and the bank total
+//   scatter    every block scans the 257 bank totals into offsets; block 0
+//              also writes offsets, segments, the MFMA tile list and meta; a
+//              route's slot is offset + running sum + its rank in the block.
+__global__ __launch_bounds__(kPermRoutes) void permute_count_kernel(const int32_t* __restrict__ ids, int T,
+                                                                    int32_t* __restrict__ block_counts,
+                                                                    uint32_t* sticky) {
+    __shared__ int cnt[kExperts];
+    for (int i = threadIdx.x; i < kExperts; i += kPermRoutes) cnt[i] = 0;
     __syncthreads();
-    const int r = blockIdx.x * kPermBlock + threadIdx.x;
+    const int r = blockIdx.x * kPermRoutes + threadIdx.x;
     uint32_t flags = 0;
-    if (r < Rall) {
-        const int b = route_bank(ids, r, R, flags);
+    if (r < T * kTop) {
+        const int b = route_bank(ids, r, T * kTop, flags);
         if (b >= 0) atomicAdd(&cnt[b], 1);
     }
     flag_or(sticky, flags);
     __syncthreads();
-    for (int i = threadIdx.x; i < kBanks; i += kPermBlock) block_counts[size_t(blockIdx.x) * kBanks + i] = cnt[i];
+    for (int i = threadIdx.x; i < kExperts; i += kPermRoutes) block_counts[size_t(blockIdx.x) * kExperts + i] = cnt[i];
 }
 
-// Single block of 256 x parts threads (2..4 parts): per-bank exclusive running
-// sums over blocks, offsets, segments and the MFMA tile list.  Thread (part,
-// bank) takes 1/parts of the blocks of banks 0..255 (its loads all in flight,
-// the part sums meet in LDS; a second pass writes the running sums).  Bank 256 (the shared
-// expert) is one count per block: thread b loads block b's, and a block-wide
-// scan in LDS gives the running sums.
-constexpr int kScanParts = 4;
-constexpr int kScanMaxPerPart = 72;          // 4 x 72 blocks x 256 routes >= 8192 tokens x 9 routes
-
-__global__ __launch_bounds__(1024) void permute_scan_kernel(int nblocks, int32_t* __restrict__ block_counts,
-                                                            int32_t* __restrict__ counts, int32_t* __restrict__ offsets,
-                                                            Segment* __restrict__ segments, int32_t* __restrict__ meta,
-                                                            Segment* __restrict__ tiles, int mfma_rows) {
-    __shared__ int part_sum[kScanParts][kExperts];
-    __shared__ int a[512], b[512], c[512], d[512];
-    __shared__ int total256;
-    const int tid = threadIdx.x, parts = int(blockDim.x) >> 8;
-    const int per = (nblocks + parts - 1) / parts;
-    const int pt = tid >> 8, bk = tid & 255, lo = pt * per;
-    const int x256 = tid < nblocks ? block_counts[size_t(tid) * kBanks + kExperts] : 0;
-    // counts of this part, 24 loads in flight per round
-    constexpr int kChunk = 24;
-    int qsum = 0;
-    for (int c0 = 0; c0 < per; c0 += kChunk) {
-        int v[kChunk];
+__global__ __launch_bounds__(256) void permute_bank_scan_kernel(int nblocks, int32_t* __restrict__ block_counts,
+                                                                int32_t* __restrict__ counts) {
+    const int bank = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+    if (bank >= kExperts) return;
+    constexpr int kRounds = 8;                       // 8 x 64 blocks = 8192 tokens
+    int v[kRounds];
 #pragma unroll
-        for (int i = 0; i < kChunk; ++i)
-            v[i] = (c0 + i < per && lo + c0 + i < nblocks) ? block_counts[size_t(lo + c0 + i) * kBanks + bk] : 0;
-#pragma unroll
-        for (int i = 0; i < kChunk; ++i) qsum += v[i];
+    for (int i = 0; i < kRounds; ++i) {
+        const int b = 64 * i + lane;
+        v[i] = b < nblocks ? block_counts[size_t(b) * kExperts + bank] : 0;
     }
-    if (tid == 0) total256 = 0;
-    __syncthreads();
-    part_sum[pt][bk] = qsum;
-    if (tid < 512) d[tid] = x256;              // scanned with a, b, c below
-    if (x256) atomicAdd(&total256, x256);
-    __syncthreads();
-    {
-        int run = 0;
-        for (int i = 0; i < pt; ++i) run += part_sum[i][bk];
-        for (int c0 = 0; c0 < per; c0 += kChunk) {
-            int v[kChunk];
+    int run = 0;
 #pragma unroll
-            for (int i = 0; i < kChunk; ++i)
-                v[i] = (c0 + i < per && lo + c0 + i < nblocks) ? block_counts[size_t(lo + c0 + i) * kBanks + bk] : 0;
+    for (int i = 0; i < kRounds; ++i) {
+        const int incl = wave_inclusive_scan(v[i]);
+        const int b = 64 * i + lane;
+        if (b < nblocks) block_counts[size_t(b) * kExperts + bank] = run + incl - v[i];
+        run += __shfl(incl, 63, 64);
+    }
+    if (lane == 0) counts[bank] = run;
+}
+
+__global__ __launch_bounds__(256) void permute_scatter_kernel(const int32_t* __restrict__ ids, int T, int shared_routes,
+                                                              const int32_t* __restrict__ block_counts,
+                                                              int32_t* __restrict__ counts, int32_t* __restrict__ offsets,
+                                                              int32_t* __restrict__ routes, Segment* __restrict__ segments,
+                                                              int32_t* __restrict__ meta, Segment* __restrict__ tiles,
+                                                              int mfma_rows) {
+    __shared__ int s_off[kBanks + 1];        // exclusive route offsets (s_off[257] = live routes)
+    __shared__ int s_tile[kBanks + 1];       // exclusive m-tile offsets (s_tile[257] = tiles)
+    __shared__ __align__(16) int bank_of[kPermRoutes];
+    const int tid = threadIdx.x, lane = tid & 63, R = T * kTop;
+    // this thread's route, its bank and the running count of earlier blocks
+    // (loaded before the offsets are ready)
+    const int r = blockIdx.x * kPermRoutes + tid;
+    uint32_t dummy = 0;
+    int b = -1, before = 0;
+    if (tid < kPermRoutes) {
+        b = r < R ? route_bank(ids, r, R, dummy) : -1;
+        if (b >= 0) before = block_counts[size_t(blockIdx.x) * kExperts + b];
+        bank_of[tid] = b;
+    }
+    if (tid < 64) {
+        // bank totals -> offsets, non-empty ranks and m-tile offsets (lane holds
+        // banks 4 lane .. 4 lane + 3; the shared bank 256 follows)
+        int tot[4], nt[4], ne[4], part = 0, ntp = 0, nep = 0;
 #pragma unroll
-            for (int i = 0; i < kChunk; ++i) {
-                if (c0 + i < per && lo + c0 + i < nblocks) block_counts[size_t(lo + c0 + i) * kBanks + bk] = run;
-                run += v[i];
+        for (int i = 0; i < 4; ++i) {
+            tot[i] = counts[4 * lane + i];
+            nt[i] = (tot[i] + mfma_rows - 1) / mfma_rows;
+            ne[i] = tot[i] > 0 ? 1 : 0;
+            part += tot[i];
+            ntp += nt[i];
+            nep += ne[i];
+        }
+        const int incl = wave_inclusive_scan(part), nt_incl = wave_inclusive_scan(ntp);
+        const int ne_incl = wave_inclusive_scan(nep);
+        int off = incl - part, tb = nt_incl - ntp, seg = ne_incl - nep;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int e = 4 * lane + i;
+            s_off[e] = off;
+            s_tile[e] = tb;
+            if (blockIdx.x == 0) {
+                offsets[e] = off;
+                if (tot[i] > 0) segments[seg] = Segment{e, off, tot[i], tb};
+            }
+            off += tot[i];
+            tb += nt[i];
+            seg += ne[i];
+        }
+        if (lane == 63) {
+            const int snt = (shared_routes + mfma_rows - 1) / mfma_rows;
+            s_off[kExperts] = off;
+            s_off[kBanks] = off + shared_routes;
+            s_tile[kExperts] = tb;
+            s_tile[kBanks] = tb + snt;
+            if (blockIdx.x == 0) {
+                offsets[kExperts] = off;
+                offsets[kBanks] = off + shared_routes;
+                counts[kExperts] = shared_routes;
+                if (shared_routes > 0) segments[seg] = Segment{kExperts, off, shared_routes, tb};
+                meta[0] = seg + (shared_routes > 0 ? 1 : 0);
+                meta[1] = tb + snt;
             }
         }
     }
-    const int e = tid;
-    int total = 0;
-    if (e < kExperts) {
-        for (int i = 0; i < parts; ++i) total += part_sum[i][e];
-    } else if (e == kExperts) {
-        total = total256;
-    }
-    if (e < kBanks) counts[e] = total;
-    const int ntile = (e < kBanks && total > 0) ? (total + mfma_rows - 1) / mfma_rows : 0;
-    if (e < 512) {
-        a[e] = e < kBanks ? total : 0;
-        b[e] = (e < kBanks && total > 0) ? 1 : 0;
-        c[e] = ntile;
-    }
     __syncthreads();
-    // inclusive Hillis-Steele scans of counts, non-empty flags, tile counts and
-    // the shared bank's per-block counts
-    for (int dd = 1; dd < 512; dd <<= 1) {
-        int va = 0, vb = 0, vc = 0, vd = 0;
-        if (e < 512 && e >= dd) { va = a[e - dd]; vb = b[e - dd]; vc = c[e - dd]; vd = d[e - dd]; }
-        __syncthreads();
-        if (e < 512) { a[e] += va; b[e] += vb; c[e] += vc; d[e] += vd; }
-        __syncthreads();
-    }
-    if (e < nblocks) block_counts[size_t(e) * kBanks + kExperts] = d[e] - x256;
-    if (e < kBanks) {
-        const int off = a[e] - total;
-        offsets[e] = off;
-        if (e == kBanks - 1) offsets[kBanks] = a[e];
-        if (total > 0) {
-            const int seg = b[e] - 1;
-            const int tile_base = c[e] - ntile;
-            segments[seg] = Segment{e, off, total, tile_base};
-            for (int k = 0; k < ntile; ++k)
-                tiles[tile_base + k] = Segment{e, off + k * mfma_rows, min(mfma_rows, total - k * mfma_rows), k};
+    // m-tiles, spread over the grid: tile i belongs to the bank e with
+    // s_tile[e] <= i < s_tile[e + 1] (binary search; empty banks have no tiles)
+    const int ntiles = s_tile[kBanks];
+    for (int i = blockIdx.x * 256 + tid; i < ntiles; i += gridDim.x * 256) {
+        int lo = 0, hi = kBanks;                    // s_tile[lo] <= i < s_tile[hi]
+        while (hi - lo > 1) {
+            const int mid = (lo + hi) >> 1;
+            if (s_tile[mid] <= i) lo = mid; else hi = mid;
         }
+        const int k = i - s_tile[lo], total = s_off[lo + 1] - s_off[lo];
+        tiles[i] = Segment{lo, s_off[lo] + k * mfma_rows, min(mfma_rows, total - k * mfma_rows), k};
     }
-    if (e == 0) { meta[0] = b[kBanks - 1]; meta[1] = c[kBanks - 1]; }
-}
-
-__global__ __launch_bounds__(kPermBlock) void permute_scatter_kernel(const int32_t* __restrict__ ids, int R, int Rall,
-                                                                     const int32_t* __restrict__ block_counts,
-                                                                     const int32_t* __restrict__ offsets,
-                                                                     int32_t* __restrict__ routes) {
-    __shared__ int bank_of[kPermBlock];
-    const int r = blockIdx.x * kPermBlock + threadIdx.x;
-    uint32_t dummy = 0;
-    const int b = r < Rall ? route_bank(ids, r, R, dummy) : -1;
-    bank_of[threadIdx.x] = b;
-    __syncthreads();
-    if (b < 0) return;
-    int rank = 0;
-    for (int j = 0; j < int(threadIdx.x); ++j) rank += bank_of[j] == b;
-    routes[offsets[b] + block_counts[size_t(blockIdx.x) * kBanks + b] + rank] = r;
+    if (tid < kPermRoutes && b >= 0) {
+        // rank in the block = earlier routes of the block with bank b: all of
+        // an earlier token's eight, the first `slot` of this token's (a token
+        // may name one expert twice); all 16 tokens' ids read at once
+        const int tok = tid >> 3, slot = tid & 7;
+        int rank = 0;
+#pragma unroll
+        for (int u = 0; u < kPermTokens; ++u) {
+            const int4 lo = *reinterpret_cast<const int4*>(&bank_of[8 * u]);
+            const int4 hi = *reinterpret_cast<const int4*>(&bank_of[8 * u + 4]);
+            const int n = u < tok ? 8 : (u == tok ? slot : 0);
+            const int hit = (n > 0 && lo.x == b) + (n > 1 && lo.y == b) + (n > 2 && lo.z == b) + (n > 3 && lo.w == b) +
+                            (n > 4 && hi.x == b) + (n > 5 && hi.y == b) + (n > 6 && hi.z == b) + (n > 7 && hi.w == b);
+            rank += hit;
+        }
+        routes[s_off[b] + before + rank] = r;
+    } else if (tid >= kPermRoutes && tid < kPermRoutes + kPermTokens) {
+        const int t = blockIdx.x * kPermTokens + (tid - kPermRoutes);
+        if (t < shared_routes) routes[s_off[kExperts] + t] = R + t;
+    }
 }
 
 hipError_t launch_permute(const int32_t* ids, int R, int T, bool with_shared, const PermuteScratch& p,
-                          uint32_t* sticky, int mfma_rows, hipStream_t s) {
-    const int Rall = R + (with_shared ? T : 0);
-    const int nblocks = (Rall + kPermBlock - 1) / kPermBlock;
-    if (nblocks > kScanParts * kScanMaxPerPart) return hipErrorInvalidValue;
-    const int scan_parts = max(2, (nblocks + kScanMaxPerPart - 1) / kScanMaxPerPart);
-    timed_launch("permute_count", permute_count_kernel, dim3(nblocks), dim3(kPermBlock), 0, s, ids, R, Rall, p.block_counts, sticky);
+                          uint32_t* sticky, int mfma_rows, hipStream_t s, bool counted) {
+    if (R != T * kTop) return hipErrorInvalidValue;
+    const int nblocks = (T + kPermTokens - 1) / kPermTokens;
+    if (nblocks > 8 * 64) return hipErrorInvalidValue;
+    if (!counted) {
+        timed_launch("permute_count", permute_count_kernel, dim3(nblocks), dim3(kPermRoutes), 0, s, ids, T,
+                     p.block_counts, sticky);
+        const hipError_t st = hipGetLastError();
+        if (st != hipSuccess) return st;
+    }
+    timed_launch("permute_scan", permute_bank_scan_kernel, dim3(kExperts / 4), dim3(256), 0, s, nblocks, p.block_counts,
+                 p.counts);
     hipError_t st = hipGetLastError();
     if (st != hipSuccess) return st;
-    timed_launch("permute_scan", permute_scan_kernel, dim3(1), dim3(256 * scan_parts), 0, s, nblocks, p.block_counts, p.counts, p.offsets, p.segments, p.meta, p.tiles,
-                                          mfma_rows);
-    st = hipGetLastError();
-    if (st != hipSuccess) return st;
-    timed_launch("permute_scatter", permute_scatter_kernel, dim3(nblocks), dim3(kPermBlock), 0, s, ids, R, Rall, p.block_counts, p.offsets, p.routes);
+    timed_launch("permute_scatter", permute_scatter_kernel, dim3(nblocks), dim3(256), 0, s, ids, T,
+                 with_shared ? T : 0, p.block_counts, p.counts, p.offsets, p.routes, p.segments, p.meta, p.tiles,
+                 mfma_rows);
     return hipGetLastError();
 }
 
