@@ -75,7 +75,10 @@ __device__ __forceinline__ float portable_exp(float x) {
     p = p * r + 0x1p+0f;
     float y = __builtin_ldexpf(p, n);
     asm volatile("" : "+v"(y));               // keep the polynomial unconditional (no per-lane branch)
-    return isnan(x) ? x : (x <= -104.f ? 0.f : (x >= 89.f ? __builtin_huge_valf() : y));
+    // special cases as three selects, innermost first
+    y = x >= 89.f ? __builtin_huge_valf() : y;
+    y = x <= -104.f ? 0.f : y;
+    return x != x ? x : y;
 }
 __device__ __forceinline__ float silu_portable(float g) { return fdiv_rn(g, 1.f + portable_exp(-g)); }
 

@@ -30,6 +30,14 @@ namespace ornith {
 
 constexpr int kMT = 64, kNT = 128, kRowWords = 68;   // 64 words (256 int8) + 4 pad
 
+// Integer dots start from the bits of kDotBias = 1.5 * 2^23, so the int32
+// result read as fp32 is kDotBias + dot exactly (|dot| < 2^19 << 2^22); with
+// nb = -sa * kDotBias (exact: sa is an fp16 value, 11 significant bits, and
+// kDotBias = 3 * 2^22) fma(sa, kDotBias + dot, nb) rounds sa * dot once:
+// RN(sa * dot) without an integer-to-float conversion.
+constexpr float kDotBias = 12582912.0f;
+constexpr int kDotBiasBits = 0x4B400000;
+
 typedef int i32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kModeGateUp = 0, kModeDown = 1, kModeHead = 2;
@@ -400,6 +408,7 @@ __global__ __launch_bounds__(256, GATEUP ? 2 : 3) void prefill_mfma_kernel(MfmaA
     __shared__ __attribute__((aligned(16))) uint32_t sA[NSTAGE][kMT * 64];
     __shared__ __attribute__((aligned(16))) float s_sa[NSTAGE][kMT];
     __shared__ __attribute__((aligned(16))) float s_ss[NSTAGE][kMT];
+    __shared__ __attribute__((aligned(16))) float s_nb[GATEUP ? NSTAGE : 1][kMT];   // -sa * kDotBias (exact)
     __shared__ int s_route[kMT];
 
     // Workgroups go to the 8 XCDs round-robin (linear block L runs on XCD
@@ -493,6 +502,7 @@ __global__ __launch_bounds__(256, GATEUP ? 2 : 3) void prefill_mfma_kernel(MfmaA
             const float sa = f16_bits_to_f32(uint16_t(rsa[slot]));
             s_sa[stage][tid] = sa;
             s_ss[stage][tid] = sa * float(rsum[slot]);
+            if constexpr (GATEUP) s_nb[stage][tid] = -sa * kDotBias;
         }
     };
     // A(0) and A(1) in flight together (A(1) through prologue-only registers)
@@ -526,6 +536,10 @@ __global__ __launch_bounds__(256, GATEUP ? 2 : 3) void prefill_mfma_kernel(MfmaA
                 for (int r = 0; r < 4; ++r) val[rt][ct][r] = 0.f;
         i32x4 acc[4][2];
         float swv[2], offv[2];
+        // gate/up dots start from kDotBias (see kDotBias); the down kernel keeps
+        // the conversion (measured: the bias costs it more than it saves there)
+        constexpr i32x4 kAccInit = GATEUP ? i32x4{kDotBiasBits, kDotBiasBits, kDotBiasBits, kDotBiasBits}
+                                          : i32x4{0, 0, 0, 0};
 
         // matrix-core dots of step ST for the L live row tiles (rows past
         // nrows in them hold copies of a live row)
@@ -550,7 +564,7 @@ __global__ __launch_bounds__(256, GATEUP ? 2 : 3) void prefill_mfma_kernel(MfmaA
 #pragma unroll
                     for (int ct = 0; ct < 2; ++ct)
                         acc[rt][ct] = __builtin_amdgcn_mfma_i32_16x16x64_i8(
-                            fa[rt], fb[ct], s ? acc[rt][ct] : i32x4{0, 0, 0, 0}, 0, 0, 0);
+                            fa[rt], fb[ct], s ? acc[rt][ct] : kAccInit, 0, 0, 0);
             }
             // the slot's scales are taken before the slot is refilled
 #pragma unroll
@@ -568,12 +582,17 @@ __global__ __launch_bounds__(256, GATEUP ? 2 : 3) void prefill_mfma_kernel(MfmaA
             for (int rt = 0; rt < L; ++rt) {
                 const float4 sa4 = *reinterpret_cast<const float4*>(&s_sa[stage][16 * rt + 4 * q]);
                 const float4 ss4 = *reinterpret_cast<const float4*>(&s_ss[stage][16 * rt + 4 * q]);
+                const float4 nb4 = GATEUP ? *reinterpret_cast<const float4*>(&s_nb[GATEUP ? stage : 0][16 * rt + 4 * q])
+                                          : float4{0.f, 0.f, 0.f, 0.f};
                 const float sa[4] = {sa4.x, sa4.y, sa4.z, sa4.w}, ss[4] = {ss4.x, ss4.y, ss4.z, ss4.w};
+                const float nb[4] = {nb4.x, nb4.y, nb4.z, nb4.w};
 #pragma unroll
                 for (int r = 0; r < 4; ++r)
 #pragma unroll
                     for (int ct = 0; ct < 2; ++ct) {
-                        const float scaled_dot = sa[r] * float(acc[rt][ct][r]);
+                        // gate/up: acc holds the bits of kDotBias + dot, one fma gives RN(sa * dot)
+                        const float scaled_dot = GATEUP ? __builtin_fmaf(sa[r], __int_as_float(acc[rt][ct][r]), nb[r])
+                                                        : sa[r] * float(acc[rt][ct][r]);
                         const float product = swv[ct] * scaled_dot;
                         const float correction = offv[ct] * ss[r];
                         val[rt][ct][r] = val[rt][ct][r] + (product + correction);
@@ -589,27 +608,48 @@ __global__ __launch_bounds__(256, GATEUP ? 2 : 3) void prefill_mfma_kernel(MfmaA
                     for (int r = 0; r < 4; ++r) asm volatile("" : "+v"(val[rt][ct][r]));
             if constexpr (g == GS - 1) {
                 // ---- epilogue of one column block ----
+                if constexpr (GATEUP) {
+                    // every row's SiLU(gate) * up unconditionally (dead rows
+                    // repeat a live row's inputs; their flags are dropped and
+                    // they are not stored), so the chains interleave
+                    float mid[L][4];
+                    uint32_t mflags[L][4];
+#pragma unroll
+                    for (int rt = 0; rt < L; ++rt)
+#pragma unroll
+                        for (int r = 0; r < 4; ++r) {
+                            float vg = val[rt][0][r], vu = val[rt][1][r];
+                            uint32_t f = 0;
+                            if (shared) {
+                                vg = bf16_round(vg);
+                                vu = bf16_round(vu);
+                                f |= (!isfinite(vg) || !isfinite(vu)) ? kFlagNonfiniteProjection : 0u;
+                                mid[rt][r] = bf16_round(a.silu_table[__float_as_uint(vg) >> 16] * vu);
+                            } else {
+                                f |= (!isfinite(vg) || !isfinite(vu)) ? kFlagNonfiniteProjection : 0u;
+                                mid[rt][r] = silu_portable(vg) * vu;
+                            }
+                            f |= !isfinite(mid[rt][r]) ? (kFlagNonfiniteMiddle | kFlagNonfiniteInput) : 0u;
+                            mflags[rt][r] = f;
+                        }
+#pragma unroll
+                    for (int rt = 0; rt < L; ++rt)
+#pragma unroll
+                        for (int r = 0; r < 4; ++r) {
+                            const int row = 16 * rt + 4 * q + r;
+                            flags |= row < nrows ? mflags[rt][r] : 0u;
+                            if (row < nrows) a.out[size_t(first + row) * kInter + 64 * nt + 16 * w + li] = mid[rt][r];
+#pragma unroll
+                            for (int ct = 0; ct < 2; ++ct) val[rt][ct][r] = 0.f;
+                        }
+                } else {
 #pragma unroll
                 for (int rt = 0; rt < L; ++rt) {
 #pragma unroll
                     for (int r = 0; r < 4; ++r) {
                         const int row = 16 * rt + 4 * q + r;
                         if (row < nrows) {
-                            if constexpr (GATEUP) {
-                                float vg = val[rt][0][r], vu = val[rt][1][r];
-                                float mid;
-                                if (shared) {
-                                    vg = bf16_round(vg);
-                                    vu = bf16_round(vu);
-                                    if (!isfinite(vg) || !isfinite(vu)) flags |= kFlagNonfiniteProjection;
-                                    mid = bf16_round(a.silu_table[__float_as_uint(vg) >> 16] * vu);
-                                } else {
-                                    if (!isfinite(vg) || !isfinite(vu)) flags |= kFlagNonfiniteProjection;
-                                    mid = silu_portable(vg) * vu;
-                                }
-                                if (!isfinite(mid)) flags |= kFlagNonfiniteMiddle | kFlagNonfiniteInput;
-                                a.out[size_t(first + row) * kInter + 64 * nt + 16 * w + li] = mid;
-                            } else {
+                            {
                                 const int route = s_route[row];
                                 const int col0 = kNT * (nt * NSUB + sub) + 32 * w + li;
 #pragma unroll
@@ -624,6 +664,7 @@ __global__ __launch_bounds__(256, GATEUP ? 2 : 3) void prefill_mfma_kernel(MfmaA
 #pragma unroll
                         for (int ct = 0; ct < 2; ++ct) val[rt][ct][r] = 0.f;
                     }
+                }
                 }
             }
         };
