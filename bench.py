@@ -49,15 +49,15 @@ DENSE_N = 6144
 # --copy-calibration); keyed by (kernel, tokens).  Commands and raw figures:
 # profiles/decode_n1_n32_hbm_traffic_pmc.md, profiles/prefill_1120_8192_hbm_traffic_pmc.md.
 MEASURED_TRAFFIC = {
-    ('route1', 1): 1162628, ('gateup1', 1): 9961807, ('down1', 1): 5125852,
-    ('route', 32): 2583516, ('topk', 32): 134473, ('sort', 32): 12783, ('gateup', 32): 176480764,
-    ('quant_middle', 32): 800766, ('down', 32): 90912586, ('reduce', 32): 2593294,
-    ('router', 1120): 14734302, ('topk', 1120): 1361783, ('act', 1120): 7040551,
-    ('gateup_mfma', 1120): 189109402, ('quant_middle', 1120): 26013078, ('down_mfma', 1120): 169427858,
-    ('reduce', 1120): 87585722,
-    ('router', 8192): 50978750, ('topk', 8192): 9338227, ('act', 8192): 50827495,
-    ('gateup_mfma', 8192): 623747520, ('quant_middle', 8192): 189703981, ('down_mfma', 8192): 844292265,
-    ('reduce', 8192): 639972559,
+    ('route1', 1): 1162556, ('gateup1', 1): 9951839, ('down1', 1): 5125692,
+    ('route', 32): 2583528, ('topk', 32): 128330, ('sort', 32): 12783, ('gateup', 32): 176480431,
+    ('quant_middle', 32): 792574, ('down', 32): 90912585, ('reduce', 32): 2593294,
+    ('router_act', 1120): 21199133, ('topk', 1120): 1395533, ('permute_scan', 1120): 760775,
+    ('permute_scatter', 1120): 335833, ('gateup_mfma', 1120): 189497152, ('quant_middle', 1120): 26013075,
+    ('down_mfma', 1120): 169431222, ('reduce', 1120): 87589739,
+    ('router', 8192): 51023188, ('topk', 8192): 9612526, ('permute_scan', 8192): 5286522,
+    ('permute_scatter', 8192): 1546388, ('act', 8192): 50827683, ('gateup_mfma', 8192): 623516069,
+    ('quant_middle', 8192): 189703930, ('down_mfma', 8192): 845859934, ('reduce', 8192): 639972378,
 }
 
 
