@@ -446,26 +446,6 @@ template <int M> __device__ __forceinline__ float butterfly_lane(float v) {
     return xor_perm_f<M>(v) + __uint_as_float(__float_as_uint(v) ^ flip);
 }
 
-// ---- split H128 of the single-token middle row ------------------------------
-// The producer of a 16-value run (k bits 0..3 of its H128 block) applies the
-// first four butterflies; the consumer holds 8 consecutive values per lane
-// (32 lanes per 256-group) with lane l' = lane & 31 holding chunk
-// half_chunk(l'), so the remaining butterflies (k bits 4, 5, 6 = chunk bits
-// 1, 2, 3) are lane bits 0, 1, 3: single DPP exchanges.
-__device__ __forceinline__ int half_chunk(int l) {
-    return ((l >> 2) & 1) | ((l & 1) << 1) | (((l >> 1) & 1) << 2) | (l & 0x18);
-}
-__device__ __forceinline__ void h128_tail_half(float v[8]) {
-#pragma unroll
-    for (int i = 0; i < 8; ++i) v[i] = butterfly_lane<1>(v[i]);
-#pragma unroll
-    for (int i = 0; i < 8; ++i) v[i] = butterfly_lane<2>(v[i]);
-#pragma unroll
-    for (int i = 0; i < 8; ++i) v[i] = butterfly_lane<8>(v[i]);
-#pragma unroll
-    for (int i = 0; i < 8; ++i) v[i] = v[i] * kInvSqrt128;
-}
-
 // quantize_half with the same results and fewer operations:
 //  - one fma(v, 0, acc) per value detects a non-finite value (the product is
 //    NaN exactly for inf and NaN); such lanes OR nonfinite_flags and zero
@@ -533,6 +513,82 @@ __device__ __forceinline__ void quantize_half_fast(float v[8], uint32_t words[2]
                ((uint32_t(q[6]) & 255u) << 24);
     words[1] = (uint32_t(q[1]) & 255u) | ((uint32_t(q[3]) & 255u) << 8) | ((uint32_t(q[5]) & 255u) << 16) |
                ((uint32_t(q[7]) & 255u) << 24);
+    sbits_out = sbits;
+    sum_out = sum;
+}
+
+// ---- strided half-wave layout of the single-token middle row ---------------
+// Lane l' = lane & 31 of a 256-group holds k = strided_base(l') + 16 j,
+// j = 0..7: k bits 0..3 and 7 come from the lane, k bits 4..6 from j, so the
+// H128 butterflies left after the producer's k bits 0..3 are in-register.
+__device__ __forceinline__ int strided_base(int l) { return (l & 15) | ((l >> 4) << 7); }
+__device__ __forceinline__ void h128_tail_strided(float v[8]) {
+#pragma unroll
+    for (int b = 1; b < 8; b <<= 1) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            if (i & b) continue;
+            const float lo = v[i], hi = v[i + b];
+            v[i] = lo + hi;
+            v[i + b] = lo - hi;
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i) v[i] = v[i] * kInvSqrt128;
+}
+// quantize_half_fast's arithmetic on the strided layout: q[j] of value j (the
+// caller places the bytes), fp16 scale bits and the group's sum of q.
+template <int QMAX>
+__device__ __forceinline__ void quantize_strided(float v[8], int q[8], uint16_t& sbits_out, int& sum_out,
+                                                 uint32_t& flags, uint32_t nonfinite_flags, uint32_t invalid_flag) {
+    float fin = 0.f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) fin = __builtin_fmaf(v[i], 0.f, fin);
+    if (fin != fin) {
+        flags |= nonfinite_flags;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) v[i] = isfinite(v[i]) ? v[i] : 0.f;
+    }
+    float absmax = 0.f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) absmax = fmaxf(absmax, fabsf(v[i]));
+    absmax = fmaxf(absmax, xor_perm_f<1>(absmax));
+    absmax = fmaxf(absmax, xor_perm_f<2>(absmax));
+    absmax = fmaxf(absmax, xor_perm_f<4>(absmax));
+    absmax = fmaxf(absmax, xor_perm_f<8>(absmax));
+    absmax = fmaxf(absmax, xor_perm_f<16>(absmax));
+    const float raw = fdiv_rn(absmax, float(QMAX));
+    const bool valid = isfinite(raw) && raw <= 65504.f;
+    if (!valid) flags |= invalid_flag;
+    const bool zero = absmax == 0.f || !valid;
+    const uint16_t sbits = f32_to_f16_bits(zero ? 1.f : fmaxf(raw, 0x1p-14f));
+    const float scale = f16_bits_to_f32(sbits);
+    const float rs = fdiv_rn(1.f, scale);
+    float qf[8];
+    bool near = false;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const float r = v[i] * rs;
+        const float n = __builtin_rintf(r);
+        near |= 0.5f - fabsf(r - n) <= 0x1p-14f;
+        qf[i] = n;
+    }
+    if (near) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) qf[i] = __builtin_rintf(fdiv_rn(v[i], scale));
+    }
+    int sum = 0;
+    const int keep = zero ? 0 : -1;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        q[i] = int(fminf(fmaxf(qf[i], -float(QMAX)), float(QMAX))) & keep;
+        sum += q[i];
+    }
+    sum += xor_perm_i<1>(sum);
+    sum += xor_perm_i<2>(sum);
+    sum += xor_perm_i<4>(sum);
+    sum += xor_perm_i<8>(sum);
+    sum += xor_perm_i<16>(sum);
     sbits_out = sbits;
     sum_out = sum;
 }

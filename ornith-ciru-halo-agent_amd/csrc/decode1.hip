@@ -94,8 +94,6 @@ __global__ __launch_bounds__(64) void decode1_route_kernel(DecodeArgs a) {
 #pragma unroll
         for (int e = 0; e < 8; ++e) if (!isfinite(v[e])) flags |= kFlagNonfiniteInput;
         h128_half(v);
-#pragma unroll
-        for (int e = 0; e < 8; ++e) if (!isfinite(v[e])) flags |= kFlagNonfiniteInput;
     } else {
 #pragma unroll
         for (int e = 0; e < 8; ++e) v[e] = 0.f;
@@ -103,7 +101,10 @@ __global__ __launch_bounds__(64) void decode1_route_kernel(DecodeArgs a) {
     uint32_t w2[2];
     uint16_t sb;
     int sum;
-    quantize_half<QMAX>(v, w2, sb, sum, flags, kFlagInvalidActivation);
+    // a non-finite transformed value raises both flags (as the separate check
+    // and the quantiser's own did)
+    quantize_half_fast<QMAX>(v, w2, sb, sum, flags, kFlagNonfiniteInput | kFlagInvalidActivation,
+                             kFlagInvalidActivation);
     *reinterpret_cast<uint2*>(a.x_words + job * 64 + 2 * lp) = make_uint2(w2[0], w2[1]);
     if (lp == 0) {
         a.x_scales[job] = sb;
@@ -234,7 +235,8 @@ __global__ __launch_bounds__(256) void decode1_gateup_kernel(DecodeArgs a) {
 // ---------------------------------------------------------------------------
 // D3: block = 16 output columns over all slots (9 waves).  Wave w quantises
 // slot w's middle row (H128 butterflies on k bits 4..6 + A8/A4 of both
-// groups, half-wave layout with chunk half_chunk(lane & 31)) while every
+// groups, strided half-wave layout: lane values 16 apart in k, so the
+// butterflies are in-register and each q is stored as a byte) while every
 // thread's down-code loads are in flight.  Thread: (slot i, group g) =
 // tid / 64 and lane / 32, chunk half h = (lane / 16) & 1, column n = lane & 15,
 // 16 code words in registers; the two halves' integer dots are added exactly,
@@ -257,10 +259,11 @@ __global__ __launch_bounds__(576) void decode1_down_kernel(DecodeArgs a) {
     const int id_in = a.reduce_ids[tid & 7];
     const float w_in = a.reduce_w[tid & 7];
     __builtin_amdgcn_sched_barrier(0);                 // keep the routing loads oldest
-    const int lp = lane & 31, gm = lane >> 5, ch = half_chunk(lp);
-    const float* mrow = a.middle + size_t(wave < nslots ? wave : nslots - 1) * kInter + gm * kGroup + ch * 8;
-    const float4 m0 = *reinterpret_cast<const float4*>(mrow);
-    const float4 m1 = *reinterpret_cast<const float4*>(mrow + 4);
+    const int lp = lane & 31, gm = lane >> 5, kb = strided_base(lp);
+    const float* mrow = a.middle + size_t(wave < nslots ? wave : nslots - 1) * kInter + gm * kGroup + kb;
+    float mv[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) mv[j] = mrow[16 * j];
     const uint16_t shared_logit = SHARED ? a.shared_logit[0] : 0;
     if (tid < kTop) {
         lbank[tid] = (id_in >= 0 && id_in < kExperts) ? id_in : -1;
@@ -285,14 +288,20 @@ __global__ __launch_bounds__(576) void decode1_down_kernel(DecodeArgs a) {
     // ---- middle quantisation, one slot per wave ----
     uint32_t flags = 0;
     if (bank >= 0) {
-        float v[8] = {m0.x, m0.y, m0.z, m0.w, m1.x, m1.y, m1.z, m1.w};
-        h128_tail_half(v);
-        uint32_t w2[2];
+        float v[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) v[j] = mv[j];
+        h128_tail_strided(v);
+        int qv[8];
         uint16_t sb;
         int sum;
-        quantize_half_fast<QMAX>(v, w2, sb, sum, flags, kFlagNonfiniteInput | kFlagInvalidActivation,
-                                 kFlagInvalidActivation);
-        *reinterpret_cast<uint2*>(&la[(2 * i + gm) * 64 + 2 * ch]) = make_uint2(w2[0], w2[1]);
+        quantize_strided<QMAX>(v, qv, sb, sum, flags, kFlagNonfiniteInput | kFlagInvalidActivation,
+                               kFlagInvalidActivation);
+        // value j (k = kb + 16 j) is byte (k & 7) >> 1 of word 2 (k >> 3) + (k & 1)
+        uint8_t* lb = reinterpret_cast<uint8_t*>(&la[(2 * i + gm) * 64]);
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+            lb[4 * (2 * ((kb >> 3) + 2 * j) + (kb & 1)) + ((kb & 7) >> 1)] = uint8_t(qv[j]);
         if (lp == 0) {
             const float sc = f16_bits_to_f32(sb);
             lsa[2 * i + gm] = sc;
