@@ -47,8 +47,6 @@ __device__ __forceinline__ void act_bf16_block(int block, const uint16_t* __rest
 #pragma unroll
         for (int e = 0; e < 16; ++e) if (!isfinite(v[e])) flags |= flag_input;
         h128_quarter(v);
-#pragma unroll
-        for (int e = 0; e < 16; ++e) if (!isfinite(v[e])) flags |= flag_input;
     } else {
 #pragma unroll
         for (int e = 0; e < 16; ++e) v[e] = 0.f;
@@ -56,7 +54,9 @@ __device__ __forceinline__ void act_bf16_block(int block, const uint16_t* __rest
     uint32_t w4[4];
     uint16_t sbits;
     int sum;
-    quantize_quarter<QMAX>(v, w4, sbits, sum, flags, flag_act);
+    // a non-finite transformed value raises both flags (as the separate check
+    // and the quantiser's own did)
+    quantize_quarter_fast<QMAX>(v, w4, sbits, sum, flags, flag_input | flag_act, flag_act);
     if (g < total) {
         *reinterpret_cast<uint4*>(words + size_t(g) * 64 + k0 / 4) = make_uint4(w4[0], w4[1], w4[2], w4[3]);
         if (l == 0) { scales[g] = sbits; sums[g] = sum; }

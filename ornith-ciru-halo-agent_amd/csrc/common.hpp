@@ -390,6 +390,72 @@ __device__ __forceinline__ void quantize_quarter(float v[16], uint32_t words[4],
     sum_out = sum;
 }
 
+// quantize_quarter with the arithmetic of quantize_half_fast (one fma per
+// value detects non-finite values, which OR nonfinite_flags and are zeroed;
+// q = rint(v * RN(1/scale)) with the exact fallback near half-integers):
+// the same words, scale and sum.
+template <int QMAX>
+__device__ __forceinline__ void quantize_quarter_fast(float v[16], uint32_t words[4], uint16_t& sbits_out,
+                                                      int& sum_out, uint32_t& flags, uint32_t nonfinite_flags,
+                                                      uint32_t invalid_flag) {
+    float fin = 0.f;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) fin = __builtin_fmaf(v[i], 0.f, fin);
+    if (fin != fin) {
+        flags |= nonfinite_flags;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) v[i] = isfinite(v[i]) ? v[i] : 0.f;
+    }
+    float absmax = 0.f;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) absmax = fmaxf(absmax, fabsf(v[i]));
+    absmax = fmaxf(absmax, row_ror_f<4>(absmax));
+    absmax = fmaxf(absmax, row_ror_f<8>(absmax));
+    absmax = fmaxf(absmax, xor_perm_f<1>(absmax));
+    absmax = fmaxf(absmax, xor_perm_f<2>(absmax));
+    const float raw = fdiv_rn(absmax, float(QMAX));
+    const bool valid = isfinite(raw) && raw <= 65504.f;
+    if (!valid) flags |= invalid_flag;
+    const bool zero = absmax == 0.f || !valid;
+    const uint16_t sbits = f32_to_f16_bits(zero ? 1.f : fmaxf(raw, 0x1p-14f));
+    const float scale = f16_bits_to_f32(sbits);
+    const float rs = fdiv_rn(1.f, scale);
+    float qf[16];
+    bool near = false;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        const float r = v[i] * rs;
+        const float n = __builtin_rintf(r);
+        near |= 0.5f - fabsf(r - n) <= 0x1p-14f;
+        qf[i] = n;
+    }
+    if (near) {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) qf[i] = __builtin_rintf(fdiv_rn(v[i], scale));
+    }
+    int q[16], sum = 0;
+    const int keep = zero ? 0 : -1;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        q[i] = int(fminf(fmaxf(qf[i], -float(QMAX)), float(QMAX))) & keep;
+        sum += q[i];
+    }
+    sum += row_ror_i<4>(sum);
+    sum += row_ror_i<8>(sum);
+    sum += xor_perm_i<1>(sum);
+    sum += xor_perm_i<2>(sum);
+#pragma unroll
+    for (int c = 0; c < 2; ++c) {
+        const int* qc = q + 8 * c;
+        words[2 * c] = (uint32_t(qc[0]) & 255u) | ((uint32_t(qc[2]) & 255u) << 8) | ((uint32_t(qc[4]) & 255u) << 16) |
+                       ((uint32_t(qc[6]) & 255u) << 24);
+        words[2 * c + 1] = (uint32_t(qc[1]) & 255u) | ((uint32_t(qc[3]) & 255u) << 8) |
+                           ((uint32_t(qc[5]) & 255u) << 16) | ((uint32_t(qc[7]) & 255u) << 24);
+    }
+    sbits_out = sbits;
+    sum_out = sum;
+}
+
 // Group quantisation of the half-wave layout (same arithmetic as
 // quantize_group_wave).  Every lane of the half gets the group's fp16 scale
 // bits and Σq; lane l' gets its two activation words 2l' = (q0,q2,q4,q6) and

@@ -73,8 +73,6 @@ __global__ __launch_bounds__(256) void decode_route_kernel(DecodeArgs a, int rou
 #pragma unroll
         for (int e = 0; e < 8; ++e) if (!isfinite(v[e])) flags |= kFlagNonfiniteInput;
         h128_half(v);
-#pragma unroll
-        for (int e = 0; e < 8; ++e) if (!isfinite(v[e])) flags |= kFlagNonfiniteInput;
     } else {
 #pragma unroll
         for (int e = 0; e < 8; ++e) v[e] = 0.f;
@@ -82,7 +80,8 @@ __global__ __launch_bounds__(256) void decode_route_kernel(DecodeArgs a, int rou
     uint32_t w2[2];
     uint16_t sb;
     int sum;
-    quantize_half<QMAX>(v, w2, sb, sum, flags, kFlagInvalidActivation);
+    quantize_half_fast<QMAX>(v, w2, sb, sum, flags, kFlagNonfiniteInput | kFlagInvalidActivation,
+                             kFlagInvalidActivation);
     const size_t g = size_t(tok) * 8 + job;
     *reinterpret_cast<uint2*>(a.x_words + g * 64 + 2 * lp) = make_uint2(w2[0], w2[1]);
     if (lp == 0) {

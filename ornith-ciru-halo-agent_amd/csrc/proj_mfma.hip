@@ -754,12 +754,11 @@ __global__ __launch_bounds__(256) void quant_middle_permuted_kernel(const float*
     }
     uint32_t flags = 0;
     h128_quarter(v);
-#pragma unroll
-    for (int e = 0; e < 16; ++e) if (!isfinite(v[e])) flags |= kFlagNonfiniteInput;
     uint32_t w4[4];
     uint16_t sbits;
     int sum;
-    quantize_quarter<QMAX>(v, w4, sbits, sum, flags, kFlagInvalidActivation);
+    quantize_quarter_fast<QMAX>(v, w4, sbits, sum, flags, kFlagNonfiniteInput | kFlagInvalidActivation,
+                                kFlagInvalidActivation);
     if (g < total) {
         *reinterpret_cast<uint4*>(words + size_t(g) * 64 + k0 / 4) = make_uint4(w4[0], w4[1], w4[2], w4[3]);
         if (l == 0) { scales[g] = sbits; sums[g] = sum; }
