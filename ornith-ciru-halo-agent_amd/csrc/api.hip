@@ -492,7 +492,8 @@ extern "C" hipError_t ornith_dense_g256_head_launch(const void* input, const voi
     if (bytes < ornith_dense_g256_head_workspace_bytes(Mcap, N)) return hipErrorInvalidValue;
     if (M == 0) return hipSuccess;
     if (!input || !codes || !metadata || !workspace || !logits_f32 || !argmax_i64 || !flags || !aligned(input, 8) ||
-        !aligned(codes, 16) || !aligned(workspace, 256) || !aligned(logits_f32, 4) || !aligned(argmax_i64, 8))
+        !aligned(codes, 16) || !aligned(workspace, 256) || !aligned(logits_f32, 16) ||
+        (logits_bf16 && !aligned(logits_bf16, 8)) || !aligned(argmax_i64, 8))
         return hipErrorInvalidValue;
     const size_t m = size_t(Mcap);
     const size_t scales = align256(m * kHidden), sums = scales + align256(m * (kHidden / kGroup) * 2);

@@ -8,19 +8,15 @@
 // value = value + (RN(sw*RN(sa*dot)) + RN(off*RN(sa*sum))) runs in ascending
 // group order on the VALU.
 //
-// Tile: one block (4 waves) per (segment m-tile of 64 routes, 128 columns).
-// Per group: the 64 gathered activation rows (256 int8 each) and the codes of
-// the 128 columns, unpacked once to int8, are staged in LDS; the next group's
-// global loads are issued into registers before the current group's MFMAs.
 // MFMA operand layout (verified on gfx950): lane i+16q supplies the 16 bytes
 // of row/column i for k-group q, A and B bytes pair positionally, and output
 // register r of lane l is C[4*(l/16)+r][l%16].  Both operands use this
 // build's byte order (even codes then odd codes per 8-value chunk), so the
 // logical k pairing matches and the integer dot is exact.
 //
-// Gate/up: the block's 128 columns are 64 gate columns and the matching 64 up
-// columns, laid out so that one lane holds the gate and up accumulators of
-// the same (route, column) and writes SiLU(gate)*up directly.
+// The same kernel body serves the routed gate/up and down projections of the
+// permuted routes and the quantised LM head (one row tile of up to 64 rows
+// over the whole vocabulary, logits and per-block argmax partials out).
 #include "kernels.hpp"
 #include "timing.hpp"
 #include "decode.hpp"
@@ -28,7 +24,7 @@
 
 namespace ornith {
 
-constexpr int kMT = 64, kNT = 128, kRowWords = 68;   // 64 words (256 int8) + 4 pad
+constexpr int kMT = 64, kNT = 128;   // routes per m-tile, columns per column block
 
 // Integer dots start from the bits of kDotBias = 1.5 * 2^23, so the int32
 // result read as fp32 is kDotBias + dot exactly (|dot| < 2^19 << 2^22); with
@@ -48,295 +44,6 @@ __device__ __forceinline__ bool arg_better(float a, int ia, float b, int ib) {
     if (na != nb) return na;
     if (na) return ia < ib;
     return a > b || (a == b && ia < ib);
-}
-
-template <int MODE, int GS, int DEPTH>
-__global__ __launch_bounds__(256, 2) void grouped_mfma_kernel(MfmaArgs a) {
-    constexpr bool GATEUP = MODE == kModeGateUp, HEAD = MODE == kModeHead;
-    __shared__ uint32_t sA[kMT * kRowWords];
-    __shared__ uint32_t sB[kNT * kRowWords];
-    __shared__ float s_sa[kMT], s_ss[kMT], s_sw[kNT], s_off[kNT];
-    __shared__ int s_route[kMT], s_row[kMT];
-
-    // Linear block b -> (m-tile b / NCB, column block b % NCB).  Workgroups go
-    // to the 8 XCDs round-robin, so every XCD sees the same column blocks of
-    // all m-tiles: an expert's column slice is fetched into one L2 and reused
-    // by the expert's following m-tiles there.
-    const int ncb = HEAD ? int(gridDim.x) : (GATEUP ? (2 * kInter) / kNT : kHidden / kNT);
-    const int nt = int(blockIdx.x) % ncb, mtile = int(blockIdx.x) / ncb;
-    Segment sg{0, 0, a.R, 0};
-    int r0 = 0;
-    if (!HEAD) {
-        if (mtile >= a.ntiles[0]) return;
-        const Segment td = a.tiles[mtile];
-        sg = Segment{td.bank, td.first, td.count, 0};
-    }
-    const int nrows = min(kMT, sg.count - r0);
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int wm = wave & 1, wn = wave >> 1;
-    const bool shared = !HEAD && sg.bank == kShared;
-    const uint32_t* codes = shared ? a.shared_codes : a.codes + size_t(sg.bank) * a.bank_words;
-    const uint32_t* meta = shared ? a.shared_meta : a.meta + size_t(sg.bank) * a.bank_meta_words;
-
-    if (tid < kMT) {
-        int route = -1, row = 0;
-        if (tid < nrows) {
-            route = HEAD ? tid : a.routes[sg.first + r0 + tid];
-            row = GATEUP ? (route < a.R ? route / kTop : route - a.R) : route;
-        }
-        s_route[tid] = route;
-        s_row[tid] = row;
-    }
-    // block column bc (0..127) -> n32 tile and column inside it; the head's
-    // last block clamps tiles past N to the last one (loaded, never written)
-    auto ntile_of = [&](int blk) {      // blk: 32-column block 0..3 of this block
-        if (GATEUP) return (blk < 2 ? 2 * nt + blk : 16 + 2 * nt + (blk - 2));
-        if (HEAD) return min(4 * nt + blk, a.N / 32 - 1);
-        return 4 * nt + blk;
-    };
-    __syncthreads();
-
-    // ---- staging loads of one group into a register slot ----
-    u32x4 ra[DEPTH][4], rb[DEPTH][4];
-    uint32_t rmeta[DEPTH];
-    uint32_t rsa[DEPTH];                // raw fp16 scale bits; converted at store time so that
-    int rsum[DEPTH];                    // no use of a load result sits behind the prefetch
-    const int a_row = tid >> 2, a_part = tid & 3;
-    // B staging: wave b_blk takes 32-column block b_blk; lane b_sub takes chunk
-    // row j = b_sub % 32 and columns 16 * (b_sub / 32) .. +15 (16 packed
-    // words).  Consecutive lanes hold consecutive chunk rows, so the unpacked
-    // int8 stores of a wave hit distinct LDS banks.
-    const int b_blk = tid >> 6, b_sub = tid & 63, b_j = b_sub & 31, b_half = b_sub >> 5;
-    // Every lane issues every load (dead rows read activation row s_row = 0 of
-    // a live tile and are dropped by the epilogue), so the in-order load
-    // counter stays exact and the waits leave the prefetched groups in flight.
-    const size_t a_base = size_t(s_row[a_row]) * (GS * 64) + a_part * 16;
-    const size_t m_base = size_t(ntile_of((tid & 127) >> 5)) * GS * 32 + (tid & 31);
-    const size_t s_base = size_t(s_row[tid & 63]) * GS;
-    auto load_group = [&](int g, int slot) {
-        const uint32_t* src = a.act_words + a_base + g * 64;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) ra[slot][i] = *reinterpret_cast<const u32x4*>(src + 4 * i);
-        const uint32_t* bsrc = codes + (size_t(ntile_of(b_blk)) * GS + g) * 1024 + b_j * 32 + b_half * 16;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) rb[slot][i] = *reinterpret_cast<const u32x4*>(bsrc + 4 * i);
-        rmeta[slot] = meta[m_base + g * 32];
-        rsa[slot] = a.act_scales[s_base + g];
-        rsum[slot] = a.act_sums[s_base + g];
-    };
-    auto store_group = [&](int slot) {
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-            *reinterpret_cast<u32x4*>(&sA[a_row * kRowWords + a_part * 16 + 4 * i]) = ra[slot][i];
-        // unpack: packed word (chunk j, column n) -> int8 words 2j (even k) and 2j+1 (odd k) of column n
-        const int j = b_j, c0 = b_blk * 32 + b_half * 16;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const uint32_t w[4] = {rb[slot][i].x, rb[slot][i].y, rb[slot][i].z, rb[slot][i].w};
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const int col = c0 + 4 * i + e;
-                *reinterpret_cast<uint2*>(&sB[col * kRowWords + 2 * j]) =
-                    make_uint2(uint32_t(code_even(w[e])), uint32_t(code_odd(w[e])));
-            }
-        }
-        if (tid < kNT) {
-            s_sw[tid] = f16_bits_to_f32(rmeta[slot] & 0xffffu);
-            s_off[tid] = f16_bits_to_f32(rmeta[slot] >> 16);
-        }
-        if (tid < kMT) {
-            const float sa = f16_bits_to_f32(uint16_t(rsa[slot]));
-            s_sa[tid] = sa;
-            s_ss[tid] = sa * float(rsum[slot]);
-        }
-    };
-
-    // wave tiles: 2 row tiles (16 rows) x 4 column tiles (16 columns)
-    int colbase[4];
-#pragma unroll
-    for (int ct = 0; ct < 4; ++ct)
-        colbase[ct] = GATEUP ? ((ct < 2 ? 0 : 64) + 32 * wn + 16 * (ct & 1)) : (64 * wn + 16 * ct);
-    const int q = lane >> 4, li = lane & 15;
-    // wave-uniform: does row tile rt (rows 32wm+16rt .. +15) hold a live row?
-    const bool live[2] = {32 * wm < nrows, 32 * wm + 16 < nrows};
-    float val[2][4][4];
-#pragma unroll
-    for (int rt = 0; rt < 2; ++rt)
-#pragma unroll
-        for (int ct = 0; ct < 4; ++ct)
-#pragma unroll
-            for (int r = 0; r < 4; ++r) val[rt][ct][r] = 0.f;
-
-#pragma unroll
-    for (int g = 0; g < DEPTH; ++g) load_group(g, g);
-    static_assert(GS % DEPTH == 0, "group ring must divide the group count");
-    // one group step; the ring slot D is a compile-time constant so the
-    // register ring never becomes an indexed private array
-    auto step = [&]<int D, bool PREFETCH>(int g) {
-        __syncthreads();                    // previous group's readers are done
-        constexpr int d = D;
-        store_group(d);
-        __syncthreads();
-        if constexpr (PREFETCH) load_group(g + DEPTH, d);   // DEPTH groups stay in flight
-        i32x4 acc[2][4];
-#pragma unroll
-        for (int rt = 0; rt < 2; ++rt)
-#pragma unroll
-            for (int ct = 0; ct < 4; ++ct) acc[rt][ct] = i32x4{0, 0, 0, 0};
-        if (!live[0]) return;                           // both row tiles past the segment's rows
-#pragma unroll
-        for (int s = 0; s < 4; ++s) {
-            i32x4 fa[2], fb[4];
-#pragma unroll
-            for (int rt = 0; rt < 2; ++rt) {
-                const uint4 v = *reinterpret_cast<const uint4*>(&sA[(32 * wm + 16 * rt + li) * kRowWords + 16 * s + 4 * q]);
-                fa[rt] = i32x4{int(v.x), int(v.y), int(v.z), int(v.w)};
-            }
-#pragma unroll
-            for (int ct = 0; ct < 4; ++ct) {
-                const uint4 v = *reinterpret_cast<const uint4*>(&sB[(colbase[ct] + li) * kRowWords + 16 * s + 4 * q]);
-                fb[ct] = i32x4{int(v.x), int(v.y), int(v.z), int(v.w)};
-            }
-#pragma unroll
-            for (int ct = 0; ct < 4; ++ct)
-                acc[0][ct] = __builtin_amdgcn_mfma_i32_16x16x64_i8(fa[0], fb[ct], acc[0][ct], 0, 0, 0);
-            if (live[1]) {
-#pragma unroll
-                for (int ct = 0; ct < 4; ++ct)
-                    acc[1][ct] = __builtin_amdgcn_mfma_i32_16x16x64_i8(fa[1], fb[ct], acc[1][ct], 0, 0, 0);
-            }
-        }
-        // fp32 group tree (dense_g256_api.h:35-37), row tiles with live rows only
-#pragma unroll
-        for (int rt = 0; rt < 2; ++rt) {
-            if (!live[rt]) continue;
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const int row = 32 * wm + 16 * rt + 4 * q + r;
-                const float sa = s_sa[row], ss = s_ss[row];
-#pragma unroll
-                for (int ct = 0; ct < 4; ++ct) {
-                    const int col = colbase[ct] + li;
-                    const float scaled_dot = sa * float(acc[rt][ct][r]);
-                    const float product = s_sw[col] * scaled_dot;
-                    const float correction = s_off[col] * ss;
-                    val[rt][ct][r] = val[rt][ct][r] + (product + correction);
-                }
-            }
-        }
-    };
-    // body with prefetch, then the last DEPTH groups without (straight-line
-    // code, so every wait count is exact)
-#pragma unroll 1
-    for (int g0 = 0; g0 < GS - DEPTH; g0 += DEPTH)
-        [&]<int... D>(std::integer_sequence<int, D...>) {
-            (step.template operator()<D, true>(g0 + D), ...);
-        }(std::make_integer_sequence<int, DEPTH>{});
-    [&]<int... D>(std::integer_sequence<int, D...>) {
-        (step.template operator()<D, false>(GS - DEPTH + D), ...);
-    }(std::make_integer_sequence<int, DEPTH>{});
-
-    // ---- epilogue ----
-    uint32_t flags = 0;
-#pragma unroll
-    for (int rt = 0; rt < 2; ++rt) {
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const int row = 32 * wm + 16 * rt + 4 * q + r;
-            if (row >= nrows) continue;
-            const int route = s_route[row];
-            if (GATEUP) {
-#pragma unroll
-                for (int ct = 0; ct < 2; ++ct) {
-                    float vg = val[rt][ct][r], vu = val[rt][ct + 2][r];
-                    float mid;
-                    if (shared) {
-                        vg = bf16_round(vg);
-                        vu = bf16_round(vu);
-                        if (!isfinite(vg) || !isfinite(vu)) flags |= kFlagNonfiniteProjection;
-                        mid = bf16_round(a.silu_table[__float_as_uint(vg) >> 16] * vu);
-                    } else {
-                        if (!isfinite(vg) || !isfinite(vu)) flags |= kFlagNonfiniteProjection;
-                        mid = silu_portable(vg) * vu;
-                    }
-                    if (!isfinite(mid)) flags |= kFlagNonfiniteMiddle | kFlagNonfiniteInput;
-                    a.out[size_t(route) * kInter + 64 * nt + colbase[ct] + li] = mid;
-                }
-            } else if (HEAD) {
-#pragma unroll
-                for (int ct = 0; ct < 4; ++ct) {
-                    const int col = kNT * nt + colbase[ct] + li;
-                    if (col >= a.N) continue;
-                    const float v = val[rt][ct][r];
-                    const size_t o = size_t(route) * a.N + col;
-                    const uint16_t b = f32_to_bf16_bits(v);
-                    if (!isfinite(v)) flags |= a.flag_projection;
-                    if ((b & 0x7f80u) == 0x7f80u) flags |= a.flag_bf16;
-                    a.out[o] = v;
-                    if (a.out_bf16) a.out_bf16[o] = b;
-                }
-            } else {
-#pragma unroll
-                for (int ct = 0; ct < 4; ++ct) {
-                    float v = val[rt][ct][r];
-                    if (shared) v = bf16_round(v);
-                    if (!isfinite(v)) flags |= kFlagNonfiniteProjection;
-                    a.out[size_t(route) * kHidden + kNT * nt + colbase[ct] + li] = v;
-                }
-            }
-        }
-    }
-    if constexpr (HEAD) {
-        // per-row best of this block's 128 columns: lane (4 columns, ascending),
-        // then the 16 lanes of the row group (xor 1..8), then the two column
-        // halves (waves wn = 0, 1) through LDS
-        __shared__ float s_bv[2][kMT];
-        __shared__ int s_bi[2][kMT];
-#pragma unroll
-        for (int rt = 0; rt < 2; ++rt) {
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                float bv = 0.f;
-                int bi = 0x7fffffff;
-#pragma unroll
-                for (int ct = 0; ct < 4; ++ct) {
-                    const int col = kNT * nt + colbase[ct] + li;
-                    if (col < a.N && (bi == 0x7fffffff || arg_better(val[rt][ct][r], col, bv, bi))) {
-                        bv = val[rt][ct][r];
-                        bi = col;
-                    }
-                }
-#define ORNITH_ARG_STEP(M)                                                                       \
-                {                                                                                \
-                    const float ov = xor_perm_f<M>(bv);                                          \
-                    const int oi = xor_perm_i<M>(bi);                                            \
-                    if (oi != 0x7fffffff && (bi == 0x7fffffff || arg_better(ov, oi, bv, bi))) { \
-                        bv = ov;                                                                 \
-                        bi = oi;                                                                 \
-                    }                                                                            \
-                }
-                ORNITH_ARG_STEP(1)
-                ORNITH_ARG_STEP(2)
-                ORNITH_ARG_STEP(4)
-                ORNITH_ARG_STEP(8)
-#undef ORNITH_ARG_STEP
-                const int row = 32 * wm + 16 * rt + 4 * q + r;
-                if (li == 0) { s_bv[wn][row] = bv; s_bi[wn][row] = bi; }
-            }
-        }
-        __syncthreads();
-        if (tid < nrows) {
-            float bv = s_bv[0][tid];
-            int bi = s_bi[0][tid];
-            const float ov = s_bv[1][tid];
-            const int oi = s_bi[1][tid];
-            if (oi != 0x7fffffff && (bi == 0x7fffffff || arg_better(ov, oi, bv, bi))) { bv = ov; bi = oi; }
-            const int nblk = (a.N + kNT - 1) / kNT;
-            a.arg_val[size_t(tid) * nblk + nt] = bv;
-            a.arg_idx[size_t(tid) * nblk + nt] = bi;
-        }
-    }
-    flag_or(a.sticky, flags);
 }
 
 // Per-row combination of the head's block partials (numpy argmax rule).
@@ -398,8 +105,10 @@ __global__ __launch_bounds__(256) void head_argmax_kernel(const float* __restric
 // and 4 row tiles of 16 rows, so partial tiles skip dead row tiles without
 // branches.
 // ---------------------------------------------------------------------------
-template <bool GATEUP, int GS, int NSUB, int DB>
-__global__ __launch_bounds__(256, GATEUP ? 2 : 3) void prefill_mfma_kernel(MfmaArgs a) {
+template <int MODE, int GS, int NSUB, int DB, int MAXL = 4>
+__global__ __launch_bounds__(256, MODE == kModeDown ? 3 : 2) void prefill_mfma_kernel(MfmaArgs a) {
+    constexpr bool GATEUP = MODE == kModeGateUp, HEAD = MODE == kModeHead;
+    constexpr bool BIAS = GATEUP || HEAD;                     // dots start from kDotBias
     constexpr int NSTEP = GS * NSUB;
     constexpr int KW = GS * 64;                               // activation words per row
     constexpr int NCB = GATEUP ? (2 * kInter) / kNT : kHidden / (kNT * NSUB);
@@ -408,8 +117,10 @@ __global__ __launch_bounds__(256, GATEUP ? 2 : 3) void prefill_mfma_kernel(MfmaA
     __shared__ __attribute__((aligned(16))) uint32_t sA[NSTAGE][kMT * 64];
     __shared__ __attribute__((aligned(16))) float s_sa[NSTAGE][kMT];
     __shared__ __attribute__((aligned(16))) float s_ss[NSTAGE][kMT];
-    __shared__ __attribute__((aligned(16))) float s_nb[GATEUP ? NSTAGE : 1][kMT];   // -sa * kDotBias (exact)
+    __shared__ __attribute__((aligned(16))) float s_nb[BIAS ? NSTAGE : 1][kMT];   // -sa * kDotBias (exact)
     __shared__ int s_route[kMT];
+    __shared__ float s_bv[HEAD ? 4 : 1][kMT];                 // head: per-wave row best
+    __shared__ int s_bi[HEAD ? 4 : 1][kMT];
 
     // Workgroups go to the 8 XCDs round-robin (linear block L runs on XCD
     // L % 8).  Two block orders:
@@ -420,14 +131,23 @@ __global__ __launch_bounds__(256, GATEUP ? 2 : 3) void prefill_mfma_kernel(MfmaA
     //    m-tile 8q + x, so all column blocks of a tile share one L2 (its
     //    activation rows are fetched once) and each XCD walks every 8th tile.
     //    At large T (full tiles, heavy experts) this cuts the L2 misses ~3x.
-    const int ntiles = a.ntiles[0];
+    // Head: one m-tile of the a.R input rows, block L = column block L.
     const int L = int(blockIdx.x);
-    const int nt = a.tile_xcd ? (L >> 3) % NCB : L % NCB;
-    const int mtile = a.tile_xcd ? 8 * (L / (8 * NCB)) + (L & 7) : L / NCB;
-    if (mtile >= ntiles) return;
-    const Segment td = a.tiles[mtile];
+    int nt, mtile;
+    Segment td;
+    if constexpr (HEAD) {
+        nt = L;
+        mtile = 0;
+        td = Segment{0, 0, a.R, 0};
+    } else {
+        const int ntiles = a.ntiles[0];
+        nt = a.tile_xcd ? (L >> 3) % NCB : L % NCB;
+        mtile = a.tile_xcd ? 8 * (L / (8 * NCB)) + (L & 7) : L / NCB;
+        if (mtile >= ntiles) return;
+        td = a.tiles[mtile];
+    }
     const int bank = td.bank, first = td.first, nrows = td.count;
-    const bool shared = bank == kShared;
+    const bool shared = !HEAD && bank == kShared;
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, li = lane & 15, q = lane >> 4;
     const uint32_t* codes = shared ? a.shared_codes : a.codes + size_t(bank) * a.bank_words;
     const uint32_t* meta = shared ? a.shared_meta : a.meta + size_t(bank) * a.bank_meta_words;
@@ -438,8 +158,8 @@ __global__ __launch_bounds__(256, GATEUP ? 2 : 3) void prefill_mfma_kernel(MfmaA
     // an access outside the activation / output buffers)
     const int a_r = tid >> 2, a_part = tid & 3;
     const int rmax = a.R + (a.shared_codes ? a.R / kTop : 0) - 1;
-    const int route_a = min(max(a.routes[first + min(a_r, nrows - 1)], 0), rmax);
-    const int route_s = min(max(a.routes[first + min(tid & 63, nrows - 1)], 0), rmax);
+    const int route_a = HEAD ? 0 : min(max(a.routes[first + min(a_r, nrows - 1)], 0), rmax);
+    const int route_s = HEAD ? 0 : min(max(a.routes[first + min(tid & 63, nrows - 1)], 0), rmax);
 
     // ---- B: code words of step st for this lane ----
     // column tile ct of step st: 32-column code tile and the column in it
@@ -449,8 +169,10 @@ __global__ __launch_bounds__(256, GATEUP ? 2 : 3) void prefill_mfma_kernel(MfmaA
             ntile = (ct ? kInter / 32 : 0) + (c >> 5);
             n = c & 31;
         } else {
+            // down / head: 32 columns per wave (the head's last block may
+            // reach past N: its tiles repeat the last one, never stored)
             const int base = kNT * (nt * NSUB + st / GS);
-            ntile = (base >> 5) + w;
+            ntile = HEAD ? min((base >> 5) + w, a.N / 32 - 1) : (base >> 5) + w;
             n = 16 * ct + li;
         }
     };
@@ -502,7 +224,7 @@ __global__ __launch_bounds__(256, GATEUP ? 2 : 3) void prefill_mfma_kernel(MfmaA
             const float sa = f16_bits_to_f32(uint16_t(rsa[slot]));
             s_sa[stage][tid] = sa;
             s_ss[stage][tid] = sa * float(rsum[slot]);
-            if constexpr (GATEUP) s_nb[stage][tid] = -sa * kDotBias;
+            if constexpr (BIAS) s_nb[stage][tid] = -sa * kDotBias;
         }
     };
     // A(0) and A(1) in flight together (A(1) through prologue-only registers)
@@ -536,10 +258,11 @@ __global__ __launch_bounds__(256, GATEUP ? 2 : 3) void prefill_mfma_kernel(MfmaA
                 for (int r = 0; r < 4; ++r) val[rt][ct][r] = 0.f;
         i32x4 acc[4][2];
         float swv[2], offv[2];
-        // gate/up dots start from kDotBias (see kDotBias); the down kernel keeps
-        // the conversion (measured: the bias costs it more than it saves there)
-        constexpr i32x4 kAccInit = GATEUP ? i32x4{kDotBiasBits, kDotBiasBits, kDotBiasBits, kDotBiasBits}
-                                          : i32x4{0, 0, 0, 0};
+        // gate/up and head dots start from kDotBias (see kDotBias); the down
+        // kernel keeps the conversion (measured: the bias costs it more than it
+        // saves there)
+        constexpr i32x4 kAccInit = BIAS ? i32x4{kDotBiasBits, kDotBiasBits, kDotBiasBits, kDotBiasBits}
+                                        : i32x4{0, 0, 0, 0};
 
         // matrix-core dots of step ST for the L live row tiles (rows past
         // nrows in them hold copies of a live row)
@@ -582,8 +305,8 @@ __global__ __launch_bounds__(256, GATEUP ? 2 : 3) void prefill_mfma_kernel(MfmaA
             for (int rt = 0; rt < L; ++rt) {
                 const float4 sa4 = *reinterpret_cast<const float4*>(&s_sa[stage][16 * rt + 4 * q]);
                 const float4 ss4 = *reinterpret_cast<const float4*>(&s_ss[stage][16 * rt + 4 * q]);
-                const float4 nb4 = GATEUP ? *reinterpret_cast<const float4*>(&s_nb[GATEUP ? stage : 0][16 * rt + 4 * q])
-                                          : float4{0.f, 0.f, 0.f, 0.f};
+                const float4 nb4 = BIAS ? *reinterpret_cast<const float4*>(&s_nb[BIAS ? stage : 0][16 * rt + 4 * q])
+                                        : float4{0.f, 0.f, 0.f, 0.f};
                 const float sa[4] = {sa4.x, sa4.y, sa4.z, sa4.w}, ss[4] = {ss4.x, ss4.y, ss4.z, ss4.w};
                 const float nb[4] = {nb4.x, nb4.y, nb4.z, nb4.w};
 #pragma unroll
@@ -591,8 +314,8 @@ __global__ __launch_bounds__(256, GATEUP ? 2 : 3) void prefill_mfma_kernel(MfmaA
 #pragma unroll
                     for (int ct = 0; ct < 2; ++ct) {
                         // gate/up: acc holds the bits of kDotBias + dot, one fma gives RN(sa * dot)
-                        const float scaled_dot = GATEUP ? __builtin_fmaf(sa[r], __int_as_float(acc[rt][ct][r]), nb[r])
-                                                        : sa[r] * float(acc[rt][ct][r]);
+                        const float scaled_dot = BIAS ? __builtin_fmaf(sa[r], __int_as_float(acc[rt][ct][r]), nb[r])
+                                                      : sa[r] * float(acc[rt][ct][r]);
                         const float product = swv[ct] * scaled_dot;
                         const float correction = offv[ct] * ss[r];
                         val[rt][ct][r] = val[rt][ct][r] + (product + correction);
@@ -642,6 +365,87 @@ __global__ __launch_bounds__(256, GATEUP ? 2 : 3) void prefill_mfma_kernel(MfmaA
 #pragma unroll
                             for (int ct = 0; ct < 2; ++ct) val[rt][ct][r] = 0.f;
                         }
+                } else if constexpr (HEAD) {
+                    // Logits go through LDS (the A ring is free once every
+                    // wave is past its last dots) and leave as whole 16-byte
+                    // row pieces; per row, the best of this block's 128
+                    // columns (numpy argmax rule): lane (2 columns), 16 lanes
+                    // (xor 1..8), 4 waves in LDS.
+                    constexpr int kLS = kNT + 4;                  // padded row stride (floats)
+                    static_assert(kMT * kLS <= NSTAGE * kMT * 64, "logit staging fits the A ring");
+                    float* sL = reinterpret_cast<float*>(&sA[0][0]);
+                    const int nblk = (a.N + kNT - 1) / kNT;
+                    __syncthreads();
+#pragma unroll
+                    for (int rt = 0; rt < L; ++rt)
+#pragma unroll
+                        for (int r = 0; r < 4; ++r) {
+                            const int row = 16 * rt + 4 * q + r;
+                            float bv = 0.f;
+                            int bi = 0x7fffffff;
+#pragma unroll
+                            for (int ct = 0; ct < 2; ++ct) {
+                                const int cl = 32 * w + 16 * ct + li, col = kNT * nt + cl;
+                                const float v = val[rt][ct][r];
+                                sL[row * kLS + cl] = v;
+                                if (col < a.N && (bi == 0x7fffffff || arg_better(v, col, bv, bi))) {
+                                    bv = v;
+                                    bi = col;
+                                }
+                                val[rt][ct][r] = 0.f;
+                            }
+#pragma unroll
+                            for (int m = 1; m < 16; m <<= 1) {
+                                float ov;
+                                int oi;
+                                if (m == 1) { ov = xor_perm_f<1>(bv); oi = xor_perm_i<1>(bi); }
+                                else if (m == 2) { ov = xor_perm_f<2>(bv); oi = xor_perm_i<2>(bi); }
+                                else if (m == 4) { ov = xor_perm_f<4>(bv); oi = xor_perm_i<4>(bi); }
+                                else { ov = xor_perm_f<8>(bv); oi = xor_perm_i<8>(bi); }
+                                if (oi != 0x7fffffff && (bi == 0x7fffffff || arg_better(ov, oi, bv, bi))) {
+                                    bv = ov;
+                                    bi = oi;
+                                }
+                            }
+                            if (li == 0) { s_bv[w][row] = bv; s_bi[w][row] = bi; }
+                        }
+                    __syncthreads();
+                    // rows of 32 float4 pieces: thread -> (row, piece), 8 rows per pass
+                    const int cols = min(kNT, a.N - kNT * nt);
+                    for (int row = tid >> 5; row < nrows; row += 8) {
+                        const int c4 = 4 * (tid & 31);
+                        if (c4 < cols) {
+                            const float4 v = *reinterpret_cast<const float4*>(&sL[row * kLS + c4]);
+                            const size_t o = size_t(row) * a.N + kNT * nt + c4;
+                            *reinterpret_cast<float4*>(a.out + o) = v;
+                            const float vv[4] = {v.x, v.y, v.z, v.w};
+                            uint16_t b16[4];
+#pragma unroll
+                            for (int e = 0; e < 4; ++e) {
+                                b16[e] = f32_to_bf16_bits(vv[e]);
+                                if (!isfinite(vv[e])) flags |= a.flag_projection;
+                                if ((b16[e] & 0x7f80u) == 0x7f80u) flags |= a.flag_bf16;
+                            }
+                            if (a.out_bf16)
+                                *reinterpret_cast<uint2*>(a.out_bf16 + o) =
+                                    make_uint2(b16[0] | (uint32_t(b16[1]) << 16), b16[2] | (uint32_t(b16[3]) << 16));
+                        }
+                    }
+                    if (tid < nrows) {
+                        float bv = s_bv[0][tid];
+                        int bi = s_bi[0][tid];
+#pragma unroll
+                        for (int ww = 1; ww < 4; ++ww) {
+                            const float ov = s_bv[ww][tid];
+                            const int oi = s_bi[ww][tid];
+                            if (oi != 0x7fffffff && (bi == 0x7fffffff || arg_better(ov, oi, bv, bi))) {
+                                bv = ov;
+                                bi = oi;
+                            }
+                        }
+                        a.arg_val[size_t(tid) * nblk + nt] = bv;
+                        a.arg_idx[size_t(tid) * nblk + nt] = bi;
+                    }
                 } else {
 #pragma unroll
                 for (int rt = 0; rt < L; ++rt) {
@@ -683,9 +487,14 @@ __global__ __launch_bounds__(256, GATEUP ? 2 : 3) void prefill_mfma_kernel(MfmaA
         }(std::make_integer_sequence<int, NSTEP>{});
     };
     // 33..48 rows run the four-tile body (a fourth instantiation costs registers)
-    if (nrows > 32) run.template operator()<4>();
-    else if (nrows > 16) run.template operator()<2>();
-    else run.template operator()<1>();
+    if constexpr (MAXL >= 4) {
+        if (nrows > 32) run.template operator()<4>();
+        else if (nrows > 16) run.template operator()<2>();
+        else run.template operator()<1>();
+    } else {
+        if (nrows > 16) run.template operator()<2>();
+        else run.template operator()<1>();
+    }
     flag_or(a.sticky, flags);
 }
 
@@ -694,10 +503,10 @@ hipError_t launch_grouped_mfma(const MfmaArgs& a, bool gateup, int max_tiles, hi
     constexpr int kDownSub = 4;     // down: 4 column blocks (512 columns) per block
     const int tiles8 = (max_tiles + 7) / 8 * 8;   // m-tiles rounded up to the 8 XCDs
     if (gateup)
-        timed_launch("gateup_mfma", prefill_mfma_kernel<true, kHidden / kGroup, 1, 2>,
+        timed_launch("gateup_mfma", prefill_mfma_kernel<kModeGateUp, kHidden / kGroup, 1, 2>,
                      dim3(tiles8 * ((2 * kInter) / kNT)), dim3(256), 0, s, a);
     else
-        timed_launch("down_mfma", prefill_mfma_kernel<false, kInter / kGroup, kDownSub, 1>,
+        timed_launch("down_mfma", prefill_mfma_kernel<kModeDown, kInter / kGroup, kDownSub, 1>,
                      dim3(tiles8 * (kHidden / (kNT * kDownSub))), dim3(256), 0, s, a);
     return hipGetLastError();
 }
@@ -705,7 +514,13 @@ hipError_t launch_grouped_mfma(const MfmaArgs& a, bool gateup, int max_tiles, hi
 hipError_t launch_head_mfma(const MfmaArgs& a, int64_t* argmax, hipStream_t s) {
     if (a.R <= 0 || a.R > kMT || a.N <= 0 || a.N % 32 != 0 || a.K != kHidden) return hipErrorInvalidValue;
     const int nblk = (a.N + kNT - 1) / kNT;
-    timed_launch("head_mfma", grouped_mfma_kernel<kModeHead, kHidden / kGroup, 2>, dim3(nblk), dim3(256), 0, s, a);
+    // up to 32 rows (the decode-side head): two row tiles at most and codes
+    // four steps ahead keep more of the weight stream in flight
+    if (a.R <= 32)
+        timed_launch("head_mfma", prefill_mfma_kernel<kModeHead, kHidden / kGroup, 1, 4, 2>, dim3(nblk), dim3(256), 0, s,
+                     a);
+    else
+        timed_launch("head_mfma", prefill_mfma_kernel<kModeHead, kHidden / kGroup, 1, 2>, dim3(nblk), dim3(256), 0, s, a);
     hipError_t st = hipGetLastError();
     if (st != hipSuccess) return st;
     timed_launch("argmax", head_argmax_kernel, dim3(a.R), dim3(256), 0, s, a.arg_val, a.arg_idx, nblk, argmax);
