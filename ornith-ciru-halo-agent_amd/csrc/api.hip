@@ -470,11 +470,12 @@ extern "C" hipError_t ornith_dense_g256_launch_n32(const void* input, const void
 
 extern "C" int ornith_dense_g256_n32_rows(void) { return 16; }
 
-// head workspace: A8 activation words, scales, sums, then the per-128-column
-// argmax partials (value, index) of every row
+// head workspace: A8 activation words, scales, sums, then the argmax partials
+// (value, index) of every row: one per 128-column block (more than 32 rows) or
+// per streaming wave (at most one per 64 columns)
 namespace {
-constexpr int kHeadBlockCols = 128;
-size_t head_partials(int Mcap, int N) { return size_t(Mcap) * size_t((N + kHeadBlockCols - 1) / kHeadBlockCols); }
+constexpr int kHeadPartCols = 64;
+size_t head_partials(int Mcap, int N) { return size_t(Mcap) * size_t((N + kHeadPartCols - 1) / kHeadPartCols); }
 }  // namespace
 
 extern "C" size_t ornith_dense_g256_head_workspace_bytes(int Mcap, int N) {

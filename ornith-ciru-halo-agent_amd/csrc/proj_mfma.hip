@@ -20,6 +20,7 @@
 #include "kernels.hpp"
 #include "timing.hpp"
 #include "decode.hpp"
+#include <algorithm>
 #include <utility>
 
 namespace ornith {
@@ -45,6 +46,12 @@ __device__ __forceinline__ bool arg_better(float a, int ia, float b, int ib) {
     if (na) return ia < ib;
     return a > b || (a == b && ia < ib);
 }
+// The same order without branches (lane masks combined bitwise), for
+// reductions across lanes.
+__device__ __forceinline__ bool arg_better_select(float a, int ia, float b, int ib) {
+    const bool na = a != a, nb = b != b, first = ia < ib;
+    return (na & (!nb | first)) | (!na & !nb & ((a > b) | ((a == b) & first)));
+}
 
 // Per-row combination of the head's block partials (numpy argmax rule).
 __global__ __launch_bounds__(256) void head_argmax_kernel(const float* __restrict__ val, const int32_t* __restrict__ idx,
@@ -54,10 +61,19 @@ __global__ __launch_bounds__(256) void head_argmax_kernel(const float* __restric
     const int row = blockIdx.x, t = threadIdx.x;
     float v = 0.f;
     int i = 0x7fffffff;
-    for (int b = t; b < nblk; b += 256) {
-        const float ov = val[size_t(row) * nblk + b];
-        const int oi = idx[size_t(row) * nblk + b];
-        if (oi != 0x7fffffff && (i == 0x7fffffff || arg_better(ov, oi, v, i))) { v = ov; i = oi; }
+    // eight independent loads per thread per round (2048 partials per round)
+    for (int b0 = 0; b0 < nblk; b0 += 8 * 256) {
+        float ov[8];
+        int oi[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            const int b = b0 + 256 * u + t;
+            ov[u] = b < nblk ? val[size_t(row) * nblk + b] : 0.f;
+            oi[u] = b < nblk ? idx[size_t(row) * nblk + b] : 0x7fffffff;
+        }
+#pragma unroll
+        for (int u = 0; u < 8; ++u)
+            if (oi[u] != 0x7fffffff && (i == 0x7fffffff || arg_better(ov[u], oi[u], v, i))) { v = ov[u]; i = oi[u]; }
     }
     bv[t] = v;
     bi[t] = i;
@@ -511,19 +527,239 @@ hipError_t launch_grouped_mfma(const MfmaArgs& a, bool gateup, int max_tiles, hi
     return hipGetLastError();
 }
 
+// ---------------------------------------------------------------------------
+// G256 LM head for up to 32 rows on the 32x32x32 int8 matrix cores.
+//
+// A block of WPB waves copies the rows' A8 activations (32 rows x 2048 int8,
+// rows past R repeating row R - 1) and per-group scales into LDS once; then
+// every wave streams its own contiguous range of 32-column code tiles (the
+// N / 32 tiles split evenly over the grid's waves) with D group-steps of
+// codes in flight, the ring running across tiles.
+//  - Codes of one (tile, group) are 32 rows j of 32 words (word (j, n): the 8
+//    codes of column n for k = 8j .. 8j + 7).  Load u (0..15) of lane
+//    n + 32h takes word (4 (u / 2) + 2h + u % 2, n): the 32 lanes of a half
+//    read one whole 128-byte row, and lane n + 32h ends up holding column n,
+//    rows 4i + 2h and 4i + 2h + 1 for MFMA i (0..7): its 16 operand bytes
+//    (even codes, odd codes per word) of k-half h.
+//  - A: lane r + 32h of MFMA i reads the matching activation words (chunks
+//    4i + 2h, 4i + 2h + 1 of the group: 16-byte piece 2i + h); row r's piece
+//    p sits at LDS slot (p & ~15) | ((p ^ r) & 15).
+//  - Output register k of lane l is C[8 (k / 4) + 4 (l / 32) + k % 4][l % 32]:
+//    the fp32 group tree (dense_g256_api.h:35-37) runs per lane over its 16
+//    rows of one column, ascending groups.
+// Logits leave straight from that layout (two 128-byte rows per store).  A
+// lane meets its columns in ascending order, so its running argmax candidate
+// per row changes only on a strictly larger value or a first NaN (numpy
+// rule); the wave writes one partial per row at the end.
+// ---------------------------------------------------------------------------
+typedef int i32x16 __attribute__((ext_vector_type(16)));
+
+template <int WPB, int D>
+__global__ __launch_bounds__(64 * WPB, 1) void head_tile_kernel(MfmaArgs a, int nwaves) {
+    constexpr int GS = kHidden / kGroup;          // 8 groups of 256
+    constexpr int RW = kHidden / 4;               // activation words per row
+    constexpr int ROWS = 32, NT = 64 * WPB;
+    static_assert(GS % D == 0, "ring slots repeat every tile");
+    __shared__ __attribute__((aligned(16))) uint32_t sA[ROWS * RW];
+    __shared__ __attribute__((aligned(16))) float s_sa[GS][ROWS];
+    __shared__ __attribute__((aligned(16))) float s_ss[GS][ROWS];
+    __shared__ __attribute__((aligned(16))) float s_nb[GS][ROWS];   // -sa * kDotBias (exact)
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int cl = lane & 31, h = lane >> 5;
+    const int R = a.R;
+
+    constexpr int APASS = ROWS * 128 / NT;        // 16-byte pieces per thread
+    static_assert(APASS % 4 == 0, "pieces move in batches of four");
+#pragma unroll
+    for (int b = 0; b < APASS; b += 4) {
+        u32x4 v[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const int i = (b + k) * NT + tid, r = i >> 7, pc = i & 127;
+            v[k] = *reinterpret_cast<const u32x4*>(a.act_words + size_t(min(r, R - 1)) * RW + 4 * pc);
+        }
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const int i = (b + k) * NT + tid, r = i >> 7, pc = i & 127;
+            *reinterpret_cast<u32x4*>(&sA[r * RW + 4 * ((pc & ~15) | ((pc ^ r) & 15))]) = v[k];
+        }
+    }
+    for (int i = tid; i < ROWS * GS; i += NT) {
+        const int r = i / GS, g = i % GS, sr = min(r, R - 1);
+        const float sa = f16_bits_to_f32(a.act_scales[sr * GS + g]);
+        s_sa[g][r] = sa;
+        s_ss[g][r] = sa * float(a.act_sums[sr * GS + g]);
+        s_nb[g][r] = -sa * kDotBias;
+    }
+    __syncthreads();
+
+    // wave rank w * blocks + block: the ranks holding one tile more than the
+    // rest (the lowest ones) spread over every CU, not a few whole blocks
+    const int gw = w * int(gridDim.x) + int(blockIdx.x);
+    if (gw >= nwaves) return;                     // no barrier follows
+    const int ntiles = a.N >> 5;
+    const int base = ntiles / nwaves, extra = ntiles % nwaves;
+    const int c0 = gw * base + min(gw, extra), cnt = base + (gw < extra ? 1 : 0);
+
+    // step st = 8 * (tile - c0) + group: 1024 code words and 32 meta words on
+    const uint32_t* cbase = a.codes + size_t(c0) * GS * 1024 + 64 * h + cl;
+    const uint32_t* mbase = a.meta + size_t(c0) * GS * 32 + cl;
+    uint32_t bw[D][16];
+    uint32_t bm[D];
+    auto load_b = [&](int st, int slot) {
+        const uint32_t* src = cbase + size_t(st) * 1024;
+#pragma unroll
+        for (int u = 0; u < 16; ++u) bw[slot][u] = src[128 * (u >> 1) + 32 * (u & 1)];
+        bm[slot] = mbase[size_t(st) * 32];
+    };
+#pragma unroll
+    for (int st = 0; st < D; ++st) load_b(st, st);
+
+    // candidate per row: value and tile (t < 256: one byte each, packed);
+    // all -inf keeps the first tile (the first column)
+    float bv[16];
+    uint32_t bt[4] = {0u, 0u, 0u, 0u};
+#pragma unroll
+    for (int k = 0; k < 16; ++k) bv[k] = -__builtin_inff();
+    float nonfinite = 0.f, nonfinite_bf16 = 0.f;  // NaN once a logit (resp. its bf16) is inf or NaN
+    constexpr i32x16 kAccInit = {kDotBiasBits, kDotBiasBits, kDotBiasBits, kDotBiasBits, kDotBiasBits, kDotBiasBits,
+                                 kDotBiasBits, kDotBiasBits, kDotBiasBits, kDotBiasBits, kDotBiasBits, kDotBiasBits,
+                                 kDotBiasBits, kDotBiasBits, kDotBiasBits, kDotBiasBits};
+
+    // one code tile: 8 groups; REFILL = a next tile exists
+    auto tile_body = [&]<bool REFILL>(int t) {
+        float val[16];
+#pragma unroll
+        for (int k = 0; k < 16; ++k) val[k] = 0.f;
+#pragma unroll
+        for (int g = 0; g < GS; ++g) {
+            const int slot = g % D;
+            i32x16 acc;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const uint32_t w0 = bw[slot][2 * i], w1 = bw[slot][2 * i + 1];
+                const i32x4 fb = {code_even(w0), code_odd(w0), code_even(w1), code_odd(w1)};
+                const u32x4 av =
+                    *reinterpret_cast<const u32x4*>(&sA[cl * RW + 4 * ((16 * g) | ((2 * i + h) ^ (cl & 15)))]);
+                const i32x4 fa = {int(av.x), int(av.y), int(av.z), int(av.w)};
+                acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa, fb, i ? acc : kAccInit, 0, 0, 0);
+            }
+            // pin the meta word here: left free, its conversion is hoisted
+            // next to the load and waits out the whole ring
+            asm volatile("" : "+v"(bm[slot]));
+            const float sw = f16_bits_to_f32(uint16_t(bm[slot] & 0xffffu));
+            const float off = f16_bits_to_f32(uint16_t(bm[slot] >> 16));
+            if (g + D < GS) load_b(8 * t + g + D, slot);
+            else if constexpr (REFILL) load_b(8 * t + g + D, slot);
+#pragma unroll
+            for (int b = 0; b < 4; ++b) {
+                const float4 sa4 = *reinterpret_cast<const float4*>(&s_sa[g][8 * b + 4 * h]);
+                const float4 ss4 = *reinterpret_cast<const float4*>(&s_ss[g][8 * b + 4 * h]);
+                const float4 nb4 = *reinterpret_cast<const float4*>(&s_nb[g][8 * b + 4 * h]);
+                const float sa[4] = {sa4.x, sa4.y, sa4.z, sa4.w}, ss[4] = {ss4.x, ss4.y, ss4.z, ss4.w};
+                const float nb[4] = {nb4.x, nb4.y, nb4.z, nb4.w};
+#pragma unroll
+                for (int c = 0; c < 4; ++c) {
+                    const int k = 4 * b + c;
+                    const float scaled_dot = __builtin_fmaf(sa[c], __int_as_float(acc[k]), nb[c]);
+                    const float product = sw * scaled_dot;
+                    const float correction = off * ss[c];
+                    val[k] = val[k] + (product + correction);
+                }
+            }
+#pragma unroll
+            for (int k = 0; k < 16; ++k) asm volatile("" : "+v"(val[k]));
+        }
+        // rows past R repeat row R - 1 bit for bit, so every lane's values
+        // may feed the flags and the candidates
+        const int col = 32 * (c0 + t) + cl;
+#pragma unroll
+        for (int k = 0; k < 16; ++k) {
+            const int row = 8 * (k >> 2) + 4 * h + (k & 3);
+            const float v = val[k];
+            const uint16_t b16 = f32_to_bf16_bits(v);
+            if (row < R) {
+                const size_t o = size_t(row) * a.N + col;
+                a.out[o] = v;
+                if (a.out_bf16) a.out_bf16[o] = b16;
+            }
+            nonfinite = __builtin_fmaf(v, 0.f, nonfinite);
+            nonfinite_bf16 = __builtin_fmaf(bf16_bits_to_f32(b16), 0.f, nonfinite_bf16);
+            const bool take = (v > bv[k]) | ((v != v) & (bv[k] == bv[k]));
+            bv[k] = take ? v : bv[k];
+            const uint32_t mask = 0xffu << (8 * (k & 3));
+            bt[k >> 2] = take ? ((bt[k >> 2] & ~mask) | (uint32_t(t) << (8 * (k & 3)))) : bt[k >> 2];
+        }
+    };
+    for (int t = 0; t + 1 < cnt; ++t) tile_body.template operator()<true>(t);
+    tile_body.template operator()<false>(cnt - 1);
+
+    // ---- per-row best of the wave: 32 lanes (xor 1..16), then one partial.
+    // Key: an order-preserving image of the value (-0 as +0, every NaN
+    // above +inf) over the complemented column, so the unsigned maximum is
+    // the numpy argmax candidate (first NaN, else first maximum).
+#pragma unroll
+    for (int k = 0; k < 16; ++k) {
+        const float v = bv[k] + 0.f;
+        const uint32_t u = __float_as_uint(v);
+        const uint32_t ord = v != v ? 0xffffffffu : ((u & 0x80000000u) ? ~u : (u | 0x80000000u));
+        const int colk = 32 * (c0 + int((bt[k >> 2] >> (8 * (k & 3))) & 0xffu)) + cl;
+        uint64_t key = (uint64_t(ord) << 32) | uint32_t(~colk);
+#pragma unroll
+        for (int m = 1; m < 32; m <<= 1) {
+            int hi = int(key >> 32), lo = int(uint32_t(key));
+            if (m == 1) { hi = xor_perm_i<1>(hi); lo = xor_perm_i<1>(lo); }
+            else if (m == 2) { hi = xor_perm_i<2>(hi); lo = xor_perm_i<2>(lo); }
+            else if (m == 4) { hi = xor_perm_i<4>(hi); lo = xor_perm_i<4>(lo); }
+            else if (m == 8) { hi = xor_perm_i<8>(hi); lo = xor_perm_i<8>(lo); }
+            else { hi = xor_perm_i<16>(hi); lo = xor_perm_i<16>(lo); }
+            const uint64_t other = (uint64_t(uint32_t(hi)) << 32) | uint32_t(lo);
+            key = other > key ? other : key;
+        }
+        const int row = 8 * (k >> 2) + 4 * h + (k & 3);
+        if (cl == 0 && row < R) {
+            const uint32_t o = uint32_t(key >> 32);
+            const float v = o == 0xffffffffu ? __builtin_nanf("") : __uint_as_float((o & 0x80000000u) ? (o & 0x7fffffffu) : ~o);
+            a.arg_idx[size_t(row) * nwaves + gw] = int(~uint32_t(key));
+            a.arg_val[size_t(row) * nwaves + gw] = v;
+        }
+    }
+    uint32_t flags = 0;
+    if (nonfinite != nonfinite) flags |= a.flag_projection;
+    if (nonfinite_bf16 != nonfinite_bf16) flags |= a.flag_bf16;
+    flag_or(a.sticky, flags);
+}
+
+// Head waves: WPB-wave blocks (one per CU), at least two code tiles per wave
+// (so the partial count per row, nwaves, stays within ceil(N / 64)).
+constexpr int kHeadWaves = 8, kHeadRing = 2;
+static int head_waves(int N) {
+    static int cus = 0;
+    if (!cus) {
+        int dev = 0;
+        if (hipGetDevice(&dev) != hipSuccess ||
+            hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+            cus = 256;
+    }
+    return std::max(1, std::min(kHeadWaves * cus, (N / 32) / 2));
+}
+
 hipError_t launch_head_mfma(const MfmaArgs& a, int64_t* argmax, hipStream_t s) {
     if (a.R <= 0 || a.R > kMT || a.N <= 0 || a.N % 32 != 0 || a.K != kHidden) return hipErrorInvalidValue;
-    const int nblk = (a.N + kNT - 1) / kNT;
-    // up to 32 rows (the decode-side head): two row tiles at most and codes
-    // four steps ahead keep more of the weight stream in flight
-    if (a.R <= 32)
-        timed_launch("head_mfma", prefill_mfma_kernel<kModeHead, kHidden / kGroup, 1, 4, 2>, dim3(nblk), dim3(256), 0, s,
-                     a);
-    else
-        timed_launch("head_mfma", prefill_mfma_kernel<kModeHead, kHidden / kGroup, 1, 2>, dim3(nblk), dim3(256), 0, s, a);
+    int nparts;
+    if (a.R <= 32) {
+        // up to 32 rows (the decode-side head): streaming waves
+        nparts = head_waves(a.N);
+        timed_launch("head_mfma", head_tile_kernel<kHeadWaves, kHeadRing>,
+                     dim3((nparts + kHeadWaves - 1) / kHeadWaves), dim3(64 * kHeadWaves), 0, s, a, nparts);
+    } else {
+        nparts = (a.N + kNT - 1) / kNT;
+        timed_launch("head_mfma", prefill_mfma_kernel<kModeHead, kHidden / kGroup, 1, 2>, dim3(nparts), dim3(256), 0,
+                     s, a);
+    }
     hipError_t st = hipGetLastError();
     if (st != hipSuccess) return st;
-    timed_launch("argmax", head_argmax_kernel, dim3(a.R), dim3(256), 0, s, a.arg_val, a.arg_idx, nblk, argmax);
+    timed_launch("argmax", head_argmax_kernel, dim3(a.R), dim3(256), 0, s, a.arg_val, a.arg_idx, nparts, argmax);
     return hipGetLastError();
 }
 

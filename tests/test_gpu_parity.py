@@ -428,7 +428,10 @@ def test_head_w8_bit_exact(device, M, N, dots):
     assert int(flags.item()) == ref_flags
 
 
-@pytest.mark.parametrize('M,N', [(1, 4096), (32, 151936)])
+# 1..16 and 17..32 rows take the streaming head (one or two row tiles; 2080
+# columns split into ranges of 4 and 5 tiles, so odd ranges pair a tile with
+# itself), 48 rows the row-tile kernel
+@pytest.mark.parametrize('M,N', [(1, 4096), (32, 151936), (17, 2080), (48, 8192)])
 def test_head_g256_logits_and_argmax(device, M, N):
     import torch
     native = _native()
@@ -448,4 +451,41 @@ def test_head_g256_logits_and_argmax(device, M, N):
     np.testing.assert_array_equal(from_dev(logits).view(np.uint32), ref_diag.view(np.uint32))
     np.testing.assert_array_equal(from_dev(lb), ref_out)
     np.testing.assert_array_equal(from_dev(am), O.argmax_first(ref_diag))
+    assert int(flags.item()) == ref_flags
+
+
+@pytest.mark.parametrize('case', ['ties', 'nan'])
+@pytest.mark.parametrize('M', [5, 20])
+def test_head_g256_argmax_ties_and_nan(device, case, M):
+    """Equal logits across every wave's range (argmax = lowest column) and NaN
+    logits in two columns (argmax = the first NaN column, both flags)."""
+    import torch
+    native = _native()
+    N = 2080
+    print(f'g256 head {case} M={M} N={N}', flush=True)
+    rng = np.random.default_rng(700 + M)
+    bank = Bank(rng, 0, N, 2048, tile=32)
+    if case == 'ties':
+        bank.codes[...] = bank.codes[0:1, :, :, 0:1]
+        bank.sbits[...] = bank.sbits[0:1]
+        bank.obits[...] = bank.obits[0:1]
+    else:
+        bank.sbits[1501, 3] = 0x7e00
+        bank.sbits[1003, 6] = 0x7e00
+    bank.meta = O.pack_meta(bank.sbits, bank.obits, 32)
+    x = bf16_normal(rng, (M, 2048))
+    ref_out, ref_diag, ref_flags = O.dense_a8(x, *bank.expert())
+    expect = O.argmax_first(ref_diag)
+    assert (expect == (0 if case == 'ties' else 1003)).all()
+    xd, cd, md = to_dev(x, device), to_dev(bank.codes, device), to_dev(bank.meta, device)
+    ws = torch.empty(native.lib().ornith_dense_g256_head_workspace_bytes(64, N), dtype=torch.uint8, device=device)
+    logits = torch.empty((M, N), dtype=torch.float32, device=device)
+    lb = torch.empty((M, N), dtype=torch.bfloat16, device=device)
+    am = torch.empty((M,), dtype=torch.int64, device=device)
+    flags = _flags(device)
+    native.dense_head(xd, cd, md, ws, logits, lb, am, flags, 64)
+    _sync()
+    np.testing.assert_array_equal(from_dev(logits).view(np.uint32), ref_diag.view(np.uint32))
+    np.testing.assert_array_equal(from_dev(lb), ref_out)
+    np.testing.assert_array_equal(from_dev(am), expect)
     assert int(flags.item()) == ref_flags
