@@ -564,6 +564,7 @@ __global__ __launch_bounds__(64 * WPB, 1) void head_tile_kernel(MfmaArgs a, int 
     __shared__ __attribute__((aligned(16))) float s_sa[GS][ROWS];
     __shared__ __attribute__((aligned(16))) float s_ss[GS][ROWS];
     __shared__ __attribute__((aligned(16))) float s_nb[GS][ROWS];   // -sa * kDotBias (exact)
+    __shared__ uint64_t s_key[WPB][16][65];       // per-wave argmax keys (padded rows)
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const int cl = lane & 31, h = lane >> 5;
     const int R = a.R;
@@ -694,34 +695,39 @@ __global__ __launch_bounds__(64 * WPB, 1) void head_tile_kernel(MfmaArgs a, int 
     for (int t = 0; t + 1 < cnt; ++t) tile_body.template operator()<true>(t);
     tile_body.template operator()<false>(cnt - 1);
 
-    // ---- per-row best of the wave: 32 lanes (xor 1..16), then one partial.
-    // Key: an order-preserving image of the value (-0 as +0, every NaN
-    // above +inf) over the complemented column, so the unsigned maximum is
-    // the numpy argmax candidate (first NaN, else first maximum).
+    // ---- per-row best of the wave, then one partial per row.  Key: an
+    // order-preserving image of the value (-0 as +0, every NaN above +inf)
+    // over the complemented column, so the unsigned maximum is the numpy
+    // argmax candidate (first NaN, else first maximum).  The 16 keys of each
+    // lane go through LDS; lane r (and r + 32) takes row r's 32 candidates
+    // (columns cl of its half), 16 each, and the two halves meet by xor 32.
 #pragma unroll
     for (int k = 0; k < 16; ++k) {
         const float v = bv[k] + 0.f;
         const uint32_t u = __float_as_uint(v);
         const uint32_t ord = v != v ? 0xffffffffu : ((u & 0x80000000u) ? ~u : (u | 0x80000000u));
         const int colk = 32 * (c0 + int((bt[k >> 2] >> (8 * (k & 3))) & 0xffu)) + cl;
-        uint64_t key = (uint64_t(ord) << 32) | uint32_t(~colk);
+        s_key[w][k][lane] = (uint64_t(ord) << 32) | uint32_t(~colk);
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    {
+        const int r = lane & 31, rh = (r >> 2) & 1, rk = 4 * (r >> 3) + (r & 3), c0h = 16 * (lane >> 5);
+        uint64_t key = s_key[w][rk][32 * rh + c0h];
 #pragma unroll
-        for (int m = 1; m < 32; m <<= 1) {
-            int hi = int(key >> 32), lo = int(uint32_t(key));
-            if (m == 1) { hi = xor_perm_i<1>(hi); lo = xor_perm_i<1>(lo); }
-            else if (m == 2) { hi = xor_perm_i<2>(hi); lo = xor_perm_i<2>(lo); }
-            else if (m == 4) { hi = xor_perm_i<4>(hi); lo = xor_perm_i<4>(lo); }
-            else if (m == 8) { hi = xor_perm_i<8>(hi); lo = xor_perm_i<8>(lo); }
-            else { hi = xor_perm_i<16>(hi); lo = xor_perm_i<16>(lo); }
-            const uint64_t other = (uint64_t(uint32_t(hi)) << 32) | uint32_t(lo);
-            key = other > key ? other : key;
+        for (int c = 1; c < 16; ++c) {
+            const uint64_t o = s_key[w][rk][32 * rh + c0h + c];
+            key = o > key ? o : key;
         }
-        const int row = 8 * (k >> 2) + 4 * h + (k & 3);
-        if (cl == 0 && row < R) {
+        const int hi = xor_perm_i<32>(int(key >> 32)), lo = xor_perm_i<32>(int(uint32_t(key)));
+        const uint64_t other = (uint64_t(uint32_t(hi)) << 32) | uint32_t(lo);
+        key = other > key ? other : key;
+        if (lane < 32 && r < R) {
             const uint32_t o = uint32_t(key >> 32);
             const float v = o == 0xffffffffu ? __builtin_nanf("") : __uint_as_float((o & 0x80000000u) ? (o & 0x7fffffffu) : ~o);
-            a.arg_idx[size_t(row) * nwaves + gw] = int(~uint32_t(key));
-            a.arg_val[size_t(row) * nwaves + gw] = v;
+            a.arg_idx[size_t(r) * nwaves + gw] = int(~uint32_t(key));
+            a.arg_val[size_t(r) * nwaves + gw] = v;
         }
     }
     uint32_t flags = 0;
