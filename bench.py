@@ -232,12 +232,13 @@ def dense_prefill_ms(T, device, steps=20):
 
 
 def head_ms(device, steps=20):
-    """G256 LM head [151936, 2048] on 32 rows: fp32 logits, bf16 logits, argmax."""
+    """G256 LM head [151936, 2048] on 32 rows: fp32 logits, bf16 logits, argmax.
+    Two weight copies alternate, so the 160 MB bank is not MALL-resident."""
     import torch
     from ornith_g256 import native, synthetic
     gen = torch.Generator(device=device)
     gen.manual_seed(78)
-    codes, meta = synthetic.bank(gen, HEAD_N, 2048, device)
+    banks = [synthetic.bank(gen, HEAD_N, 2048, device) for _ in range(2)]
     x = torch.randn((HEAD_ROWS, 2048), generator=gen, device=device).to(torch.bfloat16)
     ws = torch.empty(native.lib().ornith_dense_g256_head_workspace_bytes(64, HEAD_N), dtype=torch.uint8,
                      device=device)
@@ -245,14 +246,14 @@ def head_ms(device, steps=20):
     lb = torch.empty((HEAD_ROWS, HEAD_N), dtype=torch.bfloat16, device=device)
     am = torch.empty((HEAD_ROWS,), dtype=torch.int64, device=device)
     flags = torch.zeros(1, dtype=torch.int32, device=device)
-    call = lambda: native.dense_head(x, codes, meta, ws, logits, lb, am, flags, 64)
-    for _ in range(3):
-        call()
+    call = lambda i: native.dense_head(x, *banks[i % 2], ws, logits, lb, am, flags, 64)
+    for i in range(4):
+        call(i)
     torch.cuda.synchronize()
     a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     a.record()
-    for _ in range(steps):
-        call()
+    for i in range(steps):
+        call(i)
     b.record()
     torch.cuda.synchronize()
     return a.elapsed_time(b) / steps
