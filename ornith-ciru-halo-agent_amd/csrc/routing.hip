@@ -187,6 +187,7 @@ __global__ __launch_bounds__(256) void router_kernel(const uint16_t* __restrict_
 // group run on one XCD (workgroups go to the 8 XCDs round-robin) and share
 // its L2.
 constexpr int kRtRows = 8, kRtTokens = 64;
+constexpr int kRtBlocksPerCu = 2;                    // occupancy the tile kernels are built for
 constexpr int kPermTokens = 16;                      // tokens per permutation count / scatter block
 constexpr int kPermRoutes = kPermTokens * kTop;      // routed routes per block
 
@@ -212,9 +213,9 @@ __device__ __forceinline__ void router_tokens_block(int blk, const uint16_t* __r
 #pragma unroll
     for (int i = 0; i < 8; ++i) xv[i] = *reinterpret_cast<const u32x4*>(xrow + 8 * i);
 
-    // stage the 8 weight rows (rows past nrows repeat the last one; never stored)
+    // stage the block's weight rows (rows past nrows repeat the last one; never stored)
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
+    for (int i = 0; i < kRtRows; ++i) {
         const int p = tid + 256 * i, r = p >> 8, c = p & 255;
         const int e = min(e0 + r, nrows - 1);
         const uint16_t* row = e < kExperts ? w + size_t(e) * kHidden : shared_w;
@@ -226,10 +227,13 @@ __device__ __forceinline__ void router_tokens_block(int blk, const uint16_t* __r
     }
     __syncthreads();
 
-    // unit u = (j, s, r), u = 128j + 8s + r: row r of chunk 16q + s + 64j.  The
-    // broadcast weight reads run two units ahead through a 3-slot ring.
+    // unit u = (j, s, r), u = 16 kRtRows j + kRtRows s + r: row r of chunk
+    // 16q + s + 64j.  The broadcast weight reads run two units ahead through a
+    // 3-slot ring.
+    constexpr int kUnits = 64 * kRtRows;
     auto wread = [&](int u, float (&dst)[8]) __attribute__((always_inline)) {
-        const int j = u >> 7, sr = u & 127, s = sr >> 3, r = sr & 7, c = 16 * q + s + 64 * j;
+        const int j = u / (16 * kRtRows), sr = u % (16 * kRtRows), s = sr / kRtRows, r = sr % kRtRows;
+        const int c = 16 * q + s + 64 * j;
         const float4 w0 = *reinterpret_cast<const float4*>(&sW[r][8 * c]);
         const float4 w1 = *reinterpret_cast<const float4*>(&sW[r][8 * c + 4]);
         dst[0] = w0.x; dst[1] = w0.y; dst[2] = w0.z; dst[3] = w0.w;
@@ -250,8 +254,8 @@ __device__ __forceinline__ void router_tokens_block(int blk, const uint16_t* __r
         for (int s = 0; s < 16; ++s)
 #pragma unroll
             for (int r = 0; r < kRtRows; ++r) {
-                const int u = 128 * j + 8 * s + r, i = s & 7;
-                if (u + 2 < 512) wread(u + 2, wr[(u + 2) % 3]);
+                const int u = 16 * kRtRows * j + kRtRows * s + r, i = s & 7;
+                if (u + 2 < kUnits) wread(u + 2, wr[(u + 2) % 3]);
                 if (r == 0) {
                     bf16x8_to_f32(uint4{xv[i].x, xv[i].y, xv[i].z, xv[i].w}, xf);
                     // next line's chunk i: same segment's second half, or the next segment's first
@@ -274,17 +278,18 @@ __device__ __forceinline__ void router_tokens_block(int blk, const uint16_t* __r
         sS[q][r][lane] = p2[0] + p2[1];
     }
     __syncthreads();
-    // ((S0 + S1) + (S2 + S3)) + bias; thread -> (token, row pair)
-    const int t = tid >> 2, rp = 2 * (tid & 3), tok = tg * kRtTokens + t;
+    // ((S0 + S1) + (S2 + S3)) + bias; thread -> (token, kRtRows / 4 rows)
+    constexpr int kRowsPerThread = kRtRows / 4;
+    const int t = tid >> 2, rp = kRowsPerThread * (tid & 3), tok = tg * kRtTokens + t;
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
+    for (int i = 0; i < kRowsPerThread; ++i) {
         const int r = rp + i, e = e0 + r;
         const float v = (sS[0][r][t] + sS[1][r][t]) + (sS[2][r][t] + sS[3][r][t]);
         if (tok < T && e < nrows) logits[size_t(tok) * logit_stride + e] = (bias && e < kExperts) ? v + bias[e] : v;
     }
 }
 
-__global__ __launch_bounds__(256, 2) void router_tokens_kernel(const uint16_t* __restrict__ x, int64_t stride, int T,
+__global__ __launch_bounds__(256, kRtBlocksPerCu) void router_tokens_kernel(const uint16_t* __restrict__ x, int64_t stride, int T,
                                                                const uint16_t* __restrict__ w,
                                                                const uint16_t* __restrict__ shared_w,
                                                                const float* __restrict__ bias, float* __restrict__ logits,
@@ -296,7 +301,7 @@ __global__ __launch_bounds__(256, 2) void router_tokens_kernel(const uint16_t* _
 // layer path with the shared expert, where every token is live, so the gate
 // input does not wait for routing).  The activation blocks take the CUs the
 // last round of router tiles leaves idle.
-__global__ __launch_bounds__(256, 2) void router_act_kernel(const uint16_t* __restrict__ x, int T,
+__global__ __launch_bounds__(256, kRtBlocksPerCu) void router_act_kernel(const uint16_t* __restrict__ x, int T,
                                                             const uint16_t* __restrict__ w,
                                                             const uint16_t* __restrict__ shared_w,
                                                             const float* __restrict__ bias, float* __restrict__ logits,
@@ -357,7 +362,7 @@ bool router_act_pays(int T) {
         if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) !=
                                                     hipSuccess || cus <= 0)
             return false;
-        slots = 2 * cus;
+        slots = kRtBlocksPerCu * cus;
     }
     const int ngroups = (kExperts + 1 + kRtRows - 1) / kRtRows;
     const int tiles = ((T + kRtTokens - 1) / kRtTokens) * ngroups;   // router blocks with work
