@@ -49,15 +49,15 @@ DENSE_N = 6144
 # --copy-calibration); keyed by (kernel, tokens).  Commands and raw figures:
 # profiles/decode_n1_n32_hbm_traffic_pmc.md, profiles/prefill_1120_8192_hbm_traffic_pmc.md.
 MEASURED_TRAFFIC = {
-    ('route1', 1): 1162556, ('gateup1', 1): 9951839, ('down1', 1): 5125692,
-    ('route', 32): 2583528, ('topk', 32): 128330, ('sort', 32): 12783, ('gateup', 32): 176480431,
-    ('quant_middle', 32): 792574, ('down', 32): 90912585, ('reduce', 32): 2593294,
-    ('router_act', 1120): 21199133, ('topk', 1120): 1395533, ('permute_scan', 1120): 760775,
-    ('permute_scatter', 1120): 335833, ('gateup_mfma', 1120): 189497152, ('quant_middle', 1120): 26013075,
-    ('down_mfma', 1120): 169431222, ('reduce', 1120): 87589739,
-    ('router', 8192): 51023188, ('topk', 8192): 9612526, ('permute_scan', 8192): 5286522,
-    ('permute_scatter', 8192): 1546388, ('act', 8192): 50827683, ('gateup_mfma', 8192): 623516069,
-    ('quant_middle', 8192): 189703930, ('down_mfma', 8192): 845859934, ('reduce', 8192): 639972378,
+    ('route1', 1): 1166677, ('gateup1', 1): 9949513, ('down1', 1): 5118568,
+    ('route', 32): 2589160, ('topk', 32): 128330, ('sort', 32): 12783, ('gateup', 32): 176480657,
+    ('quant_middle', 32): 804924, ('down', 32): 90912611, ('reduce', 32): 2587151,
+    ('router_act', 1120): 21182550, ('topk', 1120): 1395533, ('permute_scan', 1120): 774086,
+    ('permute_scatter', 1120): 335852, ('gateup_mfma', 1120): 189276903, ('quant_middle', 1120): 26020114,
+    ('down_mfma', 1120): 169427032, ('reduce', 1120): 87580105,
+    ('router', 8192): 51034311, ('topk', 8192): 9612528, ('permute_scan', 8192): 5299834,
+    ('permute_scatter', 8192): 1546388, ('act', 8192): 50832614, ('gateup_mfma', 8192): 623566473,
+    ('quant_middle', 8192): 189712920, ('down_mfma', 8192): 844326551, ('reduce', 8192): 639965506,
 }
 
 
