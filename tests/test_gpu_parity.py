@@ -312,6 +312,58 @@ def test_moe_layer_bit_exact(device, moe, shared_tables, T):
     assert int(flags.item()) == ref['flags']
 
 
+@pytest.mark.parametrize('T', [1, 32, 300])
+def test_moe_layer_graph_replays(device, moe, shared_tables, T):
+    """The layer captured in a HIP graph (the bench's timed path): three
+    replays on new inputs, with eager layer calls and synchronisations in
+    between, each bit-identical to an eager call on the same input."""
+    import torch
+    native = _native()
+    w, d = moe
+    silu, sigmoid = shared_tables
+    print(f'layer graph replays T={T}', flush=True)
+    rng = np.random.default_rng(5000 + T)
+    xs_host = [bf16_normal(rng, (T, 2048)) for _ in range(4)]
+    layout = native.routed_layout(T, 'layer')
+    ws = torch.empty(layout.workspace_bytes, dtype=torch.uint8, device=device)
+    xs = torch.empty((T, 2048), dtype=torch.bfloat16, device=device)
+    out = torch.empty((T, 2048), dtype=torch.bfloat16, device=device)
+    tw = torch.empty((T, 8), dtype=torch.float32, device=device)
+    ti = torch.empty((T, 8), dtype=torch.int32, device=device)
+    sl = torch.empty((T,), dtype=torch.bfloat16, device=device)
+    flags = _flags(device)
+    args = [to_dev(w['router'], device), None, to_dev(w['gate'][0], device), d['w13'][0], d['w13'][1], d['w2'][0],
+            d['w2'][1], d['s13'][0], d['s13'][1], d['s2'][0], d['s2'][1], to_dev(silu, device),
+            to_dev(sigmoid, device), ws, tw, ti, sl, out, flags, T]
+    layer = lambda: native.moe_layer(xs, *args)
+
+    def eager(xh):
+        xs.copy_(to_dev(xh, device))
+        layer()
+        _sync()
+        return out.clone(), ti.clone(), tw.clone(), sl.clone()
+
+    refs = [eager(xh) for xh in xs_host[:3]]
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        layer()                                   # warm-up on the capture stream
+    torch.cuda.current_stream().wait_stream(side)
+    _sync()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        layer()
+    for i, xh in enumerate(xs_host[:3]):
+        eager(xs_host[3])                         # the program's own eager work in between
+        xs.copy_(to_dev(xh, device))
+        _sync()
+        g.replay()
+        _sync()
+        for got, want in zip((out, ti, tw, sl), refs[i]):
+            assert torch.equal(got.view(torch.uint8), want.view(torch.uint8)), f'replay {i}'
+    assert int(flags.item()) == 0
+
+
 def _tied_router(router, case):
     """Router rows repeated so that logits (and probabilities) tie exactly:
     'quads' -- experts 4j..4j+3 share a row (ties decided by the lower id);
