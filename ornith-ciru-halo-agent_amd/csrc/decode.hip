@@ -283,32 +283,37 @@ __global__ __launch_bounds__(512) void decode_gateup_kernel(DecodeArgs a) {
 }
 
 // ---------------------------------------------------------------------------
-// S5: block (segment, 32-column tile c).  Wave q = chunk quarter (chunks
+// S5: block (segment, CPB 32-column tiles c).  Wave q = chunk quarter (chunks
 // 8q..8q+7); lane = (group lane / 32, column lane % 32), so every load
 // instruction reads two whole 128-byte rows.  The quarters' exact integer
-// partial dots meet in LDS; the two groups' terms follow in group order.
+// partial dots meet in LDS; the two groups' terms follow in group order.  The
+// segment's routes and activations are loaded once for the block's tiles.
 // ---------------------------------------------------------------------------
-template <bool SHARED>
+template <bool SHARED, int CPB>
 __global__ __launch_bounds__(256) void decode_down_kernel(DecodeArgs a) {
     __shared__ __align__(16) uint32_t la[kRouteChunk][128];
     __shared__ float lsa[kRouteChunk][2], lss[kRouteChunk][2];
-    __shared__ int lpart[kRouteChunk][4][64];
+    __shared__ int lpart[CPB][kRouteChunk][4][64];
     __shared__ int lr[256];
     const int nseg = a.nseg[0];
     if (int(blockIdx.y) >= nseg) return;
     const Segment sg = a.segments[nseg - 1 - int(blockIdx.y)];    // shared expert's segments first
-    const int tid = threadIdx.x, lane = tid & 63, q = tid >> 6, c = blockIdx.x;
+    const int tid = threadIdx.x, lane = tid & 63, q = tid >> 6, c0 = blockIdx.x * CPB;
     const bool shared = SHARED && sg.bank == kShared;
     const uint32_t* codes = shared ? a.s2_codes : a.w2_codes + size_t(sg.bank) * kDownBankWords;
     const uint32_t* meta = shared ? a.s2_meta : a.w2_meta + size_t(sg.bank) * kDownBankMeta;
     const int route_in = a.routes[sg.first + min(tid, sg.count - 1)];
     __builtin_amdgcn_sched_barrier(0);
     const int g = lane >> 5, n = lane & 31;
-    const uint32_t* wp = codes + (size_t(c) * 2 + g) * 1024 + 8 * q * 32 + n;
-    uint32_t wr[8];
+    uint32_t wr[CPB][8], mw[CPB];
 #pragma unroll
-    for (int j = 0; j < 8; ++j) wr[j] = wp[j * 32];
-    const uint32_t mw = meta[(size_t(c) * 2 + g) * 32 + n];     // used by the epilogue thread (g, n) of every wave
+    for (int cc = 0; cc < CPB; ++cc) {
+        const uint32_t* wp = codes + (size_t(c0 + cc) * 2 + g) * 1024 + 8 * q * 32 + n;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) wr[cc][j] = wp[j * 32];
+    }
+#pragma unroll
+    for (int cc = 0; cc < CPB; ++cc) mw[cc] = meta[(size_t(c0 + cc) * 2 + g) * 32 + n];   // epilogue thread (g, n)
     if (tid < sg.count) lr[tid] = route_in;
     __syncthreads();
     uint2 areg;
@@ -337,31 +342,40 @@ __global__ __launch_bounds__(256) void decode_down_kernel(DecodeArgs a) {
         if (r0 + kRouteChunk < sg.count) load_chunk(r0 + kRouteChunk);
         for (int rr = 0; rr < nr; ++rr) {
             const uint4* ab = reinterpret_cast<const uint4*>(&la[rr][g * 64 + 16 * q]);
-            int dot = 0;
+            uint4 av[4];
 #pragma unroll
-            for (int c4 = 0; c4 < 4; ++c4) {
-                const uint4 av = ab[c4];
-                dot = dot4(code_even(wr[2 * c4]), int(av.x), dot);
-                dot = dot4(code_odd(wr[2 * c4]), int(av.y), dot);
-                dot = dot4(code_even(wr[2 * c4 + 1]), int(av.z), dot);
-                dot = dot4(code_odd(wr[2 * c4 + 1]), int(av.w), dot);
+            for (int c4 = 0; c4 < 4; ++c4) av[c4] = ab[c4];
+#pragma unroll
+            for (int cc = 0; cc < CPB; ++cc) {
+                int dot = 0;
+#pragma unroll
+                for (int c4 = 0; c4 < 4; ++c4) {
+                    dot = dot4(code_even(wr[cc][2 * c4]), int(av[c4].x), dot);
+                    dot = dot4(code_odd(wr[cc][2 * c4]), int(av[c4].y), dot);
+                    dot = dot4(code_even(wr[cc][2 * c4 + 1]), int(av[c4].z), dot);
+                    dot = dot4(code_odd(wr[cc][2 * c4 + 1]), int(av[c4].w), dot);
+                }
+                lpart[cc][rr][q][lane] = dot;
             }
-            lpart[rr][q][lane] = dot;
         }
         __syncthreads();
         if (tid < nr * 64) {
             // thread (route rr, group, column): the exact dot, then the group term
             const int rr = tid >> 6;
-            const int dot = lpart[rr][0][lane] + lpart[rr][1][lane] + lpart[rr][2][lane] + lpart[rr][3][lane];
-            const float term = tree_term(dot, lsa[rr][g], lss[rr][g], mw);
-            const float term1 = xor_perm_f<32>(term);       // group 1 of the same column
-            if (g == 0) {
-                float v = 0.f;
-                v = v + term;
-                v = v + term1;
-                if (shared) v = bf16_round(v);
-                if (!isfinite(v)) flags |= kFlagNonfiniteProjection;
-                a.route_out[size_t(lr[r0 + rr]) * kHidden + c * 32 + n] = v;
+#pragma unroll
+            for (int cc = 0; cc < CPB; ++cc) {
+                const int dot = lpart[cc][rr][0][lane] + lpart[cc][rr][1][lane] + lpart[cc][rr][2][lane] +
+                                lpart[cc][rr][3][lane];
+                const float term = tree_term(dot, lsa[rr][g], lss[rr][g], mw[cc]);
+                const float term1 = xor_perm_f<32>(term);       // group 1 of the same column
+                if (g == 0) {
+                    float v = 0.f;
+                    v = v + term;
+                    v = v + term1;
+                    if (shared) v = bf16_round(v);
+                    if (!isfinite(v)) flags |= kFlagNonfiniteProjection;
+                    a.route_out[size_t(lr[r0 + rr]) * kHidden + (c0 + cc) * 32 + n] = v;
+                }
             }
         }
     }
@@ -382,6 +396,8 @@ void carve_decode(void* base, DecodeArgs& a) {
     a.routes = static_cast<int32_t*>(take(kMaxRoutes * 4));
     a.nseg = static_cast<int32_t*>(take(8));
 }
+
+constexpr int kDownTilesPerBlock = 2;    // 32-column down tiles per block (2048 / 32 / 2 = 32 blocks per segment)
 
 template <bool ROUTER, bool SHARED, int QMAX>
 static hipError_t run(const DecodeArgs& a, hipStream_t s) {
@@ -407,7 +423,8 @@ static hipError_t run(const DecodeArgs& a, hipStream_t s) {
     if (st != hipSuccess) return st;
     st = launch_quant_middle(a.middle, RS, R, a.reduce_ids, QMAX, a.m_words, a.m_scales, a.m_sums, a.sticky, s);
     if (st != hipSuccess) return st;
-    timed_launch("down", decode_down_kernel<SHARED>, dim3(kHidden / 32, maxseg), dim3(256), 0, s, a);
+    timed_launch("down", decode_down_kernel<SHARED, kDownTilesPerBlock>, dim3(kHidden / (32 * kDownTilesPerBlock), maxseg),
+                 dim3(256), 0, s, a);
     st = hipGetLastError();
     if (st != hipSuccess) return st;
     return launch_reduce(a.route_out, a.reduce_w, a.reduce_ids, T, a.final_f32, a.out, a.shared_logit,
