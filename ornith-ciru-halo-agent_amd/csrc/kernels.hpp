@@ -92,7 +92,8 @@ struct MfmaArgs {
     const float* silu_table;
     uint32_t* sticky;
     // dense head (rows = R, identity; columns N): fp32 and bf16 logits [R, N],
-    // per-128-column argmax partials [R, ceil(N/128)], the dense flag bits
+    // argmax partials [R, partials] (one per wave of the <= 32-row kernel or per
+    // 128-column block of the 33..64-row kernel), the dense flag bits
     int N;
     uint16_t* out_bf16;
     float* arg_val; int32_t* arg_idx;
