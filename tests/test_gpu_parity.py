@@ -480,10 +480,10 @@ def test_head_w8_bit_exact(device, M, N, dots):
     assert int(flags.item()) == ref_flags
 
 
-# 1..16 and 17..32 rows take the streaming head (one or two row tiles; 2080
-# columns split into ranges of 4 and 5 tiles, so odd ranges pair a tile with
-# itself), 48 rows the row-tile kernel
-@pytest.mark.parametrize('M,N', [(1, 4096), (32, 151936), (17, 2080), (48, 8192)])
+# 1..32 rows take the 32x32x32 streaming head (2080 columns = 65 code tiles
+# over 32 waves: ranges of 2 and 3 tiles), 48 rows the row-tile kernel; 32
+# and 96 columns give a single wave with one and three tiles
+@pytest.mark.parametrize('M,N', [(1, 4096), (32, 151936), (17, 2080), (48, 8192), (5, 32), (32, 96)])
 def test_head_g256_logits_and_argmax(device, M, N):
     import torch
     native = _native()
