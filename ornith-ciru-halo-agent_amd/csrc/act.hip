@@ -117,31 +117,44 @@ __global__ __launch_bounds__(256) void transform_bf16_kernel(const uint16_t* __r
     flag_or(sticky, flags);
 }
 
-// One thread per packed code word: eight bf16 weights RN(RN(s*code)+off).
+// Four packed code words per thread (32 bf16 weights RN(RN(s*code)+off)).
+// Threads walk the code words in storage order ([N/tile, K/256, 32, tile]:
+// column fastest), four adjacent columns each, so a wave reads one contiguous
+// 1 KiB run; each word becomes its column's 16-byte run of eight weights
+// (tile / 4 lanes per chunk j, so every row gets 64 / (tile / 4) adjacent
+// runs per wave).
 __global__ __launch_bounds__(256) void dequantize_bf16_kernel(const uint32_t* __restrict__ codes,
                                                               const uint32_t* __restrict__ meta, int N, int K,
                                                               int tile, uint16_t* __restrict__ w, uint32_t* sticky) {
-    const size_t idx = size_t(blockIdx.x) * 256 + threadIdx.x;   // over N * K/8 words, row-major output order
+    const size_t idx = (size_t(blockIdx.x) * 256 + threadIdx.x) * 4;   // first of four words, storage order
     const size_t total = size_t(N) * (K / 8);
     if (idx >= total) return;
     const int groups = K / kGroup;
-    const int n = int(idx / (K / 8));
-    const int kw = int(idx % (K / 8));
-    const int g = kw / 32, j = kw % 32;
-    const uint32_t word = codes[((size_t(n / tile) * groups + g) * 32 + j) * tile + (n % tile)];
-    const uint32_t m = meta[(size_t(n / tile) * groups + g) * tile + (n % tile)];
-    const float scale = f16_bits_to_f32(m & 0xffffu), offset = f16_bits_to_f32(m >> 16);
-    uint32_t out[4];
+    const int c = int(idx % tile);                               // columns c .. c+3 of the tile
+    const size_t rest = idx / tile;                              // (column tile, group, chunk j)
+    const int j = int(rest % 32);
+    const size_t tg = rest / 32;                                 // column tile * groups + group
+    const int g = int(tg % groups), nt = int(tg / groups);
+    const int kw = g * 32 + j;
+    const uint4 words = *reinterpret_cast<const uint4*>(codes + idx);
+    const uint32_t* mp = meta + tg * tile + c;                   // metadata: 4-byte alignment only
+    const uint32_t wv[4] = {words.x, words.y, words.z, words.w}, mv[4] = {mp[0], mp[1], mp[2], mp[3]};
     uint32_t flags = 0;
 #pragma unroll
-    for (int i = 0; i < 8; i += 2) {
-        const float a = scale * float((word >> (4 * i)) & 15u) + offset;
-        const float b = scale * float((word >> (4 * i + 4)) & 15u) + offset;
-        const uint16_t ra = f32_to_bf16_bits(a), rb = f32_to_bf16_bits(b);
-        if ((ra & 0x7f80u) == 0x7f80u || (rb & 0x7f80u) == 0x7f80u) flags |= kDenseNonfiniteBf16;
-        out[i / 2] = ra | (uint32_t(rb) << 16);
+    for (int e = 0; e < 4; ++e) {
+        const float scale = f16_bits_to_f32(mv[e] & 0xffffu), offset = f16_bits_to_f32(mv[e] >> 16);
+        uint32_t out[4];
+#pragma unroll
+        for (int i = 0; i < 8; i += 2) {
+            const float a = scale * float((wv[e] >> (4 * i)) & 15u) + offset;
+            const float b = scale * float((wv[e] >> (4 * i + 4)) & 15u) + offset;
+            const uint16_t ra = f32_to_bf16_bits(a), rb = f32_to_bf16_bits(b);
+            if ((ra & 0x7f80u) == 0x7f80u || (rb & 0x7f80u) == 0x7f80u) flags |= kDenseNonfiniteBf16;
+            out[i / 2] = ra | (uint32_t(rb) << 16);
+        }
+        const int n = nt * tile + c + e;
+        *reinterpret_cast<uint4*>(w + size_t(n) * K + size_t(kw) * 8) = make_uint4(out[0], out[1], out[2], out[3]);
     }
-    *reinterpret_cast<uint4*>(w + size_t(n) * K + size_t(kw) * 8) = make_uint4(out[0], out[1], out[2], out[3]);
     flag_or(sticky, flags);
 }
 
@@ -153,8 +166,8 @@ hipError_t launch_transform_bf16(const uint16_t* x, int M, int K, uint16_t* y, u
 
 hipError_t launch_dequantize_bf16(const uint32_t* codes, const uint32_t* meta, int N, int K, int tile, uint16_t* w,
                                   uint32_t* sticky, hipStream_t s) {
-    const size_t total = size_t(N) * (K / 8);
-    timed_launch("dequantize", dequantize_bf16_kernel, dim3((total + 255) / 256), dim3(256), 0, s, codes, meta, N, K, tile, w, sticky);
+    const size_t threads = size_t(N) * (K / 8) / 4;    // tile >= 16: four words never straddle a tile row
+    timed_launch("dequantize", dequantize_bf16_kernel, dim3((threads + 255) / 256), dim3(256), 0, s, codes, meta, N, K, tile, w, sticky);
     return hipGetLastError();
 }
 
