@@ -136,9 +136,10 @@ __global__ __launch_bounds__(256) void dequantize_bf16_kernel(const uint32_t* __
     const size_t tg = rest / 32;                                 // column tile * groups + group
     const int g = int(tg % groups), nt = int(tg / groups);
     const int kw = g * 32 + j;
-    const uint4 words = *reinterpret_cast<const uint4*>(codes + idx);
-    const uint32_t* mp = meta + tg * tile + c;                   // metadata: 4-byte alignment only
-    const uint32_t wv[4] = {words.x, words.y, words.z, words.w}, mv[4] = {mp[0], mp[1], mp[2], mp[3]};
+    // codes and metadata carry 4-byte alignment only (prepare_bf16's contract)
+    const uint32_t* cp = codes + idx;
+    const uint32_t* mp = meta + tg * tile + c;
+    const uint32_t wv[4] = {cp[0], cp[1], cp[2], cp[3]}, mv[4] = {mp[0], mp[1], mp[2], mp[3]};
     uint32_t flags = 0;
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
