@@ -49,15 +49,15 @@ DENSE_N = 6144
 # --copy-calibration); keyed by (kernel, tokens).  Commands and raw figures:
 # profiles/decode_n1_n32_hbm_traffic_pmc.md, profiles/prefill_1120_8192_hbm_traffic_pmc.md.
 MEASURED_TRAFFIC = {
-    ('route1', 1): 1166677, ('gateup1', 1): 9949513, ('down1', 1): 5118568,
-    ('route', 32): 2589160, ('topk', 32): 128330, ('sort', 32): 12783, ('gateup', 32): 176480657,
-    ('quant_middle', 32): 804924, ('down', 32): 90912611, ('reduce', 32): 2587151,
-    ('router_act', 1120): 21182550, ('topk', 1120): 1395533, ('permute_scan', 1120): 774086,
-    ('permute_scatter', 1120): 335852, ('gateup_mfma', 1120): 189276903, ('quant_middle', 1120): 26020114,
-    ('down_mfma', 1120): 169427032, ('reduce', 1120): 87580105,
-    ('router', 8192): 51034311, ('topk', 8192): 9612528, ('permute_scan', 8192): 5299834,
-    ('permute_scatter', 8192): 1546388, ('act', 8192): 50832614, ('gateup_mfma', 8192): 623566473,
-    ('quant_middle', 8192): 189712920, ('down_mfma', 8192): 844326551, ('reduce', 8192): 639965506,
+    ('route1', 1): 1166652, ('gateup1', 1): 9949504, ('down1', 1): 5118494,
+    ('route', 32): 2587625, ('topk', 32): 128330, ('sort', 32): 12783, ('gateup', 32): 176480790,
+    ('quant_middle', 32): 804902, ('down', 32): 90919803, ('reduce', 32): 2587151,
+    ('router_act', 1120): 21187047, ('topk', 1120): 1395534, ('permute_scan', 1120): 774087,
+    ('permute_scatter', 1120): 335833, ('gateup_mfma', 1120): 189333643, ('quant_middle', 1120): 26020119,
+    ('down_mfma', 1120): 169450349, ('reduce', 1120): 87580019,
+    ('router', 8192): 51037662, ('topk', 8192): 9612530, ('permute_scan', 8192): 5299835,
+    ('permute_scatter', 8192): 1546389, ('act', 8192): 50822386, ('gateup_mfma', 8192): 623576104,
+    ('quant_middle', 8192): 189712996, ('down_mfma', 8192): 844245682, ('reduce', 8192): 639966906,
 }
 
 
