@@ -1,0 +1,29 @@
+"""bench.py pieces that need no GPU: the single-GPU guard and the algorithmic
+byte counts the rooflines divide by."""
+import subprocess
+import sys
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parents[1]
+sys.path.insert(0, str(ROOT))
+
+
+def test_more_than_one_gpu_is_refused():
+    r = subprocess.run([sys.executable, str(ROOT / 'bench.py'), '--gpus', '2'], capture_output=True, text=True,
+                       timeout=120, cwd=ROOT)
+    assert r.returncode != 0
+    assert 'one GPU' in (r.stdout + r.stderr)
+
+
+def test_single_token_algorithmic_bytes():
+    import bench
+    # one N=1 layer: 8 routed banks + the shared expert, A8 activations,
+    # fp32 middle rows, bf16 output (the figures the N=1 roofline divides by)
+    _, gateup, _, unit = bench.kernel_cost('gateup1', 1, 8)
+    _, down, _, _ = bench.kernel_cost('down1', 1, 8)
+    assert unit == 'GB/s'
+    assert gateup == 9 * 1_081_344 + 2048 + 9 * 512 * 4 == 9_752_576
+    assert down == 9 * 540_672 + 9 * 512 * 4 + 2048 * 2 == 4_888_576
+    # prefill matrix-core work: 2 ops per MAC over 9 routes per token
+    _, ops, _, unit = bench.kernel_cost('gateup_mfma', 1120, 96)
+    assert unit == 'TFLOP/s' and ops == 2 * 9 * 1120 * 1024 * 2048
