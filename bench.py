@@ -310,7 +310,7 @@ def main():
     args = parse()
     if args.gpus != 1:
         print(f'bench.py runs on one GPU only (asked for --gpus {args.gpus}); the multi-GPU expert-parallel '
-              f'path is not part of this build.', file=sys.stderr)
+              f'path is not part of this library.', file=sys.stderr)
         sys.exit(2)
     import torch
     from ornith_g256 import native, synthetic, tables

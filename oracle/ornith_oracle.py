@@ -2,7 +2,7 @@
 
 TEST INFRASTRUCTURE ONLY.  This module is the correctness oracle: it may be
 imported by ``tests/``, ``__graft_entry__.smoke()`` and the ``cpu_baseline``
-leg of ``bench.py``, and only as the checker.  The product path (the HIP
+leg of ``bench.py``, and only to check results.  The product path (the HIP
 library behind ``ornith_g256``) never calls it and fails loudly when the HIP
 extension is missing.
 
@@ -29,7 +29,7 @@ Pinning (what checks each function, tests/test_oracle.py):
                              special cases from the reference comments.
   * shared silu / sigmoid  - golden table shipped in the reference
                              (native/shared_math_reference.safetensors).
-  * router / top-k         - the reduction order is this build's own
+  * router / top-k         - the reduction order is this library's own
                              declared order (the reference's Triton row-dot
                              and vLLM topk_softmax orders are compiler- or
                              library-chosen and not importable here): the
@@ -512,7 +512,7 @@ def add_bf16(a_bits, b_bits):
 # the logits with a Triton row-dot (iu4_correctness/gates_projection.py:18-26,
 # 36-42) and selects experts in vLLM's topk_softmax (contract: moe_base.py:
 # 57-64, dtypes :53-54).  Both reduction orders are compiler/library-chosen,
-# so this build declares its own fixed order, restated here:
+# so this library declares its own fixed order, restated here:
 #   logit[t,e] = bias[e] + butterfly64( lane partial sums ), lane l
 #   accumulating fma(x[k], w[k], acc) sequentially over k = 8c..8c+7 for
 #   c = l, l+64, l+128, l+192.
@@ -581,7 +581,7 @@ def softmax_topk(logits, k=TOP):
 # ----------------------------------------------------------------------------
 # Token permute (routed_storage_n32_prefill.h:19-42): counts, exclusive
 # offsets and per-expert route lists.  The reference fills each list with
-# atomic cursors (any order); this build's order is stable (ascending route
+# atomic cursors (any order); this library's order is stable (ascending route
 # index), so the oracle returns that order.
 # ----------------------------------------------------------------------------
 def permute(ids, n_experts=E):

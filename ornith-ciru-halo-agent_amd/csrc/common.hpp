@@ -185,7 +185,7 @@ __device__ __forceinline__ int code_even(uint32_t w) { return int(w & 0x0f0f0f0f
 __device__ __forceinline__ int code_odd(uint32_t w) { return int((w >> 4) & 0x0f0f0f0fu); }
 __device__ __forceinline__ int dot4(int a, int b, int c) { return __builtin_amdgcn_sdot4(a, b, c, false); }
 
-// ---- Layout of quantized activations (this build's own format) ------------
+// ---- Layout of quantized activations (this library's own format) ------------
 // For row r and K chunk c (8 values k = 8c..8c+7) two int32 words are stored
 // at word index r*(K/4) + 2c and 2c+1: bytes (q[8c], q[8c+2], q[8c+4], q[8c+6])
 // and (q[8c+1], q[8c+3], q[8c+5], q[8c+7]).  Per 256-group: fp16 scale and
@@ -194,7 +194,7 @@ __device__ __forceinline__ int dot4(int a, int b, int c) { return __builtin_amdg
 // Group-256 activation quantisation on one wave.  Lane l holds the four
 // transformed values k = 4l..4l+3 of the group in v[0..3].  Implements the
 // absmax / fp16 scale / round-even / clamp recipe of
-// routed_storage_n32_consumer.cpp:44-76 with any qmax, writes this build's
+// routed_storage_n32_consumer.cpp:44-76 with any qmax, writes this library's
 // int8 layout (64 words), the scale and the sum.
 template <int QMAX>
 __device__ __forceinline__ void quantize_group_wave(float v[4], uint32_t* words, uint16_t* scale_out,

@@ -17,7 +17,7 @@
 //   S6 reduce                  slot-order combination (+ shared expert).
 //
 // Arithmetic is the reference's (routed_storage_n32_consumer.cpp:22-307); the
-// decomposition into kernels is this build's.  A single token takes the
+// decomposition into kernels is this library's.  A single token takes the
 // three-kernel path of decode1.hip.
 #include "kernels.hpp"
 #include "timing.hpp"

@@ -4,7 +4,7 @@
 // Router and top-k replace the reference's Triton row-dot
 // (iu4_correctness/gates_projection.py:18-26,36-42) and vLLM's topk_softmax
 // (contract moe_base.py:57-64, dtypes :53-54).  Both reduction orders are
-// declared by this build (the reference's are compiler/library chosen):
+// declared by this library (the reference's are compiler/library chosen):
 //   logit[t,e] = bias[e] + butterfly (masks 1,2,...,32) over 64 lanes of lane partials, lane l
 //   accumulating fma(x[k], w[k], acc) over k = 8c..8c+7 for
 //   c = l, l+64, l+128, l+192 (bf16*bf16 products are exact in fp32, so the
