@@ -95,6 +95,9 @@ def parse():
                    help='only run a plain 256 MiB device copy (PMC scale factor for FETCH_SIZE/WRITE_SIZE)')
     p.add_argument('--cpu-seconds', type=float, default=15.0)
     p.add_argument('--no-cpu-baseline', action='store_true')
+    p.add_argument('--part', choices=('head', 'dense'), default=None,
+                   help='time only the G256 LM head (32x151936) or the dense 6144x2048 prefill (1120 rows) '
+                        'and print one JSON line (for profiling those rows)')
     return p.parse_args()
 
 
@@ -319,6 +322,12 @@ def main():
         copy_calibration(dev)
         return
     native.lib()
+    if args.part == 'head':
+        print(json.dumps({'lm_head_32x151936_us': head_ms(dev, args.steps) * 1e3}))
+        return
+    if args.part == 'dense':
+        print(json.dumps({'dense_6144x2048_1120_us': dense_prefill_ms(1120, dev, args.steps) * 1e3}))
+        return
     silu, sigmoid = tables.load(dev)
     layers = [synthetic.moe_layer(10_000 + i, dev) for i in range(args.layers)]
     torch.cuda.synchronize()
