@@ -142,7 +142,9 @@ def _run_routed(native, device, d, x, w, ids, entry, Tcap=None):
                                           (3, 'ornith_routed_direct_launch_a4', 7),
                                           (70, 'ornith_routed_direct_launch_a4_prefill', 7),
                                           (20, 'ornith_routed_direct_launch_a4_prefill', 127),
-                                          (150, 'ornith_routed_direct_launch', 127)])
+                                          (150, 'ornith_routed_direct_launch', 127),
+                                          (2, 'ornith_routed_direct_launch', 127),
+                                          (33, 'ornith_routed_direct_launch', 127)])
 def test_routed_bit_exact(device, moe, T, entry, qmax):
     native = _native()
     print(f'routed T={T} {entry}', flush=True)
@@ -253,7 +255,8 @@ def test_shared_tables_bit_exact(device, moe, shared_tables, T):
 # ---------------------------------------------------------------------------
 # Router + softmax/top-8 and the whole layer
 # ---------------------------------------------------------------------------
-@pytest.mark.parametrize('T,biased', [(1, False), (33, False), (64, True), (300, True), (700, False)])
+@pytest.mark.parametrize('T,biased', [(1, False), (33, False), (64, True), (256, False), (257, True), (300, True),
+                                      (700, False)])
 def test_router_topk_bit_exact(device, moe, T, biased):
     import torch
     native = _native()
@@ -279,7 +282,7 @@ def test_router_topk_bit_exact(device, moe, T, biased):
     np.testing.assert_array_equal(from_dev(sl), O.f32_to_bf16(logits_ref[:, 256]))
 
 
-@pytest.mark.parametrize('T', [1, 32, 96, 300])
+@pytest.mark.parametrize('T', [1, 2, 32, 33, 96, 300])
 def test_moe_layer_bit_exact(device, moe, shared_tables, T):
     import torch
     native = _native()
