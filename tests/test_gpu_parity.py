@@ -315,6 +315,44 @@ def test_moe_layer_bit_exact(device, moe, shared_tables, T):
     assert int(flags.item()) == ref['flags']
 
 
+@pytest.mark.parametrize('T', [1120, 8192])
+def test_moe_layer_batch_invariance_full_size(device, moe, shared_tables, T):
+    """At the benchmark sizes, where the oracle is too slow: every token's
+    result is exact and depends on that token alone, so rows of a T-token
+    layer equal the same rows run as a 300-token layer (prefill path, itself
+    checked against the oracle), a 32-token layer (decode path) and single
+    tokens (single-token path), bit for bit, ids and weights included."""
+    import torch
+    native = _native()
+    w, d = moe
+    silu, sigmoid = shared_tables
+    print(f'layer batch invariance T={T}', flush=True)
+    rng = np.random.default_rng(6000 + T)
+    x = to_dev(bf16_normal(rng, (T, 2048)), device)
+    weights = [to_dev(w['router'], device), None, to_dev(w['gate'][0], device), d['w13'][0], d['w13'][1],
+               d['w2'][0], d['w2'][1], d['s13'][0], d['s13'][1], d['s2'][0], d['s2'][1], to_dev(silu, device),
+               to_dev(sigmoid, device)]
+
+    def layer(xs):
+        n = xs.shape[0]
+        ws = torch.empty(native.routed_layout(n, 'layer').workspace_bytes, dtype=torch.uint8, device=device)
+        out = torch.empty((n, 2048), dtype=torch.bfloat16, device=device)
+        tw = torch.empty((n, 8), dtype=torch.float32, device=device)
+        ti = torch.empty((n, 8), dtype=torch.int32, device=device)
+        sl = torch.empty((n,), dtype=torch.bfloat16, device=device)
+        flags = _flags(device)
+        native.moe_layer(xs.contiguous(), *weights, ws, tw, ti, sl, out, flags, n)
+        _sync()
+        assert int(flags.item()) == 0
+        return out, ti, tw, sl
+
+    full = layer(x)
+    for lo, hi in [(0, 300), (T - 300, T), (T // 2, T // 2 + 32), (T - 1, T), (T // 3, T // 3 + 1)]:
+        part = layer(x[lo:hi])
+        for a, b in zip(part, full):
+            assert torch.equal(a.view(torch.uint8), b[lo:hi].contiguous().view(torch.uint8)), (lo, hi)
+
+
 @pytest.mark.parametrize('T', [1, 32, 300])
 def test_moe_layer_graph_replays(device, moe, shared_tables, T):
     """The layer captured in a HIP graph (the bench's timed path): three
