@@ -70,11 +70,14 @@ def test_dense_a8_bit_exact(device, M, N, K, tile):
     assert int(flags.item()) == ref_flags
 
 
-def test_dense_prepare_bf16_bit_exact(device):
+@pytest.mark.parametrize('M,N,K', [(7, 96, 512), (1120, 6144, 2048)])
+def test_dense_prepare_bf16_bit_exact(device, M, N, K):
+    """bf16 prefill operands; 1120 x 6144 x 2048 is the benchmark's dense
+    prefill shape."""
     import torch
     native = _native()
-    rng = np.random.default_rng(99)
-    M, N, K = 7, 96, 512
+    print(f'dense prepare M={M} N={N} K={K}', flush=True)
+    rng = np.random.default_rng(99 + M)
     bank = Bank(rng, 0, N, K, tile=16)
     x = bf16_normal(rng, (M, K))
     codes, sb, ob = bank.expert()
