@@ -206,29 +206,33 @@ def roofline(times, T, unique):
 
 
 def dense_prefill_ms(T, device, steps=20):
-    """Dense G256 linear [6144, 2048] on T rows through ornith_g256::dense_out."""
+    """Dense G256 linear [6144, 2048] on T rows through ornith_g256::dense_out.
+    Up to 64 rows (the A8 GEMV, weight-streaming) 48 weight copies (312 MB)
+    rotate so the 6.5 MB bank is not MALL-resident; above, one copy."""
     import torch
     from ornith_g256 import native
     gen = torch.Generator(device=device)
     gen.manual_seed(77)
     x = torch.randn((T, 2048), generator=gen, device=device).to(torch.bfloat16)
-    codes = torch.randint(0, 2 ** 31 - 1, (DENSE_N * 2048 // 8,), generator=gen, device=device,
-                          dtype=torch.int32)
-    meta = (torch.rand((DENSE_N * 2048 // 256,), generator=gen, device=device) * 0.015 + 0.005).half()
-    meta = meta.view(torch.int16).to(torch.int32) & 0xffff
+    banks = []
+    for _ in range(48 if T <= 64 else 1):
+        codes = torch.randint(0, 2 ** 31 - 1, (DENSE_N * 2048 // 8,), generator=gen, device=device,
+                              dtype=torch.int32)
+        meta = (torch.rand((DENSE_N * 2048 // 256,), generator=gen, device=device) * 0.015 + 0.005).half()
+        banks.append((codes, meta.view(torch.int16).to(torch.int32) & 0xffff))
     layout = native.dense_layout(T, DENSE_N, 2048)
     ws = torch.empty(max(layout.workspace_bytes, T * 2048 * 2 + DENSE_N * 2048 * 2), dtype=torch.uint8,
                      device=device)
     out = torch.empty((T, DENSE_N), dtype=torch.bfloat16, device=device)
     flags = torch.zeros(1, dtype=torch.int32, device=device)
-    call = lambda: native.dense_out(x, codes, meta, ws, out, flags, T, DENSE_N, 2048, 2, 128)
-    for _ in range(3):
-        call()
+    call = lambda i: native.dense_out(x, *banks[i % len(banks)], ws, out, flags, T, DENSE_N, 2048, 2, 128)
+    for i in range(3):
+        call(i)
     torch.cuda.synchronize()
     a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     a.record()
-    for _ in range(steps):
-        call()
+    for i in range(steps):
+        call(i)
     b.record()
     torch.cuda.synchronize()
     return a.elapsed_time(b) / steps
@@ -326,7 +330,8 @@ def main():
         print(json.dumps({'lm_head_32x151936_us': head_ms(dev, args.steps) * 1e3}))
         return
     if args.part == 'dense':
-        print(json.dumps({'dense_6144x2048_1120_us': dense_prefill_ms(1120, dev, args.steps) * 1e3}))
+        print(json.dumps({'dense_6144x2048_1120_us': dense_prefill_ms(1120, dev, args.steps) * 1e3,
+                          'dense_6144x2048_1_us': dense_prefill_ms(1, dev, 48) * 1e3}))
         return
     silu, sigmoid = tables.load(dev)
     layers = [synthetic.moe_layer(10_000 + i, dev) for i in range(args.layers)]
@@ -364,6 +369,8 @@ def main():
     per_tokens[str(args.tokens)] = dict(tokens_per_s=args.tokens / (ms * 1e-3), us_per_layer=ms * 1e3,
                                         unique_experts=unique, hbm_frac=layer_gbs / HBM_PEAK_GBS,
                                         kernels_us={n: v[1] * 1e3 for n, v in times.items()})
+    if args.tokens == 1:
+        per_tokens['1']['dense_6144x2048_us'] = dense_prefill_ms(1, dev, 48) * 1e3
 
     result = {
         'metric': 'MoE layer tokens/s',

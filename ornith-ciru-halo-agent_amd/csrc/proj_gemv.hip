@@ -137,6 +137,131 @@ __global__ __launch_bounds__(256) void project_gemv_kernel(ProjArgs a, int NT, i
     }
 }
 
+// Dense weight-streaming projection for up to kStreamRows rows (decode and
+// small batches).  One block of 4 waves owns 32 consecutive output columns;
+// half-wave h of the block owns group g0 + h of the current 8-group pass.
+// Each lane keeps its 32 code words of that group in registers (every load of
+// the block is issued before the first dot), so one pass over the bank moves
+// the whole weight through HBM once however many rows there are.
+//   tile 32: lane L holds column L, words j*32 + L of block (tile, g).
+//   tile 16: lane L = 16*jp + n holds words (2i+jp)*16 + n (i < 16) of the two
+//            16-column blocks of the 32-column unit; the two half-dots of a
+//            column meet across lanes L and L^16, after which lane L keeps
+//            column L of the unit.
+// Terms go through LDS; one thread per (row, column) adds them in group order
+// (the fp32 tree of dense_g256_consumer.cpp:116-143), so results equal
+// project_gemv_kernel's bit for bit.
+constexpr int kStreamRows = 64;     // rows whose running sums stay in LDS
+constexpr int kStreamChunk = 8;     // rows per term pass (8 rows x 32 columns = 256 threads)
+
+template <int TILE>
+__global__ __launch_bounds__(256) void dense_stream_kernel(ProjArgs a) {
+    __shared__ uint32_t la[kStreamChunk][8 * 64];
+    __shared__ float lsa[kStreamChunk][8], lss[kStreamChunk][8];
+    __shared__ float lterm[kStreamChunk][8][32];
+    __shared__ float lrun[kStreamRows][32];
+
+    const int tid = threadIdx.x, hw = tid >> 5, L = tid & 31, jp = L >> 4, n16 = L & 15;
+    const int GS = a.K / kGroup, M = a.dense_rows;
+    const int col0 = blockIdx.x * 32, col = col0 + L;
+    for (int g0 = 0; g0 < GS; g0 += 8) {
+        const int g = g0 + hw, gc = min(8, GS - g0);
+        const bool gv = g < GS;
+        // Loads are unconditional (a predicated load would drain the queue):
+        // a half-wave past the last group reads group GS-1 and writes no term;
+        // a missing second 16-column block reads the first one, whose dots
+        // only reach columns >= N, which are never written.
+        const int gq = gv ? g : GS - 1;
+        uint32_t wr[32];
+        uint32_t mw;
+        if (TILE == 32) {
+            const uint32_t* wp = a.codes + (size_t(blockIdx.x) * GS + gq) * 1024 + L;
+#pragma unroll
+            for (int j = 0; j < 32; ++j) wr[j] = wp[j * 32];
+            mw = a.meta[(size_t(blockIdx.x) * GS + gq) * 32 + L];
+        } else {
+            const int tA = 2 * blockIdx.x;
+            const int tB = (tA + 1) * 16 < a.N ? tA + 1 : tA;
+            const uint32_t* pa = a.codes + (size_t(tA) * GS + gq) * 512 + jp * 16 + n16;
+            const uint32_t* pb = a.codes + (size_t(tB) * GS + gq) * 512 + jp * 16 + n16;
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                wr[i] = pa[i * 32];
+                wr[16 + i] = pb[i * 32];
+            }
+            const int cq = min(col, a.N - 1);
+            mw = a.meta[(size_t(cq >> 4) * GS + gq) * 16 + (cq & 15)];
+        }
+        for (int r0 = 0; r0 < M; r0 += kStreamChunk) {
+            const int nr = min(kStreamChunk, M - r0);
+            __syncthreads();
+            // ---- this chunk's activation words, scales and scaled sums ----
+            for (int q = tid; q < nr * gc * 16; q += 256) {
+                const int r = q / (gc * 16), w4 = q % (gc * 16);
+                *reinterpret_cast<uint4*>(&la[r][w4 * 4]) = *reinterpret_cast<const uint4*>(
+                    a.act_words + size_t(r0 + r) * (a.K / 4) + size_t(g0) * 64 + w4 * 4);
+            }
+            if (tid < nr * gc) {
+                const int r = tid / gc, gl = tid % gc;
+                const float sa = f16_bits_to_f32(a.act_scales[size_t(r0 + r) * GS + g0 + gl]);
+                lsa[r][gl] = sa;
+                lss[r][gl] = sa * float(a.act_sums[size_t(r0 + r) * GS + g0 + gl]);
+            }
+            __syncthreads();
+            for (int r = 0; r < nr; ++r) {
+                const uint32_t* ab = &la[r][hw * 64];
+                int dot;
+                if (TILE == 32) {
+                    int d = 0;
+#pragma unroll
+                    for (int c4 = 0; c4 < 16; ++c4) {
+                        const uint4 av = reinterpret_cast<const uint4*>(ab)[c4];
+                        d = dot4(code_even(wr[2 * c4]), int(av.x), d);
+                        d = dot4(code_odd(wr[2 * c4]), int(av.y), d);
+                        d = dot4(code_even(wr[2 * c4 + 1]), int(av.z), d);
+                        d = dot4(code_odd(wr[2 * c4 + 1]), int(av.w), d);
+                    }
+                    dot = d;
+                } else {
+                    int d0 = 0, d1 = 0;
+#pragma unroll
+                    for (int i = 0; i < 16; ++i) {
+                        const uint2 av = *reinterpret_cast<const uint2*>(&ab[4 * i + 2 * jp]);
+                        d0 = dot4(code_even(wr[i]), int(av.x), d0);
+                        d0 = dot4(code_odd(wr[i]), int(av.y), d0);
+                        d1 = dot4(code_even(wr[16 + i]), int(av.x), d1);
+                        d1 = dot4(code_odd(wr[16 + i]), int(av.y), d1);
+                    }
+                    const int sA = d0 + xor_perm_i<16>(d0), sB = d1 + xor_perm_i<16>(d1);
+                    dot = jp ? sB : sA;
+                }
+                if (gv) lterm[r][hw][L] = tree_term(dot, lsa[r][hw], lss[r][hw], mw);
+            }
+            __syncthreads();
+            const int r = tid >> 5;
+            if (r < nr) {
+                float v = g0 == 0 ? 0.f : lrun[r0 + r][L];
+                for (int gl = 0; gl < gc; ++gl) v = v + lterm[r][gl][L];
+                lrun[r0 + r][L] = v;
+            }
+        }
+    }
+    __syncthreads();
+    for (int q = tid; q < M * 32; q += 256) {
+        const int r = q >> 5, c = col0 + (q & 31);
+        if (c >= a.N) continue;
+        const float v = lrun[r][q & 31];
+        const size_t o = size_t(r) * a.N + c;
+        const uint16_t b = f32_to_bf16_bits(v);
+        uint32_t f = 0;
+        if (!isfinite(v)) f |= a.flag_projection;
+        if ((b & 0x7f80u) == 0x7f80u) f |= a.flag_bf16;
+        if (a.out) a.out[o] = v;
+        if (a.out_bf16) a.out_bf16[o] = b;
+        flag_or(a.sticky, f);
+    }
+}
+
 hipError_t launch_project_gemv(const ProjArgs& a, int max_segments, Out mode, hipStream_t s) {
     const int GS = a.K / kGroup;
     const int GC = GS < 8 ? GS : 8;
@@ -144,6 +269,12 @@ hipError_t launch_project_gemv(const ProjArgs& a, int max_segments, Out mode, hi
     const int ntiles = (a.N + 31) / 32;
     const dim3 grid(max_segments, (ntiles + NT - 1) / NT);
     if (max_segments <= 0) return hipSuccess;
+    if (mode == Out::Dense && !a.segments && a.dense_rows <= kStreamRows) {
+        const dim3 g((a.N + 31) / 32);
+        if (a.tile == 32) timed_launch("dense_stream", dense_stream_kernel<32>, g, dim3(256), 0, s, a);
+        else timed_launch("dense_stream", dense_stream_kernel<16>, g, dim3(256), 0, s, a);
+        return hipGetLastError();
+    }
     if (a.tile == 32) {
         if (mode == Out::Routed) timed_launch("dense_gemv", project_gemv_kernel<32, Out::Routed>, dim3(grid), dim3(256), 0, s, a, NT, GC);
         else timed_launch("dense_gemv", project_gemv_kernel<32, Out::Dense>, dim3(grid), dim3(256), 0, s, a, NT, GC);

@@ -44,7 +44,8 @@ def moe(device):
 # Dense G256 (dense_g256_consumer.cpp:172-189; dense_n32 :360-378)
 # ---------------------------------------------------------------------------
 @pytest.mark.parametrize('M,N,K,tile', [(1, 6144, 2048, 16), (1, 6144, 2048, 32), (5, 1024, 2048, 16),
-                                        (16, 2048, 512, 32), (3, 48, 768, 16), (64, 1024, 4096, 16)])
+                                        (16, 2048, 512, 32), (3, 48, 768, 16), (64, 1024, 4096, 16),
+                                        (9, 2080, 2048, 32), (2, 128, 8192, 16), (65, 96, 512, 16)])
 def test_dense_a8_bit_exact(device, M, N, K, tile):
     import torch
     native = _native()
