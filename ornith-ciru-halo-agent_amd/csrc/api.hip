@@ -229,9 +229,16 @@ hipError_t dense_run(const void* input, const void* codes, const void* meta, voi
     auto w = at<uint32_t>(ws, l.low);
     auto sc = at<uint16_t>(ws, l.scales);
     auto su = at<int32_t>(ws, l.sums);
-    TRY(launch_act_bf16(static_cast<const uint16_t*>(input), K, M, K, 127, nullptr, w, sc, su, sticky,
-                        kDenseNonfiniteInput, kDenseInvalidActivation, s));
     ProjArgs a{};
+    if (M <= kDenseFusedRows) {
+        // the projection prepares its own activations
+        a.dense_x = static_cast<const uint16_t*>(input);
+        a.flag_input = kDenseNonfiniteInput;
+        a.flag_act = kDenseInvalidActivation;
+    } else {
+        TRY(launch_act_bf16(static_cast<const uint16_t*>(input), K, M, K, 127, nullptr, w, sc, su, sticky,
+                            kDenseNonfiniteInput, kDenseInvalidActivation, s));
+    }
     a.codes = static_cast<const uint32_t*>(codes);
     a.meta = static_cast<const uint32_t*>(meta);
     a.dense_rows = M;

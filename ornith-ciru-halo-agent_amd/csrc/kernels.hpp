@@ -77,7 +77,13 @@ struct ProjArgs {
     int N, K, tile;           // tile: 16 or 32 (bank layout)
     uint32_t* sticky;
     uint32_t flag_projection, flag_bf16;
+    // dense, rows <= kDenseFusedRows: bf16 input [rows, K]; the projection
+    // kernel then prepares the activations itself (act_words unused)
+    const uint16_t* dense_x;
+    uint32_t flag_input, flag_act;
 };
+constexpr int kDenseStreamRows = 64;   // weight-streaming projection up to this many rows
+constexpr int kDenseFusedRows = 4;     // ... with activations prepared in the same kernel
 hipError_t launch_project_gemv(const ProjArgs& a, int max_segments, Out mode, hipStream_t s);
 
 // Grouped int8-MFMA projection over the permuted routes (prefill path).

@@ -13,6 +13,7 @@
 // integer dot for each route; the group tree runs in a second pass.
 #include "kernels.hpp"
 #include "timing.hpp"
+#include "act.hpp"
 
 namespace ornith {
 
@@ -148,13 +149,20 @@ __global__ __launch_bounds__(256) void project_gemv_kernel(ProjArgs a, int NT, i
 //            16-column blocks of the 32-column unit; the two half-dots of a
 //            column meet across lanes L and L^16, after which lane L keeps
 //            column L of the unit.
+// FUSED (a.dense_x set, up to kDenseFusedRows rows): the block also prepares
+// its activations from the bf16 input: the H128 +
+// group-256 int8 recipe of act_bf16_block, 16 lanes per (row, group), written
+// to LDS instead of the workspace.  Every block repeats this small amount of
+// work; the first chunk's inputs are loaded before the code words, so it runs
+// while the weights are in flight and the separate activation launch goes.
+// Otherwise the activations come from the workspace (act_words/scales/sums).
 // Terms go through LDS; one thread per (row, column) adds them in group order
 // (the fp32 tree of dense_g256_consumer.cpp:116-143), so results equal
 // project_gemv_kernel's bit for bit.
-constexpr int kStreamRows = 64;     // rows whose running sums stay in LDS
+constexpr int kStreamRows = kDenseStreamRows;   // rows whose running sums stay in LDS
 constexpr int kStreamChunk = 8;     // rows per term pass (8 rows x 32 columns = 256 threads)
 
-template <int TILE>
+template <int TILE, bool FUSED>
 __global__ __launch_bounds__(256) void dense_stream_kernel(ProjArgs a) {
     __shared__ uint32_t la[kStreamChunk][8 * 64];
     __shared__ float lsa[kStreamChunk][8], lss[kStreamChunk][8];
@@ -172,6 +180,17 @@ __global__ __launch_bounds__(256) void dense_stream_kernel(ProjArgs a) {
         // a missing second 16-column block reads the first one, whose dots
         // only reach columns >= N, which are never written.
         const int gq = gv ? g : GS - 1;
+        // input words of the first chunk's first pair pass (fused activations)
+        auto xsrc = [&](int r0, int nr, int p0) {
+            const int pc = min(p0 + (tid >> 4), nr * gc - 1);
+            return a.dense_x + size_t(r0 + pc / gc) * a.K + (g0 + pc % gc) * kGroup + quarter_base(tid & 15);
+        };
+        uint4 px0 = make_uint4(0, 0, 0, 0), px1 = px0;
+        if constexpr (FUSED) {
+            const uint16_t* xp0 = xsrc(0, min(kStreamChunk, M), 0);
+            px0 = *reinterpret_cast<const uint4*>(xp0);
+            px1 = *reinterpret_cast<const uint4*>(xp0 + 8);
+        }
         uint32_t wr[32];
         uint32_t mw;
         if (TILE == 32) {
@@ -192,20 +211,62 @@ __global__ __launch_bounds__(256) void dense_stream_kernel(ProjArgs a) {
             const int cq = min(col, a.N - 1);
             mw = a.meta[(size_t(cq >> 4) * GS + gq) * 16 + (cq & 15)];
         }
+        // the input's first use stays behind the weight loads (its wait would
+        // otherwise come before they are issued)
+        asm volatile("" : "+v"(px0.x), "+v"(px0.y), "+v"(px0.z), "+v"(px0.w), "+v"(px1.x), "+v"(px1.y), "+v"(px1.z),
+                     "+v"(px1.w));
         for (int r0 = 0; r0 < M; r0 += kStreamChunk) {
             const int nr = min(kStreamChunk, M - r0);
             __syncthreads();
             // ---- this chunk's activation words, scales and scaled sums ----
-            for (int q = tid; q < nr * gc * 16; q += 256) {
-                const int r = q / (gc * 16), w4 = q % (gc * 16);
-                *reinterpret_cast<uint4*>(&la[r][w4 * 4]) = *reinterpret_cast<const uint4*>(
-                    a.act_words + size_t(r0 + r) * (a.K / 4) + size_t(g0) * 64 + w4 * 4);
+            if constexpr (!FUSED) {
+                for (int q = tid; q < nr * gc * 16; q += 256) {
+                    const int r = q / (gc * 16), w4 = q % (gc * 16);
+                    *reinterpret_cast<uint4*>(&la[r][w4 * 4]) = *reinterpret_cast<const uint4*>(
+                        a.act_words + size_t(r0 + r) * (a.K / 4) + size_t(g0) * 64 + w4 * 4);
+                }
+                if (tid < nr * gc) {
+                    const int r = tid / gc, gl = tid % gc;
+                    const float sa = f16_bits_to_f32(a.act_scales[size_t(r0 + r) * GS + g0 + gl]);
+                    lsa[r][gl] = sa;
+                    lss[r][gl] = sa * float(a.act_sums[size_t(r0 + r) * GS + g0 + gl]);
+                }
             }
-            if (tid < nr * gc) {
-                const int r = tid / gc, gl = tid % gc;
-                const float sa = f16_bits_to_f32(a.act_scales[size_t(r0 + r) * GS + g0 + gl]);
-                lsa[r][gl] = sa;
-                lss[r][gl] = sa * float(a.act_sums[size_t(r0 + r) * GS + g0 + gl]);
+            const int pairs = FUSED ? nr * gc : 0, l = tid & 15;
+            for (int p0 = 0; p0 < pairs; p0 += 16) {
+                uint4 x0 = px0, x1 = px1;
+                if (r0 != 0 || p0 != 0) {
+                    const uint16_t* xp = xsrc(r0, nr, p0);
+                    x0 = *reinterpret_cast<const uint4*>(xp);
+                    x1 = *reinterpret_cast<const uint4*>(xp + 8);
+                }
+                const uint32_t u[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+                float v[16];
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    v[2 * e] = bf16_bits_to_f32(u[e] & 0xffffu);
+                    v[2 * e + 1] = bf16_bits_to_f32(u[e] >> 16);
+                }
+                uint32_t flags = 0;
+#pragma unroll
+                for (int e = 0; e < 16; ++e) if (!isfinite(v[e])) flags |= a.flag_input;
+                h128_quarter(v);
+                uint32_t w4[4];
+                uint16_t sbits;
+                int sum;
+                quantize_quarter_fast<127>(v, w4, sbits, sum, flags, a.flag_input | a.flag_act, a.flag_act);
+                const int pi = p0 + (tid >> 4);
+                if (pi < pairs) {
+                    const int r = pi / gc, gl = pi % gc;
+                    *reinterpret_cast<uint4*>(&la[r][gl * 64 + quarter_base(l) / 4]) =
+                        make_uint4(w4[0], w4[1], w4[2], w4[3]);
+                    if (l == 0) {
+                        const float sa = f16_bits_to_f32(sbits);
+                        lsa[r][gl] = sa;
+                        lss[r][gl] = sa * float(sum);
+                    }
+                    flag_or(a.sticky, flags);
+                }
             }
             __syncthreads();
             for (int r = 0; r < nr; ++r) {
@@ -271,8 +332,13 @@ hipError_t launch_project_gemv(const ProjArgs& a, int max_segments, Out mode, hi
     if (max_segments <= 0) return hipSuccess;
     if (mode == Out::Dense && !a.segments && a.dense_rows <= kStreamRows) {
         const dim3 g((a.N + 31) / 32);
-        if (a.tile == 32) timed_launch("dense_stream", dense_stream_kernel<32>, g, dim3(256), 0, s, a);
-        else timed_launch("dense_stream", dense_stream_kernel<16>, g, dim3(256), 0, s, a);
+        if (a.dense_x) {
+            if (a.tile == 32) timed_launch("dense_stream", dense_stream_kernel<32, true>, g, dim3(256), 0, s, a);
+            else timed_launch("dense_stream", dense_stream_kernel<16, true>, g, dim3(256), 0, s, a);
+        } else {
+            if (a.tile == 32) timed_launch("dense_stream", dense_stream_kernel<32, false>, g, dim3(256), 0, s, a);
+            else timed_launch("dense_stream", dense_stream_kernel<16, false>, g, dim3(256), 0, s, a);
+        }
         return hipGetLastError();
     }
     if (a.tile == 32) {

@@ -96,11 +96,13 @@ def test_dense_prepare_bf16_bit_exact(device, M, N, K):
     assert int(flags.item()) == 0
 
 
-def test_dense_nonfinite_flags(device):
+@pytest.mark.parametrize('M', [2, 8, 16])
+def test_dense_nonfinite_flags(device, M):
     import torch
     native = _native()
+    print(f'dense nonfinite M={M}', flush=True)
     rng = np.random.default_rng(5)
-    M, N, K = 2, 64, 256
+    N, K = 64, 256
     bank = Bank(rng, 0, N, K, tile=32)
     x = bf16_normal(rng, (M, K))
     x[1, 17] = 0x7FC0   # NaN
