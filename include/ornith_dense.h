@@ -58,7 +58,8 @@ ORNITH_EXPORT hipError_t ornith_dense_g256_prepare_bf16(
     void* transformed_bf16, void* weights_bf16, void* flags_u32,
     int M, int N, int K, hipStream_t stream);
 
-/* dense_n32/dense_g256_consumer.cpp:360-378.  N32 codes, 1<=M<=16, N%32==0, geometry==2. */
+/* dense_n32/dense_g256_consumer.cpp:360-378.  N32 codes, 1<=M<=16, N%32==0, geometry==2.
+ * Workspace regions as for ornith_dense_g256_launch. */
 ORNITH_EXPORT hipError_t ornith_dense_g256_launch_n32(
     const void* input_bf16, const void* codes, const void* metadata, void* workspace, size_t bytes,
     void* output_bf16, void* flags_u32, int M, int Mcap, int N, int K, int bits, int transform,
