@@ -45,7 +45,7 @@ ORNITH_EXPORT hipError_t ornith_dense_g256_get_layout(int Mcap, int N, int K, in
 /* dense_g256_api.h:47-50; dense_g256_consumer.cpp:172-189.  N16 codes.  transform==128,
  * geometry 0..2 (accepted; this library has one kernel family for every geometry).
  * The workspace's fp32 projection is always written; its activation words, scales
- * and sums only for M > 4 (up to 4 rows the projection kernel prepares them itself). */
+ * and sums only for M > 8 (up to 8 rows the projection kernel prepares them itself). */
 ORNITH_EXPORT hipError_t ornith_dense_g256_launch(
     const void* input_bf16, const void* codes, const void* metadata,
     void* workspace, size_t workspace_bytes, void* output_bf16, void* flags_u32,

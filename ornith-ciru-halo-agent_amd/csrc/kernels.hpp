@@ -83,7 +83,7 @@ struct ProjArgs {
     uint32_t flag_input, flag_act;
 };
 constexpr int kDenseStreamRows = 64;   // weight-streaming projection up to this many rows
-constexpr int kDenseFusedRows = 4;     // ... with activations prepared in the same kernel
+constexpr int kDenseFusedRows = 8;     // ... with activations prepared in the same kernel
 hipError_t launch_project_gemv(const ProjArgs& a, int max_segments, Out mode, hipStream_t s);
 
 // Grouped int8-MFMA projection over the permuted routes (prefill path).
