@@ -93,7 +93,7 @@ def parse():
     p.add_argument('--extra-tokens', default='32,1120,8192')
     p.add_argument('--copy-calibration', action='store_true',
                    help='only run a plain 256 MiB device copy (PMC scale factor for FETCH_SIZE/WRITE_SIZE)')
-    p.add_argument('--cpu-seconds', type=float, default=15.0)
+    p.add_argument('--oracle-seconds', type=float, default=5.0)
     p.add_argument('--no-cpu-baseline', action='store_true')
     p.add_argument('--part', choices=('head', 'dense'), default=None,
                    help='time only the G256 LM head (32x151936) or the dense 6144x2048 prefill (1120 rows) '
@@ -121,6 +121,12 @@ class LayerRunner:
         self.sl = torch.empty((T,), dtype=torch.bfloat16, device=device)
         self.flags = torch.zeros(1, dtype=torch.int32, device=device)
         self.graphs = {}
+
+    def check_flags(self):
+        """Raise if any launch of this runner set a sticky native flag."""
+        f = int(self.flags.item())
+        if f:
+            raise RuntimeError(f'native flags raised at {self.T} tokens: {f}')
 
     def step(self, i):
         L = self.layers[i % len(self.layers)]
@@ -235,6 +241,8 @@ def dense_prefill_ms(T, device, steps=20):
         call(i)
     b.record()
     torch.cuda.synchronize()
+    if int(flags.item()):
+        raise RuntimeError(f'native flags raised by the dense linear at {T} rows: {int(flags.item())}')
     wall = a.elapsed_time(b) / steps
     if T > 64:
         return wall
@@ -273,6 +281,8 @@ def head_ms(device, steps=20):
         call(i)
     b.record()
     torch.cuda.synchronize()
+    if int(flags.item()):
+        raise RuntimeError(f'native flags raised by the G256 head: {int(flags.item())}')
     return a.elapsed_time(b) / steps
 
 
@@ -288,9 +298,74 @@ def copy_calibration(device):
     print(json.dumps({'copy_bytes': n, 'copies': 10}))
 
 
-def cpu_baseline(seconds):
-    """The CPU oracle (numpy restatement of the reference A8 layer) on the host
-    cores: one N=1 layer with a shared expert, repeated for about `seconds`."""
+def cpu_model():
+    """The host CPU's model name (lscpu's "Model name", read from /proc/cpuinfo)."""
+    try:
+        for line in Path('/proc/cpuinfo').read_text().splitlines():
+            if line.startswith('model name'):
+                return line.split(':', 1)[1].strip()
+    except OSError:
+        pass
+    return 'unknown'
+
+
+def _median_seconds(fn, warmup, reps):
+    for _ in range(warmup):
+        fn()
+    times = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+    times.sort()
+    return times[len(times) // 2]
+
+
+def cpu_baseline():
+    """The reference's dequant + matmul semantics as PyTorch CPU eager
+    (oracle/cpu_eager.py) on the host cores, per benchmark configuration:
+    median of `reps` after `warmup` runs.  A reported baseline, not a target."""
+    import torch
+    sys.path.insert(0, str(ROOT))
+    from oracle import cpu_eager as CE
+    threads = torch.get_num_threads()
+    layer = CE.random_layer(7)
+    gen = torch.Generator().manual_seed(8)
+    dense_bank = CE.random_bank(gen, 0, DENSE_N, 2048)
+    head_bank = CE.random_bank(gen, 0, HEAD_N, 2048)
+    rank = torch.randperm(256, generator=torch.Generator().manual_seed(31)).float() + 1.0
+    zipf = lambda s: -s * torch.log(rank)
+    xs = {t: torch.randn((t, 2048), generator=gen).to(torch.bfloat16) for t in (1, 32, 1120, 8192)}
+    configs = {}
+
+    def record(name, tokens, seconds, sample, **extra):
+        configs[name] = dict(tokens_per_s=tokens / seconds, ms=seconds * 1e3, sample=sample, **extra)
+
+    t = _median_seconds(lambda: CE.dense(xs[1], *dense_bank), 2, 5)
+    record('dense_1x6144x2048', 1, t, 'median of 5 after 2 warm-ups')
+    t = _median_seconds(lambda: CE.moe_layer(xs[1], layer), 2, 5)
+    record('moe_n1', 1, t, 'median of 5 after 2 warm-ups')
+    t = _median_seconds(lambda: CE.moe_layer(xs[32], layer), 1, 3)
+    record('moe_n32', 32, t, 'median of 3 after 1 warm-up')
+    t = _median_seconds(lambda: CE.moe_layer(xs[1120], layer, zipf(1.1)), 1, 3)
+    record('moe_n1120_zipf1.1', 1120, t, 'median of 3 after 1 warm-up')
+    t = _median_seconds(lambda: CE.dense(xs[1120], *dense_bank), 1, 3)
+    record('dense_1120x6144x2048', 1120, t, 'median of 3 after 1 warm-up')
+    t = _median_seconds(lambda: CE.moe_layer(xs[8192], layer, zipf(1.3)), 0, 1)
+    record('moe_n8192_zipf1.3', 8192, t, 'one run (after the smaller configurations warmed the pool)')
+    t = _median_seconds(lambda: CE.dense(xs[8192][-32:].contiguous(), *head_bank), 0, 1)
+    record('lm_head_32x151936', 32, t, 'one run')
+    n1 = configs['moe_n1']
+    return dict(value=n1['tokens_per_s'], unit='tokens/s', cores=threads, kind='port',
+                sample='one N=1 MoE layer (router softmax/top-8, 8 routed + shared expert), PyTorch CPU eager fp32 '
+                       'dequantise + H128 + matmul per call, median of 5; every configuration in per_config',
+                cpu_model=cpu_model(), os_cpu_count=os.cpu_count(),
+                affinity_cpus=len(os.sched_getaffinity(0)), torch_threads=threads, per_config=configs)
+
+
+def oracle_timing(seconds):
+    """The bit-exact numpy oracle (the correctness checker, not a baseline):
+    single-token layers repeated for about `seconds`."""
     import numpy as np
     sys.path.insert(0, str(ROOT))
     sys.path.insert(0, str(ROOT / 'tests'))
@@ -313,14 +388,23 @@ def cpu_baseline(seconds):
         el = time.perf_counter() - t0
         if el >= seconds:
             break
-    try:
-        from threadpoolctl import threadpool_info
-        threads = max([i.get('num_threads', 1) for i in threadpool_info()] or [1])
-    except Exception:
-        threads = 1
-    return dict(value=runs / el, unit='tokens/s', cores=threads, kind='port',
-                sample=f'{runs} single-token MoE layers (router, top-8, 8 routed + shared expert, A8 exact) '
-                       f'in {el:.1f}s, numpy oracle, fresh expert unpacking per layer')
+    return dict(tokens_per_s=runs / el, layers=runs, seconds=el, threads=1,
+                what='numpy A8-exact oracle, single-token layers with shared expert (element-wise numpy, one thread)')
+
+
+def binding_roof(T, unique, ms):
+    """Per-layer roofline: t_mem = algorithmic bytes / HBM peak, t_mfma =
+    algorithmic MACs x 2 / matrix peak (int8, the arithmetic used; bf16 for
+    reference), binding = the larger; fractions = roof time / measured."""
+    bytes_, flops = algorithmic(T, unique)
+    t_mem = bytes_ / (HBM_PEAK_GBS * 1e9)
+    t_int8 = flops / (INT8_PEAK_TOPS * 1e12)
+    t_bf16 = flops / (BF16_PEAK_TFLOPS * 1e12)
+    t = ms * 1e-3
+    return dict(algorithmic_bytes=bytes_, algorithmic_ops=flops, t_mem_us=t_mem * 1e6, t_mfma_int8_us=t_int8 * 1e6,
+                t_mfma_bf16_us=t_bf16 * 1e6, binding='hbm' if t_mem >= t_int8 else 'mfma',
+                frac_binding=max(t_mem, t_int8) / t, frac_hbm=t_mem / t, frac_mfma_int8=t_int8 / t,
+                frac_mfma_bf16=t_bf16 / t)
 
 
 def main():
@@ -352,10 +436,11 @@ def main():
     bias_of = lambda T: synthetic.zipf_bias(zipf[T], 31, dev) if T in zipf else None
     runner = LayerRunner(layers, args.tokens, dev, silu, sigmoid, bias_of(args.tokens))
     ms = runner.time_steps(args.steps, args.warmup)
-    if int(runner.flags.item()) != 0:
-        raise RuntimeError(f'native flags raised: {int(runner.flags.item())}')
+    runner.check_flags()
     unique = runner.routed_experts_touched()
+    runner.check_flags()
     times = runner.kernel_times(args.steps)
+    runner.check_flags()
     bytes_, flops = algorithmic(args.tokens, unique)
     layer_gbs = bytes_ / (ms * 1e-3) / 1e9
 
@@ -365,12 +450,16 @@ def main():
             continue
         r = LayerRunner(layers, t, dev, silu, sigmoid, bias_of(t))
         tms = r.time_steps(max(args.layers, 40), 0)
+        r.check_flags()
         u = r.routed_experts_touched()
+        r.check_flags()
         b, f = algorithmic(t, u)
         kt = r.kernel_times(len(layers))
+        r.check_flags()
         entry = dict(tokens_per_s=t / (tms * 1e-3), us_per_layer=tms * 1e3, unique_experts=u,
                      router_zipf_s=zipf.get(t), hbm_frac=b / (tms * 1e-3) / 1e9 / HBM_PEAK_GBS,
-                     roofline=roofline(kt, t, u), kernels_us={n: v[1] * 1e3 for n, v in kt.items()})
+                     roofline=roofline(kt, t, u), layer_roof=binding_roof(t, u, tms),
+                     kernels_us={n: v[1] * 1e3 for n, v in kt.items()})
         if t == 1120:
             entry['dense_6144x2048_us'] = dense_prefill_ms(t, dev) * 1e3
         if t == 8192:
@@ -379,6 +468,7 @@ def main():
         del r
     per_tokens[str(args.tokens)] = dict(tokens_per_s=args.tokens / (ms * 1e-3), us_per_layer=ms * 1e3,
                                         unique_experts=unique, hbm_frac=layer_gbs / HBM_PEAK_GBS,
+                                        layer_roof=binding_roof(args.tokens, unique, ms),
                                         kernels_us={n: v[1] * 1e3 for n, v in times.items()})
     if args.tokens == 1:
         wall1, device1 = dense_prefill_ms(1, dev, 48)
@@ -406,7 +496,8 @@ def main():
         'per_tokens': per_tokens,
     }
     if not args.no_cpu_baseline:
-        result['cpu_baseline'] = cpu_baseline(args.cpu_seconds)
+        result['cpu_baseline'] = cpu_baseline()
+        result['oracle'] = oracle_timing(args.oracle_seconds)
     print(json.dumps(result))
 
 

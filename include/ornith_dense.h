@@ -12,7 +12,7 @@
  * workspace (dense_g256_api.h:32-38).
  * Contract differences: workspace internals are this library's own
  * (OrnithDenseG256Layout keeps the field names; unused fields have size 0);
- * input alignment 8 bytes, codes 16 bytes.
+ * input alignment 16 bytes, codes 16 bytes.
  * Flags: 1 non-finite input/transform, 2 invalid activation, 4 non-finite
  * projection, 8 non-finite bf16 (dense_g256_api.h:14-19).
  */
@@ -74,7 +74,7 @@ ORNITH_EXPORT int ornith_dense_g256_n32_rows(void);
  * 1<=M<=64 and any N%32==0 up to 262144; writes fp32 logits [M,N], bf16 logits
  * [M,N] (nullable) and the top-1 index int64 [M] (numpy's argmax rule: the
  * first NaN if any, else the first maximum).  Runs on the int8 matrix cores.
- * Alignment: logits_f32 16 bytes, logits_bf16 8 bytes, argmax 8, codes 16.
+ * Alignment: input 16 bytes, logits_f32 16, logits_bf16 8, argmax 8, codes 16.
  * Workspace: ornith_dense_g256_head_workspace_bytes(Mcap, N). */
 ORNITH_EXPORT size_t ornith_dense_g256_head_workspace_bytes(int Mcap, int N);
 ORNITH_EXPORT hipError_t ornith_dense_g256_head_launch(

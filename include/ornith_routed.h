@@ -21,7 +21,7 @@
  *   - workspace internals are this library's own; OrnithRoutedDirectLayout keeps
  *     the reference field names and order but fields this library does not use
  *     have size zero, so workspace_bytes differs from the reference's;
- *   - alignment: input 8 bytes, codes 16 bytes, workspace 256 bytes;
+ *   - alignment: input 16 bytes, codes 16 bytes, workspace 256 bytes;
  *   - Tcap <= 8192 for every entry (the reference's N16 parent allowed 2048).
  * Sticky flags (uint32, OR-ed, never cleared): 1 non-finite input/transform,
  * 2 invalid activation scale, 4 invalid expert id (other than -1), 8 non-finite

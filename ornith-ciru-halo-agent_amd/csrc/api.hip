@@ -1,10 +1,10 @@
 // extern "C" entry points.  Argument validation is host-only and runs before
 // any launch; every entry enqueues on the caller's stream and allocates
 // nothing.  The references for each entry are in include/ornith_*.h.
-#include <limits>
 #include "kernels.hpp"
 #include "timing.hpp"
 #include "decode.hpp"
+#include "validate.hpp"
 #include "../../include/ornith_routed.h"
 #include "../../include/ornith_dense.h"
 #include "../../include/ornith_moe.h"
@@ -17,8 +17,6 @@ namespace {
 
 constexpr int kMaxTokens = 8192;
 constexpr int kGateN = 2 * kInter, kDownN = kHidden;
-
-bool aligned(const void* p, size_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
 
 // Workspace plan shared by the routed, shared-slot and whole-layer entries.
 struct RoutedPlan {
@@ -170,7 +168,7 @@ hipError_t routed_launch(const void* input, const void* weights, const void* ids
     if (!input || !weights || !ids || !gate_codes || !gate_meta || !down_codes || !down_meta || !workspace || !output ||
         !flags)
         return hipErrorInvalidValue;
-    if (!aligned(input, 8) || !aligned(weights, 4) || !aligned(ids, 4) || !aligned(gate_codes, 16) ||
+    if (!aligned(input, 16) || !aligned(weights, 4) || !aligned(ids, 4) || !aligned(gate_codes, 16) ||
         !aligned(down_codes, 16) || !aligned(gate_meta, 4) || !aligned(down_meta, 4) || !aligned(workspace, 256) ||
         !aligned(output, 8) || !aligned(flags, 4))
         return hipErrorInvalidValue;
@@ -203,25 +201,6 @@ OrnithDenseG256Layout dense_layout(int Mcap, int N, int K) {
     add(l.projection, m * N * 4);
     l.workspace_bytes = cursor;
     return l;
-}
-
-struct Range { uintptr_t lo, hi; };
-bool to_range(const void* p, size_t n, Range& r) {
-    const uintptr_t lo = reinterpret_cast<uintptr_t>(p);
-    if (!p || n > std::numeric_limits<uintptr_t>::max() - lo) return false;
-    r = {lo, lo + n};
-    return true;
-}
-// Pointer, alignment and overlap checks of dense_g256_consumer.cpp:240-245:
-// entries [first_mutable, n) must not overlap any other range.
-bool check_ranges(const void* const* ptr, const size_t* sizes, const size_t* align, int n, int first_mutable) {
-    Range r[8];
-    for (int i = 0; i < n; ++i)
-        if (!aligned(ptr[i], align[i]) || !to_range(ptr[i], sizes[i], r[i])) return false;
-    for (int i = first_mutable; i < n; ++i)
-        for (int j = 0; j < n; ++j)
-            if (i != j && r[i].lo < r[j].hi && r[j].lo < r[i].hi) return false;
-    return true;
 }
 
 hipError_t dense_run(const void* input, const void* codes, const void* meta, void* ws, const OrnithDenseG256Layout& l,
@@ -289,7 +268,8 @@ extern "C" hipError_t ornith_routed_direct_launch_a4_prefill(const void* input, 
                               output, flags, T, Tcap, stream);
 }
 
-extern "C" int ornith_routed_storage_n32(void) { return 32; }
+// 32 in the N32-storage build, 16 in the N16 build (the bank tile the routed entries read)
+extern "C" int ornith_routed_storage_n32(void) { return kRoutedTile; }
 extern "C" int ornith_routed_prefill_output_tile(void) { return 32; }
 
 extern "C" hipError_t ornith_routed_shared_get_layout(int Tcap, OrnithRoutedDirectLayout* out) {
@@ -312,7 +292,7 @@ extern "C" hipError_t ornith_routed_direct_launch_shared_tables(
                          shared_gate_meta, shared_down_codes, shared_down_meta, shared_logit, shared_silu,
                          shared_sigmoid, workspace, output, shared_output, flags};
     for (const void* q : req) if (!q) return hipErrorInvalidValue;
-    if (!aligned(input, 8) || !aligned(gate_codes, 16) || !aligned(down_codes, 16) || !aligned(shared_gate_codes, 16) ||
+    if (!aligned(input, 16) || !aligned(gate_codes, 16) || !aligned(down_codes, 16) || !aligned(shared_gate_codes, 16) ||
         !aligned(shared_down_codes, 16) || !aligned(workspace, 256) || !aligned(output, 8) ||
         !aligned(shared_output, 8) || !aligned(flags, 4))
         return hipErrorInvalidValue;
@@ -322,12 +302,6 @@ extern "C" hipError_t ornith_routed_direct_launch_shared_tables(
                       static_cast<const float*>(shared_silu), static_cast<const uint16_t*>(shared_sigmoid), 127,
                       static_cast<uint16_t*>(output), static_cast<uint16_t*>(shared_output), nullptr,
                       static_cast<uint32_t*>(flags), T, stream);
-    return run_routed(p, workspace, input, static_cast<const float*>(weights), static_cast<const int32_t*>(ids),
-                      gate_codes, gate_meta, down_codes, down_meta, shared_gate_codes, shared_gate_meta,
-                      shared_down_codes, shared_down_meta, static_cast<const uint16_t*>(shared_logit),
-                      static_cast<const float*>(shared_silu), static_cast<const uint16_t*>(shared_sigmoid), 127,
-                      static_cast<uint16_t*>(output), static_cast<uint16_t*>(shared_output), nullptr,
-                      static_cast<uint32_t*>(flags), T, Tcap, stream);
 }
 
 // =============================================================================
@@ -434,11 +408,13 @@ extern "C" hipError_t ornith_dense_g256_launch(const void* input, const void* co
         return hipErrorInvalidValue;
     if (M == 0) return hipSuccess;
     if (bytes < l.workspace_bytes) return hipErrorInvalidValue;
-    const void* ptr[] = {input, codes, metadata, workspace, output, flags};
-    const size_t sizes[] = {size_t(M) * K * 2, size_t(N) * K / 2, size_t(N) * (K / kGroup) * 4, bytes,
-                            size_t(M) * N * 2, 4};
-    const size_t align[] = {8, 16, 4, 256, 2, 4};
-    if (!check_ranges(ptr, sizes, align, 6, 3)) return hipErrorInvalidValue;
+    const Buffer buffers[] = {{input, size_t(M) * K * 2, 16, false, false},
+                              {codes, size_t(N) * K / 2, 16, false, false},
+                              {metadata, size_t(N) * (K / kGroup) * 4, 4, false, false},
+                              {workspace, bytes, 256, true, false},
+                              {output, size_t(M) * N * 2, 2, true, false},
+                              {flags, 4, 4, true, false}};
+    if (!check_buffers(buffers)) return hipErrorInvalidValue;
     return dense_run(input, codes, metadata, workspace, l, at<float>(workspace, l.projection),
                      static_cast<uint16_t*>(output), static_cast<uint32_t*>(flags), M, N, K, 16, stream);
 }
@@ -448,11 +424,13 @@ extern "C" hipError_t ornith_dense_g256_prepare_bf16(const void* input, const vo
                                                      hipStream_t stream) {
     if (M < 0 || M > kMaxTokens || !dense_shape(N, K)) return hipErrorInvalidValue;
     if (M == 0) return hipSuccess;
-    const void* ptr[] = {input, codes, metadata, transformed, weights, flags};
-    const size_t sizes[] = {size_t(M) * K * 2, size_t(N) * K / 2, size_t(N) * (K / kGroup) * 4, size_t(M) * K * 2,
-                            size_t(N) * K * 2, 4};
-    const size_t align[] = {8, 4, 4, 8, 16, 4};
-    if (!check_ranges(ptr, sizes, align, 6, 3)) return hipErrorInvalidValue;
+    const Buffer buffers[] = {{input, size_t(M) * K * 2, 8, false, false},
+                              {codes, size_t(N) * K / 2, 4, false, false},
+                              {metadata, size_t(N) * (K / kGroup) * 4, 4, false, false},
+                              {transformed, size_t(M) * K * 2, 8, true, false},
+                              {weights, size_t(N) * K * 2, 16, true, false},
+                              {flags, 4, 4, true, false}};
+    if (!check_buffers(buffers)) return hipErrorInvalidValue;
     auto sticky = static_cast<uint32_t*>(flags);
     TRY(launch_transform_bf16(static_cast<const uint16_t*>(input), M, K, static_cast<uint16_t*>(transformed), sticky,
                               stream));
@@ -468,7 +446,7 @@ extern "C" hipError_t ornith_dense_g256_launch_n32(const void* input, const void
     if (M < 1 || M > 16 || M > Mcap || N % 32 || transform != 128 || geometry != 2 ||
         ornith_dense_g256_get_layout(Mcap, N, K, bits, &l) != hipSuccess || bytes < l.workspace_bytes)
         return hipErrorInvalidValue;
-    if (!input || !codes || !metadata || !workspace || !output || !flags || !aligned(input, 8) || !aligned(codes, 16) ||
+    if (!input || !codes || !metadata || !workspace || !output || !flags || !aligned(input, 16) || !aligned(codes, 16) ||
         !aligned(workspace, 256))
         return hipErrorInvalidValue;
     return dense_run(input, codes, metadata, workspace, l, at<float>(workspace, l.projection),
@@ -499,7 +477,7 @@ extern "C" hipError_t ornith_dense_g256_head_launch(const void* input, const voi
     if (Mcap < 1 || Mcap > 64 || M < 0 || M > Mcap || N <= 0 || N % 32 || N > 262144) return hipErrorInvalidValue;
     if (bytes < ornith_dense_g256_head_workspace_bytes(Mcap, N)) return hipErrorInvalidValue;
     if (M == 0) return hipSuccess;
-    if (!input || !codes || !metadata || !workspace || !logits_f32 || !argmax_i64 || !flags || !aligned(input, 8) ||
+    if (!input || !codes || !metadata || !workspace || !logits_f32 || !argmax_i64 || !flags || !aligned(input, 16) ||
         !aligned(codes, 16) || !aligned(workspace, 256) || !aligned(logits_f32, 16) ||
         (logits_bf16 && !aligned(logits_bf16, 8)) || !aligned(argmax_i64, 8))
         return hipErrorInvalidValue;

@@ -34,6 +34,33 @@ enum : uint32_t {
     kDenseNonfiniteProjection = 4, kDenseNonfiniteBf16 = 8,
 };
 
+// Routed expert banks come in tiles of ORNITH_ROUTED_TILE output columns:
+// 32 is the N32 storage (routed_storage_n32_consumer.cpp:1-2), 16 the
+// checkpoint's N16 storage read by the parent routed library
+// (routed_direct_api.h:7).  The library is built once per tile width.
+// Shared-expert banks are dense N32 banks in both builds.
+#ifndef ORNITH_ROUTED_TILE
+#define ORNITH_ROUTED_TILE 32
+#endif
+static_assert(ORNITH_ROUTED_TILE == 16 || ORNITH_ROUTED_TILE == 32, "routed tile must be 16 or 32");
+constexpr int kRoutedTile = ORNITH_ROUTED_TILE;
+constexpr int kRoutedTileLog2 = kRoutedTile == 16 ? 4 : 5;
+
+// Addressing inside one bank of `groups` 256-groups: codes [N/TW, groups, 32, TW]
+// (word j of column n, group g at word(n, g) + j * stride()), meta [N/TW, groups, TW].
+struct BankView {
+    int log2;   // log2 of the tile width TW
+    __device__ __forceinline__ size_t word(int n, int g, int groups) const {
+        return ((size_t(n >> log2) * groups + g) << (5 + log2)) + (n & ((1 << log2) - 1));
+    }
+    __device__ __forceinline__ size_t meta(int n, int g, int groups) const {
+        return ((size_t(n >> log2) * groups + g) << log2) + (n & ((1 << log2) - 1));
+    }
+    __device__ __forceinline__ int stride() const { return 1 << log2; }
+};
+// the view of a routed bank, or (shared) of a shared-expert bank
+__device__ __forceinline__ BankView bank_view(bool shared) { return BankView{shared ? 5 : kRoutedTileLog2}; }
+
 __host__ __device__ inline size_t align256(size_t n) { return (n + 255) & ~size_t(255); }
 template <class T> __host__ __device__ inline T* at(void* base, size_t offset) {
     return reinterpret_cast<T*>(static_cast<uint8_t*>(base) + offset);

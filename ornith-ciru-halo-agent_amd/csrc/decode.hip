@@ -203,13 +203,13 @@ __global__ __launch_bounds__(512) void decode_gateup_kernel(DecodeArgs a) {
     // route list first (waiting for it must not wait for the codes)
     const int route_in = a.routes[sg.first + min(tid, sg.count - 1)];
     __builtin_amdgcn_sched_barrier(0);
-    const int tile = lane < 32 ? p : 16 + p;
-    const size_t blk = size_t(tile) * 8 + g;
-    const uint32_t* wp = codes + blk * 1024 + (lane & 31);
+    const int col = (lane < 32 ? 0 : kInter) + 32 * p + (lane & 31);
+    const BankView bv = bank_view(shared);
+    const uint32_t* wp = codes + bv.word(col, g, 8);
     uint32_t wr[32];
 #pragma unroll
-    for (int j = 0; j < 32; ++j) wr[j] = wp[j * 32];
-    const uint32_t mw = meta[blk * 32 + (lane & 31)];
+    for (int j = 0; j < 32; ++j) wr[j] = wp[j * bv.stride()];
+    const uint32_t mw = meta[bv.meta(col, g, 8)];
     if (tid < sg.count) lr[tid] = route_in;
     __syncthreads();
     // staging registers for one chunk: route rr = tid / 128 holds words
@@ -306,14 +306,15 @@ __global__ __launch_bounds__(256) void decode_down_kernel(DecodeArgs a) {
     __builtin_amdgcn_sched_barrier(0);
     const int g = lane >> 5, n = lane & 31;
     uint32_t wr[CPB][8], mw[CPB];
+    const BankView bv = bank_view(shared);
 #pragma unroll
     for (int cc = 0; cc < CPB; ++cc) {
-        const uint32_t* wp = codes + (size_t(c0 + cc) * 2 + g) * 1024 + 8 * q * 32 + n;
+        const uint32_t* wp = codes + bv.word(32 * (c0 + cc) + n, g, 2) + 8 * q * bv.stride();
 #pragma unroll
-        for (int j = 0; j < 8; ++j) wr[cc][j] = wp[j * 32];
+        for (int j = 0; j < 8; ++j) wr[cc][j] = wp[j * bv.stride()];
     }
 #pragma unroll
-    for (int cc = 0; cc < CPB; ++cc) mw[cc] = meta[(size_t(c0 + cc) * 2 + g) * 32 + n];   // epilogue thread (g, n)
+    for (int cc = 0; cc < CPB; ++cc) mw[cc] = meta[bv.meta(32 * (c0 + cc) + n, g, 2)];   // epilogue thread (g, n)
     if (tid < sg.count) lr[tid] = route_in;
     __syncthreads();
     uint2 areg;

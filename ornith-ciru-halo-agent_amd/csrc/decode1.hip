@@ -173,12 +173,12 @@ __global__ __launch_bounds__(256) void decode1_gateup_kernel(DecodeArgs a) {
     const uint32_t* meta = shared ? a.s13_meta : a.w13_meta + size_t(bank) * kGateBankMeta;
     const int n = lane & 31, g = 2 * wave + (lane >> 5);
     const int col = n < 16 ? 16 * p + n : kInter + 16 * p + (n - 16);
-    const size_t blk = size_t(col >> 5) * 8 + g;
-    const uint32_t* wp = codes + blk * 1024 + (col & 31);
+    const BankView bv = bank_view(shared);
+    const uint32_t* wp = codes + bv.word(col, g, 8);
     uint32_t wr[32];
 #pragma unroll
-    for (int j = 0; j < 32; ++j) wr[j] = wp[j * 32];
-    const uint32_t mw = meta[blk * 32 + (col & 31)];
+    for (int j = 0; j < 32; ++j) wr[j] = wp[j * bv.stride()];
+    const uint32_t mw = meta[bv.meta(col, g, 8)];
     la[tid] = a0;
     la[tid + 256] = a1;
     if (tid < 8) {
@@ -274,15 +274,16 @@ __global__ __launch_bounds__(576) void decode1_down_kernel(DecodeArgs a) {
     // ---- down codes of (slot i, group g, column n, chunks 16h..16h+15) ----
     const int i = wave, g = gm, h = (lane >> 4) & 1, n = lane & 15;
     const int bank = i < nslots ? lbank[i] : -1;
-    const int tile = c >> 1, nn = 16 * (c & 1) + n;
+    const int col = 16 * c + n;
     const int lb = bank >= 0 ? bank : 0;
     const uint32_t* base = lb == kShared ? a.s2_codes : a.w2_codes + size_t(lb) * kDownBankWords;
     const uint32_t* mbase = lb == kShared ? a.s2_meta : a.w2_meta + size_t(lb) * kDownBankMeta;
-    const uint32_t* wp = base + (size_t(tile) * 2 + g) * 1024 + 16 * h * 32 + nn;
+    const BankView bv = bank_view(lb == kShared);
+    const uint32_t* wp = base + bv.word(col, g, 2) + 16 * h * bv.stride();
     uint32_t wr[16];
 #pragma unroll
-    for (int j = 0; j < 16; ++j) wr[j] = wp[j * 32];
-    const uint32_t mw = mbase[(size_t(tile) * 2 + g) * 32 + nn];
+    for (int j = 0; j < 16; ++j) wr[j] = wp[j * bv.stride()];
+    const uint32_t mw = mbase[bv.meta(col, g, 2)];
     // shared-expert gate: its table load goes out behind the codes, used at the end
     const uint16_t gate_bits = SHARED ? a.sigmoid_table[shared_logit] : 0;
     // ---- middle quantisation, one slot per wave ----

@@ -5,9 +5,9 @@
 // acc = acc + RN(sw * RN(sa * dot)) over the 16 groups in ascending order.
 // Weights keep the reference's tile layout uint32 [N/16, 128, 4, 16]: the
 // (n16 tile, group) block of 512 words (2 KiB) is contiguous.
-#include <limits>
 #include "kernels.hpp"
 #include "timing.hpp"
+#include "validate.hpp"
 #include "../../include/ornith_head.h"
 
 namespace ornith {
@@ -130,8 +130,6 @@ OrnithHeadI8Layout head_layout(int Mcap, int N) {
     return l;
 }
 
-struct Range { uintptr_t lo, hi; };
-
 }  // namespace
 }  // namespace ornith
 
@@ -157,23 +155,15 @@ extern "C" hipError_t ornith_head_i8_tile_launch(const void* input, const void* 
         return hipErrorInvalidValue;
     if (M == 0) return hipSuccess;
     if (workspace_bytes < l.workspace_bytes) return hipErrorInvalidValue;
-    const void* pointers[] = {input, weights, scales, workspace, output, group_dots, flags};
-    const size_t sizes[] = {size_t(M) * kHeadK * 2, size_t(N) * kHeadK, size_t(N) * kHeadGroups * 2, workspace_bytes,
-                            size_t(M) * N * 2, group_dots_bytes, 4};
-    const size_t alignments[] = {4, 16, 2, 256, 2, 4, 4};
-    Range r[7]{};
-    for (int i = 0; i < 7; ++i) {
-        if (i == 5 && !group_dots) continue;
-        const uintptr_t lo = reinterpret_cast<uintptr_t>(pointers[i]);
-        if (!pointers[i] || lo % alignments[i] || sizes[i] > std::numeric_limits<uintptr_t>::max() - lo)
-            return hipErrorInvalidValue;
-        r[i] = {lo, lo + sizes[i]};
-    }
-    for (int i = 3; i < 7; ++i)
-        for (int j = 0; j < 7; ++j) {
-            if (i == j || (!group_dots && (i == 5 || j == 5))) continue;
-            if (r[i].lo < r[j].hi && r[j].lo < r[i].hi) return hipErrorInvalidValue;
-        }
+    // inputs first, then the buffers this call writes (none may overlap another)
+    const Buffer buffers[] = {{input, size_t(M) * kHeadK * 2, 4, false, false},
+                              {weights, size_t(N) * kHeadK, 16, false, false},
+                              {scales, size_t(N) * kHeadGroups * 2, 2, false, false},
+                              {workspace, workspace_bytes, 256, true, false},
+                              {output, size_t(M) * N * 2, 2, true, false},
+                              {group_dots, group_dots_bytes, 4, true, true},
+                              {flags, 4, 4, true, false}};
+    if (!check_buffers(buffers)) return hipErrorInvalidValue;
     auto sticky = static_cast<uint32_t*>(flags);
     auto words = at<uint32_t>(workspace, l.activation_words);
     auto ascale = at<uint16_t>(workspace, l.activation_scales);

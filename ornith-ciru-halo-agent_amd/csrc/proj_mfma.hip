@@ -167,6 +167,8 @@ __global__ __launch_bounds__(256, MODE == kModeDown ? 3 : 2) void prefill_mfma_k
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, li = lane & 15, q = lane >> 4;
     const uint32_t* codes = shared ? a.shared_codes : a.codes + size_t(bank) * a.bank_words;
     const uint32_t* meta = shared ? a.shared_meta : a.meta + size_t(bank) * a.bank_meta_words;
+    // the head and the shared expert read dense N32 banks
+    const BankView bv = bank_view(HEAD || shared);
 
     // routes of this lane's A row (tid / 4) and scale row (tid % 64), first:
     // later waits on them must not wait on the code loads
@@ -200,13 +202,14 @@ __global__ __launch_bounds__(256, MODE == kModeDown ? 3 : 2) void prefill_mfma_k
         for (int ct = 0; ct < 2; ++ct) {
             int ntile, n;
             b_tile(st, ct, ntile, n);
-            const uint32_t* src = codes + (size_t(ntile) * GS + g) * 1024 + (2 * q) * 32 + n;
+            const int col = 32 * ntile + n;
+            const uint32_t* src = codes + bv.word(col, g, GS) + (2 * q) * bv.stride();
 #pragma unroll
             for (int s = 0; s < 4; ++s) {
-                bw[slot][ct][2 * s] = src[(8 * s) * 32];
-                bw[slot][ct][2 * s + 1] = src[(8 * s + 1) * 32];
+                bw[slot][ct][2 * s] = src[(8 * s) * bv.stride()];
+                bw[slot][ct][2 * s + 1] = src[(8 * s + 1) * bv.stride()];
             }
-            bm[slot][ct] = meta[(size_t(ntile) * GS + g) * 32 + n];
+            bm[slot][ct] = meta[bv.meta(col, g, GS)];
         }
     };
 #pragma unroll

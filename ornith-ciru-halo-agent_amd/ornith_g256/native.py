@@ -1,27 +1,44 @@
-"""ctypes bindings of the MI355X HIP library and the ornith_g256 torch ops.
+"""Host side of the MI355X Ornith G256 library: ctypes bindings and the
+``ornith_g256::*`` torch ops.
 
-Mirrors the reference's plugin-site/ornith_g256/native.py: the same custom-op
-names and signatures (ornith_g256::dense_out, routed_out, routed_out_n32,
-head_out; native.py:121-224), the same validation (native.py:113-118,
-176-180), the same error behaviour (RuntimeError on a non-zero native status,
-native.py:109-110) and the same configure() that sizes one workspace arena
-(native.py:28-104).  All launches go to torch's current stream with no host
-synchronisation.  New ops: router_topk and moe_layer (router + routed +
-shared expert in one launch sequence).
+Interface kept from the reference plugin (plugin-site/ornith_g256/native.py):
+the op names and signatures ``dense_out``, ``routed_out``, ``routed_out_n32``
+and ``head_out`` (native.py:121-212), the three layout Structures
+(native.py:11-24), ``configure(settings, capacity, shapes)`` returning the
+arena size (native.py:28-104), and the error behaviour - ``ValueError`` for a
+bad setting or tensor, ``RuntimeError`` for a non-zero native status.
 
-The library is loaded from this package's lib/ directory; if it is missing
-every entry raises - there is no CPU fallback.
+Design of this module:
+  * Two builds of one source tree serve every reference library role.  The
+    N32 build (``libornith_g256_mi355x.so``, storage marker 32) takes routed
+    banks in N32 tiles; the N16 build (``libornith_g256_mi355x_n16.so``,
+    marker 16) takes them in the checkpoint's N16 tiles.  Dense, head and
+    router entries are identical in both.
+  * ``configure`` resolves every library role to one of these builds and
+    records a ``Binding`` (the launch function per dispatch kind, with the
+    bank tile it expects).  Routed ops check that the banks they are handed
+    have that tile width, so a mismatched layout fails before any launch.
+  * Mixed prefill/decode batches are split by an explicit phase plan set with
+    ``phase_segments(...)`` (see phases.py), not by a module global.
+  * Launches go to torch's current stream and never synchronise.  There is
+    no CPU fallback: a missing library raises on first use.
 """
 from __future__ import annotations
 
+import contextvars
 import ctypes as C
+from contextlib import contextmanager
+from dataclasses import dataclass, field
 from pathlib import Path
 
 import torch
 
-_LIB = None
-_libs = {}
-_PHASE_SEGMENTS = ()
+LIB_DIR = Path(__file__).resolve().parent / 'lib'
+BUILDS = {32: 'libornith_g256_mi355x.so', 16: 'libornith_g256_mi355x_n16.so'}
+
+HIDDEN, EXPERTS, TOP = 2048, 256, 8
+HEAD_VOCAB, HEAD_MAX_ROWS = 248320, 64
+A8_ONLY_PREFILL_ROWS = 64      # _a4_prefill entries switch to A4 above this many tokens
 
 _ROUTED_FIELDS = ('workspace_bytes', 'gate_x', 'gate_low', 'gate_high', 'gate_scales', 'gate_sums', 'gate_y',
                   'middle', 'down_x', 'down_low', 'down_high', 'down_scales', 'down_sums', 'route_out', 'final_f32')
@@ -41,97 +58,84 @@ class HeadLayout(C.Structure):
                 ('workspace_bytes', 'transformed', 'activation_words', 'activation_scales', 'projection')]
 
 
-P, I, S, L = C.c_void_p, C.c_int, C.c_size_t, C.c_int64
-_SIGNATURES = {
-    'ornith_routed_direct_get_layout': ([I, C.POINTER(RoutedLayout)], I),
-    'ornith_routed_shared_get_layout': ([I, C.POINTER(RoutedLayout)], I),
-    'ornith_moe_layer_get_layout': ([I, C.POINTER(RoutedLayout)], I),
-    'ornith_routed_direct_launch': ([P] * 8 + [S] + [P] * 2 + [I] * 2 + [P], I),
-    'ornith_routed_direct_launch_a4': ([P] * 8 + [S] + [P] * 2 + [I] * 2 + [P], I),
-    'ornith_routed_direct_launch_a4_prefill': ([P] * 8 + [S] + [P] * 2 + [I] * 2 + [P], I),
-    'ornith_routed_direct_launch_shared_tables': ([P] * 15 + [S] + [P] * 3 + [I] * 2 + [P], I),
-    'ornith_routed_storage_n32': ([], I),
-    'ornith_routed_prefill_output_tile': ([], I),
-    'ornith_router_topk_launch': ([P, L] + [P] * 7 + [I, P], I),
-    'ornith_moe_layer_launch': ([P] * 15 + [S] + [P] * 5 + [I] * 2 + [P], I),
-    'ornith_mi355x_abi_version': ([], I),
+# ---------------------------------------------------------------------------
+# Library loading
+# ---------------------------------------------------------------------------
+_VP, _INT, _SZ, _I64 = C.c_void_p, C.c_int, C.c_size_t, C.c_int64
+_ROUTED_LAUNCH = [_VP] * 8 + [_SZ] + [_VP] * 2 + [_INT] * 2 + [_VP]
+_DENSE_LAUNCH = [_VP] * 4 + [_SZ] + [_VP] * 2 + [_INT] * 7 + [_VP]
+_PROTOTYPES = {
+    # routed (include/ornith_routed.h)
+    'ornith_routed_direct_get_layout': ([_INT, C.POINTER(RoutedLayout)], _INT),
+    'ornith_routed_direct_launch': (_ROUTED_LAUNCH, _INT),
+    'ornith_routed_direct_launch_a4': (_ROUTED_LAUNCH, _INT),
+    'ornith_routed_direct_launch_a4_prefill': (_ROUTED_LAUNCH, _INT),
+    'ornith_routed_shared_get_layout': ([_INT, C.POINTER(RoutedLayout)], _INT),
+    'ornith_routed_direct_launch_shared_tables': ([_VP] * 15 + [_SZ] + [_VP] * 3 + [_INT] * 2 + [_VP], _INT),
+    'ornith_routed_storage_n32': ([], _INT),
+    'ornith_routed_prefill_output_tile': ([], _INT),
+    # router + whole layer (include/ornith_moe.h)
+    'ornith_router_topk_launch': ([_VP, _I64] + [_VP] * 7 + [_INT, _VP], _INT),
+    'ornith_moe_layer_get_layout': ([_INT, C.POINTER(RoutedLayout)], _INT),
+    'ornith_moe_layer_launch': ([_VP] * 15 + [_SZ] + [_VP] * 5 + [_INT] * 2 + [_VP], _INT),
+    'ornith_mi355x_abi_version': ([], _INT),
+    # dense (include/ornith_dense.h)
     'ornith_dense_g256_abi_version': ([], C.c_uint32),
-    'ornith_dense_g256_get_layout': ([I] * 4 + [C.POINTER(DenseLayout)], I),
-    'ornith_dense_g256_launch': ([P] * 4 + [S] + [P] * 2 + [I] * 7 + [P], I),
-    'ornith_dense_g256_prepare_bf16': ([P] * 6 + [I] * 3 + [P], I),
-    'ornith_dense_g256_launch_n32': ([P] * 4 + [S] + [P] * 2 + [I] * 7 + [P], I),
-    'ornith_dense_g256_n32_rows': ([], I),
-    'ornith_dense_g256_head_workspace_bytes': ([I, I], S),
-    'ornith_dense_g256_head_launch': ([P] * 4 + [S] + [P] * 4 + [I] * 3 + [P], I),
+    'ornith_dense_g256_get_layout': ([_INT] * 4 + [C.POINTER(DenseLayout)], _INT),
+    'ornith_dense_g256_launch': (_DENSE_LAUNCH, _INT),
+    'ornith_dense_g256_prepare_bf16': ([_VP] * 6 + [_INT] * 3 + [_VP], _INT),
+    'ornith_dense_g256_launch_n32': (_DENSE_LAUNCH, _INT),
+    'ornith_dense_g256_n32_rows': ([], _INT),
+    'ornith_dense_g256_head_workspace_bytes': ([_INT, _INT], _SZ),
+    'ornith_dense_g256_head_launch': ([_VP] * 4 + [_SZ] + [_VP] * 4 + [_INT] * 3 + [_VP], _INT),
+    # W8 head (include/ornith_head.h)
     'ornith_head_i8_tile_abi_version': ([], C.c_uint32),
-    'ornith_head_i8_tile_get_layout': ([I, I, C.POINTER(HeadLayout)], I),
-    'ornith_head_i8_tile_launch': ([P] * 4 + [S] + [P] * 2 + [S] + [P] + [I] * 4 + [P], I),
-    'ornith_mi355x_timing_arm': ([C.c_char_p, I], I),
-    'ornith_mi355x_timing_read': ([C.c_char_p, C.POINTER(I), C.POINTER(C.c_double)], I),
-    'ornith_mi355x_timing_names': ([C.c_char_p, I], I),
+    'ornith_head_i8_tile_get_layout': ([_INT, _INT, C.POINTER(HeadLayout)], _INT),
+    'ornith_head_i8_tile_launch': ([_VP] * 4 + [_SZ] + [_VP] * 2 + [_SZ] + [_VP] + [_INT] * 4 + [_VP], _INT),
+    # measurement (include/ornith_timing.h)
+    'ornith_mi355x_timing_arm': ([C.c_char_p, _INT], _INT),
+    'ornith_mi355x_timing_read': ([C.c_char_p, C.POINTER(_INT), C.POINTER(C.c_double)], _INT),
+    'ornith_mi355x_timing_names': ([C.c_char_p, _INT], _INT),
 }
+# entries that only some builds of the library export (bound when present)
+_OPTIONAL: dict = {}
+
+_handles: dict[int, C.CDLL] = {}
 
 
-def library_path() -> Path:
-    return Path(__file__).resolve().parent / 'lib' / 'libornith_g256_mi355x.so'
+def library_path(tile: int = 32) -> Path:
+    """Path of the build whose routed banks use `tile`-wide tiles (32 or 16)."""
+    return LIB_DIR / BUILDS[tile]
 
 
-def lib():
-    """The loaded HIP library; raises if it has not been built."""
-    global _LIB
-    if _LIB is None:
-        path = library_path()
+def lib(tile: int = 32) -> C.CDLL:
+    """The loaded HIP library (prototypes set); raises if it was not built."""
+    handle = _handles.get(tile)
+    if handle is None:
+        path = library_path(tile)
         if not path.exists():
             raise RuntimeError(f'ornith_g256 HIP library missing: {path} (run __graft_entry__.build())')
         handle = C.CDLL(str(path))
-        for name, (args, res) in _SIGNATURES.items():
+        for name, (args, res) in _PROTOTYPES.items():
             fn = getattr(handle, name)
             fn.argtypes, fn.restype = args, res
-        _LIB = handle
-    return _LIB
+        for name, (args, res) in _OPTIONAL.items():
+            fn = getattr(handle, name, None)
+            if fn is not None:
+                fn.argtypes, fn.restype = args, res
+        if handle.ornith_routed_storage_n32() != tile:
+            raise RuntimeError(f'{path} reports routed tile {handle.ornith_routed_storage_n32()}, expected {tile}')
+        _handles[tile] = handle
+    return handle
 
 
-def configure(settings, capacity, shapes):
-    """Size the shared workspace arena (reference native.py:28-104).  The
-    library paths in settings must name this library (one .so serves the
-    dense, routed and head roles)."""
-    routed_activation_bits = settings.get('routed_activation_bits', 8)
-    routed_prefill_activation_bits = settings.get('routed_prefill_activation_bits', 8)
-    if settings.get('routed_storage_n32', False) and settings.get('routed_decode_n32', False):
-        raise ValueError('Choose sole N32 storage or N32 decode shadows')
-    if settings.get('routed_n32_max_rows', 8) not in (8, 16):
-        raise ValueError('N32 routed decode crossover must be 8 or 16 rows')
-    if routed_activation_bits not in (4, 8) or routed_prefill_activation_bits not in (4, 8):
-        raise ValueError('G256 routed activation bits must be 4 or 8')
-    if routed_activation_bits == routed_prefill_activation_bits == 4:
-        raise ValueError('Choose either global routed A4 or prefill-only routed A4')
-    if settings.get('routed_decode_n32', False) and routed_activation_bits != 8:
-        raise ValueError('N32 routed decode requires A8 verification')
-    suffix = ('_a4' if routed_activation_bits == 4 else
-              '_a4_prefill' if routed_prefill_activation_bits == 4 else '')
-    h = lib()
-    for kind in ('dense', 'routed', 'head'):
-        path = settings.get(kind + '_library')
-        if path is not None and Path(path).resolve() != library_path():
-            raise ValueError(f'{kind}_library must be {library_path()}')
-    if settings.get('routed_storage_n32', False) and h.ornith_routed_storage_n32() != 32:
-        raise ValueError('Sole N32 storage requires the full N32 consumer')
-    _libs['routed'] = getattr(h, 'ornith_routed_direct_launch' + suffix)
-    _libs['routed_verify'] = h.ornith_routed_direct_launch
-    _libs['routed_prefill'] = h.ornith_routed_direct_launch_a4
-    _libs['routed_n32'] = h.ornith_routed_direct_launch
-    sizes = []
-    for n, k in shapes:
-        layout = DenseLayout()
-        check(h.ornith_dense_g256_get_layout(capacity, n, k, 8, C.byref(layout)), 'dense layout')
-        sizes.append(layout.workspace_bytes)
-        sizes.append((capacity * k + n * k) * 2)
-    layout = RoutedLayout()
-    check(h.ornith_routed_direct_get_layout(capacity, C.byref(layout)), 'routed layout')
-    sizes.append(layout.workspace_bytes)
-    if not sizes or min(sizes) <= 0:
-        raise RuntimeError('Native workspace query failed')
-    return max(sizes)
+def _build_of(path) -> int:
+    """Which of this package's builds a configured library path names."""
+    resolved = Path(path).expanduser().resolve()
+    for tile, name in BUILDS.items():
+        if resolved == (LIB_DIR / name).resolve():
+            return tile
+    raise ValueError(f'{path} is not one of this package\'s libraries ({", ".join(BUILDS.values())} in {LIB_DIR})')
 
 
 def ptr(t):
@@ -144,95 +148,238 @@ def stream(x):
 
 def check(status, operation):
     if status:
-        raise RuntimeError(f'{operation} failed with native status {status}')
+        raise RuntimeError(f'{operation}: native status {status}')
 
 
-def validate(x, out, capacity, k):
-    if (x.ndim != 2 or x.shape[1] != k or not 0 <= x.shape[0] <= capacity
-            or x.dtype != torch.bfloat16 or x.device.type != 'cuda'
-            or out.dtype != x.dtype or out.device != x.device
-            or not x.is_contiguous() or not out.is_contiguous()):
-        raise ValueError('Native G256 requires contiguous BF16 input/output within capacity')
+# ---------------------------------------------------------------------------
+# configure(): settings -> binding + arena size
+# ---------------------------------------------------------------------------
+@dataclass
+class Binding:
+    """Launch function per dispatch kind, with the routed bank tile it reads."""
+    routed: dict = field(default_factory=dict)      # kind -> (ctypes fn, tile)
+    routed_suffix: str = ''
+    libraries: dict = field(default_factory=dict)   # role -> tile of the build serving it
+    settings_key: tuple = ()
 
 
-def routed_layout(capacity, kind='routed'):
+_binding: Binding | None = None
+
+
+def _settings_key(settings):
+    keys = ('routed_activation_bits', 'routed_prefill_activation_bits', 'routed_storage_n32', 'routed_decode_n32',
+            'routed_n32_max_rows', 'dense_library', 'routed_library', 'head_library', 'routed_n32_library')
+    return tuple((k, str(settings.get(k))) for k in keys)
+
+
+def configure(settings, capacity, shapes):
+    """Resolve the library roles, bind the launch entries and return the
+    workspace size the caller allocates once (the max over the routed
+    layout, the dense layouts plus their bf16 prefill operands, and the W8
+    head layout)."""
+    global _binding
+    a8 = settings.get('routed_activation_bits', 8)
+    a8_prefill = settings.get('routed_prefill_activation_bits', 8)
+    sole_n32 = bool(settings.get('routed_storage_n32', False))
+    n32_decode = bool(settings.get('routed_decode_n32', False))
+    if a8 not in (4, 8) or a8_prefill not in (4, 8):
+        raise ValueError(f'routed activation bits must be 4 or 8, got {a8}/{a8_prefill}')
+    if a8 == 4 and a8_prefill == 4:
+        raise ValueError('set either routed_activation_bits=4 (all tokens) or '
+                         'routed_prefill_activation_bits=4 (prefill only), not both')
+    if sole_n32 and n32_decode:
+        raise ValueError('routed_storage_n32 (N32 banks only) excludes routed_decode_n32 (N32 decode copies)')
+    if settings.get('routed_n32_max_rows', 8) not in (8, 16):
+        raise ValueError('routed_n32_max_rows must be 8 or 16')
+    if n32_decode and a8 != 8:
+        raise ValueError('routed_decode_n32 needs A8 routed activations')
+    if n32_decode and not settings.get('routed_n32_library'):
+        raise ValueError('routed_decode_n32 needs routed_n32_library')
+    if not 0 <= int(capacity) <= 8192:
+        raise ValueError(f'capacity {capacity} outside 0..8192')
+
+    roles = {}
+    for role in ('dense', 'routed', 'head'):
+        path = settings.get(role + '_library')
+        roles[role] = _build_of(path) if path is not None else (32 if role != 'routed' or sole_n32 else 16)
+    if roles['routed'] != (32 if sole_n32 else 16):
+        want = 'N32 (routed_storage_n32=True)' if sole_n32 else 'N16 (the checkpoint layout)'
+        raise ValueError(f'routed_library must be the build that reads {want} banks: {library_path(32 if sole_n32 else 16)}')
+    if n32_decode:
+        roles['routed_n32'] = _build_of(settings['routed_n32_library'])
+        if roles['routed_n32'] != 32:
+            raise ValueError(f'routed_n32_library must be {library_path(32)}')
+
+    key = _settings_key(settings)
+    if _binding is not None and _binding.settings_key != key:
+        raise RuntimeError('the native libraries are already configured with other settings in this process')
+    suffix = '_a4' if a8 == 4 else '_a4_prefill' if a8_prefill == 4 else ''
+    routed_lib = lib(roles['routed'])
+    binding = Binding(routed_suffix=suffix, libraries=dict(roles), settings_key=key)
+    binding.routed['routed'] = (getattr(routed_lib, 'ornith_routed_direct_launch' + suffix), roles['routed'])
+    binding.routed['routed_verify'] = (routed_lib.ornith_routed_direct_launch, roles['routed'])
+    binding.routed['routed_prefill'] = (routed_lib.ornith_routed_direct_launch_a4, roles['routed'])
+    if n32_decode:
+        binding.routed['routed_n32'] = (lib(32).ornith_routed_direct_launch, 32)
+
+    sizes = [routed_layout(capacity, tile=roles['routed']).workspace_bytes]
+    if n32_decode:
+        parent, shadow = routed_layout(capacity, tile=roles['routed']), routed_layout(capacity, tile=32)
+        if bytes(parent) != bytes(shadow):
+            raise ValueError('the N32 decode library must keep its parent\'s workspace layout')
+    for n, k in shapes:
+        sizes.append(dense_layout(capacity, n, k, tile=roles['dense']).workspace_bytes)
+        sizes.append((capacity * k + n * k) * 2)       # bf16 prefill operands (transformed x, dequantised W)
+    sizes.append(head_layout(HEAD_MAX_ROWS, HEAD_VOCAB, tile=roles['head']).workspace_bytes)
+    if min(sizes) <= 0:
+        raise RuntimeError('native workspace query returned an empty layout')
+    _binding = binding
+    return max(sizes)
+
+
+def reset_binding():
+    """Forget the configured binding (tests and tools that reconfigure)."""
+    global _binding
+    _binding = None
+
+
+def routed_layout(capacity, kind='routed', tile=32):
     layout = RoutedLayout()
-    fn = {'routed': lib().ornith_routed_direct_get_layout,
-          'shared': lib().ornith_routed_shared_get_layout,
-          'layer': lib().ornith_moe_layer_get_layout}[kind]
-    check(fn(capacity, C.byref(layout)), f'{kind} layout')
+    query = {'routed': 'ornith_routed_direct_get_layout', 'shared': 'ornith_routed_shared_get_layout',
+             'layer': 'ornith_moe_layer_get_layout'}[kind]
+    check(getattr(lib(tile), query)(capacity, C.byref(layout)), f'{kind} layout for {capacity} tokens')
     return layout
 
 
-def dense_layout(capacity, n, k):
+def dense_layout(capacity, n, k, tile=32):
     layout = DenseLayout()
-    check(lib().ornith_dense_g256_get_layout(capacity, n, k, 8, C.byref(layout)), 'dense layout')
+    check(lib(tile).ornith_dense_g256_get_layout(capacity, n, k, 8, C.byref(layout)), f'dense layout N{n} K{k}')
     return layout
 
 
-# ----------------------------------------------------------------------------
-# torch custom ops (reference native.py:121-224)
-# ----------------------------------------------------------------------------
+def head_layout(capacity, n, tile=32):
+    layout = HeadLayout()
+    check(lib(tile).ornith_head_i8_tile_get_layout(capacity, n, C.byref(layout)), f'W8 head layout N{n}')
+    return layout
+
+
+# ---------------------------------------------------------------------------
+# Mixed prefill/decode batches
+# ---------------------------------------------------------------------------
+_phase_plan: contextvars.ContextVar[tuple] = contextvars.ContextVar('ornith_phase_plan', default=())
+
+
+@contextmanager
+def phase_segments(segments):
+    """Within this context, ops over a batch of at least `segments[-1][1]` rows
+    run each (start, end, is_prefill) segment with its own precision: prefill
+    segments on the A4 routed entry and the bf16 dense GEMM, decode segments
+    on the A8 entries; rows past the last segment are prefill."""
+    token = _phase_plan.set(tuple((int(a), int(b), bool(p)) for a, b, p in segments))
+    try:
+        yield
+    finally:
+        _phase_plan.reset(token)
+
+
+def _active_plan(rows):
+    plan = _phase_plan.get()
+    if not plan or rows < plan[-1][1]:
+        return ()
+    if plan[-1][1] < rows:
+        plan = plan + ((plan[-1][1], rows, True),)
+    return plan
+
+
+# ---------------------------------------------------------------------------
+# Tensor checks
+# ---------------------------------------------------------------------------
+def _check_rows(x, out, capacity, k):
+    if x.ndim != 2 or x.shape[1] != k or x.dtype != torch.bfloat16 or x.device.type != 'cuda':
+        raise ValueError(f'input must be a CUDA bf16 [rows, {k}] tensor, got {tuple(x.shape)} {x.dtype}')
+    if not 0 <= x.shape[0] <= capacity:
+        raise ValueError(f'{x.shape[0]} rows exceed the configured capacity {capacity}')
+    if not x.is_contiguous() or not out.is_contiguous() or out.dtype != x.dtype or out.device != x.device:
+        raise ValueError('input and output must be contiguous bf16 tensors on one device')
+
+
+def _check_routing(x, weights, ids):
+    T = x.shape[0]
+    if (weights.dtype != torch.float32 or ids.dtype != torch.int32 or tuple(weights.shape) != (T, TOP)
+            or tuple(ids.shape) != (T, TOP) or weights.device != x.device or ids.device != x.device
+            or not weights.is_contiguous() or not ids.is_contiguous()):
+        raise ValueError(f'routing must be contiguous fp32 weights and int32 ids of shape [{T}, {TOP}]')
+
+
+def _check_banks(tile, gate, gate_meta, down, down_meta):
+    """Routed banks [256, N/tile, K/256, 32, tile] codes and [256, N/tile, K/256, tile]
+    meta (uint32 words; int32 views accepted)."""
+    for name, t, n, k, meta in (('gate', gate, 1024, 2048, False), ('gate_meta', gate_meta, 1024, 2048, True),
+                                ('down', down, 2048, 512, False), ('down_meta', down_meta, 2048, 512, True)):
+        want = (EXPERTS, n // tile, k // 256) + (() if meta else (32,)) + (tile,)
+        if t.element_size() != 4 or not t.is_contiguous():
+            raise ValueError(f'{name} must be a contiguous 32-bit tensor')
+        if t.ndim > 1 and tuple(t.shape) != want:
+            raise ValueError(f'{name} has shape {tuple(t.shape)}; this library reads N{tile} banks {want}')
+        if t.numel() != int(torch.Size(want).numel()):
+            raise ValueError(f'{name} holds {t.numel()} words, N{tile} banks need {torch.Size(want).numel()}')
+
+
+# ---------------------------------------------------------------------------
+# torch ops (reference native.py:121-212)
+# ---------------------------------------------------------------------------
+def _dense_one(x, codes, metadata, workspace, out, flags, capacity, n, k, geometry, a8_max_rows):
+    h = lib(_binding.libraries['dense'] if _binding else 32)
+    _check_rows(x, out, capacity, k)
+    rows = x.shape[0]
+    if rows > a8_max_rows:
+        # bf16 prefill semantics: bf16(H128 x) @ bf16(dequantised W).T, both
+        # operands carved from the arena (dense_g256_consumer.cpp:192-246)
+        xt = workspace[:rows * k * 2].view(torch.bfloat16).view(rows, k)
+        wt = workspace[capacity * k * 2:(capacity * k + n * k) * 2].view(torch.bfloat16).view(n, k)
+        check(h.ornith_dense_g256_prepare_bf16(ptr(x), ptr(codes), ptr(metadata), ptr(xt), ptr(wt), ptr(flags),
+                                               rows, n, k, stream(x)), 'dense bf16 operands')
+        torch.mm(xt, wt.t(), out=out)
+        return
+    check(h.ornith_dense_g256_launch(ptr(x), ptr(codes), ptr(metadata), ptr(workspace), workspace.numel(), ptr(out),
+                                     ptr(flags), rows, capacity, n, k, 8, 128, geometry, stream(x)), 'dense A8')
+
+
 @torch.library.custom_op('ornith_g256::dense_out', mutates_args={'workspace', 'out', 'flags'}, device_types='cuda')
 def dense_out(x: torch.Tensor, codes: torch.Tensor, metadata: torch.Tensor,
               workspace: torch.Tensor, out: torch.Tensor, flags: torch.Tensor,
               capacity: int, n: int, k: int, geometry: int, a8_max_rows: int) -> None:
-    if _PHASE_SEGMENTS and x.shape[0] >= _PHASE_SEGMENTS[-1][1]:
-        for start, end, prefill in _PHASE_SEGMENTS:
-            _dense_impl(x[start:end], codes, metadata, workspace, out[start:end], flags,
-                        capacity, n, k, geometry, 0 if prefill else capacity)
-        end = _PHASE_SEGMENTS[-1][1]
-        if end < x.shape[0]:
-            _dense_impl(x[end:], codes, metadata, workspace, out[end:], flags, capacity, n, k, geometry, 0)
+    plan = _active_plan(x.shape[0])
+    if not plan:
+        _dense_one(x, codes, metadata, workspace, out, flags, capacity, n, k, geometry, a8_max_rows)
         return
-    _dense_impl(x, codes, metadata, workspace, out, flags, capacity, n, k, geometry, a8_max_rows)
+    for start, end, prefill in plan:
+        _dense_one(x[start:end], codes, metadata, workspace, out[start:end], flags, capacity, n, k, geometry,
+                   0 if prefill else capacity)
 
 
-def _dense_impl(x, codes, metadata, workspace, out, flags, capacity, n, k, geometry, a8_max_rows):
-    validate(x, out, capacity, k)
-    h = lib()
-    if x.shape[0] > a8_max_rows:
-        # bf16 prefill semantics (dense_g256_consumer.cpp:192-246 + native.py:140-150):
-        # bf16(H128 x) @ bf16(dequant W).T in the arena.
-        weight_offset = capacity * k * 2
-        transformed = workspace[:x.shape[0] * k * 2].view(torch.bfloat16).view(x.shape[0], k)
-        weight = workspace[weight_offset:weight_offset + n * k * 2].view(torch.bfloat16).view(n, k)
-        check(h.ornith_dense_g256_prepare_bf16(ptr(x), ptr(codes), ptr(metadata), ptr(transformed), ptr(weight),
-                                               ptr(flags), x.shape[0], n, k, stream(x)),
-              'G256 BF16 prefill preparation')
-        torch.mm(transformed, weight.t(), out=out)
-        return
-    check(h.ornith_dense_g256_launch(ptr(x), ptr(codes), ptr(metadata), ptr(workspace), workspace.numel(),
-                                     ptr(out), ptr(flags), x.shape[0], capacity, n, k, 8, 128, geometry,
-                                     stream(x)), 'G256 dense')
+def _routed_one(kind, x, weights, ids, gate, gate_meta, down, down_meta, workspace, out, flags, capacity):
+    _check_rows(x, out, capacity, HIDDEN)
+    _check_routing(x, weights, ids)
+    if _binding is None:
+        raise RuntimeError('call native.configure(settings, capacity, shapes) before the routed ops')
+    fn, tile = _binding.routed[kind]
+    _check_banks(tile, gate, gate_meta, down, down_meta)
+    args = [ptr(t) for t in (x, weights, ids, gate, gate_meta, down, down_meta, workspace)]
+    check(fn(*args, workspace.numel(), ptr(out), ptr(flags), x.shape[0], capacity, stream(x)), f'routed ({kind})')
 
 
 @torch.library.custom_op('ornith_g256::routed_out', mutates_args={'workspace', 'out', 'flags'}, device_types='cuda')
 def routed_out(x: torch.Tensor, routes: torch.Tensor, ids: torch.Tensor,
                gate: torch.Tensor, gate_meta: torch.Tensor, down: torch.Tensor, down_meta: torch.Tensor,
                workspace: torch.Tensor, out: torch.Tensor, flags: torch.Tensor, capacity: int) -> None:
-    if _PHASE_SEGMENTS and x.shape[0] >= _PHASE_SEGMENTS[-1][1]:
-        segments = list(_PHASE_SEGMENTS)
-        if segments[-1][1] < x.shape[0]:
-            segments.append((segments[-1][1], x.shape[0], True))
-        for start, end, prefill in segments:
-            _routed_out('routed_prefill' if prefill else 'routed_verify',
-                        x[start:end], routes[start:end], ids[start:end],
-                        gate, gate_meta, down, down_meta, workspace, out[start:end], flags, capacity)
+    plan = _active_plan(x.shape[0])
+    if not plan:
+        _routed_one('routed', x, routes, ids, gate, gate_meta, down, down_meta, workspace, out, flags, capacity)
         return
-    _routed_out('routed', x, routes, ids, gate, gate_meta, down, down_meta, workspace, out, flags, capacity)
-
-
-def _routed_out(kind, x, routes, ids, gate, gate_meta, down, down_meta, workspace, out, flags, capacity):
-    validate(x, out, capacity, 2048)
-    if (routes.dtype != torch.float32 or ids.dtype != torch.int32
-            or routes.shape != (x.shape[0], 8) or ids.shape != routes.shape
-            or routes.device != x.device or ids.device != x.device
-            or not routes.is_contiguous() or not ids.is_contiguous()):
-        raise ValueError('G256 routed input requires FP32 weights and INT32 IDs [T,8]')
-    fn = _libs.get(kind) or lib().ornith_routed_direct_launch
-    check(fn(*[ptr(t) for t in (x, routes, ids, gate, gate_meta, down, down_meta, workspace)],
-             workspace.numel(), ptr(out), ptr(flags), x.shape[0], capacity, stream(x)), 'G256 ' + kind)
+    for start, end, prefill in plan:
+        _routed_one('routed_prefill' if prefill else 'routed_verify', x[start:end], routes[start:end],
+                    ids[start:end], gate, gate_meta, down, down_meta, workspace, out[start:end], flags, capacity)
 
 
 @torch.library.custom_op('ornith_g256::routed_out_n32', mutates_args={'workspace', 'out', 'flags'},
@@ -244,23 +391,23 @@ def routed_out_n32(x: torch.Tensor, routes: torch.Tensor, ids: torch.Tensor,
                    down_n32: torch.Tensor, down_meta_n32: torch.Tensor,
                    workspace: torch.Tensor, out: torch.Tensor,
                    flags: torch.Tensor, capacity: int, n32_max_rows: int = 8) -> None:
-    # This library stores routed banks in N32 only; both banks arguments must
-    # be N32 (the reference kept an N16 parent for large T, native.py:187-202).
+    # small batches read the N32 copies through the N32 build, larger ones the
+    # checkpoint's N16 banks through the N16 build (reference native.py:187-202)
     if x.shape[0] <= n32_max_rows:
-        bank = (gate_n32, gate_meta_n32, down_n32, down_meta_n32)
+        _routed_one('routed_n32', x, routes, ids, gate_n32, gate_meta_n32, down_n32, down_meta_n32, workspace, out,
+                    flags, capacity)
     else:
-        bank = (gate, gate_meta, down, down_meta)
-    _routed_out('routed_n32' if x.shape[0] <= n32_max_rows else 'routed', x, routes, ids, *bank,
-                workspace, out, flags, capacity)
+        _routed_one('routed', x, routes, ids, gate, gate_meta, down, down_meta, workspace, out, flags, capacity)
 
 
 @torch.library.custom_op('ornith_g256::head_out', mutates_args={'workspace', 'out', 'flags'}, device_types='cuda')
 def head_out(x: torch.Tensor, codes: torch.Tensor, scales: torch.Tensor,
              workspace: torch.Tensor, out: torch.Tensor, flags: torch.Tensor, geometry: int) -> None:
-    validate(x, out, 64, 2048)
-    check(lib().ornith_head_i8_tile_launch(ptr(x), ptr(codes), ptr(scales), ptr(workspace), workspace.numel(),
-                                           ptr(out), None, 0, ptr(flags), x.shape[0], 64, 248320, geometry,
-                                           stream(x)), 'W8 head')
+    _check_rows(x, out, HEAD_MAX_ROWS, HIDDEN)
+    h = lib(_binding.libraries['head'] if _binding else 32)
+    check(h.ornith_head_i8_tile_launch(ptr(x), ptr(codes), ptr(scales), ptr(workspace), workspace.numel(), ptr(out),
+                                       None, 0, ptr(flags), x.shape[0], HEAD_MAX_ROWS, HEAD_VOCAB, geometry,
+                                       stream(x)), 'W8 head')
 
 
 @torch.library.custom_op('ornith_g256::router_topk', mutates_args={'logits', 'weights', 'ids', 'shared_logit'},
@@ -268,66 +415,76 @@ def head_out(x: torch.Tensor, codes: torch.Tensor, scales: torch.Tensor,
 def router_topk(x: torch.Tensor, router_weight: torch.Tensor, bias: torch.Tensor | None,
                 shared_gate_weight: torch.Tensor | None, logits: torch.Tensor, weights: torch.Tensor,
                 ids: torch.Tensor, shared_logit: torch.Tensor) -> None:
+    """Router logits, softmax/top-8/renormalise and (optionally) the shared
+    expert's bf16 gate logit, in the library's declared reduction order."""
     T = x.shape[0]
-    if (x.ndim != 2 or x.shape[1] != 2048 or x.stride(1) != 1 or x.dtype != torch.bfloat16
-            or router_weight.shape != (256, 2048) or not router_weight.is_contiguous()
-            or logits.shape != (T, 257) or logits.dtype != torch.float32 or not logits.is_contiguous()
-            or weights.shape != (T, 8) or ids.shape != (T, 8) or ids.dtype != torch.int32):
-        raise ValueError('router_topk requires x bf16 [T,2048], W [256,2048], logits f32 [T,257], outputs [T,8]')
+    if x.ndim != 2 or x.shape[1] != HIDDEN or x.stride(1) != 1 or x.dtype != torch.bfloat16:
+        raise ValueError('router input must be bf16 [T, 2048] with unit column stride')
+    if tuple(router_weight.shape) != (EXPERTS, HIDDEN) or not router_weight.is_contiguous():
+        raise ValueError('router weight must be a contiguous bf16 [256, 2048] tensor')
+    if (tuple(logits.shape) != (T, EXPERTS + 1) or logits.dtype != torch.float32 or not logits.is_contiguous()
+            or tuple(weights.shape) != (T, TOP) or tuple(ids.shape) != (T, TOP) or ids.dtype != torch.int32):
+        raise ValueError(f'router outputs must be logits fp32 [{T}, 257], weights/ids [{T}, 8]')
     check(lib().ornith_router_topk_launch(ptr(x), x.stride(0), ptr(router_weight), ptr(bias),
                                           ptr(shared_gate_weight), ptr(logits), ptr(weights), ptr(ids),
-                                          ptr(shared_logit), T, stream(x)), 'router top-k')
+                                          ptr(shared_logit), T, stream(x)), 'router top-8')
 
 
 @dense_out.register_fake
-def _dense_fake(x, codes, metadata, workspace, out, flags, capacity, n, k, geometry, a8_max_rows):
+def _(x, codes, metadata, workspace, out, flags, capacity, n, k, geometry, a8_max_rows):
     return None
 
 
 @routed_out.register_fake
-def _routed_fake(x, routes, ids, gate, gate_meta, down, down_meta, workspace, out, flags, capacity):
+def _(x, routes, ids, gate, gate_meta, down, down_meta, workspace, out, flags, capacity):
     return None
 
 
 @routed_out_n32.register_fake
-def _routed_n32_fake(x, routes, ids, gate, gate_meta, down, down_meta, gate_n32, gate_meta_n32, down_n32,
-                     down_meta_n32, workspace, out, flags, capacity, n32_max_rows=8):
+def _(x, routes, ids, gate, gate_meta, down, down_meta, gate_n32, gate_meta_n32, down_n32, down_meta_n32,
+      workspace, out, flags, capacity, n32_max_rows=8):
     return None
 
 
 @head_out.register_fake
-def _head_fake(x, codes, scales, workspace, out, flags, geometry):
+def _(x, codes, scales, workspace, out, flags, geometry):
     return None
 
 
 @router_topk.register_fake
-def _router_fake(x, router_weight, bias, shared_gate_weight, logits, weights, ids, shared_logit):
+def _(x, router_weight, bias, shared_gate_weight, logits, weights, ids, shared_logit):
     return None
 
 
-# ----------------------------------------------------------------------------
-# Direct (non-op) helpers used by the layer driver, tests and bench.
-# ----------------------------------------------------------------------------
+# ---------------------------------------------------------------------------
+# Direct entry helpers (whole layer, shared-expert slot, G256 head)
+# ---------------------------------------------------------------------------
 def routed_shared_tables(x, routes, ids, gate, gate_meta, down, down_meta, s_gate, s_gate_meta, s_down,
-                         s_down_meta, shared_logit, silu, sigmoid, workspace, out, shared_out, flags, capacity):
-    check(lib().ornith_routed_direct_launch_shared_tables(
-        *[ptr(t) for t in (x, routes, ids, gate, gate_meta, down, down_meta, s_gate, s_gate_meta, s_down,
-                           s_down_meta, shared_logit, silu, sigmoid, workspace)],
-        workspace.numel(), ptr(out), ptr(shared_out), ptr(flags), x.shape[0], capacity, stream(x)),
-        'G256 routed shared')
+                         s_down_meta, shared_logit, silu, sigmoid, workspace, out, shared_out, flags, capacity,
+                         tile=32):
+    """Routed experts plus the shared expert as a ninth slot
+    (routed_storage_n32_consumer.cpp:385-401); shared banks are N32 dense."""
+    args = [ptr(t) for t in (x, routes, ids, gate, gate_meta, down, down_meta, s_gate, s_gate_meta, s_down,
+                             s_down_meta, shared_logit, silu, sigmoid, workspace)]
+    check(lib(tile).ornith_routed_direct_launch_shared_tables(
+        *args, workspace.numel(), ptr(out), ptr(shared_out), ptr(flags), x.shape[0], capacity, stream(x)),
+        'routed + shared slot')
 
 
 def moe_layer(x, router_weight, bias, shared_gate_weight, gate, gate_meta, down, down_meta, s_gate, s_gate_meta,
               s_down, s_down_meta, silu, sigmoid, workspace, topk_weights, topk_ids, shared_logit, out, flags,
-              capacity):
-    check(lib().ornith_moe_layer_launch(
-        *[ptr(t) for t in (x, router_weight, bias, shared_gate_weight, gate, gate_meta, down, down_meta, s_gate,
-                           s_gate_meta, s_down, s_down_meta, silu, sigmoid, workspace)],
-        workspace.numel(), *[ptr(t) for t in (topk_weights, topk_ids, shared_logit, out, flags)],
-        x.shape[0], capacity, stream(x)), 'G256 MoE layer')
+              capacity, tile=32):
+    """The whole MoE layer: router, top-8, routed experts, shared expert and
+    the routed + shared sum, in one launch sequence."""
+    args = [ptr(t) for t in (x, router_weight, bias, shared_gate_weight, gate, gate_meta, down, down_meta, s_gate,
+                             s_gate_meta, s_down, s_down_meta, silu, sigmoid, workspace)]
+    check(lib(tile).ornith_moe_layer_launch(*args, workspace.numel(),
+                                            *[ptr(t) for t in (topk_weights, topk_ids, shared_logit, out, flags)],
+                                            x.shape[0], capacity, stream(x)), 'MoE layer')
 
 
 def dense_head(x, codes, meta, workspace, logits, logits_bf16, argmax, flags, capacity):
+    """G256 4-bit LM head: fp32 (and optional bf16) logits and the argmax."""
     check(lib().ornith_dense_g256_head_launch(ptr(x), ptr(codes), ptr(meta), ptr(workspace), workspace.numel(),
                                               ptr(logits), ptr(logits_bf16), ptr(argmax), ptr(flags), x.shape[0],
                                               capacity, codes.shape[0] * 32, stream(x)), 'G256 head')
@@ -338,25 +495,25 @@ class KernelTimer:
     recorded on each launch's own stream (include/ornith_timing.h).  The
     launches themselves are unchanged."""
 
-    def __init__(self, kernel: str = '*', capacity: int = 100_000):
-        self.kernel, self.capacity = kernel, capacity
+    def __init__(self, kernel: str = '*', capacity: int = 100_000, tile: int = 32):
+        self.kernel, self.capacity, self.h = kernel, capacity, lib(tile)
 
     def __enter__(self):
-        check(lib().ornith_mi355x_timing_arm(self.kernel.encode(), self.capacity), "timing_arm")
+        check(self.h.ornith_mi355x_timing_arm(self.kernel.encode(), self.capacity), 'timing arm')
         return self
 
     def __exit__(self, *exc):
-        lib().ornith_mi355x_timing_arm(None, 0)
+        self.h.ornith_mi355x_timing_arm(None, 0)
         return False
 
     def names(self):
-        n = lib().ornith_mi355x_timing_names(None, 0)
+        n = self.h.ornith_mi355x_timing_names(None, 0)
         buf = C.create_string_buffer(n + 1)
-        lib().ornith_mi355x_timing_names(buf, n + 1)
+        self.h.ornith_mi355x_timing_names(buf, n + 1)
         return [v for v in buf.value.decode().split(',') if v]
 
     def read(self, kernel: str):
         """(launches, average milliseconds per launch) for `kernel`."""
-        count, total = C.c_int(0), C.c_double(0.0)
-        check(lib().ornith_mi355x_timing_read(kernel.encode(), C.byref(count), C.byref(total)), "timing_read")
+        count, total = _INT(0), C.c_double(0.0)
+        check(self.h.ornith_mi355x_timing_read(kernel.encode(), C.byref(count), C.byref(total)), 'timing read')
         return count.value, (total.value / count.value if count.value else 0.0)

@@ -25,27 +25,42 @@ def lib():
     return native.lib()
 
 
-def test_every_declared_symbol_is_exported(lib):
+@pytest.mark.parametrize('tile', [32, 16])
+def test_every_declared_symbol_is_exported(tile):
+    from ornith_g256 import native
+    handle = native.lib(tile)
     names = _declared_symbols()
     assert len(names) >= 23
     for n in sorted(names):
-        assert hasattr(lib, n), n
+        assert hasattr(handle, n), n
     # and nothing undeclared is exported
     import subprocess
-    from ornith_g256 import native
-    nm = subprocess.run(['nm', '-D', '--defined-only', str(native.library_path())], capture_output=True, text=True)
+    nm = subprocess.run(['nm', '-D', '--defined-only', str(native.library_path(tile))], capture_output=True, text=True)
     if nm.returncode == 0:
         exported = {l.split()[-1] for l in nm.stdout.splitlines() if ' T ' in l and 'ornith_' in l}
         assert exported == names
 
 
 def test_markers(lib):
+    from ornith_g256 import native
     assert lib.ornith_routed_storage_n32() == 32
+    assert native.lib(16).ornith_routed_storage_n32() == 16     # the N16-bank build
     assert lib.ornith_routed_prefill_output_tile() == 32
     assert lib.ornith_dense_g256_abi_version() == 1
     assert lib.ornith_dense_g256_n32_rows() == 16
     assert lib.ornith_head_i8_tile_abi_version() == 1
     assert lib.ornith_mi355x_abi_version() == 1
+
+
+def test_both_builds_share_every_layout():
+    """The N16 and N32 builds differ only in routed bank addressing: every
+    workspace layout is byte-identical (the reference's pairing rule for an
+    N32 decode library and its N16 parent, native.py:95-99)."""
+    from ornith_g256 import native
+    for tcap in (1, 16, 64, 1120, 8192):
+        for kind in ('routed', 'layer'):
+            assert bytes(native.routed_layout(tcap, kind, tile=16)) == bytes(native.routed_layout(tcap, kind, tile=32))
+    assert bytes(native.routed_layout(16, 'shared', tile=16)) == bytes(native.routed_layout(16, 'shared', tile=32))
 
 
 def test_routed_layout_contract(lib):
@@ -84,6 +99,8 @@ def test_routed_launch_validation(lib):
         args = _routed_args(1, 8, need)
         args[0] = C.c_void_p(0x1001)                              # misaligned input
         assert fn(*args) == INVALID
+        args[0] = C.c_void_p(0x1008)                              # 8- but not 16-byte aligned input
+        assert fn(*args) == INVALID
 
 
 def test_dense_validation(lib):
@@ -108,6 +125,10 @@ def test_dense_validation(lib):
     bad = list(base)
     bad[5] = p(0x100000 + 64)          # output overlaps the workspace
     assert lib.ornith_dense_g256_launch(*bad, 1, 16, 1024, 2048, 8, 128, 2, None) == INVALID
+    bad = list(base)
+    bad[0] = p(0x10008)                # input 8- but not 16-byte aligned (loaded as 16-byte words)
+    assert lib.ornith_dense_g256_launch(*bad, 1, 16, 1024, 2048, 8, 128, 2, None) == INVALID
+    assert lib.ornith_dense_g256_launch_n32(*bad, 1, 16, 1024, 2048, 8, 128, 2, None) == INVALID
     bad = list(base)
     bad[4] = ws - 1
     assert lib.ornith_dense_g256_launch(*bad, 1, 16, 1024, 2048, 8, 128, 2, None) == INVALID
@@ -158,20 +179,74 @@ def test_router_and_layer_validation(lib):
     assert lib.ornith_moe_layer_launch(*args, 1, 4, None) == INVALID
 
 
-def test_configure_sizes_arena():
+@pytest.fixture()
+def fresh_binding():
     from ornith_g256 import native
+    native.reset_binding()
+    yield native
+    native.reset_binding()
+
+
+def test_configure_sizes_arena(fresh_binding):
+    native = fresh_binding
     size = native.configure({'routed_storage_n32': True}, 64, [(12288, 2048), (1024, 2048)])
     assert size >= native.routed_layout(64).workspace_bytes
     assert size >= (64 * 2048 + 12288 * 2048) * 2
+    assert size >= native.head_layout(64, 248320).workspace_bytes
+    # the same settings again are accepted; other settings in a live process are not
+    assert native.configure({'routed_storage_n32': True}, 64, [(12288, 2048), (1024, 2048)]) == size
+    with pytest.raises(RuntimeError):
+        native.configure({'routed_storage_n32': True, 'routed_prefill_activation_bits': 4}, 64, [])
+
+
+@pytest.mark.parametrize('settings', [
+    {'routed_activation_bits': 4, 'routed_prefill_activation_bits': 4},
+    {'routed_activation_bits': 5},
+    {'routed_storage_n32': True, 'routed_decode_n32': True},
+    {'routed_n32_max_rows': 12},
+    {'routed_decode_n32': True},                                        # no routed_n32_library
+    {'routed_decode_n32': True, 'routed_activation_bits': 4, 'routed_n32_library': 'x'},
+])
+def test_configure_rejects_bad_settings(fresh_binding, settings):
     with pytest.raises(ValueError):
-        native.configure({'routed_activation_bits': 4, 'routed_prefill_activation_bits': 4}, 64, [])
+        fresh_binding.configure(settings, 64, [])
+
+
+def test_configure_matches_bank_layout_to_library(fresh_binding):
+    """Sole N32 storage needs the N32 build as routed library, the default
+    (checkpoint N16 banks) the N16 build; a mismatch is refused before any
+    launch could misread a bank."""
+    native = fresh_binding
+    with pytest.raises(ValueError, match='N32'):
+        native.configure({'routed_storage_n32': True, 'routed_library': str(native.library_path(16))}, 8, [])
+    with pytest.raises(ValueError, match='N16'):
+        native.configure({'routed_library': str(native.library_path(32))}, 8, [])
     with pytest.raises(ValueError):
-        native.configure({'routed_activation_bits': 5}, 64, [])
+        native.configure({'routed_library': '/nonexistent/libornith_routed_direct.so'}, 8, [])
+    native.configure({'routed_library': str(native.library_path(16))}, 8, [])
+    fn, tile = native._binding.routed['routed']
+    assert tile == 16
+    native.reset_binding()
+    native.configure({'routed_decode_n32': True, 'routed_n32_library': str(native.library_path(32))}, 8, [])
+    assert native._binding.routed['routed_n32'][1] == 32 and native._binding.routed['routed'][1] == 16
+
+
+def test_routed_op_refuses_banks_of_the_other_tile(fresh_binding):
+    import torch
+    native = fresh_binding
+    native.configure({'routed_storage_n32': True}, 8, [])
+    n16 = torch.empty((256, 64, 8, 32, 16), dtype=torch.int32)
+    meta = torch.empty((256, 64, 8, 16), dtype=torch.int32)
+    with pytest.raises(ValueError, match='N32'):
+        native._check_banks(32, n16, meta, n16, meta)
+    ok = (torch.empty((256, 32, 8, 32, 32), dtype=torch.int32), torch.empty((256, 32, 8, 32), dtype=torch.int32),
+          torch.empty((256, 64, 2, 32, 32), dtype=torch.int32), torch.empty((256, 64, 2, 32), dtype=torch.int32))
+    native._check_banks(32, *ok)
 
 
 def test_missing_library_fails_loudly(monkeypatch, tmp_path):
     from ornith_g256 import native
-    monkeypatch.setattr(native, '_LIB', None)
-    monkeypatch.setattr(native, 'library_path', lambda: tmp_path / 'missing.so')
+    monkeypatch.setattr(native, '_handles', {})
+    monkeypatch.setattr(native, 'LIB_DIR', tmp_path)
     with pytest.raises(RuntimeError, match='missing'):
         native.lib()

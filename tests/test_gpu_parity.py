@@ -3,8 +3,8 @@
 All calls go through the C ABI (ctypes) of the built HIP library on torch's
 current stream; the oracle only checks.  Shapes are the reference's real
 shapes (E=256, H=2048, I=512, G=256) at token counts the oracle finishes in
-seconds; larger token counts are covered by size-independent properties in
-test_gpu_properties.py.
+seconds; larger token counts are covered by size-independent properties
+(batch invariance below, and the skewed workloads in test_gpu_workloads.py).
 """
 import ctypes as C
 
@@ -45,7 +45,9 @@ def moe(device):
 # ---------------------------------------------------------------------------
 @pytest.mark.parametrize('M,N,K,tile', [(1, 6144, 2048, 16), (1, 6144, 2048, 32), (5, 1024, 2048, 16),
                                         (16, 2048, 512, 32), (3, 48, 768, 16), (64, 1024, 4096, 16),
-                                        (9, 2080, 2048, 32), (2, 128, 8192, 16), (65, 96, 512, 16)])
+                                        (9, 2080, 2048, 32), (2, 128, 8192, 16), (65, 96, 512, 16),
+                                        (8, 6144, 2048, 32), (8, 2080, 2048, 16), (7, 48, 768, 16),
+                                        (6, 1024, 2048, 32)])
 def test_dense_a8_bit_exact(device, M, N, K, tile):
     import torch
     native = _native()

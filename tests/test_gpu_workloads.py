@@ -1,0 +1,263 @@
+"""GPU checks of the benchmark workloads as specified and of the host-side
+dispatch, all through the C ABI or the ornith_g256 torch ops:
+
+* the 1120-token layer under the Zipf(1.1) router bias and the 8192-token
+  layer under Zipf(1.3) (batch invariance against smaller runs that are
+  themselves oracle-checked), and a 300-token layer under Zipf(1.3) checked
+  against the oracle (one expert holds nearly every token: many m-tiles);
+* the dense linear at the benchmark's 1120 x 6144 x 2048 prefill shape
+  through ``dense_out`` (bf16 operands + GEMM) against an fp64 dequant-matmul
+  (tolerance: the GEMM's summation order is hipBLASLt's, as in the reference);
+* the N16-bank build of the library (the reference's parent routed library
+  role) against the oracle;
+* ``routed_out`` with a mixed prefill/decode phase plan.
+"""
+import numpy as np
+import pytest
+
+from _ornith import LazyExperts, bf16_normal, from_dev, moe_weights, oracle_routed, random_routing, to_dev
+from oracle import ornith_oracle as O
+
+pytestmark = pytest.mark.gpu
+
+
+def _native():
+    from ornith_g256 import native
+    return native
+
+
+def _sync():
+    import torch
+    torch.cuda.synchronize()
+
+
+def _flags(device):
+    import torch
+    return torch.zeros(1, dtype=torch.int32, device=device)
+
+
+@pytest.fixture(scope='module')
+def moe(device):
+    w = moe_weights(1234)
+    d = {k: (to_dev(w[k].codes, device), to_dev(w[k].meta, device)) for k in ('w13', 'w2', 's13', 's2')}
+    return w, d
+
+
+def _zipf_bias(s, seed):
+    """b_e = -s * ln(rank_e), seeded rank permutation (the benchmark's router bias)."""
+    rank = np.random.default_rng(seed).permutation(256).astype(np.float64) + 1.0
+    return (-s * np.log(rank)).astype(np.float32)
+
+
+def _layer_fn(native, device, w, d, silu, sigmoid, bias, tile=32, banks=None):
+    import torch
+    banks = banks or d
+    weights = [to_dev(w['router'], device), None if bias is None else to_dev(bias, device),
+               to_dev(w['gate'][0], device), banks['w13'][0], banks['w13'][1], banks['w2'][0], banks['w2'][1],
+               d['s13'][0], d['s13'][1], d['s2'][0], d['s2'][1], to_dev(silu, device), to_dev(sigmoid, device)]
+
+    def layer(xs):
+        n = xs.shape[0]
+        ws = torch.empty(native.routed_layout(n, 'layer', tile=tile).workspace_bytes, dtype=torch.uint8,
+                         device=device)
+        out = torch.empty((n, 2048), dtype=torch.bfloat16, device=device)
+        tw = torch.empty((n, 8), dtype=torch.float32, device=device)
+        ti = torch.empty((n, 8), dtype=torch.int32, device=device)
+        sl = torch.empty((n,), dtype=torch.bfloat16, device=device)
+        flags = _flags(device)
+        native.moe_layer(xs.contiguous(), *weights, ws, tw, ti, sl, out, flags, n, tile=tile)
+        _sync()
+        return out, ti, tw, sl, int(flags.item())
+    return layer
+
+
+def _oracle_layer(w, x, bias, silu, sigmoid):
+    logits = O.router_logits(x, np.concatenate([w['router'], w['gate']]))
+    if bias is not None:
+        logits[:, :256] = (logits[:, :256] + bias[None, :]).astype(np.float32)
+    rw, ids, _ = O.softmax_topk(logits[:, :256])
+    ref = O.routed_layer_shared(x, rw, ids, LazyExperts(w['w13']), w['w13'].sbits, w['w13'].obits,
+                                LazyExperts(w['w2']), w['w2'].sbits, w['w2'].obits,
+                                *w['s13'].expert(), *w['s2'].expert(), O.f32_to_bf16(logits[:, 256]), silu, sigmoid)
+    return rw, ids, O.add_bf16(ref['out'], ref['shared_out']), ref['flags']
+
+
+# ---------------------------------------------------------------------------
+# Skewed routing
+# ---------------------------------------------------------------------------
+def test_moe_layer_zipf13_300_tokens_vs_oracle(device, moe, shared_tables):
+    """300 tokens under the Zipf(1.3) bias: the most popular expert takes
+    nearly every token (more than 128 routes, several 64-route m-tiles)."""
+    native = _native()
+    w, d = moe
+    silu, sigmoid = shared_tables
+    print('layer T=300 zipf 1.3 vs oracle', flush=True)
+    rng = np.random.default_rng(7300)
+    x = bf16_normal(rng, (300, 2048))
+    bias = _zipf_bias(1.3, 11)
+    rw, ids, expected, ref_flags = _oracle_layer(w, x, bias, silu, sigmoid)
+    counts = np.bincount(ids.reshape(-1), minlength=256)
+    assert counts.max() > 128, counts.max()
+    out, ti, tw, sl, flags = _layer_fn(native, device, w, d, silu, sigmoid, bias)(to_dev(x, device))
+    np.testing.assert_array_equal(from_dev(ti), ids)
+    np.testing.assert_array_equal(from_dev(tw).view(np.uint32), rw.view(np.uint32))
+    np.testing.assert_array_equal(from_dev(out), expected)
+    assert flags == ref_flags == 0
+
+
+@pytest.mark.parametrize('T,s', [(1120, 1.1), (8192, 1.3)])
+def test_moe_layer_zipf_full_size_batch_invariance(device, moe, shared_tables, T, s):
+    """The benchmark's skewed prefill workloads: every row of the T-token
+    layer equals the same row run in a 300-token layer (prefill path, checked
+    against the oracle above), a 32-token layer (decode path) and as a single
+    token, ids and weights included; flags stay clear."""
+    import torch
+    native = _native()
+    w, d = moe
+    silu, sigmoid = shared_tables
+    print(f'layer batch invariance T={T} zipf {s}', flush=True)
+    rng = np.random.default_rng(8000 + T)
+    x = to_dev(bf16_normal(rng, (T, 2048)), device)
+    bias = _zipf_bias(s, 11)
+    layer = _layer_fn(native, device, w, d, silu, sigmoid, bias)
+    full = layer(x)
+    assert full[4] == 0
+    counts = np.bincount(from_dev(full[1]).reshape(-1), minlength=256)
+    print(f'  top expert routes {counts.max()}, experts used {int((counts > 0).sum())}', flush=True)
+    assert counts.max() > T // 2                  # a heavily skewed expert: many m-tiles on one bank
+    for lo, hi in [(0, 300), (T - 300, T), (T // 2, T // 2 + 32), (T - 1, T), (T // 3, T // 3 + 1)]:
+        part = layer(x[lo:hi])
+        assert part[4] == 0
+        for a, b in zip(part[:4], full[:4]):
+            assert torch.equal(a.view(torch.uint8), b[lo:hi].contiguous().view(torch.uint8)), (lo, hi)
+
+
+# ---------------------------------------------------------------------------
+# Dense linear at the prefill shape through dense_out
+# ---------------------------------------------------------------------------
+def test_dense_out_prefill_1120_tolerance(device):
+    """dense_out at [1120, 2048] x [6144, 2048] (more rows than the A8
+    crossover): bf16(H128 x) @ bf16(dequantised W)^T on the GEMM.  The bf16
+    operands are bit-exact (test_gpu_parity); the GEMM's reduction order is
+    the BLAS library's, so the product is checked by tolerance against fp64:
+    cosine >= 0.9999 and max |err| <= 1e-2 * max |ref|."""
+    import torch
+    from _ornith import Bank
+    native = _native()
+    print('dense_out 1120 x 6144 x 2048', flush=True)
+    M, N, K = 1120, 6144, 2048
+    rng = np.random.default_rng(1120)
+    bank = Bank(rng, 0, N, K, tile=16)
+    x = bf16_normal(rng, (M, K))
+    ws = torch.empty((M * K + N * K) * 2, dtype=torch.uint8, device=device)
+    out = torch.empty((M, N), dtype=torch.bfloat16, device=device)
+    flags = _flags(device)
+    native.dense_out(to_dev(x, device), to_dev(bank.codes, device), to_dev(bank.meta, device), ws, out, flags,
+                     M, N, K, 2, 64)
+    _sync()
+    got = O.bf16_to_f32(from_dev(out)).astype(np.float64)
+    xt = O.bf16_to_f32(O.transform_bf16(x)).astype(np.float64)
+    wt = O.bf16_to_f32(O.dequantize_bf16(*bank.expert())).astype(np.float64)
+    ref = xt @ wt.T
+    cos = float((got.ravel() @ ref.ravel()) / (np.linalg.norm(got) * np.linalg.norm(ref)))
+    err = float(np.abs(got - ref).max() / np.abs(ref).max())
+    print(f'  cosine {cos:.7f}  max rel err {err:.2e}', flush=True)
+    assert cos >= 0.9999 and err <= 1e-2
+    assert int(flags.item()) == 0
+
+
+# ---------------------------------------------------------------------------
+# N16-bank build (the parent routed library role, routed_direct_api.h:7)
+# ---------------------------------------------------------------------------
+def _n32_to_n16(codes, meta):
+    """N32 banks -> the same weights in N16 tiles (test-side data layout)."""
+    E, nt, G = codes.shape[:3]
+    c16 = codes.reshape(E, nt, G, 32, 2, 16).permute(0, 1, 4, 2, 3, 5).contiguous().reshape(E, 2 * nt, G, 32, 16)
+    m16 = meta.reshape(E, nt, G, 2, 16).permute(0, 1, 3, 2, 4).contiguous().reshape(E, 2 * nt, G, 16)
+    return c16, m16
+
+
+@pytest.fixture(scope='module')
+def n16_banks(moe):
+    _, d = moe
+    return {k: _n32_to_n16(*d[k]) for k in ('w13', 'w2')}
+
+
+@pytest.mark.parametrize('T,entry,qmax', [(1, 'ornith_routed_direct_launch', 127),
+                                          (5, 'ornith_routed_direct_launch', 127),
+                                          (32, 'ornith_routed_direct_launch', 127),
+                                          (70, 'ornith_routed_direct_launch_a4_prefill', 7),
+                                          (100, 'ornith_routed_direct_launch', 127)])
+def test_routed_n16_build_bit_exact(device, moe, n16_banks, T, entry, qmax):
+    import torch
+    native = _native()
+    w, _ = moe
+    print(f'routed N16 build T={T} {entry}', flush=True)
+    rng = np.random.default_rng(1600 + T)
+    x = bf16_normal(rng, (T, 2048))
+    rw, ids = random_routing(rng, T)
+    ref = oracle_routed(x, rw, ids, w['w13'], w['w2'], qmax=qmax)
+    layout = native.routed_layout(T, tile=16)
+    ws = torch.empty(layout.workspace_bytes, dtype=torch.uint8, device=device)
+    out = torch.empty((T, 2048), dtype=torch.bfloat16, device=device)
+    flags = _flags(device)
+    xd, wd, idd = to_dev(x, device), to_dev(rw, device), to_dev(ids, device)
+    b = n16_banks
+    fn = getattr(native.lib(16), entry)
+    st = fn(*[native.ptr(t) for t in (xd, wd, idd, b['w13'][0], b['w13'][1], b['w2'][0], b['w2'][1], ws)],
+            ws.numel(), native.ptr(out), native.ptr(flags), T, T, native.stream(xd))
+    assert st == 0
+    _sync()
+    np.testing.assert_array_equal(from_dev(out), ref['out'])
+    assert int(flags.item()) == ref['flags']
+
+
+@pytest.mark.parametrize('T', [1, 33])
+def test_moe_layer_n16_build_bit_exact(device, moe, n16_banks, shared_tables, T):
+    native = _native()
+    w, d = moe
+    silu, sigmoid = shared_tables
+    print(f'layer N16 build T={T}', flush=True)
+    rng = np.random.default_rng(1700 + T)
+    x = bf16_normal(rng, (T, 2048))
+    rw, ids, expected, ref_flags = _oracle_layer(w, x, None, silu, sigmoid)
+    out, ti, tw, _, flags = _layer_fn(native, device, w, d, silu, sigmoid, None, tile=16,
+                                      banks=n16_banks)(to_dev(x, device))
+    np.testing.assert_array_equal(from_dev(ti), ids)
+    np.testing.assert_array_equal(from_dev(out), expected)
+    assert flags == ref_flags
+
+
+# ---------------------------------------------------------------------------
+# routed_out with a mixed prefill/decode phase plan
+# ---------------------------------------------------------------------------
+def test_routed_out_phase_segments(device, moe):
+    """A 100-token batch of a decode segment (rows 0..39, A8) followed by a
+    prefill segment (rows 40..99, A4, as the reference's phase dispatch runs
+    them, native.py:161-168) equals the oracle run per segment."""
+    import torch
+    native = _native()
+    w, d = moe
+    print('routed_out phase segments', flush=True)
+    native.reset_binding()
+    try:
+        ws_bytes = native.configure({'routed_storage_n32': True}, 128, [])
+        rng = np.random.default_rng(1800)
+        T = 100
+        x = bf16_normal(rng, (T, 2048))
+        rw, ids = random_routing(rng, T)
+        ref_a8 = oracle_routed(x[:40], rw[:40], ids[:40], w['w13'], w['w2'], qmax=127)
+        ref_a4 = oracle_routed(x[40:], rw[40:], ids[40:], w['w13'], w['w2'], qmax=7)
+        ws = torch.empty(ws_bytes, dtype=torch.uint8, device=device)
+        out = torch.empty((T, 2048), dtype=torch.bfloat16, device=device)
+        flags = _flags(device)
+        with native.phase_segments([(0, 40, False)]):
+            native.routed_out(to_dev(x, device), to_dev(rw, device), to_dev(ids, device), d['w13'][0], d['w13'][1],
+                              d['w2'][0], d['w2'][1], ws, out, flags, 128)
+        _sync()
+        got = from_dev(out)
+        np.testing.assert_array_equal(got[:40], ref_a8['out'])
+        np.testing.assert_array_equal(got[40:], ref_a4['out'])
+        assert int(flags.item()) == 0
+    finally:
+        native.reset_binding()
