@@ -52,6 +52,26 @@ ORNITH_EXPORT hipError_t ornith_moe_layer_launch(
     void* workspace, size_t bytes, void* topk_weights_f32, void* topk_ids_i32, void* shared_logit_bf16,
     void* output_bf16, void* flags_u32, int T, int Tcap, hipStream_t stream);
 
+/* No reference counterpart.  For callers that cannot allocate device memory
+ * (code under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc): ornith_moe_layer_launch without a workspace argument.  Its
+ * scratch is a static 5 MiB device array of this library (one per GPU, kept
+ * until the process ends), located with hipGetSymbolAddress on the first call
+ * per device.  0 <= T <= 32 (decode batches; larger T returns
+ * hipErrorInvalidValue); otherwise the arguments, outputs, flags and results
+ * are those of ornith_moe_layer_launch with Tcap = 32.  Nothing is allocated.
+ * Every call on one GPU shares that GPU's scratch: calls that overlap in time
+ * on one GPU (two streams, two threads) race and must be serialised by the
+ * caller; calls in one stream are ordered and safe. */
+ORNITH_EXPORT hipError_t ornith_moe_layer_launch_static(
+    const void* input_bf16, const void* router_w_bf16, const void* bias_f32, const void* shared_gate_w_bf16,
+    const void* gate_codes, const void* gate_meta, const void* down_codes, const void* down_meta,
+    const void* shared_gate_codes, const void* shared_gate_meta,
+    const void* shared_down_codes, const void* shared_down_meta,
+    const void* silu_f32, const void* sigmoid_bf16,
+    void* topk_weights_f32, void* topk_ids_i32, void* shared_logit_bf16,
+    void* output_bf16, void* flags_u32, int T, hipStream_t stream);
+
 /* Build identification (no reference counterpart): returns 1. */
 ORNITH_EXPORT int ornith_mi355x_abi_version(void);
 

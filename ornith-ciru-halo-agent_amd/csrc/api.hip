@@ -1,6 +1,7 @@
 // extern "C" entry points.  Argument validation is host-only and runs before
 // any launch; every entry enqueues on the caller's stream and allocates
 // nothing.  The references for each entry are in include/ornith_*.h.
+#include <mutex>
 #include "kernels.hpp"
 #include "timing.hpp"
 #include "decode.hpp"
@@ -383,6 +384,62 @@ extern "C" hipError_t ornith_moe_layer_launch(
                       static_cast<const uint16_t*>(shared_logit), static_cast<const float*>(silu),
                       static_cast<const uint16_t*>(sigmoid), 127, nullptr, nullptr, static_cast<uint16_t*>(output),
                       static_cast<uint32_t*>(flags), T, Tcap, stream, fused, true);
+}
+
+// ---- the whole layer without a caller workspace --------------------------------
+// Scratch of ornith_moe_layer_launch_static: the layer plan at Tcap = 32 needs
+// 4,696,320 bytes; 5 MiB per GPU, held for the life of the process.  In host
+// code `scratch` only names the symbol: its device address comes from
+// hipGetSymbolAddress, once per device, and only that address is passed on.
+namespace {
+constexpr int kStaticMaxTokens = 32;
+constexpr size_t kStaticScratchBytes = size_t(5) << 20;
+constexpr int kMaxDevices = 64;
+}  // namespace
+
+__device__ __align__(256) uint8_t scratch[kStaticScratchBytes];
+
+namespace {
+std::mutex g_scratch_lock;
+void* g_scratch_address[kMaxDevices];
+
+// The device address of `scratch` on the device that runs `stream`.
+hipError_t scratch_address(hipStream_t stream, void** out) {
+    int device = -1;
+    TRY(hipStreamGetDevice(stream, &device));
+    if (device < 0 || device >= kMaxDevices) return hipErrorInvalidDevice;
+    std::lock_guard<std::mutex> hold(g_scratch_lock);
+    if (!g_scratch_address[device]) {
+        int current = -1;
+        TRY(hipGetDevice(&current));
+        if (current != device) TRY(hipSetDevice(device));
+        void* address = nullptr;
+        const hipError_t st = hipGetSymbolAddress(&address, HIP_SYMBOL(scratch));
+        if (current != device) TRY(hipSetDevice(current));
+        if (st != hipSuccess) return st;
+        if (!address) return hipErrorInvalidSymbol;
+        g_scratch_address[device] = address;
+    }
+    *out = g_scratch_address[device];
+    return hipSuccess;
+}
+}  // namespace
+
+extern "C" hipError_t ornith_moe_layer_launch_static(
+    const void* input, const void* router_w, const void* bias, const void* shared_gate_w, const void* gate_codes,
+    const void* gate_meta, const void* down_codes, const void* down_meta, const void* shared_gate_codes,
+    const void* shared_gate_meta, const void* shared_down_codes, const void* shared_down_meta, const void* silu,
+    const void* sigmoid, void* topk_weights, void* topk_ids, void* shared_logit, void* output, void* flags, int T,
+    hipStream_t stream) {
+    if (T < 0 || T > kStaticMaxTokens) return hipErrorInvalidValue;
+    if (routed_plan(kStaticMaxTokens, true, true).l.workspace_bytes > kStaticScratchBytes) return hipErrorInvalidValue;
+    if (!T) return hipSuccess;
+    void* ws = nullptr;
+    TRY(scratch_address(stream, &ws));
+    return ornith_moe_layer_launch(input, router_w, bias, shared_gate_w, gate_codes, gate_meta, down_codes, down_meta,
+                                   shared_gate_codes, shared_gate_meta, shared_down_codes, shared_down_meta, silu,
+                                   sigmoid, ws, kStaticScratchBytes, topk_weights, topk_ids, shared_logit, output,
+                                   flags, T, kStaticMaxTokens, stream);
 }
 
 extern "C" int ornith_mi355x_abi_version(void) { return 1; }

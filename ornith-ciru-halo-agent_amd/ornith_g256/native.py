@@ -78,6 +78,7 @@ _PROTOTYPES = {
     'ornith_router_topk_launch': ([_VP, _I64] + [_VP] * 7 + [_INT, _VP], _INT),
     'ornith_moe_layer_get_layout': ([_INT, C.POINTER(RoutedLayout)], _INT),
     'ornith_moe_layer_launch': ([_VP] * 15 + [_SZ] + [_VP] * 5 + [_INT] * 2 + [_VP], _INT),
+    'ornith_moe_layer_launch_static': ([_VP] * 19 + [_INT, _VP], _INT),
     'ornith_mi355x_abi_version': ([], _INT),
     # dense (include/ornith_dense.h)
     'ornith_dense_g256_abi_version': ([], C.c_uint32),
@@ -481,6 +482,17 @@ def moe_layer(x, router_weight, bias, shared_gate_weight, gate, gate_meta, down,
     check(lib(tile).ornith_moe_layer_launch(*args, workspace.numel(),
                                             *[ptr(t) for t in (topk_weights, topk_ids, shared_logit, out, flags)],
                                             x.shape[0], capacity, stream(x)), 'MoE layer')
+
+
+def moe_layer_static(x, router_weight, bias, shared_gate_weight, gate, gate_meta, down, down_meta, s_gate,
+                     s_gate_meta, s_down, s_down_meta, silu, sigmoid, topk_weights, topk_ids, shared_logit, out, flags,
+                     tile=32):
+    """moe_layer for at most 32 tokens without a workspace: the library's own
+    static device scratch is used (one per GPU; overlapping calls on one GPU race)."""
+    args = [ptr(t) for t in (x, router_weight, bias, shared_gate_weight, gate, gate_meta, down, down_meta, s_gate,
+                             s_gate_meta, s_down, s_down_meta, silu, sigmoid, topk_weights, topk_ids, shared_logit,
+                             out, flags)]
+    check(lib(tile).ornith_moe_layer_launch_static(*args, x.shape[0], stream(x)), 'MoE layer (static scratch)')
 
 
 def dense_head(x, codes, meta, workspace, logits, logits_bf16, argmax, flags, capacity):
