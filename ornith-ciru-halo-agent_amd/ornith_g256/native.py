@@ -93,6 +93,8 @@ _PROTOTYPES = {
     'ornith_head_i8_tile_abi_version': ([], C.c_uint32),
     'ornith_head_i8_tile_get_layout': ([_INT, _INT, C.POINTER(HeadLayout)], _INT),
     'ornith_head_i8_tile_launch': ([_VP] * 4 + [_SZ] + [_VP] * 2 + [_SZ] + [_VP] + [_INT] * 4 + [_VP], _INT),
+    # storage conversion (include/ornith_storage.h)
+    'ornith_repack_n16_to_n32': ([_VP] * 4 + [_INT] * 3 + [_VP], _INT),
     # measurement (include/ornith_timing.h)
     'ornith_mi355x_timing_arm': ([C.c_char_p, _INT], _INT),
     'ornith_mi355x_timing_read': ([C.c_char_p, C.POINTER(_INT), C.POINTER(C.c_double)], _INT),

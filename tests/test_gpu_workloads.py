@@ -261,3 +261,122 @@ def test_routed_out_phase_segments(device, moe):
         assert int(flags.item()) == 0
     finally:
         native.reset_binding()
+
+
+# ---------------------------------------------------------------------------
+# Storage conversion and the quantized-layer methods (method.py, runtime.py)
+# ---------------------------------------------------------------------------
+def test_repack_kernel_matches_oracle(device):
+    """ornith_repack_n16_to_n32 against the oracle's N16 -> N32 permutation
+    (method.py:143-147) on three banks, and on a dense head-width bank."""
+    import torch
+    from ornith_g256 import storage
+    print('repack N16 -> N32', flush=True)
+    rng = np.random.default_rng(1900)
+    for banks, n, k in ((3, 96, 512), (1, 248320 // 8, 2048)):
+        c16 = rng.integers(0, 2 ** 32, size=(banks, n // 16, k // 256, 32, 16), dtype=np.uint32)
+        m16 = rng.integers(0, 2 ** 32, size=(banks, n // 16, k // 256, 16), dtype=np.uint32)
+        c32, m32 = storage.repack_n32(to_dev(c16, device), to_dev(m16, device), n, k)
+        _sync()
+        rc, rm = O.n16_to_n32(c16, m16)
+        np.testing.assert_array_equal(from_dev(c32).view(np.uint32), rc)
+        np.testing.assert_array_equal(from_dev(m32).view(np.uint32), rm)
+
+
+def _moe_module(device, d):
+    """A layer holding the checkpoint (N16, CPU uint32) form of the test
+    experts, loaded through the strict loader and moved to the GPU."""
+    import torch
+    from ornith_g256 import methods
+    layer = torch.nn.Module()
+    m = methods.G256MoEMethod('model.layers.0.mlp.experts')
+    m.create_weights(layer)
+    for proj in ('w13', 'w2'):
+        c16, m16 = _n32_to_n16(*d[proj])
+        layer.load_packed(f'{proj}_tilebank_codes', c16.cpu().view(torch.uint32))
+        layer.load_packed(f'{proj}_tilebank_metadata', m16.cpu().view(torch.uint32))
+    m.process_weights_after_loading(layer)
+    layer.to(device)
+    layer.quant_method = m
+    return layer
+
+
+@pytest.mark.parametrize('mode', ['storage_n32', 'n16', 'decode_n32'])
+def test_moe_method_through_runtime(device, moe, mode):
+    """Checkpoint banks -> loader -> Runtime (repack as configured) ->
+    G256MoEMethod.apply, for the three routed storage configurations of the
+    reference (runtime.py:35-46): sole N32 storage, N16 banks, N16 banks with
+    N32 copies for batches of at most 8 tokens."""
+    import torch
+    from ornith_g256 import methods, native
+    w, d = moe
+    print(f'MoE method runtime mode={mode}', flush=True)
+    native.reset_binding()
+    try:
+        model = torch.nn.Module()
+        model.experts = _moe_module(device, d)
+        settings = {'storage_n32': {'routed_storage_n32': True, 'routed_library': str(native.library_path(32))},
+                    'n16': {'routed_library': str(native.library_path(16))},
+                    'decode_n32': {'routed_decode_n32': True, 'routed_n32_library': str(native.library_path(32))}}[mode]
+        rt = methods.Runtime(model, settings, 64, device)
+        if mode != 'n16':
+            assert rt.repacked_bytes == 256 * (1_081_344 + 540_672)
+        rng = np.random.default_rng(1950)
+        for T in (4, 40):
+            x = bf16_normal(rng, (T, 2048))
+            rw, ids = random_routing(rng, T)
+            ref = oracle_routed(x, rw, ids, w['w13'], w['w2'])
+            out = model.experts.quant_method.apply(model.experts, to_dev(x, device), to_dev(rw, device),
+                                                   to_dev(ids, device))
+            _sync()
+            np.testing.assert_array_equal(from_dev(out), ref['out'])
+        assert rt.check_error_flags() == [0]
+    finally:
+        native.reset_binding()
+
+
+def test_dense_method_and_flag_lifecycle(device):
+    """G256LinearMethod through the runtime at one row (A8 path, bit-exact)
+    and 70 rows (bf16 operands + GEMM, tolerance); then a non-finite input
+    raises the layer's flag, which the step lifecycle turns into a fault."""
+    import torch
+    from _ornith import Bank
+    from ornith_g256 import lifecycle, methods, native
+    print('dense method + lifecycle', flush=True)
+    native.reset_binding()
+    try:
+        rng = np.random.default_rng(1990)
+        N, K = 1024, 2048
+        bank = Bank(rng, 0, N, K, tile=16)
+        model = torch.nn.Module()
+        model.proj = torch.nn.Module()
+        m = methods.G256LinearMethod('model.layers.0.self_attn.o_proj', N, K)
+        m.create_weights(model.proj)
+        model.proj.load_packed('g256_codes', torch.from_numpy(bank.codes.view(np.int32)).view(torch.uint32))
+        model.proj.load_packed('g256_metadata', torch.from_numpy(bank.meta.view(np.int32)).view(torch.uint32))
+        m.process_weights_after_loading(model.proj)
+        model.to(device)
+        model.proj.quant_method = m
+        rt = methods.Runtime(model, {'routed_storage_n32': True, 'dense_a8_max_rows': 64}, 128, device)
+        steps = rt.lifecycle()
+        tk = steps.begin('decode')
+        x1 = bf16_normal(rng, (1, K))
+        y1 = m.apply(model.proj, to_dev(x1, device))
+        x70 = bf16_normal(rng, (70, K))
+        y70 = m.apply(model.proj, to_dev(x70, device))
+        steps.snapshot(tk)
+        assert steps.complete(tk) == (0,)
+        np.testing.assert_array_equal(from_dev(y1), O.dense_a8(x1, *bank.expert())[0])
+        got = O.bf16_to_f32(from_dev(y70)).astype(np.float64)
+        ref = (O.bf16_to_f32(O.transform_bf16(x70)).astype(np.float64)
+               @ O.bf16_to_f32(O.dequantize_bf16(*bank.expert())).astype(np.float64).T)
+        cos = float((got.ravel() @ ref.ravel()) / (np.linalg.norm(got) * np.linalg.norm(ref)))
+        assert cos >= 0.9999 and np.abs(got - ref).max() <= 1e-2 * np.abs(ref).max()
+        tk = steps.begin('bad input')
+        x1[0, 5] = 0x7FC0                          # NaN
+        m.apply(model.proj, to_dev(x1, device))
+        steps.snapshot(tk)
+        with pytest.raises(lifecycle.OrnithWorkerFault, match='o_proj'):
+            steps.complete(tk)
+    finally:
+        native.reset_binding()

@@ -1,7 +1,9 @@
 """Host-side policy of the package, on the CPU: phase plans for mixed
-batches and the per-step lifecycle of the sticky native flags (with a fake
+batches, the per-step lifecycle of the sticky native flags (with a fake
 device transport, as the reference tests its lifecycle through an injected
-transport, lifecycle.py:76)."""
+transport, lifecycle.py:76), strict checkpoint admission, the repack entry's
+argument checks, the quantized-layer methods before binding and the vLLM
+registration's contracts."""
 import pytest
 
 from ornith_g256 import lifecycle as L
@@ -154,3 +156,112 @@ def test_bad_construction():
         L.StepLifecycle(['a'], 0, transport=FakeTransport(1))
     with pytest.raises(ValueError):
         L.StepLifecycle(['a', 'b'], 1, transport=FakeTransport(1))
+
+
+# ---------------------------------------------------------------------------
+# Checkpoint admission (loader.py:17-54, method.py:12-32)
+# ---------------------------------------------------------------------------
+def _meta(shape, scale=0.01, offset=-0.08):
+    import torch
+    pair = torch.tensor([scale, offset], dtype=torch.float16).view(torch.int32)
+    return pair.expand(shape).contiguous().view(torch.uint32)
+
+
+def test_bank_loader_is_strict():
+    import torch
+    from ornith_g256 import storage as S
+    shapes = S.dense_shapes(64, 512)
+    ld = S.BankLoader(shapes)
+    codes = torch.zeros(shapes['g256_codes'], dtype=torch.uint32)
+    with pytest.raises(S.AdmissionError, match='expected'):
+        ld.load('g256_codes', torch.zeros(shapes['g256_codes'], dtype=torch.int32))       # dtype
+    with pytest.raises(S.AdmissionError, match='expected'):
+        ld.load('g256_codes', torch.zeros((4, 2, 32, 32), dtype=torch.uint32))           # N32 instead of N16
+    with pytest.raises(S.AdmissionError, match='unsupported'):
+        ld.load('g256_extra', codes)
+    ld.load('g256_codes', codes)
+    with pytest.raises(S.AdmissionError, match='duplicate'):
+        ld.load('g256_codes', codes)
+    with pytest.raises(S.AdmissionError, match='incomplete'):
+        ld.seal()
+    ld.load('g256_metadata', _meta(shapes['g256_metadata']))
+    ld.seal()
+    with pytest.raises(S.AdmissionError, match='sealed'):
+        ld.load('g256_metadata', _meta(shapes['g256_metadata']))
+
+
+@pytest.mark.parametrize('scale,offset,match', [(2 ** -15, 0.0, '2\\^-14'), (float('nan'), 0.0, 'non-finite'),
+                                                (0.01, float('inf'), 'non-finite')])
+def test_metadata_admission(scale, offset, match):
+    from ornith_g256 import storage as S
+    shapes = S.dense_shapes(32, 256)
+    with pytest.raises(S.AdmissionError, match=match):
+        S.BankLoader(shapes).load('g256_metadata', _meta(shapes['g256_metadata'], scale, offset))
+
+
+def test_routed_shapes_and_prefixed_keys():
+    import torch
+    from ornith_g256 import storage as S
+    shapes = S.routed_shapes(experts=2)
+    assert shapes['w13_tilebank_codes'] == (2, 64, 8, 32, 16) and shapes['w2_tilebank_metadata'] == (2, 128, 2, 16)
+    ld = S.BankLoader(shapes)
+    with pytest.raises(S.AdmissionError, match='key'):
+        list(ld.load_prefixed([('experts.w13_tilebank_codes', torch.zeros(1))]))
+    items = [(S.ROUTED_PREFIX + k, torch.zeros(v, dtype=torch.uint32) if k.endswith('codes') else _meta(v))
+             for k, v in shapes.items()]
+    assert list(ld.load_prefixed(items)) == [k for k, _ in items]
+    ld.seal()
+    with pytest.raises(S.AdmissionError):
+        S.dense_shapes(12304, 2048)
+
+
+def test_repack_abi_validation():
+    import ctypes as C
+    from ornith_g256 import native
+    h = native.lib()
+    p = C.c_void_p
+    assert h.ornith_repack_n16_to_n32(None, None, None, None, 0, 1024, 2048, None) == 0
+    assert h.ornith_repack_n16_to_n32(p(0x1000), p(0x2000), p(0x3000), p(0x4000), 1, 1040, 2048, None) == 1  # N % 32
+    assert h.ornith_repack_n16_to_n32(p(0x1000), p(0x2000), p(0x3000), p(0x4000), 1, 1024, 2000, None) == 1  # K % 256
+    assert h.ornith_repack_n16_to_n32(None, p(0x2000), p(0x3000), p(0x4000), 1, 1024, 2048, None) == 1
+    big = 1 << 32
+    assert h.ornith_repack_n16_to_n32(p(big), p(2 * big), p(big + 64), p(4 * big), 1, 1024, 2048, None) == 1   # overlap
+
+
+# ---------------------------------------------------------------------------
+# Methods and the vLLM registration (method.py, config.py, moe_base.py)
+# ---------------------------------------------------------------------------
+def test_methods_register_n16_banks_and_refuse_unbound_use():
+    import torch
+    from ornith_g256 import methods as M
+    layer = torch.nn.Module()
+    m = M.G256MoEMethod('model.layers.0.mlp.experts')
+    m.create_weights(layer)
+    assert layer.w13_tilebank_codes.shape == (256, 64, 8, 32, 16) and layer.w13_tilebank_codes.dtype == torch.uint32
+    with pytest.raises(RuntimeError):
+        m.apply(layer, torch.zeros(1, 2048), torch.zeros(1, 8), torch.zeros(1, 8, dtype=torch.int32))
+    dense = torch.nn.Module()
+    d = M.G256LinearMethod('model.layers.0.self_attn.o_proj', 2048, 4096)
+    d.create_weights(dense)
+    assert dense.g256_codes.shape == (128, 16, 32, 16)
+    with pytest.raises(ValueError):
+        M.W8HeadMethod('lm_head', 151936, 2048)
+
+
+def test_vllm_plugin_contracts():
+    from types import SimpleNamespace as NS
+    from ornith_g256 import vllm_plugin as V
+    V.check_quant_config(dict(quant_method='ornith_g256', group_size=256, transform_block=128, activation_bits=8))
+    with pytest.raises(ValueError):
+        V.check_quant_config(dict(quant_method='ornith_g256', group_size=128, transform_block=128, activation_bits=8))
+    V.check_routing_contract(NS(scoring_func='softmax', renormalize=True))
+    with pytest.raises(ValueError):
+        V.check_routing_contract(NS(scoring_func='sigmoid', renormalize=True))
+    with pytest.raises(ValueError):
+        V.check_routing_contract(NS(e_score_correction_bias=object()))
+    assert V.ROUTED_PREFIX.search('model.language_model.layers.12.mlp.experts')
+    try:
+        import vllm  # noqa: F401
+    except ImportError:
+        with pytest.raises(ImportError):
+            V.register()
