@@ -376,7 +376,7 @@ def test_dense_method_and_flag_lifecycle(device):
         x1[0, 5] = 0x7FC0                          # NaN
         m.apply(model.proj, to_dev(x1, device))
         steps.snapshot(tk)
-        with pytest.raises(lifecycle.OrnithWorkerFault, match='o_proj'):
+        with pytest.raises(lifecycle.OrnithWorkerFault, match="'proj': 3"):
             steps.complete(tk)
     finally:
         native.reset_binding()
