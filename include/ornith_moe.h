@@ -52,6 +52,28 @@ ORNITH_EXPORT hipError_t ornith_moe_layer_launch(
     void* workspace, size_t bytes, void* topk_weights_f32, void* topk_ids_i32, void* shared_logit_bf16,
     void* output_bf16, void* flags_u32, int T, int Tcap, hipStream_t stream);
 
+/* The production shared expert of decode rows, fixed8
+ * (plugin-site/ornith_g256/iu4_correctness/shared_kernel.py:33-62, applied by
+ * shared_live.py:125-147), as one launch sequence:
+ *   gu   = dense A8 G256 projection of x with the N32 gate_up bank [1024, 2048], bf16
+ *          (ornith_dense_g256_launch_n32 arithmetic);
+ *   act  = bf16(bf16(silu_f32[bits(gate)]) * up)   (vLLM silu_and_mul: bf16 SiLU, bf16 product);
+ *   down = dense A8 projection of act with the N32 down bank [2048, 512], bf16;
+ *   out  = bf16(sigmoid_bf16[bits(bf16(x . gate_w))] * down)   (scalar gate rounded to
+ *          bf16, torch.sigmoid in bf16, bf16 product).
+ * The reference runs it in chunks of eight rows; every row is independent, so
+ * any 0 <= M <= Mcap <= 8192 is accepted.  The gate logit uses this library's
+ * declared row-dot order (the router's); the reference's Triton order is not
+ * pinnable.  Flags: the dense bits (1 non-finite input, 2 invalid activation,
+ * 4 non-finite projection, 8 non-finite bf16).
+ * Workspace: ornith_shared_fixed8_get_layout(Mcap). */
+ORNITH_EXPORT hipError_t ornith_shared_fixed8_get_layout(int Mcap, size_t* workspace_bytes);
+ORNITH_EXPORT hipError_t ornith_shared_fixed8_launch(
+    const void* input_bf16, const void* gate_up_codes, const void* gate_up_meta,
+    const void* down_codes, const void* down_meta, const void* gate_w_bf16,
+    const void* silu_f32, const void* sigmoid_bf16, void* workspace, size_t bytes,
+    void* output_bf16, void* flags_u32, int M, int Mcap, hipStream_t stream);
+
 /* No reference counterpart.  For callers that cannot allocate device memory
  * (code under HIP graph capture, tight serving loops, harnesses that forbid
  * hipMalloc): ornith_moe_layer_launch without a workspace argument.  Its

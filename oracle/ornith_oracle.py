@@ -39,6 +39,13 @@ Pinning (what checks each function, tests/test_oracle.py):
                              parity unpinned.
   * permute                - counts against numpy bincount, stable order
                              against argsort(kind='stable').
+  * h128 order, quantize, routed_layer_shared, reduce_slots, head_w8,
+    portable_exp, shared_fixed8
+                           - bit for bit against scalar statement-by-statement
+                             restatements of the reference kernels
+                             (tests/_transcribe.py), each with planted
+                             mistakes that must fail (tests/test_oracle_pins.py).
+  * add_bf16               - against torch's CPU bf16 addition on 2M pairs.
 """
 from __future__ import annotations
 
@@ -499,6 +506,29 @@ def routed_layer_shared(x_bf16, route_w, ids, w13_codes, w13_sbits, w13_obits,
         flags |= FLAG_NONFINITE_OUTPUT
     return dict(out=out, shared_out=shared_out, final=final, gate_y=gate_y,
                 middle=middle, route_out=route_out, flags=flags)
+
+
+def shared_fixed8(x_bf16, s13_codes, s13_sbits, s13_obits, s2_codes, s2_sbits, s2_obits, gate_w_bf16,
+                  silu_table_f32, sigmoid_table_bf16):
+    """Production shared expert of decode rows
+    (iu4_correctness/shared_kernel.py:33-62): two dense A8 projections with
+    bf16 outputs (dense_n32 dense_g256_consumer.cpp:360-378), vLLM
+    silu_and_mul in bf16 (SiLU rounded to bf16, then a bf16 product; SiLU
+    taken from the reference's SiLU table), the scalar gate rounded to bf16
+    (declared row-dot order) and torch.sigmoid in bf16 times down, rounded to
+    bf16.  Returns (out bf16 bits [M,2048], flags)."""
+    gu, _, f1 = dense_a8(x_bf16, s13_codes, s13_sbits, s13_obits)
+    g, up = gu[:, :I], gu[:, I:]
+    silu = bf16_round(np.asarray(silu_table_f32, np.float32)[g])
+    act = f32_to_bf16((silu * bf16_to_f32(up)).astype(np.float32))
+    down, _, f2 = dense_a8(act, s2_codes, s2_sbits, s2_obits)
+    logit = f32_to_bf16(router_logits(x_bf16, np.asarray(gate_w_bf16).reshape(1, -1))[:, 0])
+    gate = bf16_to_f32(np.asarray(sigmoid_table_bf16, np.uint16)[logit])
+    out = f32_to_bf16((gate[:, None] * bf16_to_f32(down)).astype(np.float32))
+    flags = f1 | f2
+    if ((out & 0x7F80) == 0x7F80).any():
+        flags |= DENSE_NONFINITE_BF16
+    return out, flags
 
 
 def add_bf16(a_bits, b_bits):

@@ -1,6 +1,7 @@
 // extern "C" entry points.  Argument validation is host-only and runs before
 // any launch; every entry enqueues on the caller's stream and allocates
 // nothing.  The references for each entry are in include/ornith_*.h.
+#include <algorithm>
 #include <mutex>
 #include "kernels.hpp"
 #include "timing.hpp"
@@ -384,6 +385,71 @@ extern "C" hipError_t ornith_moe_layer_launch(
                       static_cast<const uint16_t*>(shared_logit), static_cast<const float*>(silu),
                       static_cast<const uint16_t*>(sigmoid), 127, nullptr, nullptr, static_cast<uint16_t*>(output),
                       static_cast<uint32_t*>(flags), T, Tcap, stream, fused, true);
+}
+
+// ---- shared expert with the reference's fixed8 semantics --------------------------
+namespace {
+struct Fixed8Plan { size_t dense, gu, act, down, logit, bytes; };
+
+Fixed8Plan fixed8_plan(int Mcap) {
+    Fixed8Plan p{};
+    const size_t m = size_t(Mcap);
+    size_t cursor = 0;
+    auto add = [&](size_t& field, size_t bytes) { field = cursor; cursor = align256(cursor + bytes); };
+    const size_t dense = std::max(dense_layout(Mcap, kGateN, kHidden).workspace_bytes,
+                                  dense_layout(Mcap, kDownN, kInter).workspace_bytes);
+    add(p.dense, dense);
+    add(p.gu, m * kGateN * 2);
+    add(p.act, m * kInter * 2);
+    add(p.down, m * kDownN * 2);
+    add(p.logit, m * 2);
+    p.bytes = cursor;
+    return p;
+}
+}  // namespace
+
+extern "C" hipError_t ornith_shared_fixed8_get_layout(int Mcap, size_t* workspace_bytes) {
+    if (!workspace_bytes || Mcap < 0 || Mcap > kMaxTokens) return hipErrorInvalidValue;
+    *workspace_bytes = fixed8_plan(Mcap).bytes;
+    return hipSuccess;
+}
+
+extern "C" hipError_t ornith_shared_fixed8_launch(const void* input, const void* gate_up_codes,
+                                                  const void* gate_up_meta, const void* down_codes,
+                                                  const void* down_meta, const void* gate_w, const void* silu,
+                                                  const void* sigmoid, void* workspace, size_t bytes, void* output,
+                                                  void* flags, int M, int Mcap, hipStream_t stream) {
+    if (Mcap < 0 || Mcap > kMaxTokens || M < 0 || M > Mcap) return hipErrorInvalidValue;
+    const Fixed8Plan p = fixed8_plan(Mcap);
+    if (bytes < p.bytes) return hipErrorInvalidValue;
+    if (!M) return hipSuccess;
+    const Buffer buffers[] = {{input, size_t(M) * kHidden * 2, 16, false, false},
+                              {gate_up_codes, size_t(kGateN) * kHidden / 2, 16, false, false},
+                              {gate_up_meta, size_t(kGateN) * (kHidden / kGroup) * 4, 4, false, false},
+                              {down_codes, size_t(kDownN) * kInter / 2, 16, false, false},
+                              {down_meta, size_t(kDownN) * (kInter / kGroup) * 4, 4, false, false},
+                              {gate_w, size_t(kHidden) * 2, 16, false, false},
+                              {silu, size_t(65536) * 4, 4, false, false},
+                              {sigmoid, size_t(65536) * 2, 2, false, false},
+                              {workspace, bytes, 256, true, false},
+                              {output, size_t(M) * kHidden * 2, 16, true, false},
+                              {flags, 4, 4, true, false}};
+    if (!check_buffers(buffers)) return hipErrorInvalidValue;
+    auto sticky = static_cast<uint32_t*>(flags);
+    auto gu = at<uint16_t>(workspace, p.gu);
+    auto act = at<uint16_t>(workspace, p.act);
+    auto down = at<uint16_t>(workspace, p.down);
+    auto logit = at<uint16_t>(workspace, p.logit);
+    void* dws = at<void>(workspace, p.dense);
+    const OrnithDenseG256Layout lg = dense_layout(Mcap, kGateN, kHidden), ld = dense_layout(Mcap, kDownN, kInter);
+    TRY(dense_run(input, gate_up_codes, gate_up_meta, dws, lg, at<float>(dws, lg.projection), gu, sticky, M, kGateN,
+                  kHidden, 32, stream));
+    TRY(launch_fixed8_act(gu, static_cast<const uint16_t*>(input), static_cast<const uint16_t*>(gate_w),
+                          static_cast<const float*>(silu), act, logit, M, stream));
+    TRY(dense_run(act, down_codes, down_meta, dws, ld, at<float>(dws, ld.projection), down, sticky, M, kDownN, kInter,
+                  32, stream));
+    return launch_fixed8_gate(down, logit, static_cast<const uint16_t*>(sigmoid), static_cast<uint16_t*>(output), M,
+                              sticky, stream);
 }
 
 // ---- the whole layer without a caller workspace --------------------------------

@@ -130,6 +130,15 @@ hipError_t launch_transform_bf16(const uint16_t* x, int M, int K, uint16_t* y, u
 hipError_t launch_dequantize_bf16(const uint32_t* codes, const uint32_t* meta, int N, int K, int tile,
                                   uint16_t* w, uint32_t* sticky, hipStream_t s);
 
+// ---- shared expert, fixed8 semantics (shared.hip) ------------------------------
+// act [M, 512] bf16 from the bf16 gate/up projection gu [M, 1024] (tabulated
+// SiLU rounded to bf16, bf16 product) and the bf16 gate logit x . gate_w [M].
+hipError_t launch_fixed8_act(const uint16_t* gu, const uint16_t* x, const uint16_t* gate_w, const float* silu,
+                             uint16_t* act, uint16_t* logit, int M, hipStream_t s);
+// out [M, 2048] = bf16(sigmoid_table[logit] * down)
+hipError_t launch_fixed8_gate(const uint16_t* down, const uint16_t* logit, const uint16_t* sigmoid, uint16_t* out,
+                              int M, uint32_t* sticky, hipStream_t s);
+
 // ---- fill (graph-capture safe replacement for hipMemsetAsync) -------------------
 hipError_t launch_fill_u32(uint32_t* p, size_t n, uint32_t v, hipStream_t s);
 

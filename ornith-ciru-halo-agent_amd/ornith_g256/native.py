@@ -79,6 +79,8 @@ _PROTOTYPES = {
     'ornith_moe_layer_get_layout': ([_INT, C.POINTER(RoutedLayout)], _INT),
     'ornith_moe_layer_launch': ([_VP] * 15 + [_SZ] + [_VP] * 5 + [_INT] * 2 + [_VP], _INT),
     'ornith_moe_layer_launch_static': ([_VP] * 19 + [_INT, _VP], _INT),
+    'ornith_shared_fixed8_get_layout': ([_INT, C.POINTER(_SZ)], _INT),
+    'ornith_shared_fixed8_launch': ([_VP] * 9 + [_SZ] + [_VP] * 2 + [_INT] * 2 + [_VP], _INT),
     'ornith_mi355x_abi_version': ([], _INT),
     # dense (include/ornith_dense.h)
     'ornith_dense_g256_abi_version': ([], C.c_uint32),
@@ -495,6 +497,22 @@ def moe_layer_static(x, router_weight, bias, shared_gate_weight, gate, gate_meta
                              s_gate_meta, s_down, s_down_meta, silu, sigmoid, topk_weights, topk_ids, shared_logit,
                              out, flags)]
     check(lib(tile).ornith_moe_layer_launch_static(*args, x.shape[0], stream(x)), 'MoE layer (static scratch)')
+
+
+def shared_fixed8_bytes(capacity):
+    size = _SZ(0)
+    check(lib().ornith_shared_fixed8_get_layout(capacity, C.byref(size)), 'fixed8 layout')
+    return size.value
+
+
+def shared_fixed8(x, gate_up, gate_up_meta, down, down_meta, gate_weight, silu, sigmoid, workspace, out, flags,
+                  capacity):
+    """The production shared expert of decode rows (shared_kernel.py:33-62):
+    dense A8 gate/up, bf16 SiLU * up, dense A8 down, bf16 sigmoid gate."""
+    check(lib().ornith_shared_fixed8_launch(*[ptr(t) for t in (x, gate_up, gate_up_meta, down, down_meta,
+                                                               gate_weight, silu, sigmoid, workspace)],
+                                            workspace.numel(), ptr(out), ptr(flags), x.shape[0], capacity,
+                                            stream(x)), 'shared expert (fixed8)')
 
 
 def dense_head(x, codes, meta, workspace, logits, logits_bf16, argmax, flags, capacity):

@@ -275,3 +275,42 @@ def head_w8_row(x_bits, w_i8, w_scale_bits, mistake=None):
         values.append(value)
         bits.append(bf16_rne(value))
     return np.array(values, np.float32), np.array(bits, np.uint16)
+
+
+def fixed8_row(x_bits, up_bank, down_bank, gate_w_bits, silu_table, sigmoid_table, columns, mistake=None):
+    """Production shared expert of one row (iu4_correctness/shared_kernel.py:
+    33-62) for the requested output columns: dense A8 gate/up with bf16
+    outputs, act = bf16(bf16(silu) * up) (vLLM silu_and_mul), dense A8 down
+    (bf16), scalar gate = bf16(fp32 row dot), out = bf16(sigmoid_bf16 * down).
+    mistake: 'no_silu_round' (SiLU kept in fp32, as the fused ninth slot does),
+    'fp32_gate' (sigmoid applied to the unrounded fp32 logit's bf16 truncation)."""
+    row = [bf16_f32(b) for b in x_bits]
+    _, xg = transform_quantize(row)
+    codes, sb, ob = up_bank
+    gu = [bf16_rne(v) for v in projection_columns(codes, sb, ob, xg, range(2 * I))]
+    act = []
+    for c in range(I):
+        silu = F(silu_table[gu[c]])
+        if mistake != 'no_silu_round':
+            silu = bf16_f32(bf16_rne(silu))
+        act.append(bf16_rne(F(silu * bf16_f32(gu[I + c]))))
+    _, ag = transform_quantize([bf16_f32(a) for a in act])
+    codes, sb, ob = down_bank
+    down = [bf16_rne(v) for v in projection_columns(codes, sb, ob, ag, columns)]
+    # scalar gate: lane partials over k = 8c..8c+7, c = lane + 64 i, then the xor butterfly
+    lanes = []
+    for lane in range(64):
+        acc = F(0)
+        for i in range(4):
+            for j in range(8):
+                k = (64 * i + lane) * 8 + j
+                acc = F(np.float64(acc) + np.float64(row[k]) * np.float64(bf16_f32(gate_w_bits[k])))
+        lanes.append(acc)
+    lanes = np.array(lanes, np.float32)
+    for off in (1, 2, 4, 8, 16, 32):
+        lanes = (lanes + lanes[np.arange(64) ^ off]).astype(np.float32)
+    logit_bits = bf16_rne(lanes[0])
+    if mistake == 'fp32_gate':
+        logit_bits = int(np.float32(lanes[0]).view(np.uint32)) >> 16
+    gate = bf16_f32(sigmoid_table[logit_bits])
+    return [bf16_rne(F(gate * bf16_f32(d))) for d in down]

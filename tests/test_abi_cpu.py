@@ -187,6 +187,20 @@ def fresh_binding():
     native.reset_binding()
 
 
+def test_fixed8_validation(lib):
+    from ornith_g256 import native
+    size = native.shared_fixed8_bytes(8)
+    assert size > 0 and native.shared_fixed8_bytes(16) > size
+    with pytest.raises(RuntimeError):
+        native.shared_fixed8_bytes(8193)
+    p = C.c_void_p(0x10000)
+    fn = lib.ornith_shared_fixed8_launch
+    assert fn(*([p] * 9), size, p, p, 0, 8, None) == 0                    # M == 0: nothing touched
+    assert fn(*([p] * 9), size - 1, p, p, 1, 8, None) == INVALID          # short workspace
+    assert fn(*([p] * 9), size, p, p, 9, 8, None) == INVALID              # M > Mcap
+    assert fn(*([p] * 9), size, p, p, 1, 8, None) == INVALID              # overlapping buffers
+
+
 def test_configure_sizes_arena(fresh_binding):
     native = fresh_binding
     size = native.configure({'routed_storage_n32': True}, 64, [(12288, 2048), (1024, 2048)])

@@ -380,3 +380,31 @@ def test_dense_method_and_flag_lifecycle(device):
             steps.complete(tk)
     finally:
         native.reset_binding()
+
+
+# ---------------------------------------------------------------------------
+# Production shared expert (fixed8, shared_kernel.py:33-62)
+# ---------------------------------------------------------------------------
+@pytest.mark.parametrize('M', [1, 8, 13, 70])
+def test_shared_fixed8_bit_exact(device, moe, shared_tables, M):
+    """The reference's fixed8 shared expert (dense A8 gate/up, bf16 SiLU * up,
+    dense A8 down, bf16 sigmoid gate) against the oracle, bit for bit; M = 13
+    and 70 span the reference's eight-row chunks and the dense kernels'
+    fused / separate activation paths."""
+    import torch
+    native = _native()
+    w, d = moe
+    silu, sigmoid = shared_tables
+    print(f'shared fixed8 M={M}', flush=True)
+    rng = np.random.default_rng(2100 + M)
+    x = bf16_normal(rng, (M, 2048))
+    ref, ref_flags = O.shared_fixed8(x, *w['s13'].expert(), *w['s2'].expert(), w['gate'][0], silu, sigmoid)
+    ws = torch.empty(native.shared_fixed8_bytes(max(M, 8)), dtype=torch.uint8, device=device)
+    out = torch.empty((M, 2048), dtype=torch.bfloat16, device=device)
+    flags = _flags(device)
+    native.shared_fixed8(to_dev(x, device), d['s13'][0], d['s13'][1], d['s2'][0], d['s2'][1],
+                         to_dev(w['gate'][0], device), to_dev(silu, device), to_dev(sigmoid, device), ws, out, flags,
+                         max(M, 8))
+    _sync()
+    np.testing.assert_array_equal(from_dev(out), ref)
+    assert int(flags.item()) == ref_flags == 0

@@ -184,3 +184,24 @@ def test_portable_exp_equals_transcription():
     got = O.portable_exp(x)
     ref = np.array([S.portable_exp(v) for v in x], np.float32)
     np.testing.assert_array_equal(got.view(np.uint32), ref.view(np.uint32))
+
+
+# ---------------------------------------------------------------------------
+# shared_fixed8: one row against the transcription of shared_kernel.py:33-62
+# ---------------------------------------------------------------------------
+def test_shared_fixed8_equals_transcription_and_planted_mistakes_fail(shared_tables):
+    silu, sigmoid = shared_tables
+    rng = np.random.default_rng(108)
+    s13, s2 = Bank(rng, 0, 1024, 2048), Bank(rng, 0, 2048, 512)
+    x = bf16_normal(rng, (2, 2048))
+    gw = bf16_normal(rng, (2048,), 0.02)
+    out, flags = O.shared_fixed8(x, *s13.expert(), *s2.expert(), gw, silu, sigmoid)
+    assert flags == 0
+    cols = list(range(0, 2048, 61))
+    for r in range(2):
+        ref = S.fixed8_row(x[r], s13.expert(), s2.expert(), gw, silu, sigmoid, cols)
+        np.testing.assert_array_equal(out[r, cols], np.array(ref, np.uint16))
+    for mistake in ('no_silu_round', 'fp32_gate'):
+        bad = np.concatenate([S.fixed8_row(x[r], s13.expert(), s2.expert(), gw, silu, sigmoid, cols, mistake)
+                              for r in range(2)]).astype(np.uint16)
+        assert not np.array_equal(out[:, cols].reshape(-1), bad), mistake
