@@ -95,7 +95,7 @@ def parse():
                    help='only run a plain 256 MiB device copy (PMC scale factor for FETCH_SIZE/WRITE_SIZE)')
     p.add_argument('--oracle-seconds', type=float, default=5.0)
     p.add_argument('--no-cpu-baseline', action='store_true')
-    p.add_argument('--part', choices=('head', 'dense'), default=None,
+    p.add_argument('--part', choices=('head', 'dense', 'w8head'), default=None,
                    help='time only the G256 LM head (32x151936) or the dense 6144x2048 prefill (1120 rows) '
                         'and print one JSON line (for profiling those rows)')
     return p.parse_args()
@@ -286,6 +286,49 @@ def head_ms(device, steps=20):
     return a.elapsed_time(b) / steps
 
 
+def w8_head_us(device, rows=(1, 8, 64), steps=20):
+    """The reference's W8 G128 LM head [248320, 2048] (head_i8_tile_api.h:22)
+    at each row count: microseconds per call with two 520 MB weight copies
+    alternating (not MALL-resident), plus the kernel's average and its HBM
+    rate over the weight and scale bytes."""
+    import torch
+    from ornith_g256 import native
+    gen = torch.Generator(device=device)
+    gen.manual_seed(79)
+    N = native.HEAD_VOCAB
+    banks = [(torch.randint(-2 ** 31, 2 ** 31, (N // 16, 128, 4, 16), generator=gen, dtype=torch.int64,
+                            device=device).to(torch.int32),
+              (torch.rand((N, 16), generator=gen, device=device) * 0.0015 + 0.0005).half()) for _ in range(2)]
+    layout = native.head_layout(64, N)
+    ws = torch.empty(layout.workspace_bytes, dtype=torch.uint8, device=device)
+    flags = torch.zeros(1, dtype=torch.int32, device=device)
+    result = {}
+    for m in rows:
+        x = torch.randn((m, 2048), generator=gen, device=device).to(torch.bfloat16)
+        out = torch.empty((m, N), dtype=torch.bfloat16, device=device)
+        call = lambda i: native.head_out(x, *banks[i % 2], ws, out, flags, 2)
+        for i in range(4):
+            call(i)
+        torch.cuda.synchronize()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        for i in range(steps):
+            call(i)
+        b.record()
+        torch.cuda.synchronize()
+        with native.KernelTimer('head_w8_mfma') as kt:
+            for i in range(steps):
+                call(i)
+            torch.cuda.synchronize()
+            _, kms = kt.read('head_w8_mfma')
+        weight_bytes = N * 2048 + N * 16 * 2
+        result[str(m)] = dict(us_per_call=a.elapsed_time(b) / steps * 1e3, kernel_us=kms * 1e3,
+                              weight_gbs=weight_bytes / (kms * 1e-3) / 1e9)
+    if int(flags.item()):
+        raise RuntimeError(f'native flags raised by the W8 head: {int(flags.item())}')
+    return result
+
+
 def copy_calibration(device):
     """A plain 256 MiB device-to-device copy, ten times (PMC scale factor)."""
     import torch
@@ -423,6 +466,9 @@ def main():
     if args.part == 'head':
         print(json.dumps({'lm_head_32x151936_us': head_ms(dev, args.steps) * 1e3}))
         return
+    if args.part == 'w8head':
+        print(json.dumps({'w8_head_248320': w8_head_us(dev, steps=args.steps)}))
+        return
     if args.part == 'dense':
         wall1, device1 = dense_prefill_ms(1, dev, 48)
         print(json.dumps({'dense_6144x2048_1120_us': dense_prefill_ms(1120, dev, args.steps) * 1e3,
@@ -466,6 +512,7 @@ def main():
             entry['lm_head_32x151936_us'] = head_ms(dev) * 1e3
         per_tokens[str(t)] = entry
         del r
+    heads = {'w8_248320x2048': w8_head_us(dev)}
     per_tokens[str(args.tokens)] = dict(tokens_per_s=args.tokens / (ms * 1e-3), us_per_layer=ms * 1e3,
                                         unique_experts=unique, hbm_frac=layer_gbs / HBM_PEAK_GBS,
                                         layer_roof=binding_roof(args.tokens, unique, ms),
@@ -494,6 +541,7 @@ def main():
         'roofline': roofline(times, args.tokens, unique),
         'layer_hbm_frac': layer_gbs / HBM_PEAK_GBS,
         'per_tokens': per_tokens,
+        'heads': heads,
     }
     if not args.no_cpu_baseline:
         result['cpu_baseline'] = cpu_baseline()

@@ -11,7 +11,8 @@
  * Contract differences: workspace internals are this library's own (the
  * layout struct keeps the reference field names, `transformed` has size 0);
  * weights must be 16-byte aligned.  `geometry` 0..2 is accepted and does not
- * change results.
+ * change results: every row count runs on the int8 matrix cores
+ * (v_mfma_i32_16x16x64_i8, rows in tiles of 16, each weight byte read once).
  * Flags: 1 non-finite input/transform, 2 invalid activation, 4 non-finite
  * projection, 8 non-finite bf16 (head_i8_tile_api.h:16-21).
  */
@@ -45,6 +46,15 @@ ORNITH_EXPORT hipError_t ornith_head_i8_tile_launch(
     void* workspace, size_t workspace_bytes, void* output_bf16,
     void* group_dots_i32, size_t group_dots_bytes, void* flags_u32,
     int M, int Mcap, int N, int geometry, hipStream_t stream);
+
+/* Greedy sampling hand-off after a head (no C counterpart in the reference,
+ * which takes torch.argmax of the bf16 logits downstream): argmax_i64[m] =
+ * the column of row m's maximum bf16 logit (the first NaN if the row has
+ * one, else the first maximum, as torch.argmax / numpy.argmax).  logits
+ * bf16 [M, N] with row stride ld >= N elements; M == 0 or N == 0 returns
+ * hipSuccess without touching memory. */
+ORNITH_EXPORT hipError_t ornith_logits_argmax_launch(const void* logits_bf16, int M, int N, int64_t ld,
+                                                     void* argmax_i64, hipStream_t stream);
 
 #ifdef __cplusplus
 }

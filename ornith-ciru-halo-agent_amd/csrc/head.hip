@@ -5,6 +5,7 @@
 // acc = acc + RN(sw * RN(sa * dot)) over the 16 groups in ascending order.
 // Weights keep the reference's tile layout uint32 [N/16, 128, 4, 16]: the
 // (n16 tile, group) block of 512 words (2 KiB) is contiguous.
+#include <algorithm>
 #include "kernels.hpp"
 #include "timing.hpp"
 #include "validate.hpp"
@@ -63,56 +64,172 @@ __global__ __launch_bounds__(256) void head_encode_kernel(const uint16_t* __rest
     flag_or(sticky, flags);
 }
 
-// One block per n16 tile: the 16 group blocks (32 KiB) are staged in LDS,
-// thread (group g, column n) forms the integer dot of every row.
-template <bool DOTS>
-__global__ __launch_bounds__(256) void head_project_kernel(const uint32_t* __restrict__ w,
-                                                           const uint16_t* __restrict__ wscale,
-                                                           const uint32_t* __restrict__ act,
-                                                           const uint16_t* __restrict__ ascale, int M, int N,
-                                                           float* __restrict__ diag, uint16_t* __restrict__ out,
-                                                           int32_t* __restrict__ group_dots, uint32_t* sticky) {
-    __shared__ uint32_t lw[kHeadGroups * 528];    // 512 words + 16 pad per group
-    __shared__ uint32_t la[512];
-    __shared__ float lterm[kHeadGroups][16];
-    const int tid = threadIdx.x, tile = blockIdx.x;
-    const uint32_t* src = w + size_t(tile) * (kHeadGroups * 512);
-    for (int q = tid; q < kHeadGroups * 128; q += 256) {
-        const int g = q >> 7, within = (q & 127) * 4;
-        *reinterpret_cast<uint4*>(&lw[g * 528 + within]) = *reinterpret_cast<const uint4*>(src + g * 512 + within);
+// ---------------------------------------------------------------------------
+// Projection on the int8 matrix cores (v_mfma_i32_16x16x64_i8).
+//
+// A block of 8 waves copies the M rows' A8 words (MT tiles of 16 rows, rows
+// past M repeating row M - 1) and their group scales into LDS once; each
+// wave then streams its own contiguous range of 16-column tiles (the N / 16
+// tiles split evenly over all waves of the grid), D groups of weights in
+// flight, the ring running across tiles.
+//  - Weights of one (tile, group) are 2 KiB: words [kq 0..7][kr 0..3][n 0..15],
+//    word (kq, kr, n) = the four K bytes 16 kq + 4 kr .. +3 of column n.  For
+//    k-step s (64 K) lane n + 16q loads words (4s + q, 0..3, n): the 16
+//    contiguous K bytes 64 s + 16 q .. +15 of column n, its B operand.
+//  - A: lane r + 16q reads row r's same 16 bytes from LDS; 16-byte piece p of
+//    row r sits at slot (p & ~15) | ((p ^ r) & 15).
+//  - C: register k of lane n + 16q is row 4q + k, column n.  Dots start from
+//    the bits of kDotBias (|dot| <= 128 * 127 * 127 < 2^22), so
+//    fma(sa, acc, -sa * kDotBias) is RN(sa * dot); term = RN(sw * that);
+//    value = value + term, ascending groups (head_i8_tile_consumer.cpp:96-104).
+// ---------------------------------------------------------------------------
+constexpr float kW8DotBias = 12582912.0f;          // 1.5 * 2^23
+constexpr int kW8DotBiasBits = 0x4B400000;
+constexpr int kW8Waves = 8;
+typedef int w8_i32x4 __attribute__((ext_vector_type(4)));
+
+template <int MT, int D, bool DOTS>
+__global__ __launch_bounds__(64 * kW8Waves, 1) void head_w8_mfma_kernel(
+    const uint32_t* __restrict__ w, const uint16_t* __restrict__ wscale, const uint32_t* __restrict__ act,
+    const uint16_t* __restrict__ ascale, int M, int N, int nwaves, float* __restrict__ diag,
+    uint16_t* __restrict__ out, int32_t* __restrict__ group_dots, uint32_t* sticky) {
+    constexpr int ROWS = 16 * MT, RW = kHeadK / 4, NT = 64 * kW8Waves;
+    static_assert(kHeadGroups % D == 0, "ring slots repeat every tile");
+    __shared__ __attribute__((aligned(16))) uint32_t sA[ROWS * RW];
+    __shared__ __attribute__((aligned(16))) float s_sa[kHeadGroups][ROWS];
+    __shared__ __attribute__((aligned(16))) float s_nb[kHeadGroups][ROWS];
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, li = lane & 15, q = lane >> 4;
+
+    for (int i = tid; i < ROWS * (RW / 4); i += NT) {
+        const int r = i / (RW / 4), pc = i % (RW / 4);
+        const u32x4 v = *reinterpret_cast<const u32x4*>(act + size_t(min(r, M - 1)) * RW + 4 * pc);
+        *reinterpret_cast<u32x4*>(&sA[r * RW + 4 * ((pc & ~15) | ((pc ^ r) & 15))]) = v;
     }
-    const int g = tid >> 4, n = tid & 15;
-    const int col = tile * 16 + n;
-    const float sw = f16_bits_to_f32(wscale[size_t(col) * kHeadGroups + g]);
-    uint32_t flags = 0;
-    for (int row = 0; row < M; ++row) {
-        __syncthreads();
-        for (int q = tid; q < 512; q += 256) la[q] = act[size_t(row) * 512 + q];
-        __syncthreads();
-        // block word (kword/4 - 8g)*64 + (kword&3)*16 + n, kword = 32g + i
-        const uint32_t* wb = &lw[g * 528 + n];
-        const uint32_t* ab = &la[g * 32];
-        int dot = 0;
-#pragma unroll 8
-        for (int i = 0; i < 32; ++i) dot = dot4(int(wb[(i >> 2) * 64 + (i & 3) * 16]), int(ab[i]), dot);
-        if (DOTS) group_dots[(size_t(row) * N + col) * kHeadGroups + g] = dot;
-        const float sa = f16_bits_to_f32(ascale[size_t(row) * kHeadGroups + g]);
-        const float scaled = sa * float(dot);
-        lterm[g][n] = sw * scaled;
-        __syncthreads();
-        if (tid < 16) {
-            float v = 0.f;
+    for (int i = tid; i < ROWS * kHeadGroups; i += NT) {
+        const int r = i / kHeadGroups, g = i % kHeadGroups;
+        const float sa = f16_bits_to_f32(ascale[min(r, M - 1) * kHeadGroups + g]);
+        s_sa[g][r] = sa;
+        s_nb[g][r] = -sa * kW8DotBias;
+    }
+    __syncthreads();
+
+    const int gw = wv * int(gridDim.x) + int(blockIdx.x);
+    if (gw >= nwaves) return;                         // no barrier follows
+    const int ntiles = N >> 4;
+    const int base = ntiles / nwaves, extra = ntiles % nwaves;
+    const int t0 = gw * base + min(gw, extra), cnt = base + (gw < extra ? 1 : 0);
+    if (cnt == 0) return;
+
+    // step st = 16 * (tile - t0) + group: 512 weight words and the lane
+    // column's scale per step
+    const uint32_t* wbase = w + size_t(t0) * (kHeadGroups * 512) + 64 * q + li;
+    const uint16_t* sbase = wscale + size_t(16 * t0 + li) * kHeadGroups;
+    uint32_t bw[D][8];
+    uint16_t bs[D];
+    auto load_b = [&](int st, int slot) {
+        const uint32_t* src = wbase + size_t(st) * 512;
 #pragma unroll
-            for (int gg = 0; gg < kHeadGroups; ++gg) v = v + lterm[gg][tid];
-            const size_t o = size_t(row) * N + tile * 16 + tid;
-            const uint16_t b = f32_to_bf16_bits(v);
-            if (!isfinite(v)) flags |= kDenseNonfiniteProjection;
-            if ((b & 0x7f80u) == 0x7f80u) flags |= kDenseNonfiniteBf16;
-            diag[o] = v;
-            out[o] = b;
+        for (int u = 0; u < 8; ++u) bw[slot][u] = src[256 * (u >> 2) + 16 * (u & 3)];
+        bs[slot] = sbase[size_t(st >> 4) * (16 * kHeadGroups) + (st & 15)];
+    };
+#pragma unroll
+    for (int st = 0; st < D; ++st) load_b(st, st);
+    uint32_t flags = 0;
+    constexpr w8_i32x4 kInit = {kW8DotBiasBits, kW8DotBiasBits, kW8DotBiasBits, kW8DotBiasBits};
+
+    for (int t = 0; t < cnt; ++t) {
+        const int col = 16 * (t0 + t) + li;
+        float val[MT][4];
+#pragma unroll
+        for (int rt = 0; rt < MT; ++rt)
+#pragma unroll
+            for (int k = 0; k < 4; ++k) val[rt][k] = 0.f;
+        const bool refill = t + 1 < cnt;
+        // D groups per pass (compile-time ring slots); the passes stay a loop so
+        // the A fragments of one pass only are live
+#pragma unroll 1
+        for (int g0 = 0; g0 < kHeadGroups; g0 += D) {
+#pragma unroll
+            for (int slot = 0; slot < D; ++slot) {
+                const int g = g0 + slot;
+                w8_i32x4 acc[MT];
+#pragma unroll
+                for (int s = 0; s < 2; ++s) {
+                    const w8_i32x4 fb = {int(bw[slot][4 * s]), int(bw[slot][4 * s + 1]), int(bw[slot][4 * s + 2]),
+                                         int(bw[slot][4 * s + 3])};
+#pragma unroll
+                    for (int rt = 0; rt < MT; ++rt) {
+                        const int r = 16 * rt + li, p = 8 * g + 4 * s + q;
+                        const u32x4 av =
+                            *reinterpret_cast<const u32x4*>(&sA[r * RW + 4 * ((p & ~15) | ((p ^ r) & 15))]);
+                        const w8_i32x4 fa = {int(av.x), int(av.y), int(av.z), int(av.w)};
+                        acc[rt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(fa, fb, s ? acc[rt] : kInit, 0, 0, 0);
+                    }
+                }
+                const float sw = f16_bits_to_f32(bs[slot]);
+                if (g + D < kHeadGroups || refill) load_b(16 * t + g + D, slot);
+#pragma unroll
+                for (int rt = 0; rt < MT; ++rt) {
+                    const float4 sa4 = *reinterpret_cast<const float4*>(&s_sa[g][16 * rt + 4 * q]);
+                    const float4 nb4 = *reinterpret_cast<const float4*>(&s_nb[g][16 * rt + 4 * q]);
+                    const float sa[4] = {sa4.x, sa4.y, sa4.z, sa4.w}, nb[4] = {nb4.x, nb4.y, nb4.z, nb4.w};
+#pragma unroll
+                    for (int k = 0; k < 4; ++k) {
+                        const float scaled = __builtin_fmaf(sa[k], __int_as_float(acc[rt][k]), nb[k]);
+                        const float term = sw * scaled;
+                        val[rt][k] = val[rt][k] + term;
+                        if constexpr (DOTS) {
+                            const int row = 16 * rt + 4 * q + k;
+                            if (row < M)
+                                group_dots[(size_t(row) * N + col) * kHeadGroups + g] = acc[rt][k] - kW8DotBiasBits;
+                        }
+                    }
+                }
+            }
         }
+#pragma unroll
+        for (int rt = 0; rt < MT; ++rt)
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                const int row = 16 * rt + 4 * q + k;
+                if (row >= M) continue;
+                const float v = val[rt][k];
+                const uint16_t b = f32_to_bf16_bits(v);
+                if (!isfinite(v)) flags |= kDenseNonfiniteProjection;
+                if ((b & 0x7f80u) == 0x7f80u) flags |= kDenseNonfiniteBf16;
+                const size_t o = size_t(row) * N + col;
+                diag[o] = v;
+                out[o] = b;
+            }
     }
     flag_or(sticky, flags);
+}
+
+// Per-row argmax of bf16 logits [M, N] (row stride ld): the first NaN if any,
+// else the first maximum (torch.argmax / numpy).  One block per row; every
+// thread scans a strided slice, keys are order-preserving images of the value
+// over the complemented column, so the unsigned maximum is the answer.
+__global__ __launch_bounds__(256) void logits_argmax_kernel(const uint16_t* __restrict__ logits, int N, int64_t ld,
+                                                            int64_t* __restrict__ argmax) {
+    __shared__ uint64_t s_best[256];
+    const int row = blockIdx.x, tid = threadIdx.x;
+    const uint16_t* src = logits + size_t(row) * size_t(ld);
+    uint64_t best = 0;
+    for (int c = tid; c < N; c += 256) {
+        const uint32_t b = src[c];
+        const bool nan = (b & 0x7fffu) > 0x7f80u;
+        const uint32_t mag = (b & 0x8000u) ? ((b & 0x7fffu) ? (~b & 0xffffu) : 0x8000u) : (b | 0x8000u);
+        const uint32_t ord = nan ? 0x1ffffu : mag;        // every NaN above +inf
+        const uint64_t key = (uint64_t(ord) << 32) | uint32_t(~c);
+        best = key > best ? key : best;
+    }
+    s_best[tid] = best;
+    __syncthreads();
+    for (int s = 128; s > 0; s >>= 1) {
+        if (tid < s) s_best[tid] = s_best[tid] > s_best[tid + s] ? s_best[tid] : s_best[tid + s];
+        __syncthreads();
+    }
+    if (tid == 0) argmax[row] = int64_t(~uint32_t(s_best[0]));
 }
 
 bool head_shape(int N) { return N == 256 || N == 1024 || N == 4096 || N == 65536 || N == 248320; }
@@ -168,18 +285,49 @@ extern "C" hipError_t ornith_head_i8_tile_launch(const void* input, const void* 
     auto words = at<uint32_t>(workspace, l.activation_words);
     auto ascale = at<uint16_t>(workspace, l.activation_scales);
     const int waves = M * kHeadGroups;
-    timed_launch("head_encode", head_encode_kernel, dim3((waves + 3) / 4), dim3(256), 0, stream, static_cast<const uint16_t*>(input), M, words, ascale,
-                                                            sticky);
+    timed_launch("head_encode", head_encode_kernel, dim3((waves + 3) / 4), dim3(256), 0, stream,
+                 static_cast<const uint16_t*>(input), M, words, ascale, sticky);
     hipError_t st = hipGetLastError();
     if (st != hipSuccess) return st;
     auto diag = at<float>(workspace, l.projection);
-    if (group_dots)
-        timed_launch("head_project", head_project_kernel<true>, dim3(N / 16), dim3(256), 0, stream,
-            static_cast<const uint32_t*>(weights), static_cast<const uint16_t*>(scales), words, ascale, M, N, diag,
-            static_cast<uint16_t*>(output), static_cast<int32_t*>(group_dots), sticky);
-    else
-        timed_launch("head_project", head_project_kernel<false>, dim3(N / 16), dim3(256), 0, stream,
-            static_cast<const uint32_t*>(weights), static_cast<const uint16_t*>(scales), words, ascale, M, N, diag,
-            static_cast<uint16_t*>(output), nullptr, sticky);
+    int dev = 0, cus = 0;
+    if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) !=
+                                                hipSuccess || cus <= 0)
+        cus = 256;
+    const int ntiles = N / 16;
+    const int blocks = std::min(cus, (ntiles + kW8Waves - 1) / kW8Waves);
+    const int nwaves = std::min(blocks * kW8Waves, ntiles);
+    const auto W = static_cast<const uint32_t*>(weights);
+    const auto S = static_cast<const uint16_t*>(scales);
+    auto out = static_cast<uint16_t*>(output);
+    auto dots = static_cast<int32_t*>(group_dots);
+    auto go = [&](auto kernel) {
+        timed_launch("head_w8_mfma", kernel, dim3(blocks), dim3(64 * kW8Waves), 0, stream, W, S, words, ascale, M, N,
+                     nwaves, diag, out, dots, sticky);
+    };
+    const int mt = (M + 15) / 16;
+    if (group_dots) {
+        if (mt == 1) go(head_w8_mfma_kernel<1, 4, true>);
+        else if (mt == 2) go(head_w8_mfma_kernel<2, 4, true>);
+        else if (mt == 3) go(head_w8_mfma_kernel<3, 2, true>);
+        else go(head_w8_mfma_kernel<4, 2, true>);
+    } else {
+        if (mt == 1) go(head_w8_mfma_kernel<1, 4, false>);
+        else if (mt == 2) go(head_w8_mfma_kernel<2, 4, false>);
+        else if (mt == 3) go(head_w8_mfma_kernel<3, 2, false>);
+        else go(head_w8_mfma_kernel<4, 2, false>);
+    }
+    return hipGetLastError();
+}
+
+extern "C" hipError_t ornith_logits_argmax_launch(const void* logits_bf16, int M, int N, int64_t ld,
+                                                  void* argmax_i64, hipStream_t stream) {
+    if (M < 0 || N < 0 || ld < N) return hipErrorInvalidValue;
+    if (!M || !N) return hipSuccess;
+    const Buffer buffers[] = {{logits_bf16, (size_t(M - 1) * size_t(ld) + size_t(N)) * 2, 2, false, false},
+                              {argmax_i64, size_t(M) * 8, 8, true, false}};
+    if (!check_buffers(buffers)) return hipErrorInvalidValue;
+    timed_launch("logits_argmax", logits_argmax_kernel, dim3(M), dim3(256), 0, stream,
+                 static_cast<const uint16_t*>(logits_bf16), N, ld, static_cast<int64_t*>(argmax_i64));
     return hipGetLastError();
 }

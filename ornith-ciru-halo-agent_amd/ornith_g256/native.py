@@ -97,6 +97,7 @@ _PROTOTYPES = {
     'ornith_head_i8_tile_launch': ([_VP] * 4 + [_SZ] + [_VP] * 2 + [_SZ] + [_VP] + [_INT] * 4 + [_VP], _INT),
     # storage conversion (include/ornith_storage.h)
     'ornith_repack_n16_to_n32': ([_VP] * 4 + [_INT] * 3 + [_VP], _INT),
+    'ornith_logits_argmax_launch': ([_VP, _INT, _INT, _I64, _VP, _VP], _INT),
     # measurement (include/ornith_timing.h)
     'ornith_mi355x_timing_arm': ([C.c_char_p, _INT], _INT),
     'ornith_mi355x_timing_read': ([C.c_char_p, C.POINTER(_INT), C.POINTER(C.c_double)], _INT),
@@ -513,6 +514,15 @@ def shared_fixed8(x, gate_up, gate_up_meta, down, down_meta, gate_weight, silu, 
                                                                gate_weight, silu, sigmoid, workspace)],
                                             workspace.numel(), ptr(out), ptr(flags), x.shape[0], capacity,
                                             stream(x)), 'shared expert (fixed8)')
+
+
+def logits_argmax(logits, out):
+    """Greedy hand-off: out int64 [M] = argmax of each row of bf16 logits [M, N]
+    (first NaN, else first maximum)."""
+    if logits.dtype != torch.bfloat16 or logits.ndim != 2 or logits.stride(1) != 1 or out.dtype != torch.int64:
+        raise ValueError('logits must be bf16 [M, N] with unit column stride; out int64 [M]')
+    check(lib().ornith_logits_argmax_launch(ptr(logits), logits.shape[0], logits.shape[1], logits.stride(0),
+                                            ptr(out), stream(logits)), 'logits argmax')
 
 
 def dense_head(x, codes, meta, workspace, logits, logits_bf16, argmax, flags, capacity):

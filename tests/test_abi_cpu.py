@@ -187,6 +187,15 @@ def fresh_binding():
     native.reset_binding()
 
 
+def test_logits_argmax_validation(lib):
+    p = C.c_void_p(0x10000)
+    fn = lib.ornith_logits_argmax_launch
+    assert fn(None, 0, 100, 100, None, None) == 0          # M == 0
+    assert fn(p, 2, 100, 99, p, None) == INVALID            # ld < N
+    assert fn(None, 2, 100, 100, p, None) == INVALID        # null logits
+    assert fn(p, 2, 100, 100, C.c_void_p(0x10004), None) == INVALID   # misaligned / overlapping output
+
+
 def test_fixed8_validation(lib):
     from ornith_g256 import native
     size = native.shared_fixed8_bytes(8)

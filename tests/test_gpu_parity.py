@@ -493,10 +493,15 @@ def test_moe_layer_single_token_ties(device, moe, shared_tables, case):
 # ---------------------------------------------------------------------------
 # Heads
 # ---------------------------------------------------------------------------
-@pytest.mark.parametrize('M,N,dots', [(1, 256, False), (3, 1024, True), (40, 4096, False)])
+# Rows run in tiles of 16 on the matrix cores: 1..64 rows cover one to four
+# row tiles (40 and 33 leave partial tiles); 65536 and 248320 are the
+# reference's full head widths (head_i8_tile_api.h:22).
+@pytest.mark.parametrize('M,N,dots', [(1, 256, False), (3, 1024, True), (40, 4096, False), (64, 4096, True),
+                                      (33, 1024, False), (17, 256, True), (1, 65536, False), (64, 248320, False)])
 def test_head_w8_bit_exact(device, M, N, dots):
     import torch
     native = _native()
+    print(f'W8 head M={M} N={N} dots={dots}', flush=True)
     rng = np.random.default_rng(500 + M)
     w8 = rng.integers(-127, 128, size=(N, 2048), dtype=np.int64).astype(np.int8)
     sbits = O.f32_to_f16_bits(rng.uniform(0.0005, 0.002, size=(N, 16)).astype(np.float32))
@@ -520,6 +525,11 @@ def test_head_w8_bit_exact(device, M, N, dots):
     np.testing.assert_array_equal(from_dev(out), ref_out)
     diag = from_dev(ws[layout.projection:layout.projection + M * N * 4].view(torch.float32)).reshape(M, N)
     np.testing.assert_array_equal(diag.view(np.uint32), ref_diag.view(np.uint32))
+    # greedy hand-off on the bf16 logits
+    am = torch.empty((M,), dtype=torch.int64, device=device)
+    native.logits_argmax(out, am)
+    _sync()
+    np.testing.assert_array_equal(from_dev(am), O.argmax_first(O.bf16_to_f32(ref_out)))
     if dots:
         tx = O.h128(O.bf16_to_f32(x))
         q, _, _, _ = O.quantize(tx, 127, group=128)
@@ -527,6 +537,35 @@ def test_head_w8_bit_exact(device, M, N, dots):
                              w8.reshape(N, 16, 128).astype(np.int64))
         np.testing.assert_array_equal(from_dev(gd), ref_dots)
     assert int(flags.item()) == ref_flags
+
+
+@pytest.mark.parametrize('case', ['ties', 'nan', 'signed_zero', 'neg_inf'])
+def test_logits_argmax_rules(device, case):
+    """The greedy hand-off follows torch/numpy argmax: the first maximum, the
+    first NaN if any, -0 equal to +0, all -inf gives column 0."""
+    import torch
+    native = _native()
+    rng = np.random.default_rng(77)
+    M, N = 6, 5000
+    v = rng.standard_normal((M, N)).astype(np.float32)
+    if case == 'ties':
+        v[:, [17, 400, 4999]] = 9.0
+        v[3, :] = 1.0
+    elif case == 'nan':
+        v[:, 2500] = np.nan
+        v[:, 3000] = np.nan
+        v[1, 0] = np.nan
+    elif case == 'signed_zero':
+        v[:] = -1.0
+        v[:, 100] = -0.0
+        v[:, 50] = 0.0
+    else:
+        v[:] = -np.inf
+    bits = O.f32_to_bf16(v)
+    am = torch.empty((M,), dtype=torch.int64, device=device)
+    native.logits_argmax(to_dev(bits, device), am)
+    _sync()
+    np.testing.assert_array_equal(from_dev(am), O.argmax_first(O.bf16_to_f32(bits)))
 
 
 # 1..32 rows take the 32x32x32 streaming head (2080 columns = 65 code tiles
