@@ -167,7 +167,9 @@ __global__ __launch_bounds__(64 * kW8Waves, 1) void head_w8_mfma_kernel(
                     }
                 }
                 const float sw = f16_bits_to_f32(bs[slot]);
-                if (g + D < kHeadGroups || refill) load_b(16 * t + g + D, slot);
+                // always refill (the wave's last steps reload the current one:
+                // a predicated load would make every later wait drain the queue)
+                load_b(g + D < kHeadGroups || refill ? 16 * t + g + D : 16 * t + g, slot);
 #pragma unroll
                 for (int rt = 0; rt < MT; ++rt) {
                     const float4 sa4 = *reinterpret_cast<const float4*>(&s_sa[g][16 * rt + 4 * q]);
