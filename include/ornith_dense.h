@@ -58,6 +58,20 @@ ORNITH_EXPORT hipError_t ornith_dense_g256_prepare_bf16(
     void* transformed_bf16, void* weights_bf16, void* flags_u32,
     int M, int N, int K, hipStream_t stream);
 
+/* dense_g256_consumer.cpp:192-246 + the torch.mm that follows it (plugin-site/
+ * ornith_g256/native.py:140-150) as one operation: out bf16 [M,N] =
+ * bf16(H128 x) @ bf16(RN(RN(scale*code)+offset))^T with fp32 accumulation,
+ * reading the N16 codes directly (no dequantised weight copy).  The
+ * summation order is this library's (the reference's is hipBLASLt's), so the
+ * product agrees with it within fp32-accumulation tolerance.  Workspace: at
+ * least round_up(M,16)*K*2 bytes (the transformed activations, in the
+ * library's matrix-core fragment order), 256-byte aligned; output 16-byte
+ * aligned.
+ * Flags: 1 non-finite input/transform, 8 non-finite bf16 operand. */
+ORNITH_EXPORT hipError_t ornith_dense_g256_gemm_bf16(
+    const void* input_bf16, const void* codes, const void* metadata, void* workspace, size_t workspace_bytes,
+    void* output_bf16, void* flags_u32, int M, int N, int K, hipStream_t stream);
+
 /* dense_n32/dense_g256_consumer.cpp:360-378.  N32 codes, 1<=M<=16, N%32==0, geometry==2.
  * Workspace regions as for ornith_dense_g256_launch. */
 ORNITH_EXPORT hipError_t ornith_dense_g256_launch_n32(

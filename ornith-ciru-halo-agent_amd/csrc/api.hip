@@ -535,7 +535,7 @@ extern "C" hipError_t ornith_dense_g256_launch(const void* input, const void* co
                               {codes, size_t(N) * K / 2, 16, false, false},
                               {metadata, size_t(N) * (K / kGroup) * 4, 4, false, false},
                               {workspace, bytes, 256, true, false},
-                              {output, size_t(M) * N * 2, 2, true, false},
+                              {output, size_t(M) * N * 2, 16, true, false},
                               {flags, 4, 4, true, false}};
     if (!check_buffers(buffers)) return hipErrorInvalidValue;
     return dense_run(input, codes, metadata, workspace, l, at<float>(workspace, l.projection),
@@ -555,10 +555,30 @@ extern "C" hipError_t ornith_dense_g256_prepare_bf16(const void* input, const vo
                               {flags, 4, 4, true, false}};
     if (!check_buffers(buffers)) return hipErrorInvalidValue;
     auto sticky = static_cast<uint32_t*>(flags);
-    TRY(launch_transform_bf16(static_cast<const uint16_t*>(input), M, K, static_cast<uint16_t*>(transformed), sticky,
-                              stream));
+    TRY(launch_transform_bf16_fast(static_cast<const uint16_t*>(input), M, K, static_cast<uint16_t*>(transformed),
+                                   sticky, stream));
     return launch_dequantize_bf16(static_cast<const uint32_t*>(codes), static_cast<const uint32_t*>(metadata), N, K, 16,
                                   static_cast<uint16_t*>(weights), sticky, stream);
+}
+
+extern "C" hipError_t ornith_dense_g256_gemm_bf16(const void* input, const void* codes, const void* metadata,
+                                                  void* workspace, size_t bytes, void* output, void* flags, int M,
+                                                  int N, int K, hipStream_t stream) {
+    if (M < 0 || M > kMaxTokens || !dense_shape(N, K)) return hipErrorInvalidValue;
+    if (M == 0) return hipSuccess;
+    const size_t xt_bytes = size_t(M + 15) / 16 * 16 * K * 2;
+    const Buffer buffers[] = {{input, size_t(M) * K * 2, 16, false, false},
+                              {codes, size_t(N) * K / 2, 4, false, false},
+                              {metadata, size_t(N) * (K / kGroup) * 4, 4, false, false},
+                              {workspace, bytes, 256, true, false},
+                              {output, size_t(M) * N * 2, 16, true, false},
+                              {flags, 4, 4, true, false}};
+    if (bytes < xt_bytes || !check_buffers(buffers)) return hipErrorInvalidValue;
+    auto sticky = static_cast<uint32_t*>(flags);
+    auto xt = static_cast<uint16_t*>(workspace);
+    TRY(launch_transform_bf16_frag(static_cast<const uint16_t*>(input), M, K, xt, sticky, stream));
+    return launch_dense_gemm_bf16(xt, static_cast<const uint32_t*>(codes), static_cast<const uint32_t*>(metadata), M, N,
+                                  K, static_cast<uint16_t*>(output), sticky, stream);
 }
 
 extern "C" hipError_t ornith_dense_g256_launch_n32(const void* input, const void* codes, const void* metadata,

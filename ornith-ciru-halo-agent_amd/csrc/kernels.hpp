@@ -130,6 +130,16 @@ hipError_t launch_transform_bf16(const uint16_t* x, int M, int K, uint16_t* y, u
 hipError_t launch_dequantize_bf16(const uint32_t* codes, const uint32_t* meta, int N, int K, int tile,
                                   uint16_t* w, uint32_t* sticky, hipStream_t s);
 
+// ---- dense bf16 GEMM reading 4-bit codes (gemm.hip) ---------------------------
+// y = bf16(H128 x) [M, K] row-major (flags: 1 non-finite input/transform, 8 non-finite bf16)
+hipError_t launch_transform_bf16_fast(const uint16_t* x, int M, int K, uint16_t* y, uint32_t* sticky, hipStream_t s);
+// the same values in matrix-core fragment order over round_up(M, 16) rows
+// (padding rows zero): (r, k) at ((r / 16 * K / 32 + k / 32) * 64 + 16 (k % 32 / 8) + r % 16) * 8 + k % 8
+hipError_t launch_transform_bf16_frag(const uint16_t* x, int M, int K, uint16_t* y, uint32_t* sticky, hipStream_t s);
+// out bf16 [M, N] = y @ bf16(dequant(N16 codes, meta))^T, fp32 accumulation; y in fragment order
+hipError_t launch_dense_gemm_bf16(const uint16_t* xt, const uint32_t* codes, const uint32_t* meta, int M, int N, int K,
+                                  uint16_t* out, uint32_t* sticky, hipStream_t s);
+
 // ---- shared expert, fixed8 semantics (shared.hip) ------------------------------
 // act [M, 512] bf16 from the bf16 gate/up projection gu [M, 1024] (tabulated
 // SiLU rounded to bf16, bf16 product) and the bf16 gate logit x . gate_w [M].

@@ -23,7 +23,7 @@ LIBDIR = PKG / 'lib'
 VARIANTS = {32: 'libornith_g256_mi355x.so', 16: 'libornith_g256_mi355x_n16.so'}
 LIBNAME = VARIANTS[32]
 SOURCES = ['act.hip', 'routing.hip', 'proj_gemv.hip', 'proj_mfma.hip', 'decode.hip', 'decode1.hip', 'head.hip',
-           'timing.hip', 'storage.hip', 'shared.hip', 'api.hip']
+           'timing.hip', 'storage.hip', 'shared.hip', 'gemm.hip', 'api.hip']
 HIPCC = os.environ.get('HIPCC', '/opt/rocm/bin/hipcc')
 FLAGS = ['--offload-arch=gfx950', '-O3', '-std=c++20', '-fPIC', '-ffp-contract=off',
          '-fhip-fp32-correctly-rounded-divide-sqrt', '-fvisibility=hidden',

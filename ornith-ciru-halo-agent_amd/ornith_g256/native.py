@@ -88,6 +88,7 @@ _PROTOTYPES = {
     'ornith_dense_g256_launch': (_DENSE_LAUNCH, _INT),
     'ornith_dense_g256_prepare_bf16': ([_VP] * 6 + [_INT] * 3 + [_VP], _INT),
     'ornith_dense_g256_launch_n32': (_DENSE_LAUNCH, _INT),
+    'ornith_dense_g256_gemm_bf16': ([_VP] * 4 + [_SZ] + [_VP] * 2 + [_INT] * 3 + [_VP], _INT),
     'ornith_dense_g256_n32_rows': ([], _INT),
     'ornith_dense_g256_head_workspace_bytes': ([_INT, _INT], _SZ),
     'ornith_dense_g256_head_launch': ([_VP] * 4 + [_SZ] + [_VP] * 4 + [_INT] * 3 + [_VP], _INT),
@@ -334,10 +335,25 @@ def _check_banks(tile, gate, gate_meta, down, down_meta):
 # ---------------------------------------------------------------------------
 # torch ops (reference native.py:121-212)
 # ---------------------------------------------------------------------------
+def gemm_preferred(rows: int, n: int, k: int) -> bool:
+    """Which bf16 prefill route is faster for a [rows, k] x [n, k] linear,
+    as measured on MI355X over 65..8192 rows: the GEMM reading the 4-bit
+    codes for k <= 512 at every row count, and for k <= 2048 while
+    rows * n <= 8 Mi; bf16 operands + hipBLASLt otherwise (large products,
+    where the library kernel's efficiency wins, and k >= 4096)."""
+    return k <= 512 or (k <= 2048 and rows * n <= 8 << 20)
+
+
 def _dense_one(x, codes, metadata, workspace, out, flags, capacity, n, k, geometry, a8_max_rows):
     h = lib(_binding.libraries['dense'] if _binding else 32)
     _check_rows(x, out, capacity, k)
     rows = x.shape[0]
+    if rows > a8_max_rows and gemm_preferred(rows, n, k):
+        # bf16 prefill semantics on this library's GEMM: the transformed rows
+        # (padded to 16) take the arena's front, within capacity * k * 2 + n * k * 2
+        check(h.ornith_dense_g256_gemm_bf16(ptr(x), ptr(codes), ptr(metadata), ptr(workspace), workspace.numel(),
+                                            ptr(out), ptr(flags), rows, n, k, stream(x)), 'dense bf16 GEMM')
+        return
     if rows > a8_max_rows:
         # bf16 prefill semantics: bf16(H128 x) @ bf16(dequantised W).T, both
         # operands carved from the arena (dense_g256_consumer.cpp:192-246)

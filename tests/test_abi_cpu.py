@@ -140,6 +140,16 @@ def test_dense_validation(lib):
     # prepare_bf16
     assert lib.ornith_dense_g256_prepare_bf16(*([None] * 6), 0, 1024, 2048, None) == 0
     assert lib.ornith_dense_g256_prepare_bf16(*([None] * 6), 1, 1024, 2048, None) == INVALID
+    # gemm_bf16: workspace round_up(M, 16) * K * 2 bytes, 256-aligned; output 16-aligned
+    p = C.c_void_p
+    need = 32 * 2048 * 2
+    args = lambda ws_bytes, out: (p(0x100000), p(0x2000000), p(0x3000000), p(0x4000000), ws_bytes, p(out),
+                                  p(0x6000000))
+    assert lib.ornith_dense_g256_gemm_bf16(*args(need, 0x5000000), 0, 1024, 2048, None) == 0
+    assert lib.ornith_dense_g256_gemm_bf16(*args(need - 1, 0x5000000), 17, 1024, 2048, None) == INVALID
+    assert lib.ornith_dense_g256_gemm_bf16(*args(need, 0x5000008), 17, 1024, 2048, None) == INVALID
+    assert lib.ornith_dense_g256_gemm_bf16(*args(need, 0x5000000), 17, 1000, 2048, None) == INVALID   # N % 16
+    assert lib.ornith_dense_g256_gemm_bf16(*args(need, 0x5000000), -1, 1024, 2048, None) == INVALID
 
 
 def test_head_validation(lib):

@@ -135,18 +135,19 @@ def test_moe_layer_zipf_full_size_batch_invariance(device, moe, shared_tables, T
 # ---------------------------------------------------------------------------
 # Dense linear at the prefill shape through dense_out
 # ---------------------------------------------------------------------------
-def test_dense_out_prefill_1120_tolerance(device):
-    """dense_out at [1120, 2048] x [6144, 2048] (more rows than the A8
-    crossover): bf16(H128 x) @ bf16(dequantised W)^T on the GEMM.  The bf16
-    operands are bit-exact (test_gpu_parity); the GEMM's reduction order is
-    the BLAS library's, so the product is checked by tolerance against fp64:
+@pytest.mark.parametrize('M,N,K', [(1120, 6144, 2048), (300, 512, 4096), (2100, 4096, 2048)])
+def test_dense_out_prefill_tolerance(device, M, N, K):
+    """dense_out with more rows than the A8 crossover: bf16(H128 x) @
+    bf16(dequantised W)^T, on the code-reading GEMM (1120 x 6144 x 2048) or
+    on bf16 operands + hipBLASLt (K = 4096; 2100 x 4096 rows x columns).  The
+    bf16 operands are bit-exact (test_gpu_parity); the reduction order is
+    the kernel's own, so the product is checked by tolerance against fp64:
     cosine >= 0.9999 and max |err| <= 1e-2 * max |ref|."""
     import torch
     from _ornith import Bank
     native = _native()
-    print('dense_out 1120 x 6144 x 2048', flush=True)
-    M, N, K = 1120, 6144, 2048
-    rng = np.random.default_rng(1120)
+    print(f'dense_out {M} x {N} x {K} (GEMM route: {native.gemm_preferred(M, N, K)})', flush=True)
+    rng = np.random.default_rng(M + N)
     bank = Bank(rng, 0, N, K, tile=16)
     x = bf16_normal(rng, (M, K))
     ws = torch.empty((M * K + N * K) * 2, dtype=torch.uint8, device=device)
@@ -408,3 +409,47 @@ def test_shared_fixed8_bit_exact(device, moe, shared_tables, M):
     _sync()
     np.testing.assert_array_equal(from_dev(out), ref)
     assert int(flags.item()) == ref_flags == 0
+
+
+# ---------------------------------------------------------------------------
+# Dense linear on the bf16 matrix cores, reading the 4-bit codes
+# ---------------------------------------------------------------------------
+@pytest.mark.parametrize('M,N,K', [(1120, 6144, 2048), (65, 96, 512), (300, 1040, 768), (257, 128, 8192)])
+def test_dense_gemm_bf16_tolerance(device, M, N, K):
+    """ornith_dense_g256_gemm_bf16 against fp64 products of the exact bf16
+    operands (bf16(H128 x), bf16 dequantised weights): cosine >= 0.9999 and
+    max |err| <= 1e-2 * max |ref|; partial row and column blocks included."""
+    import torch
+    from _ornith import Bank
+    native = _native()
+    print(f'dense gemm bf16 M={M} N={N} K={K}', flush=True)
+    rng = np.random.default_rng(3000 + M)
+    bank = Bank(rng, 0, N, K, tile=16)
+    x = bf16_normal(rng, (M, K))
+    Mp = (M + 15) // 16 * 16                      # the transformed rows, padded with zero rows
+    ws = torch.empty(Mp * K * 2, dtype=torch.uint8, device=device)
+    out = torch.empty((M, N), dtype=torch.bfloat16, device=device)
+    flags = _flags(device)
+    xd, cd, md = to_dev(x, device), to_dev(bank.codes, device), to_dev(bank.meta, device)   # alive until the sync
+    assert native.lib().ornith_dense_g256_gemm_bf16(native.ptr(xd), native.ptr(cd), native.ptr(md), native.ptr(ws),
+                                                    ws.numel() - 2, native.ptr(out), native.ptr(flags), M, N, K,
+                                                    native.stream(xd)) != 0                     # workspace too small
+    st = native.lib().ornith_dense_g256_gemm_bf16(native.ptr(xd), native.ptr(cd), native.ptr(md), native.ptr(ws),
+                                                  ws.numel(), native.ptr(out), native.ptr(flags), M, N, K,
+                                                  native.stream(xd))
+    assert st == 0
+    _sync()
+    xt = O.transform_bf16(x)
+    # fragment order: (r, k) at ((r // 16 * K // 32 + k // 32) * 64 + 16 * (k % 32 // 8) + r % 16) * 8 + k % 8
+    frag = from_dev(ws.view(torch.bfloat16)).reshape(Mp // 16, K // 32, 4, 16, 8)
+    rows = frag.transpose(0, 3, 1, 2, 4).reshape(Mp, K)
+    np.testing.assert_array_equal(rows[:M], xt)
+    assert not rows[M:].view(np.uint16).any()
+    got = O.bf16_to_f32(from_dev(out)).astype(np.float64)
+    ref = (O.bf16_to_f32(xt).astype(np.float64)
+           @ O.bf16_to_f32(O.dequantize_bf16(*bank.expert())).astype(np.float64).T)
+    cos = float((got.ravel() @ ref.ravel()) / (np.linalg.norm(got) * np.linalg.norm(ref)))
+    err = float(np.abs(got - ref).max() / np.abs(ref).max())
+    print(f'  cosine {cos:.8f}  max rel err {err:.2e}', flush=True)
+    assert cos >= 0.9999 and err <= 1e-2
+    assert int(flags.item()) == 0
