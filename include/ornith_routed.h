@@ -1,15 +1,19 @@
 /* Routed G256 MoE C ABI of the MI355X (gfx950) Ornith library.
  *
- * Drop-in for the reference's routed libraries (libornith_routed_direct.so,
- * libornith_routed_storage_n32.so): same symbol names, argument order and
- * meaning, return codes and sticky-flag bits.  Each declaration cites the
- * reference interface it replaces.
+ * Drop-in for the reference's routed libraries: same symbol names, argument
+ * order and meaning, return codes and sticky-flag bits.  Each declaration
+ * cites the reference interface it replaces.  The library is built twice
+ * from the same sources, one build per routed bank layout:
+ *   libornith_g256_mi355x_n16.so - N16 banks, for libornith_routed_direct.so
+ *                                  (routed_direct_api.h:7; ornith_routed_storage_n32 returns 16);
+ *   libornith_g256_mi355x.so     - N32 banks, for libornith_routed_storage_n32.so
+ *                                  (routed_storage_n32_consumer.cpp:1-2; returns 32).
  *
- * Storage (unchanged from the reference, N32 banks as in
- * kernels/routed_storage/routed_storage_n32_consumer.cpp:1-2):
- *   codes    uint32 [E=256, N/32, K/256, 32, 32]; word ((e*N/32 + n/32)*K/256 + g)*1024 + j*32 + n%32
+ * Storage (unchanged from the reference; T = 32 for the N32 build, 16 for the N16 build):
+ *   codes    uint32 [E=256, N/T, K/256, 32, T]; word ((e*N/T + n/T)*K/256 + g)*32*T + j*T + n%T
  *            packs K values 256g+8j .. +7 of row n, low nibble first (unsigned 4-bit).
- *   metadata uint32 [E, N/32, K/256, 32] = fp16 scale | fp16 offset << 16; w = scale*code + offset.
+ *   metadata uint32 [E, N/T, K/256, T] = fp16 scale | fp16 offset << 16; w = scale*code + offset.
+ *   The shared-expert banks of the *_shared_tables and layer entries are N32 in both builds.
  *   gate_up: N=1024 (gate rows 0..511, up rows 512..1023), K=2048; down: N=2048, K=512.
  *
  * Arithmetic (bit-exact with the reference A8/A4 paths): fp32 H128 of each
