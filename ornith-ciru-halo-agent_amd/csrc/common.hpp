@@ -15,6 +15,7 @@ namespace ornith {
 
 // native 4 x u32 vector: array elements of this type stay in registers
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kExperts = 256, kTop = 8, kHidden = 2048, kInter = 512, kGroup = 256;
 constexpr int kShared = kExperts;            // bank id of the always-on shared expert
