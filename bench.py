@@ -68,6 +68,8 @@ def kernel_cost(name, T, unique):
     mfma amounts are the int8 ops of the exact integer dots (2 per MAC)."""
     banks = unique + 1
     routes = 9 * T
+    if name == 'layer1':            # the whole single-token layer in one launch
+        return 'hbm', banks * EXPERT_BYTES + ROUTER_BYTES + T * 2048 * 2 * 2, HBM_PEAK_GBS, 'GB/s'
     if name in ('route1', 'route'):
         return 'hbm', ROUTER_BYTES + T * 2048 * 2, HBM_PEAK_GBS, 'GB/s'
     if name in ('gateup1', 'gateup'):

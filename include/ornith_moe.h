@@ -97,6 +97,16 @@ ORNITH_EXPORT hipError_t ornith_moe_layer_launch_static(
 /* Build identification (no reference counterpart): returns 1. */
 ORNITH_EXPORT int ornith_mi355x_abi_version(void);
 
+/* No reference counterpart.  Which kernels run a single-token (T == 1) routed
+ * or whole-layer call, process-wide: 0 (default) the one-launch kernel
+ * wherever its 256 blocks are resident at once on the device (else the three
+ * kernels), 1 always the three kernels; -1 queries.  Returns the previous
+ * setting, or -1 for another value.  Results are identical either way.  The
+ * one-launch kernel raises sticky flag 64 if a block gave up waiting for
+ * another block's hand-off (only possible when the grid could not be
+ * resident at once, e.g. CUs taken by other work for tens of ms). */
+ORNITH_EXPORT int ornith_mi355x_single_token_path(int path);
+
 #ifdef __cplusplus
 }
 #endif

@@ -510,6 +510,12 @@ extern "C" hipError_t ornith_moe_layer_launch_static(
 
 extern "C" int ornith_mi355x_abi_version(void) { return 1; }
 
+extern "C" int ornith_mi355x_single_token_path(int path) {
+    if (path < -1 || path > 1) return -1;
+    if (path == -1) return g_single_token_mode.load();
+    return g_single_token_mode.exchange(path);
+}
+
 // =============================================================================
 // Dense
 // =============================================================================

@@ -386,7 +386,7 @@ __global__ __launch_bounds__(256) void decode_down_kernel(DecodeArgs a) {
 // ---------------------------------------------------------------------------
 size_t decode_scratch_bytes() {
     return align256(size_t(kDecodeMaxTokens) * kLogitStride * 4) + align256(kMaxSegments * sizeof(Segment)) +
-           align256(kMaxRoutes * 4) + align256(8);
+           align256(kMaxRoutes * 4) + align256(8) + align256(4) + align256(size_t(kLayer1Words) * 8);
 }
 
 void carve_decode(void* base, DecodeArgs& a) {
@@ -396,6 +396,8 @@ void carve_decode(void* base, DecodeArgs& a) {
     a.segments = static_cast<Segment*>(take(kMaxSegments * sizeof(Segment)));
     a.routes = static_cast<int32_t*>(take(kMaxRoutes * 4));
     a.nseg = static_cast<int32_t*>(take(8));
+    a.l1_seq = static_cast<uint32_t*>(take(4));
+    a.l1_words = static_cast<uint64_t*>(take(size_t(kLayer1Words) * 8));
 }
 
 constexpr int kDownTilesPerBlock = 2;    // 32-column down tiles per block (2048 / 32 / 2 = 32 blocks per segment)

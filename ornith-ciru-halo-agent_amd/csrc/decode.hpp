@@ -1,6 +1,7 @@
 // Decode-path (T <= 32) arguments and launcher.
 #pragma once
 #include "kernels.hpp"
+#include <atomic>
 
 namespace ornith {
 
@@ -10,6 +11,22 @@ constexpr int64_t kGateBankWords = int64_t(2 * kInter) * kHidden / 8;
 constexpr int64_t kGateBankMeta = int64_t(2 * kInter) * (kHidden / kGroup);
 constexpr int64_t kDownBankWords = int64_t(kHidden) * kInter / 8;
 constexpr int64_t kDownBankMeta = int64_t(kHidden) * (kInter / kGroup);
+
+// Hand-off words of the single-token layer kernel (decode1.hip): router
+// logit e at kLayer1Spread * e, middle rows of the nine slots at
+// kLayer1Middle, block L's arrival word at kLayer1Arrive + kLayer1Spread * L.
+// Words that different blocks write sit 64 bytes apart: 257 single-word
+// stores into a few shared cache lines serialise (measured ~0.85 us more
+// before the last reader sees them); each producer of the middle rows writes
+// a whole 128-byte line.
+constexpr int kLayer1Blocks = 256;
+constexpr int kLayer1Spread = 8;
+constexpr int kLayer1Middle = kLayer1Spread * 320;
+constexpr int kLayer1Arrive = kLayer1Middle + (kTop + 1) * kInter;
+constexpr int kLayer1Words = kLayer1Arrive + kLayer1Spread * kLayer1Blocks;
+// sticky flag of this library: a single-token layer block gave up waiting for
+// another block's hand-off (the grid was not resident at once)
+constexpr uint32_t kFlagHandoffTimeout = 64;
 
 struct DecodeArgs {
     int T;
@@ -34,6 +51,8 @@ struct DecodeArgs {
     uint32_t* m_words; uint16_t* m_scales; int32_t* m_sums;   // quantised middle rows (2..32 tokens)
     float* route_out;                  // [RS, 2048]
     float* logits; Segment* segments; int32_t* routes; int32_t* nseg;
+    // single-token layer kernel: call sequence number and tagged hand-off words
+    uint32_t* l1_seq; uint64_t* l1_words;
     // outputs
     float* final_f32; uint16_t* out; uint16_t* shared_out; uint16_t* layer_out;
     uint32_t* sticky;
@@ -42,6 +61,8 @@ struct DecodeArgs {
 size_t decode_scratch_bytes();
 void carve_decode(void* base, DecodeArgs& a);
 hipError_t launch_decode(const DecodeArgs& a, bool router, bool shared, int qmax, hipStream_t s);
+// single-token path: 0 automatic (one launch where the grid is resident), 1 three kernels
+extern std::atomic<int> g_single_token_mode;
 hipError_t launch_decode1(const DecodeArgs& a, bool router, bool shared, int qmax, hipStream_t s);
 
 }  // namespace ornith

@@ -26,6 +26,7 @@
 #include "timing.hpp"
 #include "topk.hpp"
 #include "decode.hpp"
+#include <atomic>
 
 namespace ornith {
 
@@ -369,6 +370,484 @@ __global__ __launch_bounds__(576) void decode1_down_kernel(DecodeArgs a) {
     flag_or(a.sticky, flags);
 }
 
+// ---------------------------------------------------------------------------
+// The whole single-token layer in one launch: 256 blocks of 9 waves, all
+// resident at once (the launcher checks the occupancy; otherwise the three
+// kernels above run).  Values that cross blocks -- the 257 router logits and
+// the nine middle rows -- travel as 64-bit words (tag << 32 | value bits),
+// each written and read with one agent-scope atomic access.  The tag hashes
+// the call's sequence number with the word's index, so a reader knows a word
+// belongs to this call once its tag matches: no fence, counter or kernel
+// boundary sits between producer and consumer, and a stale word (an earlier
+// call, another workspace) does not match.  Every wait is bounded; a block
+// that gives up raises kFlagHandoffTimeout and finishes on what it has.
+//
+// Block L (linear launch index; XCDs take blocks round-robin):
+//   wave 8    router row L (block 0 also the shared gate row), published as
+//             a tagged logit as soon as it is formed;
+//   waves 4-7 H128 + A8 quantisation of x into LDS (every block its own);
+//             then wave 4 waits for the 257 logits and selects the experts;
+//   waves 0-3 gate-up: 16 gate + 16 up columns of routed slot s (XCD-paired
+//             as decode1_gateup_kernel); blocks of slot 0 also do the same
+//             columns of the shared expert, whose codes load at once; waves
+//             0 and 1 publish the 16 middle values of the routed and shared
+//             unit;
+//   blocks L < 128 then finish 16 output columns as decode1_down_kernel:
+//             wave i's down codes of slot i load as soon as the experts are
+//             known (behind the gate-up codes on waves 0-3), so a wave's
+//             loads have landed before it waits for slot i's middle row (a
+//             wave's loads complete in order: a wait for a hand-off word
+//             queued behind a weight load would wait for the weights);
+//             then the H128 tail and A8 of the middle row, the dots, the
+//             tree and the slot-order sum.
+// Every wave reads the sequence number at its start and has it before the
+// block's first barrier, after which the block publishes an arrival word;
+// block 0 advances the number once every block has arrived.  The arithmetic
+// is that of the three kernels above, operation for operation.
+namespace {
+__device__ __forceinline__ uint32_t l1_tag(uint32_t seq, uint32_t idx) {
+    uint32_t h = seq * 0x9E3779B9u ^ (idx + 0x7F4A7C15u) * 0x85EBCA77u;
+    h ^= h >> 16;
+    h *= 0x7FEB352Du;
+    h ^= h >> 15;
+    h *= 0x846CA68Bu;
+    h ^= h >> 16;
+    return h;
+}
+__device__ __forceinline__ void l1_put(uint64_t* w, uint32_t idx, uint32_t seq, uint32_t bits) {
+    __hip_atomic_store(w + idx, (uint64_t(l1_tag(seq, idx)) << 32) | bits, __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ uint64_t l1_get(uint64_t* w, uint32_t idx) {
+    return __hip_atomic_load(w + idx, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+constexpr int kHandoffSpins = 1 << 15;
+// Waits until this wave's N words idx[] carry this call's tags; val[] gets
+// their value bits.  One round of N loads at a time, all issued before any is
+// checked; PAUSE (s_sleep units of 64 clocks) between rounds.  Wave-uniform;
+// false after kHandoffSpins rounds.
+template <int N, int PAUSE>
+__device__ __forceinline__ bool l1_wait(uint64_t* w, const uint32_t (&idx)[N], uint32_t seq, uint32_t (&val)[N]) {
+    uint32_t want[N];
+#pragma unroll
+    for (int i = 0; i < N; ++i) want[i] = l1_tag(seq, idx[i]);
+    for (int spin = 0; spin < kHandoffSpins; ++spin) {
+        uint64_t r[N];
+#pragma unroll
+        for (int i = 0; i < N; ++i) r[i] = l1_get(w, idx[i]);
+        bool ok = true;
+#pragma unroll
+        for (int i = 0; i < N; ++i) {
+            val[i] = uint32_t(r[i]);
+            ok = ok && uint32_t(r[i] >> 32) == want[i];
+        }
+        if (__builtin_amdgcn_ballot_w64(!ok) == 0) return true;
+        if (PAUSE) __builtin_amdgcn_s_sleep(PAUSE);
+    }
+    return false;
+}
+// Waits until an LDS counter of this block reaches n (bounded; the waves
+// that count it are this block's own and wait for nothing else).
+__device__ __forceinline__ void lds_wait(uint32_t* counter, uint32_t n) {
+    for (int spin = 0; spin < (1 << 22); ++spin) {
+        if (__hip_atomic_load(counter, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) >= n) return;
+        __builtin_amdgcn_s_sleep(1);
+    }
+}
+constexpr int kLayer1DownBlocks = kHidden / 16;
+}  // namespace
+
+template <bool ROUTER, bool SHARED, int QMAX>
+__global__ __launch_bounds__(576) void layer1_kernel(DecodeArgs a) {
+    __shared__ __align__(16) uint32_t lx[8 * 64];               // A8 words of x
+    __shared__ float lxa[8], lxs[8];                            // group scale, scale * sum
+    __shared__ float lterm[2][8][32];                           // gate-up terms: shared unit, routed unit
+    __shared__ __align__(16) uint64_t s_cand[65];
+    __shared__ uint2 s_sel[kTop];
+    __shared__ int lbank[kSlots];
+    __shared__ float lw8[kTop];
+    __shared__ uint32_t lshared_logit;
+    __shared__ __align__(16) uint32_t lm[kSlots * 2 * 64];      // A8 words of the middle rows
+    __shared__ float lma[kSlots * 2], lms[kSlots * 2];
+    __shared__ float lro[kSlots][16];
+    __shared__ uint32_t lseq[kSlots];
+    __shared__ uint32_t lsync[2];   // waves done: x quantisation (4), shared-unit dots (4)
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, L = int(blockIdx.x);
+    uint64_t* W = a.l1_words;
+    const uint32_t seq = __hip_atomic_load(a.l1_seq, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const int gu = xcd_paired_block(L), s = gu >> 5, p = gu & 31;   // routed gate-up unit (slot s, pair p)
+    const bool down_block = L < kLayer1DownBlocks;
+    const int c = xcd_paired_block(L & (kLayer1DownBlocks - 1));   // down columns 16c..16c+15
+    const bool shared_unit = SHARED && s == 0;
+    uint32_t flags = 0;
+    // gate-up thread (n, g): column n of the pair (0..15 gate, 16..31 up), group g
+    const int n = lane & 31, g = 2 * (wave & 3) + (lane >> 5);
+    const int gcol = n < 16 ? 16 * p + n : kInter + 16 * p + (n - 16);
+    // down thread (decode1_down_kernel's): slot = wave, group dg, chunk half dh, column dn
+    const int lp = lane & 31;
+    const int dg = lane >> 5, dh = (lane >> 4) & 1, dn = lane & 15, dcol = 16 * c + dn;
+
+    // ---- loads with no dependency: router row(s), shared-unit codes, x ----
+    uint4 rv[4], rv2[4], xv[4];
+    if (ROUTER && wave == 8) {
+        const uint16_t* wrow = a.router_w + size_t(L) * kHidden;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            rv[i] = *reinterpret_cast<const uint4*>(wrow + (i * 64 + lane) * 8);
+            xv[i] = *reinterpret_cast<const uint4*>(a.x + (i * 64 + lane) * 8);
+        }
+        if (SHARED && L == 0) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) rv2[i] = *reinterpret_cast<const uint4*>(a.shared_gate_w + (i * 64 + lane) * 8);
+        }
+    }
+    uint32_t ws[32], wd[16], mws = 0, mwd = 0;
+    if (shared_unit && wave < 4) {
+        const BankView bv = bank_view(true);
+        const uint32_t* wp = a.s13_codes + bv.word(gcol, g, 8);
+#pragma unroll
+        for (int j = 0; j < 32; ++j) ws[j] = wp[j * bv.stride()];
+        mws = a.s13_meta[bv.meta(gcol, g, 8)];
+    }
+    const int job = 2 * (wave - 4) + (lane >> 5);
+    uint4 raw{};
+    if (wave >= 4 && wave < 8) raw = *reinterpret_cast<const uint4*>(a.x + job * kGroup + lp * 8);
+    if (tid == 0) {
+        lsync[0] = 0;
+        lsync[1] = 0;
+    }
+    __syncthreads();
+    // ---- router row(s) in the declared order of decode1_route_kernel, published at once ----
+    if (ROUTER && wave == 8) {
+        auto row = [&](const uint4 (&wv)[4]) {
+            float acc = 0.f;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const uint32_t xw[4] = {xv[i].x, xv[i].y, xv[i].z, xv[i].w};
+                const uint32_t ww[4] = {wv[i].x, wv[i].y, wv[i].z, wv[i].w};
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    acc = __builtin_fmaf(bf16_bits_to_f32(xw[j] & 0xffffu), bf16_bits_to_f32(ww[j] & 0xffffu), acc);
+                    acc = __builtin_fmaf(bf16_bits_to_f32(xw[j] >> 16), bf16_bits_to_f32(ww[j] >> 16), acc);
+                }
+            }
+            return wave_butterfly_sum(acc);
+        };
+        float v = row(rv);
+        if (a.bias) v = v + a.bias[L];
+        if (lane == 0) l1_put(W, kLayer1Spread * L, seq, __float_as_uint(v));
+        if (SHARED && L == 0) {
+            const float v2 = row(rv2);
+            if (lane == 0) l1_put(W, kLayer1Spread * kExperts, seq, __float_as_uint(v2));
+        }
+    }
+    int id_in = -1;
+    float w_in = 0.f;
+    uint32_t shared_logit_bits = 0;
+    if (!ROUTER && wave == 4) {
+        id_in = a.ids_in[lane & 7];
+        w_in = a.reduce_w[lane & 7];
+        if (SHARED) shared_logit_bits = a.shared_logit[0];
+    }
+    // gate-up dots of one unit from codes in registers, into lterm[u]
+    auto gate_dots = [&](const uint32_t (&wr)[32], uint32_t mw, int u) {
+        const uint4* ab = reinterpret_cast<const uint4*>(&lx[g * 64]);
+        int dot = 0;
+#pragma unroll
+        for (int c4 = 0; c4 < 16; ++c4) {
+            const uint4 av = ab[c4];
+            dot = dot4(code_even(wr[2 * c4]), int(av.x), dot);
+            dot = dot4(code_odd(wr[2 * c4]), int(av.y), dot);
+            dot = dot4(code_even(wr[2 * c4 + 1]), int(av.z), dot);
+            dot = dot4(code_odd(wr[2 * c4 + 1]), int(av.w), dot);
+        }
+        lterm[u][g][n] = tree_term(dot, lxa[g], lxs[g], mw);
+    };
+    // gate-up epilogue of one unit on one wave (decode1_gateup_kernel's wave
+    // 0), then the 16 middle values are published
+    auto gate_epilogue = [&](int u, int slot, bool table) {
+        // lane c < 32 sums column c over the groups in ascending order (gate
+        // columns 0..15, up 16..31); lane l < 16 takes up from lane l + 16
+        float v = 0.f;
+#pragma unroll
+        for (int gg = 0; gg < 8; ++gg) v = v + lterm[u][gg][lane & 31];
+        float vg = v, vu = xor_perm_f<16>(v);
+        float mid;
+        uint32_t f = 0;
+        if (table) {
+            vg = bf16_round(vg);
+            vu = bf16_round(vu);
+            if (!isfinite(vg) || !isfinite(vu)) f |= kFlagNonfiniteProjection;
+            mid = bf16_round(a.silu_table[__float_as_uint(vg) >> 16] * vu);
+        } else {
+            if (!isfinite(vg) || !isfinite(vu)) f |= kFlagNonfiniteProjection;
+            mid = silu_portable(vg) * vu;
+        }
+        if (!isfinite(mid)) f |= kFlagNonfiniteMiddle | kFlagNonfiniteInput;
+        mid = butterfly_lane<1>(mid);
+        mid = butterfly_lane<2>(mid);
+        mid = butterfly_lane<4>(mid);
+        mid = butterfly_lane<8>(mid);
+        if (lane < 16) {
+            l1_put(W, kLayer1Middle + slot * kInter + p * 16 + lane, seq, __float_as_uint(mid));
+            flags |= f;
+        }
+    };
+    // ---- quantised gate input (decode1_route_kernel's second part) ----
+    if (wave >= 4 && wave < 8) {
+        bool live = true;
+        if (!ROUTER && !SHARED) {
+            live = false;
+#pragma unroll
+            for (int j = 0; j < kTop; ++j) {
+                const int id = a.ids_in[j];
+                live |= id >= 0 && id < kExperts;
+            }
+        }
+        const uint32_t rw[4] = {raw.x, raw.y, raw.z, raw.w};
+        float v[8];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            v[2 * e] = bf16_bits_to_f32(rw[e] & 0xffffu);
+            v[2 * e + 1] = bf16_bits_to_f32(rw[e] >> 16);
+        }
+        if (live) {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) if (!isfinite(v[e])) flags |= kFlagNonfiniteInput;
+            h128_half(v);
+        } else {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) v[e] = 0.f;
+        }
+        uint32_t w2[2];
+        uint16_t sb;
+        int sum;
+        quantize_half_fast<QMAX>(v, w2, sb, sum, flags, kFlagNonfiniteInput | kFlagInvalidActivation,
+                                 kFlagInvalidActivation);
+        // only block 0 reports the input's flags (every block sees the same x)
+        if (L != 0) flags = 0;
+        lx[job * 64 + 2 * lp] = w2[0];
+        lx[job * 64 + 2 * lp + 1] = w2[1];
+        if (lp == 0) {
+            const float sc = f16_bits_to_f32(sb);
+            lxa[job] = sc;
+            lxs[job] = sc * float(sum);
+        }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+        if (lane == 0) __hip_atomic_fetch_add(&lsync[0], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    }
+    // ---- shared unit (blocks of slot 0) as soon as x is quantised: its
+    // middle row leaves long before the routed ones ----
+    if (shared_unit && wave < 4) {
+        lds_wait(&lsync[0], 4u);
+        gate_dots(ws, mws, 0);
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+        if (lane == 0) __hip_atomic_fetch_add(&lsync[1], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+        if (wave == 1) {
+            lds_wait(&lsync[1], 4u);
+            gate_epilogue(0, kTop, true);
+        }
+    }
+    // ---- routing on wave 4 ----
+    if (wave == 4) {
+        if (ROUTER) {
+            // the 256 expert logits, and the shared gate logit when there is one
+            constexpr int NW = SHARED ? 5 : 4;
+            uint32_t idx[NW], got[NW];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) idx[i] = uint32_t(kLayer1Spread * (lane + 64 * i));
+            if constexpr (SHARED) idx[NW - 1] = kLayer1Spread * kExperts;
+            if (!l1_wait<NW, 0>(W, idx, seq, got)) flags |= kFlagHandoffTimeout;
+            float lg[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) lg[i] = __uint_as_float(got[i]);
+            uint32_t k[4];
+            softmax_keys(lg, k);
+            top8_rank_lds(k, s_cand, s_sel);
+            float tot = 0.f;
+#pragma unroll
+            for (int j = 0; j < kTop; ++j) tot = tot + __uint_as_float(s_sel[j].x);
+            if (lane < kTop) {
+                const uint2 pick = s_sel[lane];
+                const float wgt = fdiv_rn(__uint_as_float(pick.x), tot);
+                lbank[lane] = int(pick.y);
+                lw8[lane] = wgt;
+                if (L == 0) {
+                    a.topk_w[lane] = wgt;
+                    a.topk_ids[lane] = int(pick.y);
+                }
+            }
+            if constexpr (SHARED) {
+                const uint16_t sl = f32_to_bf16_bits(__uint_as_float(got[NW - 1]));
+                if (lane == 0) lshared_logit = sl;
+                if (L == 0 && lane == 0) a.shared_logit[0] = sl;
+            }
+        } else {
+            if (lane < kTop) {
+                lbank[lane] = (id_in >= 0 && id_in < kExperts) ? id_in : -1;
+                lw8[lane] = w_in;
+            }
+            if (lane == 0) lshared_logit = shared_logit_bits;
+        }
+        if (lane == kTop) lbank[kTop] = SHARED ? kShared : -1;
+    }
+    // every wave has its sequence number before the arrival word leaves
+    if (lane == 0) lseq[wave] = seq;
+    __syncthreads();
+    if (tid == 0) l1_put(W, kLayer1Arrive + kLayer1Spread * L, seq, lseq[0]);
+
+    // the down codes of slot `wave`
+    const int dbank = down_block ? lbank[wave] : -1;
+    auto load_down = [&]() {
+        const int lb = dbank >= 0 ? dbank : 0;
+        const bool sh = lb == kShared;
+        const BankView bv = bank_view(sh);
+        const uint32_t* wp = (sh ? a.s2_codes : a.w2_codes + size_t(lb) * kDownBankWords) + bv.word(dcol, dg, 2) +
+                             16 * dh * bv.stride();
+#pragma unroll
+        for (int j = 0; j < 16; ++j) wd[j] = wp[j * bv.stride()];
+        mwd = (sh ? a.s2_meta : a.w2_meta + size_t(lb) * kDownBankMeta)[bv.meta(dcol, dg, 2)];
+    };
+
+    // ---- routed gate-up (waves 0-3); down codes right behind ----
+    int bank = -1;
+    if (wave < 4) {
+        bank = lbank[s];
+        if (!ROUTER && bank < 0) {
+            const int id = a.ids_in[s];
+            if (id != -1 && p == 0 && tid == 0) flags |= kFlagInvalidExpert;
+        }
+        const int lb = bank >= 0 ? bank : 0;
+        const BankView bv = bank_view(false);
+        const uint32_t* wp = a.w13_codes + size_t(lb) * kGateBankWords + bv.word(gcol, g, 8);
+        uint32_t wr[32];
+#pragma unroll
+        for (int j = 0; j < 32; ++j) wr[j] = wp[j * bv.stride()];
+        const uint32_t mw = a.w13_meta[size_t(lb) * kGateBankMeta + bv.meta(gcol, g, 8)];
+        // the routed dots always run (an empty slot's are not used), so no
+        // load is left pending past this branch
+        gate_dots(wr, mw, 1);
+    }
+    // down codes behind the gate-up stream (they are needed only after the
+    // middle hand-off); one load site for every wave keeps them in the same
+    // registers, and nothing waits for them before the dots
+    if (down_block) load_down();
+    uint32_t gate_raw = 0;                  // bf16 sigmoid gate, used by the last step only
+    if (SHARED && down_block && wave == 0) gate_raw = a.sigmoid_table[lshared_logit];
+    __syncthreads();
+    if (wave == 0 && bank >= 0) gate_epilogue(1, s, false);
+    if (!down_block) {
+        flag_or(a.sticky, flags);
+        return;
+    }
+
+    // ---- middle row of slot `wave`: wait, H128 tail, A8 (decode1_down_kernel) ----
+    const int gm = lane >> 5, kb = strided_base(lp);
+    uint64_t arrival[4] = {0, 0, 0, 0};
+    if (dbank >= 0) {
+        uint32_t idx[8], val[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) idx[j] = uint32_t(kLayer1Middle + wave * kInter + gm * kGroup + kb + 16 * j);
+        if (!l1_wait<8, 1>(W, idx, seq, val)) flags |= kFlagHandoffTimeout;
+        if (L == 0 && wave == 0) {
+            // every block published its arrival long ago: read the words
+            // now, check them at the end
+#pragma unroll
+            for (int i = 0; i < 4; ++i) arrival[i] = l1_get(W, uint32_t(kLayer1Arrive + kLayer1Spread * (lane + 64 * i)));
+        }
+        float v[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) v[j] = __uint_as_float(val[j]);
+        h128_tail_strided(v);
+        int qv[8];
+        uint16_t sb;
+        int sum;
+        quantize_strided<QMAX>(v, qv, sb, sum, flags, kFlagNonfiniteInput | kFlagInvalidActivation,
+                               kFlagInvalidActivation);
+        uint8_t* lb = reinterpret_cast<uint8_t*>(&lm[(2 * wave + gm) * 64]);
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+            lb[4 * (2 * ((kb >> 3) + 2 * j) + (kb & 1)) + ((kb & 7) >> 1)] = uint8_t(qv[j]);
+        if (lp == 0) {
+            const float sc = f16_bits_to_f32(sb);
+            lma[2 * wave + gm] = sc;
+            lms[2 * wave + gm] = sc * float(sum);
+        }
+    }
+    // the quantised row is this wave's own: no block barrier before its dots
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    // ---- down dots: the two chunk halves joined exactly, then the two-group tree ----
+    float term = 0.f;
+    if (dbank >= 0) {
+        const uint4* ab = reinterpret_cast<const uint4*>(&lm[(2 * wave + dg) * 64 + 32 * dh]);
+        int dot = 0;
+#pragma unroll
+        for (int c4 = 0; c4 < 8; ++c4) {
+            const uint4 av = ab[c4];
+            dot = dot4(code_even(wd[2 * c4]), int(av.x), dot);
+            dot = dot4(code_odd(wd[2 * c4]), int(av.y), dot);
+            dot = dot4(code_even(wd[2 * c4 + 1]), int(av.z), dot);
+            dot = dot4(code_odd(wd[2 * c4 + 1]), int(av.w), dot);
+        }
+        dot += xor_perm_i<16>(dot);
+        term = tree_term(dot, lma[2 * wave + dg], lms[2 * wave + dg], mwd);
+    }
+    const float term1 = xor_perm_f<32>(term);
+    if (dbank >= 0 && lane < 16) {
+        float v = 0.f;
+        v = v + term;
+        v = v + term1;
+        if (wave == kTop) v = bf16_round(v);
+        if (!isfinite(v)) flags |= kFlagNonfiniteProjection;
+        lro[wave][dn] = v;
+    }
+    __syncthreads();
+    if (tid < 16) {
+        const int col = 16 * c + tid;
+        int lb8[kTop];
+        float ro[kTop], w8[kTop];
+#pragma unroll
+        for (int sl = 0; sl < kTop; ++sl) {
+            lb8[sl] = lbank[sl];
+            ro[sl] = lro[sl][tid];
+            w8[sl] = lw8[sl];
+        }
+        float sum = 0.f;
+#pragma unroll
+        for (int sl = 0; sl < kTop; ++sl) {
+            const float t = sum + ro[sl] * w8[sl];
+            sum = lb8[sl] >= 0 ? t : sum;
+        }
+        const uint16_t o = f32_to_bf16_bits(sum);
+        if (!isfinite(sum) || (o & 0x7f80u) == 0x7f80u) flags |= kFlagNonfiniteOutput;
+        if (a.final_f32) a.final_f32[col] = sum;
+        if (a.out) a.out[col] = o;
+        if (SHARED) {
+            asm volatile("" : "+v"(gate_raw));   // keep the gate's load unwaited until here
+            const float gate = bf16_bits_to_f32(gate_raw);
+            const float sv = lro[kTop][tid] * gate;
+            if (!isfinite(sv)) flags |= kFlagNonfiniteOutput;
+            const uint16_t so = f32_to_bf16_bits(sv);
+            if (a.shared_out) a.shared_out[col] = so;
+            if (a.layer_out) a.layer_out[col] = f32_to_bf16_bits(bf16_bits_to_f32(o) + bf16_bits_to_f32(so));
+        }
+    }
+    // ---- block 0 advances the sequence number once every block has arrived ----
+    if (L == 0 && wave == 0) {
+        uint32_t idx[4], val[4];
+        bool ok = true;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            idx[i] = uint32_t(kLayer1Arrive + kLayer1Spread * (lane + 64 * i));
+            ok = ok && uint32_t(arrival[i] >> 32) == l1_tag(seq, idx[i]);
+        }
+        if (__builtin_amdgcn_ballot_w64(!ok) != 0 && !l1_wait<4, 1>(W, idx, seq, val)) flags |= kFlagHandoffTimeout;
+        if (lane == 0) __hip_atomic_store(a.l1_seq, seq + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    flag_or(a.sticky, flags);
+}
+
 template <bool ROUTER, bool SHARED, int QMAX>
 static hipError_t run1(const DecodeArgs& a, hipStream_t s) {
     const int rows = ROUTER ? (SHARED ? kExperts + 1 : kExperts) : 0;
@@ -383,13 +862,44 @@ static hipError_t run1(const DecodeArgs& a, hipStream_t s) {
     return hipGetLastError();
 }
 
+// Whether 256 blocks of the one-launch kernel are resident at once on the
+// current device (checked once per device).
+template <bool ROUTER, bool SHARED, int QMAX>
+static bool layer1_fits() {
+    constexpr int kMaxDevices = 64;
+    static std::atomic<int> state[kMaxDevices];   // 0 unknown, 1 fits, 2 does not
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return false;
+    int st = state[dev].load(std::memory_order_relaxed);
+    if (st == 0) {
+        int per_cu = 0, cus = 0;
+        const bool ok = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, layer1_kernel<ROUTER, SHARED, QMAX>, 576,
+                                                                     0) == hipSuccess &&
+                        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess &&
+                        per_cu * cus >= kLayer1Blocks;
+        st = ok ? 1 : 2;
+        state[dev].store(st, std::memory_order_relaxed);
+    }
+    return st == 1;
+}
+
+std::atomic<int> g_single_token_mode{0};   // 0 automatic, 1 three kernels
+
+template <bool ROUTER, bool SHARED, int QMAX>
+static hipError_t run1_any(const DecodeArgs& a, hipStream_t s) {
+    const int mode = g_single_token_mode.load(std::memory_order_relaxed);
+    if (mode == 1 || !layer1_fits<ROUTER, SHARED, QMAX>()) return run1<ROUTER, SHARED, QMAX>(a, s);
+    timed_launch("layer1", layer1_kernel<ROUTER, SHARED, QMAX>, dim3(kLayer1Blocks), dim3(576), 0, s, a);
+    return hipGetLastError();
+}
+
 hipError_t launch_decode1(const DecodeArgs& a, bool router, bool shared, int qmax, hipStream_t s) {
     if (a.T != 1) return hipErrorInvalidValue;
-    if (router && shared) return run1<true, true, 127>(a, s);
-    if (router) return run1<true, false, 127>(a, s);
-    if (shared) return run1<false, true, 127>(a, s);
-    if (qmax == 127) return run1<false, false, 127>(a, s);
-    return run1<false, false, 7>(a, s);
+    if (router && shared) return run1_any<true, true, 127>(a, s);
+    if (router) return run1_any<true, false, 127>(a, s);
+    if (shared) return run1_any<false, true, 127>(a, s);
+    if (qmax == 127) return run1_any<false, false, 127>(a, s);
+    return run1_any<false, false, 7>(a, s);
 }
 
 }  // namespace ornith

@@ -82,6 +82,7 @@ _PROTOTYPES = {
     'ornith_shared_fixed8_get_layout': ([_INT, C.POINTER(_SZ)], _INT),
     'ornith_shared_fixed8_launch': ([_VP] * 9 + [_SZ] + [_VP] * 2 + [_INT] * 2 + [_VP], _INT),
     'ornith_mi355x_abi_version': ([], _INT),
+    'ornith_mi355x_single_token_path': ([_INT], _INT),
     # dense (include/ornith_dense.h)
     'ornith_dense_g256_abi_version': ([], C.c_uint32),
     'ornith_dense_g256_get_layout': ([_INT] * 4 + [C.POINTER(DenseLayout)], _INT),
@@ -546,6 +547,17 @@ def dense_head(x, codes, meta, workspace, logits, logits_bf16, argmax, flags, ca
     check(lib().ornith_dense_g256_head_launch(ptr(x), ptr(codes), ptr(meta), ptr(workspace), workspace.numel(),
                                               ptr(logits), ptr(logits_bf16), ptr(argmax), ptr(flags), x.shape[0],
                                               capacity, codes.shape[0] * 32, stream(x)), 'G256 head')
+
+
+def single_token_path(path=None, tile=32):
+    """Which kernels run single-token (T == 1) routed and layer calls, for
+    the process: 0 the one-launch kernel wherever its grid is resident at
+    once, 1 the three kernels; None only queries.  Returns the previous
+    setting.  Results are identical either way."""
+    prev = lib(tile).ornith_mi355x_single_token_path(-1 if path is None else int(path))
+    if prev < 0:
+        raise ValueError(f'single-token path must be 0 or 1, got {path}')
+    return prev
 
 
 class KernelTimer:

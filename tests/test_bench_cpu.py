@@ -24,6 +24,12 @@ def test_single_token_algorithmic_bytes():
     assert unit == 'GB/s'
     assert gateup == 9 * 1_081_344 + 2048 + 9 * 512 * 4 == 9_752_576
     assert down == 9 * 540_672 + 9 * 512 * 4 + 2048 * 2 == 4_888_576
+    # the one-launch single-token layer: every byte the layer must read or
+    # write once (9 expert banks, router + shared gate row, x in, out)
+    _, whole, _, unit = bench.kernel_cost('layer1', 1, 8)
+    assert unit == 'GB/s'
+    assert whole == 9 * (1_081_344 + 540_672) + 256 * 2048 * 2 + 2048 * 2 + 2048 * 2 * 2 == 15_659_008
+    assert whole == bench.algorithmic(1, 8)[0]
     # prefill matrix-core work: 2 ops per MAC over 9 routes per token
     _, ops, _, unit = bench.kernel_cost('gateup_mfma', 1120, 96)
     assert unit == 'TFLOP/s' and ops == 2 * 9 * 1120 * 1024 * 2048
