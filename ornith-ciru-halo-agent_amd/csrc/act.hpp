@@ -16,7 +16,7 @@ __device__ __forceinline__ void act_bf16_block(int block, const uint16_t* __rest
                                                uint32_t* __restrict__ words, uint16_t* __restrict__ scales,
                                                int32_t* __restrict__ sums, uint32_t* sticky, uint32_t flag_input,
                                                uint32_t flag_act) {
-    const int wave = (block * 4) + (threadIdx.x >> 6);
+    const int wave = (block * 4) + ((threadIdx.x >> 6) & 3);     // 4 waves per block index
     const int lane = threadIdx.x & 63, l = lane & 15;
     const int total = rows * groups;
     const int g = 4 * wave + (lane >> 4);

@@ -18,25 +18,6 @@
 
 namespace ornith {
 
-// ---------------------------------------------------------------------------
-// Router logits.  The declared butterfly is a balanced tree over the 64 lane
-// partials (every pair sum is formed once and fp32 addition commutes), so
-//   logit = ((S0 + S1) + (S2 + S3)) + bias,
-// Sq = balanced-tree sum of partials 16q..16q+15, and partial l is the fma
-// chain over chunks l, l+64, l+128, l+192.
-// Block = 4 waves on a tile of 32 router rows x 32 tokens; wave q forms Sq.
-// A thread owns 4 rows x 4 tokens.  At step s every wave accumulates partial
-// 16q+s of its 16 outputs from fp32 operands staged in LDS (the block stages
-// the 16 chunks of the step; the next step's global loads are in flight
-// meanwhile).  Two steps make a pair sum, which is folded into a
-// binary-counter stack of quad / octet sums.  Sq meet in LDS at the end.
-// Blocks with blockIdx.x == 8 form the shared-expert gate row (row 256), one
-// token per wave at a time, with the lane-partial butterfly itself.
-// ---------------------------------------------------------------------------
-constexpr int kRouterTile = 32;
-constexpr int kRouterIStride = 8 * kRouterTile + 4;       // [i][j][row] with a 4-float pad per i
-constexpr int kRouterWaveStride = 4 * kRouterIStride;
-
 __device__ __forceinline__ void bf16x8_to_f32(const uint4 v, float f[8]) {
     const uint32_t u[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
@@ -46,274 +27,192 @@ __device__ __forceinline__ void bf16x8_to_f32(const uint4 v, float f[8]) {
     }
 }
 
-__global__ __launch_bounds__(256) void router_kernel(const uint16_t* __restrict__ x, int64_t stride, int T,
-                                                     const uint16_t* __restrict__ w,
-                                                     const uint16_t* __restrict__ shared_w,
-                                                     const float* __restrict__ bias, float* __restrict__ logits,
-                                                     int64_t logit_stride) {
-    __shared__ __align__(16) float Wl[4 * kRouterWaveStride];
-    __shared__ __align__(16) float Xl[4 * kRouterWaveStride];
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int t0 = blockIdx.y * kRouterTile;
-
-    if (blockIdx.x == kExperts / kRouterTile) {
-        for (int t = t0 + wave; t < min(T, t0 + kRouterTile); t += 4) {
-            float acc = 0.f;
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                float xf[8], wf[8];
-                bf16x8_to_f32(*reinterpret_cast<const uint4*>(x + t * stride + (lane + 64 * i) * 8), xf);
-                bf16x8_to_f32(*reinterpret_cast<const uint4*>(shared_w + (lane + 64 * i) * 8), wf);
-#pragma unroll
-                for (int j = 0; j < 8; ++j) acc = __builtin_fmaf(xf[j], wf[j], acc);
-            }
-            const float v = wave_butterfly_sum(acc);
-            if (lane == 0) logits[size_t(t) * logit_stride + kExperts] = v;
-        }
-        return;
-    }
-
-    const int r0 = blockIdx.x * kRouterTile;
-    // staging: (row-or-token m, wave q, chunk i) for p = tid + 256e
-    uint4 pw[2], px[2];
-    const uint16_t* wp[2];
-    const uint16_t* xp[2];
-    int soff[2];
-#pragma unroll
-    for (int e = 0; e < 2; ++e) {
-        const int p = tid + 256 * e, m = p & 31, qi = p >> 5, q = qi >> 2, i = qi & 3;
-        const int k0 = (16 * q + 64 * i) * 8;               // chunk 16q + s + 64i starts at k0 + 8s
-        wp[e] = w + size_t(r0 + m) * kHidden + k0;
-        xp[e] = x + min(t0 + m, T - 1) * stride + k0;
-        soff[e] = q * kRouterWaveStride + i * kRouterIStride + m;
-    }
-    auto load_step = [&](int s) {
-#pragma unroll
-        for (int e = 0; e < 2; ++e) {
-            pw[e] = *reinterpret_cast<const uint4*>(wp[e] + 8 * s);
-            px[e] = *reinterpret_cast<const uint4*>(xp[e] + 8 * s);
-        }
-    };
-    auto store_step = [&]() {
-#pragma unroll
-        for (int e = 0; e < 2; ++e) {
-            float fw[8], fx[8];
-            bf16x8_to_f32(pw[e], fw);
-            bf16x8_to_f32(px[e], fx);
-#pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                Wl[soff[e] + j * kRouterTile] = fw[j];
-                Xl[soff[e] + j * kRouterTile] = fx[j];
-            }
-        }
-    };
-
-    const int rg = lane & 7, tg = lane >> 3;
-    const float* wbase = Wl + wave * kRouterWaveStride + 4 * rg;
-    const float* xbase = Xl + wave * kRouterWaveStride + 4 * tg;
-    float quad[16], octet[16], half16[16];
-    // one partial (32 fma per output, chunk-major) of all 16 outputs
-    auto partial = [&](float acc[16]) {
-#pragma unroll
-        for (int o = 0; o < 16; ++o) acc[o] = 0.f;
-#pragma unroll 1
-        for (int i = 0; i < 4; ++i)
-#pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                const float4 wv = *reinterpret_cast<const float4*>(wbase + i * kRouterIStride + j * kRouterTile);
-                const float4 xv = *reinterpret_cast<const float4*>(xbase + i * kRouterIStride + j * kRouterTile);
-                const float wr[4] = {wv.x, wv.y, wv.z, wv.w}, xr[4] = {xv.x, xv.y, xv.z, xv.w};
-#pragma unroll
-                for (int a = 0; a < 4; ++a)
-#pragma unroll
-                    for (int b = 0; b < 4; ++b) acc[4 * a + b] = __builtin_fmaf(xr[b], wr[a], acc[4 * a + b]);
-            }
-    };
-
-    // -0 + v == v exactly for every v, so the 16-sum can start from -0
-#pragma unroll
-    for (int o = 0; o < 16; ++o) { quad[o] = 0.f; octet[o] = 0.f; half16[o] = -0.f; }
-    load_step(0);
-#pragma unroll 1
-    for (int sp = 0; sp < 8; ++sp) {
-        float acc0[16], acc1[16];
-        __syncthreads();
-        store_step();
-        __syncthreads();
-        load_step(2 * sp + 1);
-        partial(acc0);
-        __syncthreads();
-        store_step();
-        __syncthreads();
-        if (sp < 7) load_step(2 * sp + 2);
-        partial(acc1);
-        // pair sum of partials 2sp, 2sp+1 folded into the quad / octet / 16 stack
-        // (sp is uniform: the selects pick whole stack levels)
-        const bool odd = sp & 1, odd2 = sp & 2;
-#pragma unroll
-        for (int o = 0; o < 16; ++o) {
-            const float pair = acc0[o] + acc1[o];
-            const float q4 = quad[o] + pair;            // used when sp is odd
-            const float o8 = octet[o] + q4;             // used when sp % 4 == 3
-            quad[o] = odd ? quad[o] : pair;
-            octet[o] = (odd && !odd2) ? q4 : octet[o];
-            half16[o] = (odd && odd2) ? half16[o] + o8 : half16[o];
-        }
-    }
-    // Sq of this wave -> LDS, then ((S0 + S1) + (S2 + S3)) + bias
-    __syncthreads();
-    float* Sl = Wl;                                     // [q][token][row], 4 x 32 x 32
-#pragma unroll
-    for (int a = 0; a < 4; ++a)
-#pragma unroll
-        for (int b = 0; b < 4; ++b) Sl[wave * 1024 + (4 * tg + b) * 32 + 4 * rg + a] = half16[4 * a + b];
-    __syncthreads();
-#pragma unroll
-    for (int m = 0; m < 4; ++m) {
-        const int o = tid + 256 * m, row = o & 31, tok = o >> 5;
-        const float v = (Sl[o] + Sl[1024 + o]) + (Sl[2048 + o] + Sl[3072 + o]);
-        if (t0 + tok < T) logits[size_t(t0 + tok) * logit_stride + r0 + row] = bias ? v + bias[r0 + row] : v;
-    }
-}
-
-// Router logits for large T, lane = token (same declared order as above).
-// Block = 64 tokens x 8 router rows; wave q forms Sq (partials 16q..16q+15)
-// of all 512 outputs, one token per lane.  The block's 8 weight rows are
-// staged once as fp32 in LDS and read by broadcast (every lane of a wave
-// reads the same address).  A lane walks its token's chunks in memory order,
-// 16q..16q+15 then +64, +128, +192 (one full 128-byte line per 8 chunks),
-// updating the 16 partial chains at once; the 16 partials are then summed in
-// the balanced tree.  Blocks are laid out so that the row groups of one token
-// group run on one XCD (workgroups go to the 8 XCDs round-robin) and share
-// its L2.
-constexpr int kRtRows = 8, kRtTokens = 64;
-constexpr int kRtBlocksPerCu = 2;                    // occupancy the tile kernels are built for
 constexpr int kPermTokens = 16;                      // tokens per permutation count / scatter block
 constexpr int kPermRoutes = kPermTokens * kTop;      // routed routes per block
 
-__device__ __forceinline__ void router_tokens_block(int blk, const uint16_t* __restrict__ x, int64_t stride, int T,
-                                                    const uint16_t* __restrict__ w,
-                                                    const uint16_t* __restrict__ shared_w,
-                                                    const float* __restrict__ bias, float* __restrict__ logits,
-                                                    int64_t logit_stride, int nrows, int ntg) {
-    __shared__ __align__(16) float sW[kRtRows][kHidden];       // fp32 weights of the block's rows
-    __shared__ __align__(16) float sS[4][kRtRows][kRtTokens];  // Sq per wave
-    const int ngroups = (nrows + kRtRows - 1) / kRtRows;
+// ---------------------------------------------------------------------------
+// Router logits for large T on the matrix cores (declared order above).  A
+// K = 1 fp32 matrix-core step d = RN(a * b + c) equals v_fma_f32 bit for bit
+// (measured for v_mfma_f32_32x32x1_2b_f32 on every operand class: normal,
+// denormal, zero, inf, NaN), and a product of two bf16 values is exact in
+// fp32, so one step per k advances the fma chains of two partials (its two
+// blocks) for a whole 32-expert x 32-token tile.  The 32 x 32 form does
+// twice the multiply-adds per converted operand of the 16 x 16 one; the
+// bf16 -> fp32 conversions are vector-ALU work that the fp32 matrix steps
+// wait for, so that halves their cost.
+// The butterfly is a balanced tree over the 64 lane partials (every pair sum
+// is formed once and fp32 addition commutes).  Block = 16 waves on one tile;
+// wave q carries partials 4q..4q+3 (chunk p + 64j, j = quarter of K, k
+// ascending) in two steps per k (blocks b = partials 4q + b and 4q + 2 + b)
+// and sums them as (P0 + P1) + (P2 + P3); the 16 wave sums meet in LDS in
+// the balanced 16-leaf tree.
+// Lane layout of a step: block b takes expert row i and token row i from lane
+// 32 b + i; its output (i, j) lands in lane 32 ((i / 4) % 2) + j, register
+// 16 b + 4 (i / 8) + i % 4.
+// The shared-expert gate row (row 256) runs on the vector ALUs beside the
+// tiles: the eight expert-group blocks of a token group each take 4 of its
+// tokens, lane p forming partial p from the staged rows, then the butterfly.
+// ---------------------------------------------------------------------------
+typedef float f32x32 __attribute__((ext_vector_type(32)));
+typedef __attribute__((address_space(3))) void lds_void;
+constexpr int kRmTile = 32, kRmWaves = 16;
+constexpr int kRmGroups = kExperts / kRmTile;              // expert groups (tiles) per token group
+constexpr int kRmQuarter = kHidden / 4;                    // k per staged quarter
+constexpr int kRmRowBytes = 2 * kRmQuarter + 16;           // staged row + a 16-byte pad (conflict-free columns)
+
+__device__ __forceinline__ void router_mfma_block(int blk, const uint16_t* __restrict__ x, int64_t stride, int T,
+                                                  const uint16_t* __restrict__ w,
+                                                  const uint16_t* __restrict__ shared_w,
+                                                  const float* __restrict__ bias, float* __restrict__ logits,
+                                                  int64_t logit_stride, int ntg) {
+    // two buffers (separate arrays, so the compiler sees that loads into one
+    // do not alias reads of the other) of one K quarter of the tile's 32
+    // expert rows (rows 0..31) and 32 token rows (rows 32..63), bf16, rows
+    // kRmRowBytes apart; the shared-expert row whole; the Sq exchange reuses
+    // buffer 0
+    constexpr int kBuf = 2 * kRmTile * kRmRowBytes;
+    __shared__ __align__(16) uint8_t lds0[kBuf];
+    __shared__ __align__(16) uint8_t lds1[kBuf];
+    __shared__ __align__(16) uint8_t lshared[2 * kHidden];
+    static_assert(kRmWaves * kRmTile * kRmTile * 4 <= kBuf, "Sq exchange fits buffer 0");
+    // the expert groups of one token group run on one XCD (its x rows stay in that L2)
     const int idx = blk >> 3;
-    const int tg = 8 * (idx / ngroups) + (blk & 7), rg = idx % ngroups;
+    const int tg = 8 * (idx / kRmGroups) + (blk & 7), eg = idx % kRmGroups;
     if (tg >= ntg) return;
-    const int tid = threadIdx.x, lane = tid & 63, q = tid >> 6;
-    const int e0 = rg * kRtRows;
-
-    // this lane's token (tokens past T repeat the last one; never stored)
-    const uint16_t* xrow = x + size_t(min(tg * kRtTokens + lane, T - 1)) * stride + 8 * (16 * q);
-    // chunk s (0..15) of segment j: 16q + s + 64j; a line of 8 chunks in registers,
-    // each slot refilled with the next line's chunk once converted
-    u32x4 xv[8];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int q = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave-uniform: row pointers stay scalar
+    const int b = lane >> 5, i = lane & 31;
+    const int e0 = eg * kRmTile, t0 = tg * kRmTile;
+    const bool has_shared = shared_w != nullptr;
+    // staging straight into LDS: wave q loads rows q, q + 16 (experts) and
+    // q + 32, q + 48 (tokens; past the end they repeat the last one), lane =
+    // 16-byte chunk of the quarter
+    const uint16_t* src[4];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) xv[i] = *reinterpret_cast<const u32x4*>(xrow + 8 * i);
-
-    // stage the block's weight rows (rows past nrows repeat the last one; never stored)
-#pragma unroll
-    for (int i = 0; i < kRtRows; ++i) {
-        const int p = tid + 256 * i, r = p >> 8, c = p & 255;
-        const int e = min(e0 + r, nrows - 1);
-        const uint16_t* row = e < kExperts ? w + size_t(e) * kHidden : shared_w;
-        const uint4 v = *reinterpret_cast<const uint4*>(row + 8 * c);
-        float f[8];
-        bf16x8_to_f32(v, f);
-        *reinterpret_cast<float4*>(&sW[r][8 * c]) = float4{f[0], f[1], f[2], f[3]};
-        *reinterpret_cast<float4*>(&sW[r][8 * c + 4]) = float4{f[4], f[5], f[6], f[7]};
+    for (int n = 0; n < 4; ++n) {
+        const int r = q + 16 * n;
+        src[n] = n < 2 ? w + size_t(e0 + r) * kHidden : x + size_t(min(t0 + r - kRmTile, T - 1)) * stride;
     }
-    __syncthreads();
-
-    // unit u = (j, s, r), u = 16 kRtRows j + kRtRows s + r: row r of chunk
-    // 16q + s + 64j.  The broadcast weight reads run two units ahead through a
-    // 3-slot ring.
-    constexpr int kUnits = 64 * kRtRows;
-    auto wread = [&](int u, float (&dst)[8]) __attribute__((always_inline)) {
-        const int j = u / (16 * kRtRows), sr = u % (16 * kRtRows), s = sr / kRtRows, r = sr % kRtRows;
-        const int c = 16 * q + s + 64 * j;
-        const float4 w0 = *reinterpret_cast<const float4*>(&sW[r][8 * c]);
-        const float4 w1 = *reinterpret_cast<const float4*>(&sW[r][8 * c + 4]);
-        dst[0] = w0.x; dst[1] = w0.y; dst[2] = w0.z; dst[3] = w0.w;
-        dst[4] = w1.x; dst[5] = w1.y; dst[6] = w1.z; dst[7] = w1.w;
+    auto stage = [&](int jq, uint8_t* dst) __attribute__((always_inline)) {
+#pragma unroll
+        for (int n = 0; n < 4; ++n)
+            __builtin_amdgcn_global_load_lds(src[n] + kRmQuarter * jq + 8 * lane,
+                                             (lds_void*)(dst + (q + 16 * n) * kRmRowBytes), 16, 0, 0);
     };
-    // acc[s][r]: partial 16q + s of row r, fma chain over chunks j = 0..3, k ascending
-    float acc[16][kRtRows];
+    // this lane's operands: expert row i and token row i, chunk 4q + b (first
+    // step) and 4q + 2 + b (second step) of the quarter
+    const int abase = i * kRmRowBytes + 16 * (4 * q + b), bbase = (kRmTile + i) * kRmRowBytes + 16 * (4 * q + b);
+    // shared row: waves eg and eg + 8 of block eg take token rows q and
+    // 16 + q (4 tokens per block), lane = partial
+    const bool mine = has_shared && (q & 7) == eg;
+    float sacc[2] = {0.f, 0.f};
+    f32x32 acc[2] = {f32x32{}, f32x32{}};
+    stage(0, lds0);
+    if (has_shared && q < 4)
+        __builtin_amdgcn_global_load_lds(shared_w + kRmQuarter * q + 8 * lane, (lds_void*)(lshared + 1024 * q), 16, 0,
+                                         0);
+    __syncthreads();
 #pragma unroll
-    for (int s = 0; s < 16; ++s)
+    for (int jq = 0; jq < 4; ++jq) {
+        const uint8_t* sb = jq & 1 ? lds1 : lds0;
+        if (jq < 3) stage(jq + 1, jq & 1 ? lds0 : lds1);  // its last readers passed the previous barrier
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-        for (int r = 0; r < kRtRows; ++r) acc[s][r] = 0.f;
-    float wr[3][8], xf[8];
-    wread(0, wr[0]);
-    wread(1, wr[1]);
+        for (int s = 0; s < 2; ++s) {
+            const uint4 wv = *reinterpret_cast<const uint4*>(sb + abase + 32 * s);
+            const uint4 xv = *reinterpret_cast<const uint4*>(sb + bbase + 32 * s);
+            const uint32_t uw[4] = {wv.x, wv.y, wv.z, wv.w};
+            const uint32_t ux[4] = {xv.x, xv.y, xv.z, xv.w};
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
-#pragma unroll
-        for (int s = 0; s < 16; ++s)
-#pragma unroll
-            for (int r = 0; r < kRtRows; ++r) {
-                const int u = 16 * kRtRows * j + kRtRows * s + r, i = s & 7;
-                if (u + 2 < kUnits) wread(u + 2, wr[(u + 2) % 3]);
-                if (r == 0) {
-                    bf16x8_to_f32(uint4{xv[i].x, xv[i].y, xv[i].z, xv[i].w}, xf);
-                    // next line's chunk i: same segment's second half, or the next segment's first
-                    const int nc = s < 8 ? 64 * j + 8 + i : 64 * (j + 1) + i;
-                    if (s < 8 || j < 3) xv[i] = *reinterpret_cast<const u32x4*>(xrow + 8 * nc);
-                }
-#pragma unroll
-                for (int k = 0; k < 8; ++k) acc[s][r] = __builtin_fmaf(xf[k], wr[u % 3][k], acc[s][r]);
+            for (int h = 0; h < 4; ++h) {
+                acc[s] = __builtin_amdgcn_mfma_f32_32x32x1f32(__uint_as_float(uw[h] << 16),
+                                                              __uint_as_float(ux[h] << 16), acc[s], 0, 0, 0);
+                acc[s] = __builtin_amdgcn_mfma_f32_32x32x1f32(__uint_as_float(uw[h] & 0xffff0000u),
+                                                              __uint_as_float(ux[h] & 0xffff0000u), acc[s], 0, 0, 0);
             }
-    // Sq = balanced tree over the 16 partials
+        }
+        if (mine) {
+            float wf[8], xf[8];
+            bf16x8_to_f32(*reinterpret_cast<const uint4*>(lshared + 2 * kRmQuarter * jq + 16 * lane), wf);
 #pragma unroll
-    for (int r = 0; r < kRtRows; ++r) {
-        float p8[8], p4[4], p2[2];
+            for (int u = 0; u < 2; ++u) {
+                bf16x8_to_f32(*reinterpret_cast<const uint4*>(sb + (kRmTile + q + 16 * u) * kRmRowBytes + 16 * lane), xf);
 #pragma unroll
-        for (int i = 0; i < 8; ++i) p8[i] = acc[2 * i][r] + acc[2 * i + 1][r];
+                for (int k = 0; k < 8; ++k) sacc[u] = __builtin_fmaf(xf[k], wf[k], sacc[u]);
+            }
+        }
+        __syncthreads();                                  // (waits for this wave's staging loads first)
+    }
+    if (mine) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) p4[i] = p8[2 * i] + p8[2 * i + 1];
+        for (int u = 0; u < 2; ++u) {
+            float v = sacc[u];
 #pragma unroll
-        for (int i = 0; i < 2; ++i) p2[i] = p4[2 * i] + p4[2 * i + 1];
-        sS[q][r][lane] = p2[0] + p2[1];
+            for (int m = 1; m < 64; m *= 2) v = v + __shfl_xor(v, m);
+            const int t = t0 + 16 * u + q;
+            if (lane == 0 && t < T) logits[size_t(t) * logit_stride + kExperts] = v;
+        }
+    }
+    // (P0 + P1) + (P2 + P3): the two blocks of each step hold the same (i, j)
+    // in registers r and 16 + r
+    float sq[16];
+#pragma unroll
+    for (int r = 0; r < 16; ++r) sq[r] = (acc[0][r] + acc[0][16 + r]) + (acc[1][r] + acc[1][16 + r]);
+    // exchange as [wave][token j][expert i], 16-byte group i / 4 stored at
+    // group (i / 4) ^ (j & 7): registers 4g..4g+3 are rows 8g + 4 (lane / 32)
+    // + 0..3, one 16-byte store each, conflict-free, and so are the reads
+    float* sS = reinterpret_cast<float*>(lds0);
+    const int j = lane & 31;
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+        const int grp = 2 * g + b;                        // rows 4 grp .. 4 grp + 3
+        *reinterpret_cast<float4*>(sS + (q * kRmTile + j) * kRmTile + 4 * (grp ^ (j & 7))) =
+            make_float4(sq[4 * g], sq[4 * g + 1], sq[4 * g + 2], sq[4 * g + 3]);
     }
     __syncthreads();
-    // ((S0 + S1) + (S2 + S3)) + bias; thread -> (token, kRtRows / 4 rows)
-    constexpr int kRowsPerThread = kRtRows / 4;
-    const int t = tid >> 2, rp = kRowsPerThread * (tid & 3), tok = tg * kRtTokens + t;
+    {
+        const int er = tid & 31, tc = tid >> 5, e = e0 + er, t = t0 + tc;
+        const int off = tc * kRmTile + 4 * ((er >> 2) ^ (tc & 7)) + (er & 3);
+        float lv[kRmWaves];
 #pragma unroll
-    for (int i = 0; i < kRowsPerThread; ++i) {
-        const int r = rp + i, e = e0 + r;
-        const float v = (sS[0][r][t] + sS[1][r][t]) + (sS[2][r][t] + sS[3][r][t]);
-        if (tok < T && e < nrows) logits[size_t(tok) * logit_stride + e] = (bias && e < kExperts) ? v + bias[e] : v;
+        for (int u = 0; u < kRmWaves; ++u) lv[u] = sS[u * kRmTile * kRmTile + off];
+#pragma unroll
+        for (int step = 1; step < kRmWaves; step *= 2)
+#pragma unroll
+            for (int u = 0; u < kRmWaves; u += 2 * step) lv[u] = lv[u] + lv[u + step];
+        if (t < T) logits[size_t(t) * logit_stride + e] = bias ? lv[0] + bias[e] : lv[0];
     }
 }
 
-__global__ __launch_bounds__(256, kRtBlocksPerCu) void router_tokens_kernel(const uint16_t* __restrict__ x, int64_t stride, int T,
-                                                               const uint16_t* __restrict__ w,
-                                                               const uint16_t* __restrict__ shared_w,
-                                                               const float* __restrict__ bias, float* __restrict__ logits,
-                                                               int64_t logit_stride, int nrows, int ntg) {
-    router_tokens_block(int(blockIdx.x), x, stride, T, w, shared_w, bias, logits, logit_stride, nrows, ntg);
+__global__ __launch_bounds__(kRmWaves * 64) void router_mfma_kernel(const uint16_t* __restrict__ x, int64_t stride, int T,
+                                                                     const uint16_t* __restrict__ w,
+                                                                     const uint16_t* __restrict__ shared_w,
+                                                                     const float* __restrict__ bias,
+                                                                     float* __restrict__ logits, int64_t logit_stride,
+                                                                     int ntg) {
+    router_mfma_block(int(blockIdx.x), x, stride, T, w, shared_w, bias, logits, logit_stride, ntg);
 }
 
 // Router tiles followed by the activation quantisation of the same rows (the
 // layer path with the shared expert, where every token is live, so the gate
-// input does not wait for routing).  The activation blocks take the CUs the
-// last round of router tiles leaves idle.
-__global__ __launch_bounds__(256, kRtBlocksPerCu) void router_act_kernel(const uint16_t* __restrict__ x, int T,
-                                                            const uint16_t* __restrict__ w,
-                                                            const uint16_t* __restrict__ shared_w,
-                                                            const float* __restrict__ bias, float* __restrict__ logits,
-                                                            int64_t logit_stride, int nrows, int ntg, int router_blocks,
-                                                            uint32_t* __restrict__ words, uint16_t* __restrict__ scales,
-                                                            int32_t* __restrict__ sums, uint32_t* sticky) {
+// input does not wait for routing).  An activation block of 16 waves does the
+// work of four 4-wave act_bf16_block indices.
+__global__ __launch_bounds__(kRmWaves * 64) void router_mfma_act_kernel(const uint16_t* __restrict__ x, int T,
+                                                                         const uint16_t* __restrict__ w,
+                                                                         const uint16_t* __restrict__ shared_w,
+                                                                         const float* __restrict__ bias,
+                                                                         float* __restrict__ logits,
+                                                                         int64_t logit_stride, int ntg,
+                                                                         int router_blocks,
+                                                                         uint32_t* __restrict__ words,
+                                                                         uint16_t* __restrict__ scales,
+                                                                         int32_t* __restrict__ sums, uint32_t* sticky) {
     const int b = int(blockIdx.x);
     if (b < router_blocks)
-        router_tokens_block(b, x, kHidden, T, w, shared_w, bias, logits, logit_stride, nrows, ntg);
+        router_mfma_block(b, x, kHidden, T, w, shared_w, bias, logits, logit_stride, ntg);
     else
-        act_bf16_block<127>(b - router_blocks, x, kHidden, T, kHidden / kGroup, nullptr, words, scales, sums, sticky,
-                            kFlagNonfiniteInput, kFlagInvalidActivation);
+        act_bf16_block<127>(4 * (b - router_blocks) + (int(threadIdx.x) >> 8), x, kHidden, T, kHidden / kGroup,
+                            nullptr, words, scales, sums, sticky, kFlagNonfiniteInput, kFlagInvalidActivation);
 }
 
 // One wave per (router row, batch of 8 tokens): the choice for small and
@@ -342,33 +241,30 @@ hipError_t launch_router(const uint16_t* x, int64_t stride, int T, const uint16_
                      bias, logits, logit_stride, nrows);
         return hipGetLastError();
     }
-    const int nrows = kExperts + (shared_w ? 1 : 0);
-    const int ngroups = (nrows + kRtRows - 1) / kRtRows;
-    const int ntg = (T + kRtTokens - 1) / kRtTokens;
-    const int blocks = ((ntg + 7) / 8) * 8 * ngroups;     // token groups padded to a multiple of the 8 XCDs
-    timed_launch("router", router_tokens_kernel, dim3(blocks), dim3(256), 0, s, x, stride, T, w, shared_w, bias, logits,
-                 logit_stride, nrows, ntg);
+    const int ntg = (T + kRmTile - 1) / kRmTile;
+    const int blocks = ((ntg + 7) / 8) * 8 * kRmGroups;   // token groups padded to a multiple of the 8 XCDs
+    timed_launch("router", router_mfma_kernel, dim3(blocks), dim3(kRmWaves * 64), 0, s, x, stride, T, w, shared_w,
+                 bias, logits, logit_stride, ntg);
     return hipGetLastError();
 }
 
-// The fused launch runs its activation blocks at the router's occupancy (two
-// blocks per CU); it pays when they fit the slots the last round of router
-// tiles leaves idle (about 4 activation blocks per router-tile time).
+// The tile kernel holds one block per CU (its LDS).  The fused launch pays
+// when the activation blocks fit the CUs the last round of router tiles
+// leaves idle (an activation block takes under half a tile's time).
 bool router_act_pays(int T) {
     if (T <= kRouterRowsMaxTokens) return false;
-    static int slots = 0;
-    if (!slots) {
-        int dev = 0, cus = 0;
-        if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) !=
-                                                    hipSuccess || cus <= 0)
+    static int cus = 0;
+    if (!cus) {
+        int dev = 0, n = 0;
+        if (hipGetDevice(&dev) != hipSuccess ||
+            hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
             return false;
-        slots = kRtBlocksPerCu * cus;
+        cus = n;
     }
-    const int ngroups = (kExperts + 1 + kRtRows - 1) / kRtRows;
-    const int tiles = ((T + kRtTokens - 1) / kRtTokens) * ngroups;   // router blocks with work
-    const int tail = tiles % slots;
-    const int idle = tail ? slots - tail : 0;
-    const int act_blocks = ((T * (kHidden / kGroup) + 3) / 4 + 3) / 4;
+    const int tiles = ((T + kRmTile - 1) / kRmTile) * kRmGroups;   // router blocks with work
+    const int tail = tiles % cus;
+    const int idle = tail ? cus - tail : 0;
+    const int act_blocks = ((T * (kHidden / kGroup) + 3) / 4 + kRmWaves - 1) / kRmWaves;
     return act_blocks <= 2 * idle;
 }
 
@@ -376,14 +272,12 @@ hipError_t launch_router_act(const uint16_t* x, int T, const uint16_t* w, const 
                              float* logits, int64_t logit_stride, uint32_t* words, uint16_t* scales, int32_t* sums,
                              uint32_t* sticky, hipStream_t s) {
     if (T <= kRouterRowsMaxTokens || !shared_w) return hipErrorInvalidValue;
-    const int nrows = kExperts + 1;
-    const int ngroups = (nrows + kRtRows - 1) / kRtRows;
-    const int ntg = (T + kRtTokens - 1) / kRtTokens;
-    const int router_blocks = ((ntg + 7) / 8) * 8 * ngroups;
+    const int ntg = (T + kRmTile - 1) / kRmTile;
+    const int router_blocks = ((ntg + 7) / 8) * 8 * kRmGroups;
     const int act_waves = (T * (kHidden / kGroup) + 3) / 4;
-    const int act_blocks = (act_waves + 3) / 4;
-    timed_launch("router_act", router_act_kernel, dim3(router_blocks + act_blocks), dim3(256), 0, s, x, T, w, shared_w,
-                 bias, logits, logit_stride, nrows, ntg, router_blocks, words, scales, sums, sticky);
+    const int act_blocks = (act_waves + kRmWaves - 1) / kRmWaves;
+    timed_launch("router_act", router_mfma_act_kernel, dim3(router_blocks + act_blocks), dim3(kRmWaves * 64), 0, s, x,
+                 T, w, shared_w, bias, logits, logit_stride, ntg, router_blocks, words, scales, sums, sticky);
     return hipGetLastError();
 }
 
