@@ -35,7 +35,7 @@ sys.path.insert(0, str(ROOT / 'ornith-ciru-halo-agent_amd'))
 
 HBM_PEAK_GBS = 8000.0
 INT8_PEAK_TOPS = 5000.0          # MI355X dense int8 MFMA
-FP32_PEAK_TFLOPS = 157.3         # MI355X vector fp32
+FP32_PEAK_TFLOPS = 157.3         # MI355X dense fp32 matrix peak
 BF16_PEAK_TFLOPS = 2500.0
 GATEUP_BYTES = 1024 * 2048 // 2 + 4 * 1024 * 8       # one gate-up bank: u4 codes + fp16 scale|offset words
 DOWN_BYTES = 2048 * 512 // 2 + 4 * 2048 * 2          # one down bank
@@ -49,9 +49,9 @@ DENSE_N = 6144
 # --copy-calibration); keyed by (kernel, tokens).  Commands and raw figures:
 # profiles/decode_n1_n32_hbm_traffic_pmc.md, profiles/prefill_1120_8192_hbm_traffic_pmc.md.
 MEASURED_TRAFFIC = {
-    ('route1', 1): 1166652, ('gateup1', 1): 9949504, ('down1', 1): 5118494,
-    ('route', 32): 2587625, ('topk', 32): 128330, ('sort', 32): 12783, ('gateup', 32): 176480790,
-    ('quant_middle', 32): 804902, ('down', 32): 90919803, ('reduce', 32): 2587151,
+    ('layer1', 1): 16731184, ('route1', 1): 1166652, ('gateup1', 1): 9949504, ('down1', 1): 5118494,
+    ('route', 32): 2587638, ('topk', 32): 128301, ('sort', 32): 12911, ('gateup', 32): 176476796,
+    ('quant_middle', 32): 804861, ('down', 32): 90919862, ('reduce', 32): 2591275,
     ('router_act', 1120): 21187047, ('topk', 1120): 1395534, ('permute_scan', 1120): 774087,
     ('permute_scatter', 1120): 335833, ('gateup_mfma', 1120): 189333643, ('quant_middle', 1120): 26020119,
     ('down_mfma', 1120): 169450349, ('reduce', 1120): 87580019,
@@ -80,8 +80,8 @@ def kernel_cost(name, T, unique):
         return 'mfma', 2 * routes * 1024 * 2048, INT8_PEAK_TOPS, 'TFLOP/s'
     if name == 'down_mfma':
         return 'mfma', 2 * routes * 2048 * 512, INT8_PEAK_TOPS, 'TFLOP/s'
-    if name in ('router', 'router_act'):
-        return 'valu', 2 * T * 257 * 2048, FP32_PEAK_TFLOPS, 'TFLOP/s'
+    if name in ('router', 'router_act'):      # exact K=1 fp32 matrix steps (the shared-gate row on the VALU)
+        return 'mfma', 2 * T * 257 * 2048, FP32_PEAK_TFLOPS, 'TFLOP/s'
     return 'hbm', T * 2048 * 2, HBM_PEAK_GBS, 'GB/s'
 
 
