@@ -100,8 +100,9 @@ __global__ __launch_bounds__(256) void transform_bf16_kernel(const uint16_t* __r
 constexpr int kBM = 256, kBN = 64, kBK = 32, kRing = 4;
 
 // 16-byte chunk `chunk` (0..3) of column c's 64-byte LDS row, rotated by the
-// column so that 16 consecutive columns read at one chunk spread over the banks
-__device__ __forceinline__ int b_slot(int c, int chunk) { return c * 64 + ((chunk ^ ((c >> 2) & 3)) << 4); }
+// column so that any 8 consecutive columns at one chunk fill the 8 slots of a
+// 128-byte bank line (a 16-byte access serves 8 lanes per LDS cycle)
+__device__ __forceinline__ int b_slot(int c, int chunk) { return c * 64 + ((chunk ^ ((c >> 1) & 3)) << 4); }
 
 __global__ __launch_bounds__(256, 2) void dense_gemm_bf16_kernel(const uint16_t* __restrict__ xt,
                                                                  const uint32_t* __restrict__ codes,
@@ -122,6 +123,7 @@ __global__ __launch_bounds__(256, 2) void dense_gemm_bf16_kernel(const uint16_t*
     if (tile >= nblocks_m * nblocks_n) return;
     const int nb = tile % nblocks_n, mb = tile / nblocks_n;
     const int row0 = mb * kBM, col0 = nb * kBN;
+    const bool wave_live = row0 + 64 * wm < M;
     const int G = K / kGroup, S = K / kBK;
 
     // ---- B: column c = lane, word jw = wave of the step's four (32 k) ----
@@ -228,13 +230,16 @@ __global__ __launch_bounds__(256, 2) void dense_gemm_bf16_kernel(const uint16_t*
             bf16x8 fn[4];
             read_b((u + 1) % kRing, fn);
             dequant(nslot, nslot, u < 6 ? acur : anext);
-            // products (weights x activations): lane (li, q) gets row li, columns 4 q + 0..3
+            // products (weights x activations): lane (li, q) gets row li, columns 4 q + 0..3;
+            // a wave whose 64 rows all lie past M only dequantises its share of B
+            if (wave_live) {
 #pragma unroll
-            for (int rt = 0; rt < 4; ++rt) {
-                const bf16x8 fa = __builtin_bit_cast(bf16x8, ra[slot][rt]);
+                for (int rt = 0; rt < 4; ++rt) {
+                    const bf16x8 fa = __builtin_bit_cast(bf16x8, ra[slot][rt]);
 #pragma unroll
-                for (int ct = 0; ct < 4; ++ct)
-                    acc[rt][ct] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fb[ct], fa, acc[rt][ct], 0, 0, 0);
+                    for (int ct = 0; ct < 4; ++ct)
+                        acc[rt][ct] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fb[ct], fa, acc[rt][ct], 0, 0, 0);
+                }
             }
             // refills issued here, kRing steps ahead of their use (the scheduler
             // may not sink them towards their uses): A slot with step
