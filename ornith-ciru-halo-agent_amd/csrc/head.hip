@@ -292,10 +292,7 @@ extern "C" hipError_t ornith_head_i8_tile_launch(const void* input, const void* 
     hipError_t st = hipGetLastError();
     if (st != hipSuccess) return st;
     auto diag = at<float>(workspace, l.projection);
-    int dev = 0, cus = 0;
-    if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) !=
-                                                hipSuccess || cus <= 0)
-        cus = 256;
+    const int cus = device_cu_count();
     const int ntiles = N / 16;
     const int blocks = std::min(cus, (ntiles + kW8Waves - 1) / kW8Waves);
     const int nwaves = std::min(blocks * kW8Waves, ntiles);

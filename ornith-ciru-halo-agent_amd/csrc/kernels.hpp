@@ -2,8 +2,24 @@
 // wrapper enqueues on the caller's stream and returns hipGetLastError().
 #pragma once
 #include "common.hpp"
+#include <atomic>
 
 namespace ornith {
+
+// Compute units of the current device, queried once per device (256 on
+// MI355X; `fallback` if the query fails).
+inline int device_cu_count(int fallback = 256) {
+    constexpr int kMaxDevices = 64;
+    static std::atomic<int> cached[kMaxDevices];
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return fallback;
+    int n = cached[dev].load(std::memory_order_relaxed);
+    if (n <= 0) {
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) return fallback;
+        cached[dev].store(n, std::memory_order_relaxed);
+    }
+    return n;
+}
 
 // A run of consecutive entries of the permuted route list that all use one
 // weight bank (expert id 0..255, or kShared for the shared expert).

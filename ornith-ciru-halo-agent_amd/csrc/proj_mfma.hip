@@ -742,16 +742,7 @@ __global__ __launch_bounds__(64 * WPB, 1) void head_tile_kernel(MfmaArgs a, int 
 // Head waves: WPB-wave blocks (one per CU), at least two code tiles per wave
 // (so the partial count per row, nwaves, stays within ceil(N / 64)).
 constexpr int kHeadWaves = 8, kHeadRing = 2;
-static int head_waves(int N) {
-    static int cus = 0;
-    if (!cus) {
-        int dev = 0;
-        if (hipGetDevice(&dev) != hipSuccess ||
-            hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
-            cus = 256;
-    }
-    return std::max(1, std::min(kHeadWaves * cus, (N / 32) / 2));
-}
+static int head_waves(int N) { return std::max(1, std::min(kHeadWaves * device_cu_count(), (N / 32) / 2)); }
 
 hipError_t launch_head_mfma(const MfmaArgs& a, int64_t* argmax, hipStream_t s) {
     if (a.R <= 0 || a.R > kMT || a.N <= 0 || a.N % 32 != 0 || a.K != kHidden) return hipErrorInvalidValue;

@@ -60,127 +60,136 @@ constexpr int kRmGroups = kExperts / kRmTile;              // expert groups (til
 constexpr int kRmQuarter = kHidden / 4;                    // k per staged quarter
 constexpr int kRmRowBytes = 2 * kRmQuarter + 16;           // staged row + a 16-byte pad (conflict-free columns)
 
-__device__ __forceinline__ void router_mfma_block(int blk, const uint16_t* __restrict__ x, int64_t stride, int T,
-                                                  const uint16_t* __restrict__ w,
-                                                  const uint16_t* __restrict__ shared_w,
-                                                  const float* __restrict__ bias, float* __restrict__ logits,
-                                                  int64_t logit_stride, int ntg) {
+// Persistent: block b runs on XCD b % 8 and walks that XCD's tiles (token
+// groups tg = x (mod 8), all eight expert groups, so a token group's x rows
+// stay in the XCD's L2), tile c, c + B, c + 2B, ... of the XCD's list for
+// c = b / 8 and B = blocks / 8.  The next tile's first quarter is staged
+// during the last quarter of the current one, and the Sq exchange uses the
+// buffer that quarter leaves free, so a tile boundary costs only the exchange.
+__device__ __forceinline__ void router_mfma_run(int blk, int nblk, const uint16_t* __restrict__ x, int64_t stride,
+                                                int T, const uint16_t* __restrict__ w,
+                                                const uint16_t* __restrict__ shared_w, const float* __restrict__ bias,
+                                                float* __restrict__ logits, int64_t logit_stride, int ntg) {
     // two buffers (separate arrays, so the compiler sees that loads into one
-    // do not alias reads of the other) of one K quarter of the tile's 32
+    // do not alias reads of the other) of one K quarter of a tile's 32
     // expert rows (rows 0..31) and 32 token rows (rows 32..63), bf16, rows
-    // kRmRowBytes apart; the shared-expert row whole; the Sq exchange reuses
-    // buffer 0
+    // kRmRowBytes apart; the shared-expert row whole
     constexpr int kBuf = 2 * kRmTile * kRmRowBytes;
     __shared__ __align__(16) uint8_t lds0[kBuf];
     __shared__ __align__(16) uint8_t lds1[kBuf];
     __shared__ __align__(16) uint8_t lshared[2 * kHidden];
-    static_assert(kRmWaves * kRmTile * kRmTile * 4 <= kBuf, "Sq exchange fits buffer 0");
-    // the expert groups of one token group run on one XCD (its x rows stay in that L2)
-    const int idx = blk >> 3;
-    const int tg = 8 * (idx / kRmGroups) + (blk & 7), eg = idx % kRmGroups;
-    if (tg >= ntg) return;
+    static_assert(kRmWaves * kRmTile * kRmTile * 4 <= kBuf, "Sq exchange fits a buffer");
+    const int xcd = blk & 7, c = blk >> 3, B = nblk >> 3;
+    const int ntiles = 8 * ((ntg - xcd + 7) / 8);              // this XCD's tiles: 8 per token group
+    if (c >= ntiles) return;
     const int tid = threadIdx.x, lane = tid & 63;
     const int q = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave-uniform: row pointers stay scalar
     const int b = lane >> 5, i = lane & 31;
-    const int e0 = eg * kRmTile, t0 = tg * kRmTile;
     const bool has_shared = shared_w != nullptr;
     // staging straight into LDS: wave q loads rows q, q + 16 (experts) and
     // q + 32, q + 48 (tokens; past the end they repeat the last one), lane =
     // 16-byte chunk of the quarter
-    const uint16_t* src[4];
+    auto stage = [&](int u, int jq, uint8_t* dst) __attribute__((always_inline)) {
+        const int tg = 8 * (u >> 3) + xcd, e0 = (u & 7) * kRmTile, t0 = tg * kRmTile;
 #pragma unroll
-    for (int n = 0; n < 4; ++n) {
-        const int r = q + 16 * n;
-        src[n] = n < 2 ? w + size_t(e0 + r) * kHidden : x + size_t(min(t0 + r - kRmTile, T - 1)) * stride;
-    }
-    auto stage = [&](int jq, uint8_t* dst) __attribute__((always_inline)) {
-#pragma unroll
-        for (int n = 0; n < 4; ++n)
-            __builtin_amdgcn_global_load_lds(src[n] + kRmQuarter * jq + 8 * lane,
+        for (int n = 0; n < 4; ++n) {
+            const int r = q + 16 * n;
+            const uint16_t* row = n < 2 ? w + size_t(e0 + r) * kHidden
+                                        : x + size_t(min(t0 + r - kRmTile, T - 1)) * stride;
+            __builtin_amdgcn_global_load_lds(row + kRmQuarter * jq + 8 * lane,
                                              (lds_void*)(dst + (q + 16 * n) * kRmRowBytes), 16, 0, 0);
+        }
     };
     // this lane's operands: expert row i and token row i, chunk 4q + b (first
     // step) and 4q + 2 + b (second step) of the quarter
     const int abase = i * kRmRowBytes + 16 * (4 * q + b), bbase = (kRmTile + i) * kRmRowBytes + 16 * (4 * q + b);
-    // shared row: waves eg and eg + 8 of block eg take token rows q and
-    // 16 + q (4 tokens per block), lane = partial
-    const bool mine = has_shared && (q & 7) == eg;
-    float sacc[2] = {0.f, 0.f};
-    f32x32 acc[2] = {f32x32{}, f32x32{}};
-    stage(0, lds0);
+    stage(c, 0, lds0);
     if (has_shared && q < 4)
         __builtin_amdgcn_global_load_lds(shared_w + kRmQuarter * q + 8 * lane, (lds_void*)(lshared + 1024 * q), 16, 0,
                                          0);
     __syncthreads();
+    for (int u = c; u < ntiles; u += B) {
+        const int tg = 8 * (u >> 3) + xcd, eg = u & 7, e0 = eg * kRmTile, t0 = tg * kRmTile;
+        const bool next = u + B < ntiles;
+        // shared row: waves eg and eg + 8 of the tile take token rows q and
+        // 16 + q (4 tokens per tile), lane = partial
+        const bool mine = has_shared && (q & 7) == eg;
+        float sacc[2] = {0.f, 0.f};
+        f32x32 acc[2] = {f32x32{}, f32x32{}};
 #pragma unroll
-    for (int jq = 0; jq < 4; ++jq) {
-        const uint8_t* sb = jq & 1 ? lds1 : lds0;
-        if (jq < 3) stage(jq + 1, jq & 1 ? lds0 : lds1);  // its last readers passed the previous barrier
-        __builtin_amdgcn_sched_barrier(0);
+        for (int jq = 0; jq < 4; ++jq) {
+            const uint8_t* sb = jq & 1 ? lds1 : lds0;
+            // the target buffer's last readers passed the previous barrier
+            if (jq < 3) stage(u, jq + 1, jq & 1 ? lds0 : lds1);
+            else if (next) stage(u + B, 0, lds0);
+            __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-        for (int s = 0; s < 2; ++s) {
-            const uint4 wv = *reinterpret_cast<const uint4*>(sb + abase + 32 * s);
-            const uint4 xv = *reinterpret_cast<const uint4*>(sb + bbase + 32 * s);
-            const uint32_t uw[4] = {wv.x, wv.y, wv.z, wv.w};
-            const uint32_t ux[4] = {xv.x, xv.y, xv.z, xv.w};
+            for (int s = 0; s < 2; ++s) {
+                const uint4 wv = *reinterpret_cast<const uint4*>(sb + abase + 32 * s);
+                const uint4 xv = *reinterpret_cast<const uint4*>(sb + bbase + 32 * s);
+                const uint32_t uw[4] = {wv.x, wv.y, wv.z, wv.w};
+                const uint32_t ux[4] = {xv.x, xv.y, xv.z, xv.w};
 #pragma unroll
-            for (int h = 0; h < 4; ++h) {
-                acc[s] = __builtin_amdgcn_mfma_f32_32x32x1f32(__uint_as_float(uw[h] << 16),
-                                                              __uint_as_float(ux[h] << 16), acc[s], 0, 0, 0);
-                acc[s] = __builtin_amdgcn_mfma_f32_32x32x1f32(__uint_as_float(uw[h] & 0xffff0000u),
-                                                              __uint_as_float(ux[h] & 0xffff0000u), acc[s], 0, 0, 0);
+                for (int h = 0; h < 4; ++h) {
+                    acc[s] = __builtin_amdgcn_mfma_f32_32x32x1f32(__uint_as_float(uw[h] << 16),
+                                                                  __uint_as_float(ux[h] << 16), acc[s], 0, 0, 0);
+                    acc[s] = __builtin_amdgcn_mfma_f32_32x32x1f32(__uint_as_float(uw[h] & 0xffff0000u),
+                                                                  __uint_as_float(ux[h] & 0xffff0000u), acc[s], 0, 0,
+                                                                  0);
+                }
             }
+            if (mine) {
+                float wf[8], xf[8];
+                bf16x8_to_f32(*reinterpret_cast<const uint4*>(lshared + 2 * kRmQuarter * jq + 16 * lane), wf);
+#pragma unroll
+                for (int v = 0; v < 2; ++v) {
+                    bf16x8_to_f32(*reinterpret_cast<const uint4*>(sb + (kRmTile + q + 16 * v) * kRmRowBytes + 16 * lane),
+                                  xf);
+#pragma unroll
+                    for (int k = 0; k < 8; ++k) sacc[v] = __builtin_fmaf(xf[k], wf[k], sacc[v]);
+                }
+            }
+            __syncthreads();                              // (waits for this wave's staging loads first)
         }
         if (mine) {
-            float wf[8], xf[8];
-            bf16x8_to_f32(*reinterpret_cast<const uint4*>(lshared + 2 * kRmQuarter * jq + 16 * lane), wf);
 #pragma unroll
-            for (int u = 0; u < 2; ++u) {
-                bf16x8_to_f32(*reinterpret_cast<const uint4*>(sb + (kRmTile + q + 16 * u) * kRmRowBytes + 16 * lane), xf);
-#pragma unroll
-                for (int k = 0; k < 8; ++k) sacc[u] = __builtin_fmaf(xf[k], wf[k], sacc[u]);
+            for (int v = 0; v < 2; ++v) {
+                const float sv = wave_butterfly_sum(sacc[v]);
+                const int t = t0 + 16 * v + q;
+                if (lane == 0 && t < T) logits[size_t(t) * logit_stride + kExperts] = sv;
             }
         }
-        __syncthreads();                                  // (waits for this wave's staging loads first)
-    }
-    if (mine) {
+        // (P0 + P1) + (P2 + P3): the two blocks of each step hold the same
+        // (i, j) in registers r and 16 + r
+        float sq[16];
 #pragma unroll
-        for (int u = 0; u < 2; ++u) {
-            float v = sacc[u];
+        for (int r = 0; r < 16; ++r) sq[r] = (acc[0][r] + acc[0][16 + r]) + (acc[1][r] + acc[1][16 + r]);
+        // exchange in buffer 1 (free after the last quarter) as [wave][token j]
+        // [expert i], 16-byte group i / 4 stored at group (i / 4) ^ (j & 7):
+        // registers 4g..4g+3 are rows 8g + 4 (lane / 32) + 0..3, one 16-byte
+        // store each, conflict-free, and so are the reads
+        float* sS = reinterpret_cast<float*>(lds1);
+        const int j = lane & 31;
 #pragma unroll
-            for (int m = 1; m < 64; m *= 2) v = v + __shfl_xor(v, m);
-            const int t = t0 + 16 * u + q;
-            if (lane == 0 && t < T) logits[size_t(t) * logit_stride + kExperts] = v;
+        for (int g = 0; g < 4; ++g) {
+            const int grp = 2 * g + b;                    // rows 4 grp .. 4 grp + 3
+            *reinterpret_cast<float4*>(sS + (q * kRmTile + j) * kRmTile + 4 * (grp ^ (j & 7))) =
+                make_float4(sq[4 * g], sq[4 * g + 1], sq[4 * g + 2], sq[4 * g + 3]);
         }
-    }
-    // (P0 + P1) + (P2 + P3): the two blocks of each step hold the same (i, j)
-    // in registers r and 16 + r
-    float sq[16];
+        __syncthreads();
+        {
+            const int er = tid & 31, tc = tid >> 5, e = e0 + er, t = t0 + tc;
+            const int off = tc * kRmTile + 4 * ((er >> 2) ^ (tc & 7)) + (er & 3);
+            float lv[kRmWaves];
 #pragma unroll
-    for (int r = 0; r < 16; ++r) sq[r] = (acc[0][r] + acc[0][16 + r]) + (acc[1][r] + acc[1][16 + r]);
-    // exchange as [wave][token j][expert i], 16-byte group i / 4 stored at
-    // group (i / 4) ^ (j & 7): registers 4g..4g+3 are rows 8g + 4 (lane / 32)
-    // + 0..3, one 16-byte store each, conflict-free, and so are the reads
-    float* sS = reinterpret_cast<float*>(lds0);
-    const int j = lane & 31;
+            for (int v = 0; v < kRmWaves; ++v) lv[v] = sS[v * kRmTile * kRmTile + off];
 #pragma unroll
-    for (int g = 0; g < 4; ++g) {
-        const int grp = 2 * g + b;                        // rows 4 grp .. 4 grp + 3
-        *reinterpret_cast<float4*>(sS + (q * kRmTile + j) * kRmTile + 4 * (grp ^ (j & 7))) =
-            make_float4(sq[4 * g], sq[4 * g + 1], sq[4 * g + 2], sq[4 * g + 3]);
-    }
-    __syncthreads();
-    {
-        const int er = tid & 31, tc = tid >> 5, e = e0 + er, t = t0 + tc;
-        const int off = tc * kRmTile + 4 * ((er >> 2) ^ (tc & 7)) + (er & 3);
-        float lv[kRmWaves];
+            for (int step = 1; step < kRmWaves; step *= 2)
 #pragma unroll
-        for (int u = 0; u < kRmWaves; ++u) lv[u] = sS[u * kRmTile * kRmTile + off];
-#pragma unroll
-        for (int step = 1; step < kRmWaves; step *= 2)
-#pragma unroll
-            for (int u = 0; u < kRmWaves; u += 2 * step) lv[u] = lv[u] + lv[u + step];
-        if (t < T) logits[size_t(t) * logit_stride + e] = bias ? lv[0] + bias[e] : lv[0];
+                for (int v = 0; v < kRmWaves; v += 2 * step) lv[v] = lv[v] + lv[v + step];
+            if (t < T) logits[size_t(t) * logit_stride + e] = bias ? lv[0] + bias[e] : lv[0];
+        }
+        __syncthreads();                                  // buffer 1 free for the next tile's second quarter
     }
 }
 
@@ -190,7 +199,7 @@ __global__ __launch_bounds__(kRmWaves * 64) void router_mfma_kernel(const uint16
                                                                      const float* __restrict__ bias,
                                                                      float* __restrict__ logits, int64_t logit_stride,
                                                                      int ntg) {
-    router_mfma_block(int(blockIdx.x), x, stride, T, w, shared_w, bias, logits, logit_stride, ntg);
+    router_mfma_run(int(blockIdx.x), int(gridDim.x), x, stride, T, w, shared_w, bias, logits, logit_stride, ntg);
 }
 
 // Router tiles followed by the activation quantisation of the same rows (the
@@ -209,7 +218,7 @@ __global__ __launch_bounds__(kRmWaves * 64) void router_mfma_act_kernel(const ui
                                                                          int32_t* __restrict__ sums, uint32_t* sticky) {
     const int b = int(blockIdx.x);
     if (b < router_blocks)
-        router_mfma_block(b, x, kHidden, T, w, shared_w, bias, logits, logit_stride, ntg);
+        router_mfma_run(b, router_blocks, x, kHidden, T, w, shared_w, bias, logits, logit_stride, ntg);
     else
         act_bf16_block<127>(4 * (b - router_blocks) + (int(threadIdx.x) >> 8), x, kHidden, T, kHidden / kGroup,
                             nullptr, words, scales, sums, sticky, kFlagNonfiniteInput, kFlagInvalidActivation);
@@ -231,6 +240,13 @@ __global__ __launch_bounds__(256) void router_rows_kernel(const uint16_t* __rest
     router_rows_wave(x, stride, T, t0, wrow, has_bias ? bias[row] : 0.f, has_bias, logits, logit_stride, row);
 }
 
+// Persistent tile blocks: 8 B (B per XCD), at most one per CU and at most the
+// tiles an XCD has (8 per token group).
+static int router_mfma_blocks(int ntg) {
+    const int per_xcd = std::max(1, std::min(device_cu_count() / 8, 8 * ((ntg + 7) / 8)));
+    return 8 * per_xcd;
+}
+
 hipError_t launch_router(const uint16_t* x, int64_t stride, int T, const uint16_t* w, const uint16_t* shared_w,
                          const float* bias, float* logits, int64_t logit_stride, hipStream_t s) {
     if (T <= 0) return hipSuccess;
@@ -242,26 +258,20 @@ hipError_t launch_router(const uint16_t* x, int64_t stride, int T, const uint16_
         return hipGetLastError();
     }
     const int ntg = (T + kRmTile - 1) / kRmTile;
-    const int blocks = ((ntg + 7) / 8) * 8 * kRmGroups;   // token groups padded to a multiple of the 8 XCDs
-    timed_launch("router", router_mfma_kernel, dim3(blocks), dim3(kRmWaves * 64), 0, s, x, stride, T, w, shared_w,
-                 bias, logits, logit_stride, ntg);
+    timed_launch("router", router_mfma_kernel, dim3(router_mfma_blocks(ntg)), dim3(kRmWaves * 64), 0, s, x, stride, T,
+                 w, shared_w, bias, logits, logit_stride, ntg);
     return hipGetLastError();
 }
 
-// The tile kernel holds one block per CU (its LDS).  The fused launch pays
-// when the activation blocks fit the CUs the last round of router tiles
-// leaves idle (an activation block takes under half a tile's time).
+// The tile kernel holds one block per CU (its LDS), each walking its share of
+// the tiles.  The fused launch pays when the activation blocks fit the CUs
+// left idle by the tiles' last round (an activation block takes under half a
+// tile's time).
 bool router_act_pays(int T) {
     if (T <= kRouterRowsMaxTokens) return false;
-    static int cus = 0;
-    if (!cus) {
-        int dev = 0, n = 0;
-        if (hipGetDevice(&dev) != hipSuccess ||
-            hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
-            return false;
-        cus = n;
-    }
-    const int tiles = ((T + kRmTile - 1) / kRmTile) * kRmGroups;   // router blocks with work
+    const int cus = device_cu_count(0);
+    if (cus <= 0) return false;
+    const int tiles = ((T + kRmTile - 1) / kRmTile) * kRmGroups;
     const int tail = tiles % cus;
     const int idle = tail ? cus - tail : 0;
     const int act_blocks = ((T * (kHidden / kGroup) + 3) / 4 + kRmWaves - 1) / kRmWaves;
@@ -273,7 +283,7 @@ hipError_t launch_router_act(const uint16_t* x, int T, const uint16_t* w, const 
                              uint32_t* sticky, hipStream_t s) {
     if (T <= kRouterRowsMaxTokens || !shared_w) return hipErrorInvalidValue;
     const int ntg = (T + kRmTile - 1) / kRmTile;
-    const int router_blocks = ((ntg + 7) / 8) * 8 * kRmGroups;
+    const int router_blocks = router_mfma_blocks(ntg);
     const int act_waves = (T * (kHidden / kGroup) + 3) / 4;
     const int act_blocks = (act_waves + kRmWaves - 1) / kRmWaves;
     timed_launch("router_act", router_mfma_act_kernel, dim3(router_blocks + act_blocks), dim3(kRmWaves * 64), 0, s, x,
