@@ -107,6 +107,15 @@ ORNITH_EXPORT int ornith_mi355x_abi_version(void);
  * resident at once, e.g. CUs taken by other work for tens of ms). */
 ORNITH_EXPORT int ornith_mi355x_single_token_path(int path);
 
+/* No reference counterpart.  Which kernels run the router, top-8 and sort of
+ * a 2..32-token whole-layer call, process-wide: 0 (default) one launch whose
+ * blocks hand logits and ids to each other, wherever its grid is resident at
+ * once on the device (else three kernels), 1 always three kernels; -1
+ * queries.  Returns the previous setting, or -1 for another value.  Results
+ * are identical either way; the one launch raises sticky flag 64 like the
+ * single-token one. */
+ORNITH_EXPORT int ornith_mi355x_decode_route_path(int path);
+
 #ifdef __cplusplus
 }
 #endif

@@ -454,7 +454,7 @@ extern "C" hipError_t ornith_shared_fixed8_launch(const void* input, const void*
 
 // ---- the whole layer without a caller workspace --------------------------------
 // Scratch of ornith_moe_layer_launch_static: the layer plan at Tcap = 32 needs
-// 4,696,320 bytes; 5 MiB per GPU, held for the life of the process.  In host
+// 4,784,896 bytes; 5 MiB per GPU, held for the life of the process.  In host
 // code `scratch` only names the symbol: its device address comes from
 // hipGetSymbolAddress, once per device, and only that address is passed on.
 namespace {
@@ -514,6 +514,12 @@ extern "C" int ornith_mi355x_single_token_path(int path) {
     if (path < -1 || path > 1) return -1;
     if (path == -1) return g_single_token_mode.load();
     return g_single_token_mode.exchange(path);
+}
+
+extern "C" int ornith_mi355x_decode_route_path(int path) {
+    if (path < -1 || path > 1) return -1;
+    if (path == -1) return g_route_select_mode.load();
+    return g_route_select_mode.exchange(path);
 }
 
 // =============================================================================

@@ -199,6 +199,20 @@ __device__ __forceinline__ float wave_butterfly_sum(float v) {
     return (r0 + r1) + (r2 + r3);
 }
 
+// Inclusive prefix sum over the 64 lanes by DPP (no LDS): Hillis-Steele
+// within each row of 16 (row_shr 1, 2, 4, 8; lanes shifted in from outside
+// the row add 0), then row_bcast 15 into rows 1 and 3 and row_bcast 31 into
+// rows 2 and 3.
+__device__ __forceinline__ int wave_prefix_sum(int v) {
+    v += __builtin_amdgcn_update_dpp(0, v, 0x111, 0xF, 0xF, false);
+    v += __builtin_amdgcn_update_dpp(0, v, 0x112, 0xF, 0xF, false);
+    v += __builtin_amdgcn_update_dpp(0, v, 0x114, 0xF, 0xF, false);
+    v += __builtin_amdgcn_update_dpp(0, v, 0x118, 0xF, 0xF, false);
+    v += __builtin_amdgcn_update_dpp(0, v, 0x142, 0xA, 0xF, false);
+    v += __builtin_amdgcn_update_dpp(0, v, 0x143, 0xC, 0xF, false);
+    return v;
+}
+
 __device__ __forceinline__ void flag_or(uint32_t* sticky, uint32_t bits) {
     if (bits) atomicOr(sticky, bits);
 }

@@ -1,5 +1,6 @@
 // Decode path for 2..32 tokens: the routed MoE layer as seven kernels, none of
-// which waits on another block (kernel boundaries carry every hand-off).
+// which waits on another block (kernel boundaries carry every hand-off), or,
+// with the router, five, the first of which hands values between its blocks.
 //
 //   S1 decode_route_kernel     router logits, one wave per (router row, batch
 //                              of 8 tokens), and the quantised gate input
@@ -7,6 +8,8 @@
 //   S2 topk                    softmax/top-8, one wave per token (routing.hip),
 //      decode_sort_kernel      then one block: stable counting sort of the
 //                              routes into per-bank segments.
+//   (With the router, S1 and S2 run by default as one launch whose blocks
+//   hand logits and ids to each other: decode_route_select_kernel.)
 //   S3 decode_gateup_kernel    block (segment, 16 gate + 16 up columns): the
 //                              codes stay in registers while the segment's
 //                              routes stream through four at a time; exact
@@ -17,12 +20,13 @@
 //   S6 reduce                  slot-order combination (+ shared expert).
 //
 // Arithmetic is the reference's (routed_storage_n32_consumer.cpp:22-307); the
-// decomposition into kernels is this library's.  A single token takes the
-// three-kernel path of decode1.hip.
+// decomposition into kernels is this library's.  A single token takes
+// decode1.hip.
 #include "kernels.hpp"
 #include "timing.hpp"
 #include "topk.hpp"
 #include "decode.hpp"
+#include "handoff.hpp"
 
 namespace ornith {
 
@@ -99,45 +103,55 @@ __global__ __launch_bounds__(256) void decode_route_kernel(DecodeArgs a, int rou
 // histograms, prefixed per bank) + earlier lanes of its own chunk (readlane
 // scan inside the wave).
 // ---------------------------------------------------------------------------
-constexpr int kSortChunks = (kMaxRoutes + 63) / 64;
 constexpr int kSegRoutes = 8;          // a segment longer than this is split into pieces of 8 routes
 constexpr int kMaxSegments = kDecodeBanks + kMaxRoutes / kSegRoutes;
 
-template <bool SHARED>
-__global__ __launch_bounds__(512) void decode_sort_kernel(DecodeArgs a, const int32_t* __restrict__ ids) {
-    __shared__ int s_hist[kSortChunks][kDecodeBanks];
+// NT threads, route r = tid + NT j (j < ceil(routes / NT)) in chunk r / 64,
+// so a wave's lanes hold one chunk at a time.  ids: the token-major expert
+// ids, global or LDS.
+template <bool SHARED, int NT>
+__device__ __forceinline__ void sort_routes_block(const DecodeArgs& a, const int32_t* ids) {
+    constexpr int kRounds = (kMaxRoutes + NT - 1) / NT, kChunks = kRounds * NT / 64;
+    __shared__ int s_hist[kChunks][kDecodeBanks];
     __shared__ int s_total[kDecodeBanks], s_off[kDecodeBanks];
     const int T = a.T, R = T * kTop, Rall = R + (SHARED ? T : 0);
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    for (int i = tid; i < kSortChunks * kDecodeBanks; i += 512) (&s_hist[0][0])[i] = 0;
+    for (int i = tid; i < kChunks * kDecodeBanks; i += NT) (&s_hist[0][0])[i] = 0;
     uint32_t flags = 0;
-    int bank = -1;
-    const int r = tid;
-    if (r < R) {
-        const int id = ids[r];
-        bank = (id >= 0 && id < kExperts) ? id : -1;
-        if (bank < 0 && id != -1) flags |= kFlagInvalidExpert;
-    } else if (r < Rall) {
-        bank = kShared;
+    int bank[kRounds], rank_in[kRounds];
+#pragma unroll
+    for (int j = 0; j < kRounds; ++j) {
+        const int r = tid + NT * j;
+        bank[j] = -1;
+        if (r < R) {
+            const int id = ids[r];
+            bank[j] = (id >= 0 && id < kExperts) ? id : -1;
+            if (bank[j] < 0 && id != -1) flags |= kFlagInvalidExpert;
+        } else if (r < Rall) {
+            bank[j] = kShared;
+        }
     }
     __syncthreads();
-    if (bank >= 0) atomicAdd(&s_hist[wave][bank], 1);
-    int rank_in = 0;
+#pragma unroll
+    for (int j = 0; j < kRounds; ++j) {
+        if (bank[j] >= 0) atomicAdd(&s_hist[wave + (NT / 64) * j][bank[j]], 1);
+        rank_in[j] = 0;
 #pragma unroll 8
-    for (int l = 0; l < 64; ++l) {
-        const int bl = __builtin_amdgcn_readlane(bank, l);
-        rank_in += (l < lane && bl == bank) ? 1 : 0;
+        for (int l = 0; l < 64; ++l) {
+            const int bl = __builtin_amdgcn_readlane(bank[j], l);
+            rank_in[j] += (l < lane && bl == bank[j]) ? 1 : 0;
+        }
     }
     __syncthreads();
-    if (tid < kDecodeBanks) {
+    for (int bk = tid; bk < kDecodeBanks; bk += NT) {
         int run = 0;
 #pragma unroll
-        for (int k = 0; k < kSortChunks; ++k) {
-            const int c = s_hist[k][tid];
-            s_hist[k][tid] = run;
+        for (int k = 0; k < kChunks; ++k) {
+            const int c = s_hist[k][bk];
+            s_hist[k][bk] = run;
             run += c;
         }
-        s_total[tid] = run;
+        s_total[bk] = run;
     }
     __syncthreads();
     if (wave == 0) {
@@ -152,12 +166,7 @@ __global__ __launch_bounds__(512) void decode_sort_kernel(DecodeArgs a, const in
             tc += c[i];
             tn += nz[i];
         }
-        int ic = tc, in = tn;
-#pragma unroll
-        for (int d = 1; d < 64; d <<= 1) {
-            const int oc = __shfl_up(ic, d, 64), on = __shfl_up(in, d, 64);
-            if (lane >= d) { ic += oc; in += on; }
-        }
+        const int ic = wave_prefix_sum(tc), in = wave_prefix_sum(tn);
         int runc = ic - tc, runn = in - tn;
 #pragma unroll
         for (int i = 0; i < 5; ++i) {
@@ -173,7 +182,185 @@ __global__ __launch_bounds__(512) void decode_sort_kernel(DecodeArgs a, const in
         if (lane == 63) { a.nseg[0] = in; a.nseg[1] = ic; }
     }
     __syncthreads();
-    if (bank >= 0) a.routes[s_off[bank] + s_hist[wave][bank] + rank_in] = r;
+#pragma unroll
+    for (int j = 0; j < kRounds; ++j)
+        if (bank[j] >= 0)
+            a.routes[s_off[bank[j]] + s_hist[wave + (NT / 64) * j][bank[j]] + rank_in[j]] = tid + NT * j;
+    flag_or(a.sticky, flags);
+}
+
+// The same order when every token's ids are distinct (the router's top-8):
+// a route's rank in its bank is the number of earlier tokens that chose the
+// bank, so one 32-bit token mask per bank (T <= 32) replaces the chunk
+// histograms and the in-wave rank loops.
+template <bool SHARED, int NT>
+__device__ __forceinline__ void sort_routes_masks(const DecodeArgs& a, const int32_t* ids) {
+    __shared__ uint32_t s_mask[kDecodeBanks];
+    __shared__ int s_off[kDecodeBanks];
+    const int T = a.T, R = T * kTop, Rall = R + (SHARED ? T : 0);
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const uint32_t all = T >= 32 ? 0xffffffffu : (1u << T) - 1u;
+    for (int i = tid; i < kDecodeBanks; i += NT) s_mask[i] = (SHARED && i == kShared) ? all : 0u;
+    uint32_t flags = 0;
+    __syncthreads();
+    for (int r = tid; r < R; r += NT) {
+        const int id = ids[r];
+        if (id >= 0 && id < kExperts) atomicOr(&s_mask[id], 1u << (r >> 3));
+        else if (id != -1) flags |= kFlagInvalidExpert;
+    }
+    __syncthreads();
+    if (wave == 0) {
+        // exclusive scans of counts and of segment pieces over 257 banks,
+        // 5 banks per lane (lane-serial) then a wave scan of the lane totals
+        int c[5], nz[5], tc = 0, tn = 0;
+#pragma unroll
+        for (int i = 0; i < 5; ++i) {
+            const int b = lane * 5 + i;
+            c[i] = b < kDecodeBanks ? __popc(s_mask[b]) : 0;
+            nz[i] = (c[i] + kSegRoutes - 1) / kSegRoutes;
+            tc += c[i];
+            tn += nz[i];
+        }
+        const int ic = wave_prefix_sum(tc), in = wave_prefix_sum(tn);
+        int runc = ic - tc, runn = in - tn;
+#pragma unroll
+        for (int i = 0; i < 5; ++i) {
+            const int b = lane * 5 + i;
+            if (b < kDecodeBanks) {
+                s_off[b] = runc;
+                for (int k = 0; k < nz[i]; ++k)
+                    a.segments[runn + k] = Segment{b, runc + k * kSegRoutes, min(kSegRoutes, c[i] - k * kSegRoutes), 0};
+            }
+            runc += c[i];
+            runn += nz[i];
+        }
+        if (lane == 63) { a.nseg[0] = in; a.nseg[1] = ic; }
+    }
+    __syncthreads();
+    for (int r = tid; r < Rall; r += NT) {
+        int bank = kShared, t = r - R;
+        if (r < R) {
+            const int id = ids[r];
+            bank = (id >= 0 && id < kExperts) ? id : -1;
+            t = r >> 3;
+        }
+        if (bank >= 0) a.routes[s_off[bank] + __popc(s_mask[bank] & ((1u << t) - 1u))] = r;
+    }
+    flag_or(a.sticky, flags);
+}
+
+// DISTINCT: the ids are the router's top-8 (distinct within a token)
+template <bool SHARED, bool DISTINCT>
+__global__ __launch_bounds__(512) void decode_sort_kernel(DecodeArgs a, const int32_t* __restrict__ ids) {
+    if constexpr (DISTINCT) sort_routes_masks<SHARED, 512>(a, ids);
+    else sort_routes_block<SHARED, 512>(a, ids);
+}
+
+// ---------------------------------------------------------------------------
+// S1 + S2 in one launch (router and shared expert, 2..32 tokens).  Blocks of
+// 4 waves take the waves of S1 (router row waves, then the gate-input waves);
+// each router wave also publishes its logits as tagged words (handoff.hpp).
+// Wave w of block L < ceil(T / 4) then selects token 4L + w from the tagged
+// logits (the per-token selection of routing.hip's top-k) and publishes its
+// eight ids; block 0 gathers the ids and runs the sort above.  Every block
+// publishes an arrival word after its first barrier (by then every wave has
+// read the sequence number); block 0 advances the number once all have
+// arrived.  Waits are bounded (kFlagHandoffTimeout); the launcher uses this
+// kernel only when the whole grid is resident at once.
+// ---------------------------------------------------------------------------
+template <bool SHARED, int QMAX>
+__global__ __launch_bounds__(256) void decode_route_select_kernel(DecodeArgs a, int router_waves) {
+    __shared__ __align__(16) uint64_t s_cand[4][66];
+    __shared__ uint2 s_sel[4][kTop];
+    __shared__ int32_t s_ids[kDecodeMaxTokens * kTop];
+    const int T = a.T, lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int L = int(blockIdx.x), gw = L * 4 + wave;
+    uint64_t* W = a.l1_words;
+    const uint32_t seq = __hip_atomic_load(a.l1_seq, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    uint32_t flags = 0;
+    if (gw < router_waves) {
+        const int nb = (T + kTokenBatch - 1) / kTokenBatch;
+        const int row = gw / nb, t0 = (gw % nb) * kTokenBatch;
+        const uint16_t* wrow = row < kExperts ? a.router_w + size_t(row) * kHidden : a.shared_gate_w;
+        const bool has_bias = a.bias && row < kExperts;
+        router_rows_wave(a.x, kHidden, T, t0, wrow, has_bias ? a.bias[row] : 0.f, has_bias, a.logits, kLogitStride,
+                         row, W, seq, uint32_t(kDecodeRouteLogit + kDecodeMaxTokens * row + t0));
+    } else if (gw - router_waves < T * 4) {
+        // quantised gate input: wave q handles groups 2(q%4), 2(q%4)+1 of token q/4
+        const int q = gw - router_waves;
+        const int tok = q >> 2, job = (q & 3) * 2 + (lane >> 5), lp = lane & 31;
+        const uint4 raw = *reinterpret_cast<const uint4*>(a.x + size_t(tok) * kHidden + job * kGroup + lp * 8);
+        const uint32_t rw[4] = {raw.x, raw.y, raw.z, raw.w};
+        float v[8];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            v[2 * e] = bf16_bits_to_f32(rw[e] & 0xffffu);
+            v[2 * e + 1] = bf16_bits_to_f32(rw[e] >> 16);
+        }
+#pragma unroll
+        for (int e = 0; e < 8; ++e) if (!isfinite(v[e])) flags |= kFlagNonfiniteInput;
+        h128_half(v);
+        uint32_t w2[2];
+        uint16_t sb;
+        int sum;
+        quantize_half_fast<QMAX>(v, w2, sb, sum, flags, kFlagNonfiniteInput | kFlagInvalidActivation,
+                                 kFlagInvalidActivation);
+        const size_t g = size_t(tok) * 8 + job;
+        *reinterpret_cast<uint2*>(a.x_words + g * 64 + 2 * lp) = make_uint2(w2[0], w2[1]);
+        if (lp == 0) {
+            a.x_scales[g] = sb;
+            a.x_sums[g] = sum;
+        }
+    }
+    __syncthreads();                                   // every wave holds seq
+    if (threadIdx.x == 0) l1_put(W, kDecodeRouteArrive + 8 * L, seq, 1u);
+
+    // ---- selection of token 4L + wave ----
+    const int t = L * 4 + wave;
+    if (t < T) {
+        uint32_t idx[5], got[5];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) idx[i] = kDecodeRouteLogit + kDecodeMaxTokens * (lane + 64 * i) + t;
+        idx[4] = SHARED ? kDecodeRouteLogit + kDecodeMaxTokens * kExperts + t : idx[3];   // the shared gate row
+        if (!l1_wait<5, 0>(W, idx, seq, got)) flags |= kFlagHandoffTimeout;
+        float v[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) v[i] = __uint_as_float(got[i]);
+        uint32_t k[4];
+        softmax_keys(v, k);
+        top8_rank_lds(k, s_cand[wave], s_sel[wave]);
+        float tot = 0.f;
+#pragma unroll
+        for (int j = 0; j < kTop; ++j) tot = tot + __uint_as_float(s_sel[wave][j].x);
+        if (lane < kTop) {
+            const uint2 pick = s_sel[wave][lane];
+            a.topk_w[size_t(t) * kTop + lane] = fdiv_rn(__uint_as_float(pick.x), tot);
+            a.topk_ids[size_t(t) * kTop + lane] = int(pick.y);
+            l1_put(W, kDecodeRouteIds + kTop * t + lane, seq, pick.y);
+        }
+        if (SHARED && lane == 0) a.shared_logit[t] = f32_to_bf16_bits(__uint_as_float(got[4]));
+    }
+
+    // ---- block 0: gather the ids, sort, advance the sequence number ----
+    if (L == 0) {
+        const int R = T * kTop;
+        if (wave * 64 < R) {                           // R <= 256: one id word per thread
+            const int r = min(wave * 64 + lane, R - 1);
+            uint32_t idx[1] = {uint32_t(kDecodeRouteIds + r)}, got[1];
+            if (!l1_wait<1, 0>(W, idx, seq, got)) flags |= kFlagHandoffTimeout;
+            if (wave * 64 + lane < R) s_ids[wave * 64 + lane] = int32_t(got[0]);
+        }
+        __syncthreads();
+        sort_routes_masks<SHARED, 256>(a, s_ids);
+        if (wave == 0) {
+            const int nblocks = int(gridDim.x);
+            uint32_t idx[5], got[5];
+#pragma unroll
+            for (int i = 0; i < 5; ++i) idx[i] = kDecodeRouteArrive + 8 * min(lane + 64 * i, nblocks - 1);
+            if (!l1_wait<5, 1>(W, idx, seq, got)) flags |= kFlagHandoffTimeout;
+            if (lane == 0) __hip_atomic_store(a.l1_seq, seq + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+    }
     flag_or(a.sticky, flags);
 }
 
@@ -386,7 +573,7 @@ __global__ __launch_bounds__(256) void decode_down_kernel(DecodeArgs a) {
 // ---------------------------------------------------------------------------
 size_t decode_scratch_bytes() {
     return align256(size_t(kDecodeMaxTokens) * kLogitStride * 4) + align256(kMaxSegments * sizeof(Segment)) +
-           align256(kMaxRoutes * 4) + align256(8) + align256(4) + align256(size_t(kLayer1Words) * 8);
+           align256(kMaxRoutes * 4) + align256(8) + align256(4) + align256(size_t(kHandoffWords) * 8);
 }
 
 void carve_decode(void* base, DecodeArgs& a) {
@@ -397,28 +584,65 @@ void carve_decode(void* base, DecodeArgs& a) {
     a.routes = static_cast<int32_t*>(take(kMaxRoutes * 4));
     a.nseg = static_cast<int32_t*>(take(8));
     a.l1_seq = static_cast<uint32_t*>(take(4));
-    a.l1_words = static_cast<uint64_t*>(take(size_t(kLayer1Words) * 8));
+    a.l1_words = static_cast<uint64_t*>(take(size_t(kHandoffWords) * 8));
 }
 
 constexpr int kDownTilesPerBlock = 2;    // 32-column down tiles per block (2048 / 32 / 2 = 32 blocks per segment)
+
+// Whether `blocks` blocks of the one-launch route kernel are resident at once
+// on the current device (occupancy checked once per device).
+template <bool SHARED, int QMAX>
+static bool route_select_fits(int blocks) {
+    constexpr int kMaxDevices = 64;
+    static std::atomic<int> capacity[kMaxDevices];   // resident blocks; 0 unknown, -1 query failed
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return false;
+    int cap = capacity[dev].load(std::memory_order_relaxed);
+    if (cap == 0) {
+        int per_cu = 0;
+        cap = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, decode_route_select_kernel<SHARED, QMAX>, 256, 0) ==
+                          hipSuccess && per_cu > 0
+                  ? per_cu * device_cu_count(0)
+                  : -1;
+        capacity[dev].store(cap, std::memory_order_relaxed);
+    }
+    return cap >= blocks;
+}
+
+std::atomic<int> g_route_select_mode{0};   // 0 automatic, 1 separate route / top-k / sort kernels
 
 template <bool ROUTER, bool SHARED, int QMAX>
 static hipError_t run(const DecodeArgs& a, hipStream_t s) {
     const int T = a.T, R = T * kTop, RS = R + (SHARED ? T : 0);
     const int router_waves = ROUTER ? (SHARED ? kExperts + 1 : kExperts) * ((T + kTokenBatch - 1) / kTokenBatch) : 0;
     const int s1_waves = router_waves + T * 4;
-    timed_launch("route", decode_route_kernel<ROUTER, SHARED, QMAX>, dim3((s1_waves + 3) / 4), dim3(256), 0, s, a,
-                 router_waves);
-    hipError_t st = hipGetLastError();
-    if (st != hipSuccess) return st;
-    if (ROUTER) {
-        st = launch_topk(a.logits, kLogitStride, T, a.topk_w, a.topk_ids, SHARED ? a.logits + kExperts : nullptr,
-                         kLogitStride, SHARED ? a.shared_logit : nullptr, s);
+    hipError_t st;
+    bool fused = false;
+    if constexpr (ROUTER) {
+        const int fused_blocks = (s1_waves + 3) / 4;
+        if (fused_blocks <= kDecodeRouteMaxBlocks && g_route_select_mode.load(std::memory_order_relaxed) == 0 &&
+            route_select_fits<SHARED, QMAX>(fused_blocks)) {
+            timed_launch("route_select", decode_route_select_kernel<SHARED, QMAX>, dim3(fused_blocks), dim3(256), 0, s,
+                         a, router_waves);
+            st = hipGetLastError();
+            if (st != hipSuccess) return st;
+            fused = true;
+        }
+    }
+    if (!fused) {
+        timed_launch("route", decode_route_kernel<ROUTER, SHARED, QMAX>, dim3((s1_waves + 3) / 4), dim3(256), 0, s, a,
+                     router_waves);
+        st = hipGetLastError();
+        if (st != hipSuccess) return st;
+        if (ROUTER) {
+            st = launch_topk(a.logits, kLogitStride, T, a.topk_w, a.topk_ids, SHARED ? a.logits + kExperts : nullptr,
+                             kLogitStride, SHARED ? a.shared_logit : nullptr, s);
+            if (st != hipSuccess) return st;
+        }
+        timed_launch("sort", decode_sort_kernel<SHARED, ROUTER>, dim3(1), dim3(512), 0, s, a, ROUTER ? a.topk_ids : a.ids_in);
+        st = hipGetLastError();
         if (st != hipSuccess) return st;
     }
-    timed_launch("sort", decode_sort_kernel<SHARED>, dim3(1), dim3(512), 0, s, a, ROUTER ? a.topk_ids : a.ids_in);
-    st = hipGetLastError();
-    if (st != hipSuccess) return st;
     // segments: at most one per non-empty bank plus one per extra 8 routes
     const int maxseg = min(R, kExperts) + (SHARED ? 1 : 0) + (R + (SHARED ? T : 0)) / kSegRoutes;
     timed_launch("gateup", decode_gateup_kernel<SHARED>, dim3(kInter / 32, maxseg), dim3(512), 0, s, a);

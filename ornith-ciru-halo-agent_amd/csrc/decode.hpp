@@ -24,8 +24,19 @@ constexpr int kLayer1Spread = 8;
 constexpr int kLayer1Middle = kLayer1Spread * 320;
 constexpr int kLayer1Arrive = kLayer1Middle + (kTop + 1) * kInter;
 constexpr int kLayer1Words = kLayer1Arrive + kLayer1Spread * kLayer1Blocks;
-// sticky flag of this library: a single-token layer block gave up waiting for
-// another block's hand-off (the grid was not resident at once)
+// Hand-off words of the 2..32-token route kernel (decode.hip), in the same
+// region: logit (row e, token t) at kDecodeRouteLogit + 32 e + t (a router
+// wave's 8 tokens are one 64-byte run), token t's expert id of slot s at
+// kDecodeRouteIds + 8 t + s, block L's arrival word at kDecodeRouteArrive + 8 L.
+constexpr int kDecodeRouteLogit = 0;
+constexpr int kDecodeRouteIds = kDecodeRouteLogit + (kExperts + 1) * kDecodeMaxTokens;
+constexpr int kDecodeRouteArrive = kDecodeRouteIds + kDecodeMaxTokens * kTop;
+constexpr int kDecodeRouteMaxBlocks = 320;
+constexpr int kDecodeRouteWords = kDecodeRouteArrive + 8 * kDecodeRouteMaxBlocks;
+constexpr int kHandoffWords = kLayer1Words > kDecodeRouteWords ? kLayer1Words : kDecodeRouteWords;
+// sticky flag of this library: a block of a one-launch kernel (single-token
+// layer, 2..32-token route) gave up waiting for another block's hand-off (the
+// grid was not resident at once)
 constexpr uint32_t kFlagHandoffTimeout = 64;
 
 struct DecodeArgs {
@@ -51,7 +62,8 @@ struct DecodeArgs {
     uint32_t* m_words; uint16_t* m_scales; int32_t* m_sums;   // quantised middle rows (2..32 tokens)
     float* route_out;                  // [RS, 2048]
     float* logits; Segment* segments; int32_t* routes; int32_t* nseg;
-    // single-token layer kernel: call sequence number and tagged hand-off words
+    // one-launch kernels (single-token layer, 2..32-token route): call
+    // sequence number and tagged hand-off words (kHandoffWords)
     uint32_t* l1_seq; uint64_t* l1_words;
     // outputs
     float* final_f32; uint16_t* out; uint16_t* shared_out; uint16_t* layer_out;
@@ -63,6 +75,9 @@ void carve_decode(void* base, DecodeArgs& a);
 hipError_t launch_decode(const DecodeArgs& a, bool router, bool shared, int qmax, hipStream_t s);
 // single-token path: 0 automatic (one launch where the grid is resident), 1 three kernels
 extern std::atomic<int> g_single_token_mode;
+// 2..32 tokens with the router: 0 automatic (route, top-k and sort in one launch
+// where the grid is resident), 1 three kernels
+extern std::atomic<int> g_route_select_mode;
 hipError_t launch_decode1(const DecodeArgs& a, bool router, bool shared, int qmax, hipStream_t s);
 
 }  // namespace ornith

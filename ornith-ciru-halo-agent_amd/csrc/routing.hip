@@ -372,15 +372,7 @@ __device__ __forceinline__ int route_bank(const int32_t* ids, int r, int R, uint
     return -1;
 }
 
-__device__ __forceinline__ int wave_inclusive_scan(int v) {
-    const int lane = threadIdx.x & 63;
-#pragma unroll
-    for (int d = 1; d < 64; d <<= 1) {
-        const int u = __shfl_up(v, d, 64);
-        if (lane >= d) v += u;
-    }
-    return v;
-}
+__device__ __forceinline__ int wave_inclusive_scan(int v) { return wave_prefix_sum(v); }
 
 size_t permute_scratch_bytes(int Rcap, int Tcap) {
     const size_t rall = size_t(Rcap) + size_t(Tcap);

@@ -8,6 +8,7 @@
 // kernels where the selection latency is on the critical path).
 #pragma once
 #include "common.hpp"
+#include "handoff.hpp"
 
 namespace ornith {
 
@@ -23,10 +24,12 @@ __device__ __forceinline__ void cswap(uint32_t& ka, int& ia, uint32_t& kb, int& 
 // wave, in the declared order (routing.hip): lane l forms the fma chain over
 // chunks l, l+64, l+128, l+192, then the butterfly; + bias.  Every token row
 // is loaded before the first fma (rows past T repeat the last token and are
-// not written), so the loads overlap.
+// not written), so the loads overlap.  With `words`, token t0 + t's logit is
+// also published as tagged word word0 + t (handoff.hpp), by lane t.
 __device__ __forceinline__ void router_rows_wave(const uint16_t* __restrict__ x, int64_t stride, int T, int t0,
                                                  const uint16_t* __restrict__ wrow, float bias, bool has_bias,
-                                                 float* __restrict__ logits, int64_t logit_stride, int row) {
+                                                 float* __restrict__ logits, int64_t logit_stride, int row,
+                                                 uint64_t* words = nullptr, uint32_t seq = 0, uint32_t word0 = 0) {
     constexpr int kBatch = 8;
     const int lane = threadIdx.x & 63, nt = min(kBatch, T - t0);
     uint4 wv[4];
@@ -54,14 +57,17 @@ __device__ __forceinline__ void router_rows_wave(const uint16_t* __restrict__ x,
             }
         }
     }
+    float pub = 0.f;
 #pragma unroll
     for (int t = 0; t < kBatch; ++t) {
         if (t < nt) {
             float v = wave_butterfly_sum(acc[t]);
             if (has_bias) v = v + bias;
             if (lane == 0) logits[size_t(t0 + t) * logit_stride + row] = v;
+            if (lane == t) pub = v;
         }
     }
+    if (words && lane < nt) l1_put(words, word0 + lane, seq, __float_as_uint(pub));
 }
 
 // Softmax probabilities of one token as order keys: lane l holds experts l,

@@ -83,6 +83,7 @@ _PROTOTYPES = {
     'ornith_shared_fixed8_launch': ([_VP] * 9 + [_SZ] + [_VP] * 2 + [_INT] * 2 + [_VP], _INT),
     'ornith_mi355x_abi_version': ([], _INT),
     'ornith_mi355x_single_token_path': ([_INT], _INT),
+    'ornith_mi355x_decode_route_path': ([_INT], _INT),
     # dense (include/ornith_dense.h)
     'ornith_dense_g256_abi_version': ([], C.c_uint32),
     'ornith_dense_g256_get_layout': ([_INT] * 4 + [C.POINTER(DenseLayout)], _INT),
@@ -557,6 +558,17 @@ def single_token_path(path=None, tile=32):
     prev = lib(tile).ornith_mi355x_single_token_path(-1 if path is None else int(path))
     if prev < 0:
         raise ValueError(f'single-token path must be 0 or 1, got {path}')
+    return prev
+
+
+def decode_route_path(path=None, tile=32):
+    """Which kernels run the router, top-8 and sort of 2..32-token layer
+    calls, for the process: 0 one launch wherever its grid is resident at
+    once, 1 three kernels; None only queries.  Returns the previous setting.
+    Results are identical either way."""
+    prev = lib(tile).ornith_mi355x_decode_route_path(-1 if path is None else int(path))
+    if prev < 0:
+        raise ValueError(f'decode route path must be 0 or 1, got {path}')
     return prev
 
 
