@@ -52,11 +52,11 @@ MEASURED_TRAFFIC = {
     ('layer1', 1): 16731184, ('route1', 1): 1166652, ('gateup1', 1): 9949504, ('down1', 1): 5118494,
     ('route', 32): 2587638, ('topk', 32): 128301, ('sort', 32): 12911, ('gateup', 32): 176476796,
     ('quant_middle', 32): 804861, ('down', 32): 90919862, ('reduce', 32): 2591275,
-    ('router_act', 1120): 21187047, ('topk', 1120): 1395534, ('permute_scan', 1120): 774087,
+    ('topk', 1120): 1395534,
     ('permute_scatter', 1120): 335833, ('gateup_mfma', 1120): 189333643, ('quant_middle', 1120): 26020119,
     ('down_mfma', 1120): 169450349, ('reduce', 1120): 87580019,
-    ('router', 8192): 51037662, ('topk', 8192): 9612530, ('permute_scan', 8192): 5299835,
-    ('permute_scatter', 8192): 1546389, ('act', 8192): 50822386, ('gateup_mfma', 8192): 623576104,
+    ('topk', 8192): 9612530,
+    ('permute_scatter', 8192): 1546389, ('gateup_mfma', 8192): 623576104,
     ('quant_middle', 8192): 189712996, ('down_mfma', 8192): 844245682, ('reduce', 8192): 639966906,
 }
 
@@ -80,8 +80,10 @@ def kernel_cost(name, T, unique):
         return 'mfma', 2 * routes * 1024 * 2048, INT8_PEAK_TOPS, 'TFLOP/s'
     if name == 'down_mfma':
         return 'mfma', 2 * routes * 2048 * 512, INT8_PEAK_TOPS, 'TFLOP/s'
-    if name in ('router', 'router_act'):      # exact K=1 fp32 matrix steps (the shared-gate row on the VALU)
+    if name == 'router':      # exact K=1 fp32 matrix steps (the shared-gate row on the VALU)
         return 'mfma', 2 * T * 257 * 2048, FP32_PEAK_TFLOPS, 'TFLOP/s'
+    if name == 'permute_scan_act':  # the scan's block counts are noise beside the gate-input quantisation
+        return 'hbm', T * 2048 * 2 + T * 2048 + T * 8 * (2 + 4), HBM_PEAK_GBS, 'GB/s'
     return 'hbm', T * 2048 * 2, HBM_PEAK_GBS, 'GB/s'
 
 

@@ -8,8 +8,8 @@ namespace ornith {
 // Quarter-wave groups (common.hpp): each 16-lane quarter owns one 256-group,
 // lane l holding its 16 values k = quarter_base(l) + i; four groups per wave
 // (flattened (row, group) index 4 * wave + quarter).
-// Block `block` of the grid (four waves); also run by the router launch of
-// the layer path, whose trailing blocks do this work (routing.hip).
+// Block `block` of the grid (four waves); also run by trailing blocks of the
+// permutation's bank-scan launch (routing.hip).
 template <int QMAX>
 __device__ __forceinline__ void act_bf16_block(int block, const uint16_t* __restrict__ x, int64_t stride, int rows,
                                                int groups, const int32_t* __restrict__ ids,

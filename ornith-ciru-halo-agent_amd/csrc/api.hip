@@ -23,7 +23,7 @@ constexpr int kGateN = 2 * kInter, kDownN = kHidden;
 // Workspace plan shared by the routed, shared-slot and whole-layer entries.
 struct RoutedPlan {
     OrnithRoutedDirectLayout l;
-    size_t permute, logits, decode;
+    size_t permute, logits, router_split, decode;
 };
 
 RoutedPlan routed_plan(int Tcap, bool shared_slot, bool layer) {
@@ -47,6 +47,7 @@ RoutedPlan routed_plan(int Tcap, bool shared_slot, bool layer) {
     add(p.l.final_f32, t * kHidden * 4);
     add(p.permute, permute_scratch_bytes(int(t * kTop), shared_slot ? int(t) : 0));
     if (layer) add(p.logits, t * kLogitStride * 4);
+    if (layer) add(p.router_split, router_split_bytes(Tcap));
     add(p.decode, decode_scratch_bytes());
     p.l.workspace_bytes = cursor;
     return p;
@@ -59,15 +60,17 @@ hipError_t run_routed(const RoutedPlan& p, void* ws, const void* input, const fl
                       const void* sg_codes, const void* sg_meta, const void* sd_codes, const void* sd_meta,
                       const uint16_t* shared_logit, const float* silu, const uint16_t* sigmoid, int qmax,
                       uint16_t* out, uint16_t* shared_out, uint16_t* layer_out, uint32_t* sticky, int T, int Tcap,
-                      hipStream_t s, bool act_done = false, bool counted = false) {
+                      hipStream_t s, bool counted = false) {
     const bool shared = sg_codes != nullptr;
     const int R = T * kTop, RS = R + (shared ? T : 0);
     const PermuteScratch ps = carve_permute(at<void>(ws, p.permute), Tcap * kTop, shared ? Tcap : 0);
-    TRY(launch_permute(ids, R, T, shared, ps, sticky, 64, s, counted));
     auto gw = at<uint32_t>(ws, p.l.gate_low);
     auto gs = at<uint16_t>(ws, p.l.gate_scales);
     auto gsum = at<int32_t>(ws, p.l.gate_sums);
-    if (!act_done)
+    // the A8 gate input rides on the bank-scan launch (the A4 one has its own)
+    const ActJob act{static_cast<const uint16_t*>(input), T, shared ? nullptr : ids, gw, gs, gsum};
+    TRY(launch_permute(ids, R, T, shared, ps, sticky, 64, s, counted, qmax == 127 ? &act : nullptr));
+    if (qmax != 127)
         TRY(launch_act_bf16(static_cast<const uint16_t*>(input), kHidden, T, kHidden, qmax, shared ? nullptr : ids, gw,
                             gs, gsum, sticky, kFlagNonfiniteInput, kFlagInvalidActivation, s));
     const int max_tiles = (RS + 63) / 64 + (R < kExperts ? R : kExperts) + (shared ? 1 : 0);
@@ -360,31 +363,23 @@ extern "C" hipError_t ornith_moe_layer_launch(
                           static_cast<const uint16_t*>(sigmoid), 127, nullptr, nullptr, static_cast<uint16_t*>(output),
                           static_cast<uint32_t*>(flags), T, stream, router_w, bias, shared_gate_w,
                           static_cast<float*>(topk_weights), static_cast<int32_t*>(topk_ids));
-    // The router launch can also quantise the gate input (every token is live
-    // with the shared expert): same words as launch_act_bf16.
-    const bool fused = router_act_pays(T);
     auto logits = at<float>(workspace, p.logits);
+    // the last token groups' logits may be completed by the top-k launch
+    float* split = router_split_groups(T) ? at<float>(workspace, p.router_split) : nullptr;
     // top-8 also counts the routed banks per 16-token block (permutation step 1)
     const PermuteScratch ps = carve_permute(at<void>(workspace, p.permute), Tcap * kTop, Tcap);
-    if (fused) {
-        TRY(launch_router_act(static_cast<const uint16_t*>(input), T, static_cast<const uint16_t*>(router_w),
-                              static_cast<const uint16_t*>(shared_gate_w), static_cast<const float*>(bias), logits,
-                              kLogitStride, at<uint32_t>(workspace, p.l.gate_low),
-                              at<uint16_t>(workspace, p.l.gate_scales), at<int32_t>(workspace, p.l.gate_sums),
-                              static_cast<uint32_t*>(flags), stream));
-    } else {
-        TRY(launch_router(static_cast<const uint16_t*>(input), kHidden, T, static_cast<const uint16_t*>(router_w),
-                          static_cast<const uint16_t*>(shared_gate_w), static_cast<const float*>(bias), logits,
-                          kLogitStride, stream));
-    }
+    TRY(launch_router(static_cast<const uint16_t*>(input), kHidden, T, static_cast<const uint16_t*>(router_w),
+                      static_cast<const uint16_t*>(shared_gate_w), static_cast<const float*>(bias), logits,
+                      kLogitStride, stream, split));
     TRY(launch_topk(logits, kLogitStride, T, static_cast<float*>(topk_weights), static_cast<int32_t*>(topk_ids),
-                    logits + kExperts, kLogitStride, static_cast<uint16_t*>(shared_logit), stream, ps.block_counts));
+                    logits + kExperts, kLogitStride, static_cast<uint16_t*>(shared_logit), stream, ps.block_counts,
+                    split, static_cast<const float*>(bias)));
     return run_routed(p, workspace, input, static_cast<const float*>(topk_weights),
                       static_cast<const int32_t*>(topk_ids), gate_codes, gate_meta, down_codes, down_meta,
                       shared_gate_codes, shared_gate_meta, shared_down_codes, shared_down_meta,
                       static_cast<const uint16_t*>(shared_logit), static_cast<const float*>(silu),
                       static_cast<const uint16_t*>(sigmoid), 127, nullptr, nullptr, static_cast<uint16_t*>(output),
-                      static_cast<uint32_t*>(flags), T, Tcap, stream, fused, true);
+                      static_cast<uint32_t*>(flags), T, Tcap, stream, true);
 }
 
 // ---- shared expert with the reference's fixed8 semantics --------------------------

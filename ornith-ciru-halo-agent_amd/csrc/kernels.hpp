@@ -53,28 +53,40 @@ hipError_t launch_act_middle(const float* gate_y, int RS, int R, const int32_t* 
 // ---- routing ---------------------------------------------------------------
 constexpr int kRouterRowsMaxTokens = 256;      // wave-per-row router up to here, token-tiled beyond
 // Router logits [T, 256 (+1)] in the declared order; shared_w (nullable) adds
-// column 256, the shared-expert gate logit.
+// column 256, the shared-expert gate logit.  split_sums (nullable,
+// router_split_bytes): for T > kRouterRowsMaxTokens the last
+// router_split_groups(T) token groups run as eighth-tile units whose partial
+// sums launch_topk completes (their logits are final only after it).
 hipError_t launch_router(const uint16_t* x, int64_t stride, int T, const uint16_t* w, const uint16_t* shared_w,
-                         const float* bias, float* logits, int64_t logit_stride, hipStream_t s);
-// The same router logits for T > 256 tokens (contiguous x, shared row
-// present) in one launch with the A8 gate-input quantisation of x
-// (launch_act_bf16 with ids == nullptr).
-hipError_t launch_router_act(const uint16_t* x, int T, const uint16_t* w, const uint16_t* shared_w, const float* bias,
-                             float* logits, int64_t logit_stride, uint32_t* words, uint16_t* scales, int32_t* sums,
-                             uint32_t* sticky, hipStream_t s);
-// Whether the fused launch beats router + activation launches at T tokens.
-bool router_act_pays(int T);
+                         const float* bias, float* logits, int64_t logit_stride, hipStream_t s,
+                         float* split_sums = nullptr);
+int router_split_groups(int T);
+size_t router_split_bytes(int Tcap);
 // block_counts != nullptr (the layer path) also does the permutation's count
 // step: launch_permute(..., counted = true) then skips it.
+// split_sums (with bias): the logits of the last router_split_groups(T) token
+// groups are completed here from the router's eighth-tile sums (and written
+// back to logits).
 hipError_t launch_topk(const float* logits, int64_t logit_stride, int T, float* weights, int32_t* ids,
                        const float* shared_logit_f32, int64_t shared_stride, uint16_t* shared_logit_bf16,
-                       hipStream_t s, int32_t* block_counts = nullptr);
+                       hipStream_t s, int32_t* block_counts = nullptr, const float* split_sums = nullptr,
+                       const float* bias = nullptr);
+// The A8 gate-input quantisation of contiguous bf16 rows (launch_act_bf16 with
+// K = stride = kHidden, qmax 127): rows with no live id are skipped when ids
+// is given.
+struct ActJob {
+    const uint16_t* x; int rows; const int32_t* ids;
+    uint32_t* words; uint16_t* scales; int32_t* sums;
+};
 // Stable counting sort of route ids by bank.  Routes 0..R-1 use ids[r];
-// when with_shared, routes R..R+T-1 use the shared bank.
+// when with_shared, routes R..R+T-1 use the shared bank.  act (nullable):
+// that quantisation runs as trailing blocks of the bank-scan launch (its 64
+// blocks leave the rest of the chip idle).
 size_t permute_scratch_bytes(int Rcap, int Tcap);
 PermuteScratch carve_permute(void* base, int Rcap, int Tcap);
 hipError_t launch_permute(const int32_t* ids, int R, int T, bool with_shared, const PermuteScratch& p,
-                          uint32_t* sticky, int mfma_rows, hipStream_t s, bool counted = false);
+                          uint32_t* sticky, int mfma_rows, hipStream_t s, bool counted = false,
+                          const ActJob* act = nullptr);
 
 // ---- projections -----------------------------------------------------------
 enum class Out { Routed, Dense };

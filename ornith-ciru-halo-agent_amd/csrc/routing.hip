@@ -60,6 +60,103 @@ constexpr int kRmGroups = kExperts / kRmTile;              // expert groups (til
 constexpr int kRmQuarter = kHidden / 4;                    // k per staged quarter
 constexpr int kRmRowBytes = 2 * kRmQuarter + 16;           // staged row + a 16-byte pad (conflict-free columns)
 
+// Token groups past full_tg (the tiles that would otherwise make a short last
+// round on a few CUs) are split into units of one eighth of a tile: unit
+// (tile, j) forms lane partials 8j..8j+7 of the tile's 32 x 32 logits and
+// sums them as ((P0 + P1) + (P2 + P3)) + ((P4 + P5) + (P6 + P7)) -- levels 1-3
+// of the balanced tree -- into split_sums[tile][j][token][expert]; the top-k
+// kernel adds levels 4-6 in the same order, then the bias.  Units spread over
+// every block (unit u = blk, blk + nblk, ...).  The unit's rows are staged
+// whole (its 32 chunks of each of the 64 rows, 32 KB) piece-major, so the
+// column reads are conflict-free; waves 0-3 carry the partials (two per
+// step, as in the tiles), and for j == 0 waves 4-7 form the shared-gate
+// logits of tokens 4 eg .. 4 eg + 3 of the tile straight from memory.
+__device__ __forceinline__ void router_split_units(int blk, int nblk, const uint16_t* __restrict__ x, int64_t stride,
+                                                   int T, const uint16_t* __restrict__ w,
+                                                   const uint16_t* __restrict__ shared_w,
+                                                   float* __restrict__ logits, int64_t logit_stride, int ntg,
+                                                   int full_tg, float* __restrict__ split_sums, uint8_t* lds0,
+                                                   uint8_t* lds1) {
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int q = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int b = lane >> 5, i = lane & 31;
+    const int nunits = 64 * (ntg - full_tg);
+    for (int u = blk; u < nunits; u += nblk) {
+        const int tile = u >> 3, j = u & 7;                // tile = 8 (tg - full_tg) + eg
+        const int tg = full_tg + (tile >> 3), eg = tile & 7, e0 = eg * kRmTile, t0 = tg * kRmTile;
+        // piece p = 8 jq + c (chunk 8j + c of quarter jq) of row r at (64 p + r) * 16;
+        // wave q stages pieces 2q, 2q + 1, lane = row
+        {
+            const uint16_t* row = lane < kRmTile ? w + size_t(e0 + lane) * kHidden
+                                                 : x + size_t(min(t0 + lane - kRmTile, T - 1)) * stride;
+#pragma unroll
+            for (int n = 0; n < 2; ++n) {
+                const int p = 2 * q + n, jq = p >> 3, cc = p & 7;
+                __builtin_amdgcn_global_load_lds(row + kRmQuarter * jq + 8 * (8 * j + cc),
+                                                 (lds_void*)(lds0 + 1024 * p), 16, 0, 0);
+            }
+        }
+        __syncthreads();
+        if (q < 4) {
+            // wave q: partials 8j + 2q + b, chunk 2q + b of each quarter
+            f32x32 acc = f32x32{};
+#pragma unroll
+            for (int jq = 0; jq < 4; ++jq) {
+                const int p = 8 * jq + 2 * q + b;
+                const uint4 wv = *reinterpret_cast<const uint4*>(lds0 + (64 * p + i) * 16);
+                const uint4 xv = *reinterpret_cast<const uint4*>(lds0 + (64 * p + kRmTile + i) * 16);
+                const uint32_t uw[4] = {wv.x, wv.y, wv.z, wv.w};
+                const uint32_t ux[4] = {xv.x, xv.y, xv.z, xv.w};
+#pragma unroll
+                for (int h = 0; h < 4; ++h) {
+                    acc = __builtin_amdgcn_mfma_f32_32x32x1f32(__uint_as_float(uw[h] << 16),
+                                                               __uint_as_float(ux[h] << 16), acc, 0, 0, 0);
+                    acc = __builtin_amdgcn_mfma_f32_32x32x1f32(__uint_as_float(uw[h] & 0xffff0000u),
+                                                               __uint_as_float(ux[h] & 0xffff0000u), acc, 0, 0, 0);
+                }
+            }
+            // level 1 (the step's two blocks), then the [wave][token][expert] exchange
+            float* sS = reinterpret_cast<float*>(lds1);
+            const int jt = lane & 31;
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                const int grp = 2 * g + b;
+                *reinterpret_cast<float4*>(sS + (q * kRmTile + jt) * kRmTile + 4 * (grp ^ (jt & 7))) =
+                    make_float4(acc[4 * g] + acc[16 + 4 * g], acc[4 * g + 1] + acc[17 + 4 * g],
+                                acc[4 * g + 2] + acc[18 + 4 * g], acc[4 * g + 3] + acc[19 + 4 * g]);
+            }
+        } else if (q < 8 && j == 0 && shared_w) {
+            // shared-gate logit of token 4 eg + (q - 4) of the tile, lane = partial
+            const int t = t0 + 4 * eg + (q - 4);
+            const uint16_t* xr = x + size_t(min(t, T - 1)) * stride;
+            float sacc = 0.f;
+#pragma unroll
+            for (int jq = 0; jq < 4; ++jq) {
+                float xf[8], wf[8];
+                bf16x8_to_f32(*reinterpret_cast<const uint4*>(xr + kRmQuarter * jq + 8 * lane), xf);
+                bf16x8_to_f32(*reinterpret_cast<const uint4*>(shared_w + kRmQuarter * jq + 8 * lane), wf);
+#pragma unroll
+                for (int k = 0; k < 8; ++k) sacc = __builtin_fmaf(xf[k], wf[k], sacc);
+            }
+            const float v = wave_butterfly_sum(sacc);
+            if (lane == 0 && t < T) logits[size_t(t) * logit_stride + kExperts] = v;
+        }
+        __syncthreads();
+        {
+            // levels 2-3 over the four waves; thread = (expert er, token tc)
+            const float* sS = reinterpret_cast<const float*>(lds1);
+            const int er = tid & 31, tc = (tid >> 5) & 31;
+            const int off = tc * kRmTile + 4 * ((er >> 2) ^ (tc & 7)) + (er & 3);
+            if (tid < kRmTile * kRmTile) {
+                const float v = (sS[off] + sS[kRmTile * kRmTile + off]) +
+                                (sS[2 * kRmTile * kRmTile + off] + sS[3 * kRmTile * kRmTile + off]);
+                split_sums[(size_t(tile) * 8 + j) * (kRmTile * kRmTile) + tc * kRmTile + er] = v;
+            }
+        }
+        __syncthreads();                                  // both buffers free for the next unit
+    }
+}
+
 // Persistent: block b runs on XCD b % 8 and walks that XCD's tiles (token
 // groups tg = x (mod 8), all eight expert groups, so a token group's x rows
 // stay in the XCD's L2), tile c, c + B, c + 2B, ... of the XCD's list for
@@ -69,7 +166,8 @@ constexpr int kRmRowBytes = 2 * kRmQuarter + 16;           // staged row + a 16-
 __device__ __forceinline__ void router_mfma_run(int blk, int nblk, const uint16_t* __restrict__ x, int64_t stride,
                                                 int T, const uint16_t* __restrict__ w,
                                                 const uint16_t* __restrict__ shared_w, const float* __restrict__ bias,
-                                                float* __restrict__ logits, int64_t logit_stride, int ntg) {
+                                                float* __restrict__ logits, int64_t logit_stride, int ntg, int full_tg,
+                                                float* __restrict__ split_sums) {
     // two buffers (separate arrays, so the compiler sees that loads into one
     // do not alias reads of the other) of one K quarter of a tile's 32
     // expert rows (rows 0..31) and 32 token rows (rows 32..63), bf16, rows
@@ -80,8 +178,7 @@ __device__ __forceinline__ void router_mfma_run(int blk, int nblk, const uint16_
     __shared__ __align__(16) uint8_t lshared[2 * kHidden];
     static_assert(kRmWaves * kRmTile * kRmTile * 4 <= kBuf, "Sq exchange fits a buffer");
     const int xcd = blk & 7, c = blk >> 3, B = nblk >> 3;
-    const int ntiles = 8 * ((ntg - xcd + 7) / 8);              // this XCD's tiles: 8 per token group
-    if (c >= ntiles) return;
+    const int ntiles = 8 * ((full_tg - xcd + 7) / 8);          // this XCD's whole tiles: 8 per token group
     const int tid = threadIdx.x, lane = tid & 63;
     const int q = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave-uniform: row pointers stay scalar
     const int b = lane >> 5, i = lane & 31;
@@ -103,7 +200,7 @@ __device__ __forceinline__ void router_mfma_run(int blk, int nblk, const uint16_
     // this lane's operands: expert row i and token row i, chunk 4q + b (first
     // step) and 4q + 2 + b (second step) of the quarter
     const int abase = i * kRmRowBytes + 16 * (4 * q + b), bbase = (kRmTile + i) * kRmRowBytes + 16 * (4 * q + b);
-    stage(c, 0, lds0);
+    if (c < ntiles) stage(c, 0, lds0);
     if (has_shared && q < 4)
         __builtin_amdgcn_global_load_lds(shared_w + kRmQuarter * q + 8 * lane, (lds_void*)(lshared + 1024 * q), 16, 0,
                                          0);
@@ -191,37 +288,21 @@ __device__ __forceinline__ void router_mfma_run(int blk, int nblk, const uint16_
         }
         __syncthreads();                                  // buffer 1 free for the next tile's second quarter
     }
+    if (split_sums) router_split_units(blk, nblk, x, stride, T, w, shared_w, logits, logit_stride, ntg, full_tg,
+                                       split_sums, lds0, lds1);
 }
 
+// full_tg < ntg: token groups full_tg .. ntg - 1 run as eighth-tile units
+// into split_sums.
 __global__ __launch_bounds__(kRmWaves * 64) void router_mfma_kernel(const uint16_t* __restrict__ x, int64_t stride, int T,
                                                                      const uint16_t* __restrict__ w,
                                                                      const uint16_t* __restrict__ shared_w,
                                                                      const float* __restrict__ bias,
                                                                      float* __restrict__ logits, int64_t logit_stride,
-                                                                     int ntg) {
-    router_mfma_run(int(blockIdx.x), int(gridDim.x), x, stride, T, w, shared_w, bias, logits, logit_stride, ntg);
-}
-
-// Router tiles followed by the activation quantisation of the same rows (the
-// layer path with the shared expert, where every token is live, so the gate
-// input does not wait for routing).  An activation block of 16 waves does the
-// work of four 4-wave act_bf16_block indices.
-__global__ __launch_bounds__(kRmWaves * 64) void router_mfma_act_kernel(const uint16_t* __restrict__ x, int T,
-                                                                         const uint16_t* __restrict__ w,
-                                                                         const uint16_t* __restrict__ shared_w,
-                                                                         const float* __restrict__ bias,
-                                                                         float* __restrict__ logits,
-                                                                         int64_t logit_stride, int ntg,
-                                                                         int router_blocks,
-                                                                         uint32_t* __restrict__ words,
-                                                                         uint16_t* __restrict__ scales,
-                                                                         int32_t* __restrict__ sums, uint32_t* sticky) {
-    const int b = int(blockIdx.x);
-    if (b < router_blocks)
-        router_mfma_run(b, router_blocks, x, kHidden, T, w, shared_w, bias, logits, logit_stride, ntg);
-    else
-        act_bf16_block<127>(4 * (b - router_blocks) + (int(threadIdx.x) >> 8), x, kHidden, T, kHidden / kGroup,
-                            nullptr, words, scales, sums, sticky, kFlagNonfiniteInput, kFlagInvalidActivation);
+                                                                     int ntg, int full_tg,
+                                                                     float* __restrict__ split_sums) {
+    router_mfma_run(int(blockIdx.x), int(gridDim.x), x, stride, T, w, shared_w, bias, logits, logit_stride, ntg,
+                    full_tg, split_sums);
 }
 
 // One wave per (router row, batch of 8 tokens): the choice for small and
@@ -248,7 +329,7 @@ static int router_mfma_blocks(int ntg) {
 }
 
 hipError_t launch_router(const uint16_t* x, int64_t stride, int T, const uint16_t* w, const uint16_t* shared_w,
-                         const float* bias, float* logits, int64_t logit_stride, hipStream_t s) {
+                         const float* bias, float* logits, int64_t logit_stride, hipStream_t s, float* split_sums) {
     if (T <= 0) return hipSuccess;
     if (T <= kRouterRowsMaxTokens) {
         const int nrows = kExperts + (shared_w ? 1 : 0);
@@ -258,37 +339,30 @@ hipError_t launch_router(const uint16_t* x, int64_t stride, int T, const uint16_
         return hipGetLastError();
     }
     const int ntg = (T + kRmTile - 1) / kRmTile;
+    const int full_tg = ntg - (split_sums ? router_split_groups(T) : 0);
     timed_launch("router", router_mfma_kernel, dim3(router_mfma_blocks(ntg)), dim3(kRmWaves * 64), 0, s, x, stride, T,
-                 w, shared_w, bias, logits, logit_stride, ntg);
+                 w, shared_w, bias, logits, logit_stride, ntg, full_tg, full_tg < ntg ? split_sums : nullptr);
     return hipGetLastError();
 }
 
 // The tile kernel holds one block per CU (its LDS), each walking its share of
-// the tiles.  The fused launch pays when the activation blocks fit the CUs
-// left idle by the tiles' last round (an activation block takes under half a
-// tile's time).
-bool router_act_pays(int T) {
-    if (T <= kRouterRowsMaxTokens) return false;
-    const int cus = device_cu_count(0);
-    if (cus <= 0) return false;
-    const int tiles = ((T + kRmTile - 1) / kRmTile) * kRmGroups;
-    const int tail = tiles % cus;
-    const int idle = tail ? cus - tail : 0;
-    const int act_blocks = ((T * (kHidden / kGroup) + 3) / 4 + kRmWaves - 1) / kRmWaves;
-    return act_blocks <= 2 * idle;
+// the tiles.  When the token groups past the last whole round are few (at
+// most 2 eighth-tile units per block), they go to units over every block,
+// so the launch ends about a unit after its last whole round (a unit costs
+// its loads' latency besides an eighth of a tile's products, so larger
+// remainders stay whole tiles).
+int router_split_groups(int T) {
+    if (T <= kRouterRowsMaxTokens) return 0;
+    const int cus = device_cu_count(), per = cus / 8, ntg = (T + kRmTile - 1) / kRmTile;
+    if (per <= 0 || ntg < per) return 0;
+    const int left = ntg % per;
+    return 64 * left <= 2 * cus ? left : 0;
 }
 
-hipError_t launch_router_act(const uint16_t* x, int T, const uint16_t* w, const uint16_t* shared_w, const float* bias,
-                             float* logits, int64_t logit_stride, uint32_t* words, uint16_t* scales, int32_t* sums,
-                             uint32_t* sticky, hipStream_t s) {
-    if (T <= kRouterRowsMaxTokens || !shared_w) return hipErrorInvalidValue;
-    const int ntg = (T + kRmTile - 1) / kRmTile;
-    const int router_blocks = router_mfma_blocks(ntg);
-    const int act_waves = (T * (kHidden / kGroup) + 3) / 4;
-    const int act_blocks = (act_waves + kRmWaves - 1) / kRmWaves;
-    timed_launch("router_act", router_mfma_act_kernel, dim3(router_blocks + act_blocks), dim3(kRmWaves * 64), 0, s, x,
-                 T, w, shared_w, bias, logits, logit_stride, ntg, router_blocks, words, scales, sums, sticky);
-    return hipGetLastError();
+size_t router_split_bytes(int Tcap) {
+    if (Tcap <= kRouterRowsMaxTokens) return 0;
+    const int groups = std::max(1, 2 * device_cu_count() / 64);
+    return size_t(groups) * 64 * kRmTile * kRmTile * sizeof(float);
 }
 
 // ---------------------------------------------------------------------------
@@ -303,11 +377,13 @@ hipError_t launch_router_act(const uint16_t* x, int T, const uint16_t* w, const 
 // tokens (block_counts[blockIdx.x][bank], the count step of the permutation;
 // WAVES is then its 16-token block).
 template <int WAVES, bool COUNT>
-__global__ __launch_bounds__(64 * WAVES) void topk_kernel(const float* __restrict__ logits, int64_t logit_stride, int T,
+__global__ __launch_bounds__(64 * WAVES) void topk_kernel(float* __restrict__ logits, int64_t logit_stride, int T,
                                                           float* __restrict__ weights, int32_t* __restrict__ ids,
                                                           const float* __restrict__ shared_logit, int64_t shared_stride,
                                                           uint16_t* __restrict__ shared_bf16,
-                                                          int32_t* __restrict__ block_counts) {
+                                                          int32_t* __restrict__ block_counts,
+                                                          const float* __restrict__ split, int split_t0,
+                                                          const float* __restrict__ bias) {
     __shared__ __align__(16) uint64_t s_cand[WAVES][66];
     __shared__ uint2 s_sel[WAVES][kTop];
     __shared__ int s_hist[COUNT ? kExperts : 1];
@@ -319,8 +395,34 @@ __global__ __launch_bounds__(64 * WAVES) void topk_kernel(const float* __restric
     }
     if (t < T) {
         float v[4];
+        if (split && t >= split_t0) {
+            // levels 4-6 of the router's balanced tree over its eighth-tile sums, then the bias
+            // (all 32 sums and the bias loaded before any is used: one round trip)
+            const int tile0 = 8 * ((t - split_t0) / kRmTile), tl = t % kRmTile;
+            float p[4][8], bv[4] = {};
 #pragma unroll
-        for (int i = 0; i < 4; ++i) v[i] = logits[size_t(t) * logit_stride + lane + 64 * i];
+            for (int i = 0; i < 4; ++i) {
+                const int e = lane + 64 * i;
+                const float* S = split + size_t(tile0 + e / kRmTile) * 8 * (kRmTile * kRmTile) +
+                                 tl * kRmTile + e % kRmTile;
+#pragma unroll
+                for (int j = 0; j < 8; ++j) p[i][j] = S[j * (kRmTile * kRmTile)];
+            }
+            if (bias) {
+#pragma unroll
+                for (int i = 0; i < 4; ++i) bv[i] = bias[lane + 64 * i];
+            }
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                float lv = ((p[i][0] + p[i][1]) + (p[i][2] + p[i][3])) + ((p[i][4] + p[i][5]) + (p[i][6] + p[i][7]));
+                if (bias) lv = lv + bv[i];
+                v[i] = lv;
+                logits[size_t(t) * logit_stride + lane + 64 * i] = lv;
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) v[i] = logits[size_t(t) * logit_stride + lane + 64 * i];
+        }
         uint32_t k[4];
         softmax_keys(v, k);
         top8_rank_lds(k, s_cand[w], s_sel[w]);
@@ -344,15 +446,19 @@ __global__ __launch_bounds__(64 * WAVES) void topk_kernel(const float* __restric
 
 hipError_t launch_topk(const float* logits, int64_t logit_stride, int T, float* weights, int32_t* ids,
                        const float* shared_logit, int64_t shared_stride, uint16_t* shared_bf16, hipStream_t s,
-                       int32_t* block_counts) {
+                       int32_t* block_counts, const float* split_sums, const float* bias) {
     if (T <= 0) return hipSuccess;
+    const int split_groups = split_sums ? router_split_groups(T) : 0;
+    const float* split = split_groups ? split_sums : nullptr;
+    const int split_t0 = ((T + kRmTile - 1) / kRmTile - split_groups) * kRmTile;
+    float* lg = const_cast<float*>(logits);        // written back only for the split tokens
     if (block_counts)
         timed_launch("topk", topk_kernel<kPermTokens, true>, dim3((T + kPermTokens - 1) / kPermTokens),
-                     dim3(64 * kPermTokens), 0, s, logits, logit_stride, T, weights, ids, shared_logit, shared_stride,
-                     shared_bf16, block_counts);
+                     dim3(64 * kPermTokens), 0, s, lg, logit_stride, T, weights, ids, shared_logit, shared_stride,
+                     shared_bf16, block_counts, split, split_t0, bias);
     else
-        timed_launch("topk", topk_kernel<4, false>, dim3((T + 3) / 4), dim3(256), 0, s, logits, logit_stride, T,
-                     weights, ids, shared_logit, shared_stride, shared_bf16, block_counts);
+        timed_launch("topk", topk_kernel<4, false>, dim3((T + 3) / 4), dim3(256), 0, s, lg, logit_stride, T,
+                     weights, ids, shared_logit, shared_stride, shared_bf16, block_counts, split, split_t0, bias);
     return hipGetLastError();
 }
 
@@ -431,9 +537,9 @@ __global__ __launch_bounds__(kPermRoutes) void permute_count_kernel(const int32_
     for (int i = threadIdx.x; i < kExperts; i += kPermRoutes) block_counts[size_t(blockIdx.x) * kExperts + i] = cnt[i];
 }
 
-__global__ __launch_bounds__(256) void permute_bank_scan_kernel(int nblocks, int32_t* __restrict__ block_counts,
-                                                                int32_t* __restrict__ counts) {
-    const int bank = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+__device__ __forceinline__ void permute_bank_scan_block(int blk, int nblocks, int32_t* __restrict__ block_counts,
+                                                        int32_t* __restrict__ counts) {
+    const int bank = blk * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
     if (bank >= kExperts) return;
     constexpr int kRounds = 8;                       // 8 x 64 blocks = 8192 tokens
     int v[kRounds];
@@ -451,6 +557,24 @@ __global__ __launch_bounds__(256) void permute_bank_scan_kernel(int nblocks, int
         run += __shfl(incl, 63, 64);
     }
     if (lane == 0) counts[bank] = run;
+}
+
+__global__ __launch_bounds__(256) void permute_bank_scan_kernel(int nblocks, int32_t* __restrict__ block_counts,
+                                                                int32_t* __restrict__ counts) {
+    permute_bank_scan_block(int(blockIdx.x), nblocks, block_counts, counts);
+}
+
+// The bank scan's kExperts / 4 blocks, then the activation quantisation's
+// (act_bf16_block indices 0, 1, ...; neither part waits on the other).
+__global__ __launch_bounds__(256) void permute_bank_scan_act_kernel(int nblocks, int32_t* __restrict__ block_counts,
+                                                                    int32_t* __restrict__ counts, ActJob act,
+                                                                    uint32_t* sticky) {
+    const int b = int(blockIdx.x);
+    if (b < kExperts / 4)
+        permute_bank_scan_block(b, nblocks, block_counts, counts);
+    else
+        act_bf16_block<127>(b - kExperts / 4, act.x, kHidden, act.rows, kHidden / kGroup, act.ids, act.words,
+                            act.scales, act.sums, sticky, kFlagNonfiniteInput, kFlagInvalidActivation);
 }
 
 __global__ __launch_bounds__(256) void permute_scatter_kernel(const int32_t* __restrict__ ids, int T, int shared_routes,
@@ -554,7 +678,7 @@ __global__ __launch_bounds__(256) void permute_scatter_kernel(const int32_t* __r
 }
 
 hipError_t launch_permute(const int32_t* ids, int R, int T, bool with_shared, const PermuteScratch& p,
-                          uint32_t* sticky, int mfma_rows, hipStream_t s, bool counted) {
+                          uint32_t* sticky, int mfma_rows, hipStream_t s, bool counted, const ActJob* act) {
     if (R != T * kTop) return hipErrorInvalidValue;
     const int nblocks = (T + kPermTokens - 1) / kPermTokens;
     if (nblocks > 8 * 64) return hipErrorInvalidValue;
@@ -564,8 +688,15 @@ hipError_t launch_permute(const int32_t* ids, int R, int T, bool with_shared, co
         const hipError_t st = hipGetLastError();
         if (st != hipSuccess) return st;
     }
-    timed_launch("permute_scan", permute_bank_scan_kernel, dim3(kExperts / 4), dim3(256), 0, s, nblocks, p.block_counts,
-                 p.counts);
+    if (act) {
+        // act_bf16_block: four 4-group waves per block index
+        const int act_blocks = (act->rows * (kHidden / kGroup) + 15) / 16;
+        timed_launch("permute_scan_act", permute_bank_scan_act_kernel, dim3(kExperts / 4 + act_blocks), dim3(256), 0,
+                     s, nblocks, p.block_counts, p.counts, *act, sticky);
+    } else {
+        timed_launch("permute_scan", permute_bank_scan_kernel, dim3(kExperts / 4), dim3(256), 0, s, nblocks,
+                     p.block_counts, p.counts);
+    }
     hipError_t st = hipGetLastError();
     if (st != hipSuccess) return st;
     timed_launch("permute_scatter", permute_scatter_kernel, dim3(nblocks), dim3(256), 0, s, ids, T,
