@@ -129,11 +129,12 @@ __global__ __launch_bounds__(256, MODE == kModeDown ? 3 : 2) void prefill_mfma_k
     constexpr int KW = GS * 64;                               // activation words per row
     constexpr int NCB = GATEUP ? (2 * kInter) / kNT : kHidden / (kNT * NSUB);
     constexpr int NSTAGE = GS < 3 ? GS : 3;                   // A stages in LDS
+    constexpr int NSC = NSTAGE;                               // scale stages (with their A words)
     static_assert(GS >= 2, "two A stages are filled in the prologue");
     __shared__ __attribute__((aligned(16))) uint32_t sA[NSTAGE][kMT * 64];
-    __shared__ __attribute__((aligned(16))) float s_sa[NSTAGE][kMT];
-    __shared__ __attribute__((aligned(16))) float s_ss[NSTAGE][kMT];
-    __shared__ __attribute__((aligned(16))) float s_nb[BIAS ? NSTAGE : 1][kMT];   // -sa * kDotBias (exact)
+    __shared__ __attribute__((aligned(16))) float s_sa[NSC][kMT];
+    __shared__ __attribute__((aligned(16))) float s_ss[NSC][kMT];
+    __shared__ __attribute__((aligned(16))) float s_nb[BIAS ? NSC : 1][kMT];   // -sa * kDotBias (exact)
     __shared__ int s_route[kMT];
     __shared__ float s_bv[HEAD ? 4 : 1][kMT];                 // head: per-wave row best
     __shared__ int s_bi[HEAD ? 4 : 1][kMT];
@@ -223,27 +224,32 @@ __global__ __launch_bounds__(256, MODE == kModeDown ? 3 : 2) void prefill_mfma_k
 
     // ---- A: activation words of group g, 64 bytes per lane ----
     const uint32_t* a_src = a.act_words + size_t(act_row(a_r, route_a)) * KW + 16 * a_part;
+    // register k of the staging thread holds piece 4 a_part + (k + a_part) % 4
+    // of its row: the 8 lanes of each LDS store phase (2 rows x 4 parts) then
+    // hit 8 distinct 16-byte bank groups
+    auto a_piece = [&](int k) { return (k + a_part) & 3; };
     const size_t sa_base = size_t(act_row(tid & 63, route_s)) * GS;
     u32x4 ra[1][4];                 // one register slot: A(g) is loaded one step before its LDS store
     uint32_t rsa[1];
     int rsum[1];
     auto load_a = [&](int g, int slot) {
 #pragma unroll
-        for (int k = 0; k < 4; ++k) ra[slot][k] = *reinterpret_cast<const u32x4*>(a_src + g * 64 + 4 * k);
+        for (int k = 0; k < 4; ++k) ra[slot][k] = *reinterpret_cast<const u32x4*>(a_src + g * 64 + 4 * a_piece(k));
         rsa[slot] = a.act_scales[sa_base + g];
         rsum[slot] = a.act_sums[sa_base + g];
     };
-    auto store_a = [&](int slot, int stage) {
+    auto store_a = [&](int slot, int stage, int g) {
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
-            const int piece = (4 * a_part + k) ^ (a_r & 15);
+            const int piece = (4 * a_part + a_piece(k)) ^ (a_r & 15);
             *reinterpret_cast<u32x4*>(&sA[stage][a_r * 64 + 4 * piece]) = ra[slot][k];
         }
         if (tid < kMT) {
+            const int sc = g % NSC;
             const float sa = f16_bits_to_f32(uint16_t(rsa[slot]));
-            s_sa[stage][tid] = sa;
-            s_ss[stage][tid] = sa * float(rsum[slot]);
-            if constexpr (BIAS) s_nb[stage][tid] = -sa * kDotBias;
+            s_sa[sc][tid] = sa;
+            s_ss[sc][tid] = sa * float(rsum[slot]);
+            if constexpr (BIAS) s_nb[sc][tid] = -sa * kDotBias;
         }
     };
     // A(0) and A(1) in flight together (A(1) through prologue-only registers)
@@ -252,15 +258,15 @@ __global__ __launch_bounds__(256, MODE == kModeDown ? 3 : 2) void prefill_mfma_k
     int rsum1;
     load_a(0, 0);
 #pragma unroll
-    for (int k = 0; k < 4; ++k) ra1[k] = *reinterpret_cast<const u32x4*>(a_src + 64 + 4 * k);
+    for (int k = 0; k < 4; ++k) ra1[k] = *reinterpret_cast<const u32x4*>(a_src + 64 + 4 * a_piece(k));
     rsa1 = a.act_scales[sa_base + 1];
     rsum1 = a.act_sums[sa_base + 1];
-    store_a(0, 0);
+    store_a(0, 0, 0);
 #pragma unroll
     for (int k = 0; k < 4; ++k) ra[0][k] = ra1[k];
     rsa[0] = rsa1;
     rsum[0] = rsum1;
-    store_a(0, 1);
+    store_a(0, 1, 1);
     if (!GATEUP && tid < kMT) s_route[tid] = tid < nrows ? route_s : -1;   // read after the first barrier
     if (GS > 2) load_a(2, 0);
     __syncthreads();
@@ -275,8 +281,8 @@ __global__ __launch_bounds__(256, MODE == kModeDown ? 3 : 2) void prefill_mfma_k
             for (int ct = 0; ct < 2; ++ct)
 #pragma unroll
                 for (int r = 0; r < 4; ++r) val[rt][ct][r] = 0.f;
-        i32x4 acc[4][2];
-        float swv[2], offv[2];
+        i32x4 acc[1][4][2];
+        float swv[1][2], offv[1][2];
         // gate/up and head dots start from kDotBias (see kDotBias); the down
         // kernel keeps the conversion (measured: the bias costs it more than it
         // saves there)
@@ -286,7 +292,7 @@ __global__ __launch_bounds__(256, MODE == kModeDown ? 3 : 2) void prefill_mfma_k
         // matrix-core dots of step ST for the L live row tiles (rows past
         // nrows in them hold copies of a live row)
         auto mfma_step = [&]<int ST>() {
-            constexpr int g = ST % GS, stage = g % NSTAGE, bslot = ST % DB;
+            constexpr int g = ST % GS, stage = g % NSTAGE, bslot = ST % DB, ab = 0;
 #pragma unroll
             for (int s = 0; s < 4; ++s) {
                 i32x4 fa[4], fb[2];
@@ -305,26 +311,26 @@ __global__ __launch_bounds__(256, MODE == kModeDown ? 3 : 2) void prefill_mfma_k
                 for (int rt = 0; rt < L; ++rt)
 #pragma unroll
                     for (int ct = 0; ct < 2; ++ct)
-                        acc[rt][ct] = __builtin_amdgcn_mfma_i32_16x16x64_i8(
-                            fa[rt], fb[ct], s ? acc[rt][ct] : kAccInit, 0, 0, 0);
+                        acc[ab][rt][ct] = __builtin_amdgcn_mfma_i32_16x16x64_i8(
+                            fa[rt], fb[ct], s ? acc[ab][rt][ct] : kAccInit, 0, 0, 0);
             }
             // the slot's scales are taken before the slot is refilled
 #pragma unroll
             for (int ct = 0; ct < 2; ++ct) {
-                swv[ct] = f16_bits_to_f32(uint16_t(bm[bslot][ct] & 0xffffu));
-                offv[ct] = f16_bits_to_f32(uint16_t(bm[bslot][ct] >> 16));
+                swv[ab][ct] = f16_bits_to_f32(uint16_t(bm[bslot][ct] & 0xffffu));
+                offv[ab][ct] = f16_bits_to_f32(uint16_t(bm[bslot][ct] >> 16));
             }
             if constexpr (ST + DB < NSTEP) load_b(ST + DB, bslot);
         };
 
         // fp32 group tree of step ST (dense_g256_api.h:35-37), ascending groups
         auto tree_step = [&]<int ST>() {
-            constexpr int g = ST % GS, sub = ST / GS, stage = g % NSTAGE;
+            constexpr int g = ST % GS, sub = ST / GS, sc = g % NSC, ab = 0;
 #pragma unroll
             for (int rt = 0; rt < L; ++rt) {
-                const float4 sa4 = *reinterpret_cast<const float4*>(&s_sa[stage][16 * rt + 4 * q]);
-                const float4 ss4 = *reinterpret_cast<const float4*>(&s_ss[stage][16 * rt + 4 * q]);
-                const float4 nb4 = BIAS ? *reinterpret_cast<const float4*>(&s_nb[BIAS ? stage : 0][16 * rt + 4 * q])
+                const float4 sa4 = *reinterpret_cast<const float4*>(&s_sa[sc][16 * rt + 4 * q]);
+                const float4 ss4 = *reinterpret_cast<const float4*>(&s_ss[sc][16 * rt + 4 * q]);
+                const float4 nb4 = BIAS ? *reinterpret_cast<const float4*>(&s_nb[BIAS ? sc : 0][16 * rt + 4 * q])
                                         : float4{0.f, 0.f, 0.f, 0.f};
                 const float sa[4] = {sa4.x, sa4.y, sa4.z, sa4.w}, ss[4] = {ss4.x, ss4.y, ss4.z, ss4.w};
                 const float nb[4] = {nb4.x, nb4.y, nb4.z, nb4.w};
@@ -333,10 +339,10 @@ __global__ __launch_bounds__(256, MODE == kModeDown ? 3 : 2) void prefill_mfma_k
 #pragma unroll
                     for (int ct = 0; ct < 2; ++ct) {
                         // gate/up: acc holds the bits of kDotBias + dot, one fma gives RN(sa * dot)
-                        const float scaled_dot = BIAS ? __builtin_fmaf(sa[r], __int_as_float(acc[rt][ct][r]), nb[r])
-                                                      : sa[r] * float(acc[rt][ct][r]);
-                        const float product = swv[ct] * scaled_dot;
-                        const float correction = offv[ct] * ss[r];
+                        const float scaled_dot = BIAS ? __builtin_fmaf(sa[r], __int_as_float(acc[ab][rt][ct][r]), nb[r])
+                                                      : sa[r] * float(acc[ab][rt][ct][r]);
+                        const float product = swv[ab][ct] * scaled_dot;
+                        const float correction = offv[ab][ct] * ss[r];
                         val[rt][ct][r] = val[rt][ct][r] + (product + correction);
                     }
             }
@@ -352,35 +358,59 @@ __global__ __launch_bounds__(256, MODE == kModeDown ? 3 : 2) void prefill_mfma_k
                 // ---- epilogue of one column block ----
                 if constexpr (GATEUP) {
                     // every row's SiLU(gate) * up unconditionally (dead rows
-                    // repeat a live row's inputs; their flags are dropped and
-                    // they are not stored), so the chains interleave
+                    // repeat the last live row's inputs, so their values and
+                    // flags equal that row's; they are not stored), one
+                    // straight-line loop per path so the chains interleave
                     float mid[L][4];
-                    uint32_t mflags[L][4];
+                    bool finite = true;
+                    if (shared) {
 #pragma unroll
-                    for (int rt = 0; rt < L; ++rt)
+                        for (int rt = 0; rt < L; ++rt)
 #pragma unroll
-                        for (int r = 0; r < 4; ++r) {
-                            float vg = val[rt][0][r], vu = val[rt][1][r];
-                            uint32_t f = 0;
-                            if (shared) {
-                                vg = bf16_round(vg);
-                                vu = bf16_round(vu);
-                                f |= (!isfinite(vg) || !isfinite(vu)) ? kFlagNonfiniteProjection : 0u;
+                            for (int r = 0; r < 4; ++r) {
+                                const float vg = bf16_round(val[rt][0][r]), vu = bf16_round(val[rt][1][r]);
                                 mid[rt][r] = bf16_round(a.silu_table[__float_as_uint(vg) >> 16] * vu);
-                            } else {
-                                f |= (!isfinite(vg) || !isfinite(vu)) ? kFlagNonfiniteProjection : 0u;
-                                mid[rt][r] = silu_portable(vg) * vu;
+                                finite = finite && isfinite(vg) && isfinite(vu) && isfinite(mid[rt][r]);
                             }
-                            f |= !isfinite(mid[rt][r]) ? (kFlagNonfiniteMiddle | kFlagNonfiniteInput) : 0u;
-                            mflags[rt][r] = f;
-                        }
+                    } else {
+                        // a non-finite gate or up value always gives a
+                        // non-finite middle value here (NaN, inf * x, x / inf
+                        // or 0 * inf), so the middle value alone decides
+#pragma unroll
+                        for (int rt = 0; rt < L; ++rt)
+#pragma unroll
+                            for (int r = 0; r < 4; ++r) {
+                                mid[rt][r] = silu_portable(val[rt][0][r]) * val[rt][1][r];
+                                finite = finite && isfinite(mid[rt][r]);
+                            }
+                    }
+                    if (__builtin_amdgcn_ballot_w64(!finite) != 0) {
+                        // the exact flags of this lane's live rows (rare)
+#pragma unroll
+                        for (int rt = 0; rt < L; ++rt)
+#pragma unroll
+                            for (int r = 0; r < 4; ++r) {
+                                float vg = val[rt][0][r], vu = val[rt][1][r];
+                                if (shared) {
+                                    vg = bf16_round(vg);
+                                    vu = bf16_round(vu);
+                                }
+                                uint32_t f = (!isfinite(vg) || !isfinite(vu)) ? kFlagNonfiniteProjection : 0u;
+                                f |= !isfinite(mid[rt][r]) ? (kFlagNonfiniteMiddle | kFlagNonfiniteInput) : 0u;
+                                flags |= 16 * rt + 4 * q + r < nrows ? f : 0u;
+                            }
+                    }
+                    // byte offsets from a.out fit 32 bits (rows < 2^22), so each
+                    // store is one add from this lane's first row
+                    const uint32_t obase = (uint32_t(first + 4 * q) * kInter + 64 * nt + 16 * w + li) * 4u;
+                    const int live = nrows - 4 * q;       // rows 4q + j of the tile are live for j < live
 #pragma unroll
                     for (int rt = 0; rt < L; ++rt)
 #pragma unroll
                         for (int r = 0; r < 4; ++r) {
-                            const int row = 16 * rt + 4 * q + r;
-                            flags |= row < nrows ? mflags[rt][r] : 0u;
-                            if (row < nrows) a.out[size_t(first + row) * kInter + 64 * nt + 16 * w + li] = mid[rt][r];
+                            if (16 * rt + r < live)
+                                *reinterpret_cast<float*>(reinterpret_cast<char*>(a.out) + obase +
+                                                          uint32_t(16 * rt + r) * (kInter * 4u)) = mid[rt][r];
 #pragma unroll
                             for (int ct = 0; ct < 2; ++ct) val[rt][ct][r] = 0.f;
                         }
@@ -497,7 +527,7 @@ __global__ __launch_bounds__(256, MODE == kModeDown ? 3 : 2) void prefill_mfma_k
                 constexpr int ST = S;
                 __syncthreads();            // A of step ST visible; stage (ST+2)%3 free
                 if constexpr (ST + 2 < GS) {
-                    store_a(0, (ST + 2) % NSTAGE);
+                    store_a(0, (ST + 2) % NSTAGE, ST + 2);
                     if constexpr (ST + 3 < GS) load_a(ST + 3, 0);
                 }
                 mfma_step.template operator()<ST>();
@@ -505,8 +535,14 @@ __global__ __launch_bounds__(256, MODE == kModeDown ? 3 : 2) void prefill_mfma_k
             }(), ...);
         }(std::make_integer_sequence<int, NSTEP>{});
     };
-    // 33..48 rows run the four-tile body (a fourth instantiation costs registers)
-    if constexpr (MAXL >= 4) {
+    // gate/up: 33..48 rows run a three-tile body; down: the four-tile one (a
+    // fourth instantiation there costs it registers and 5 % of its time)
+    if constexpr (MAXL >= 4 && GATEUP) {
+        if (nrows > 48) run.template operator()<4>();
+        else if (nrows > 32) run.template operator()<3>();
+        else if (nrows > 16) run.template operator()<2>();
+        else run.template operator()<1>();
+    } else if constexpr (MAXL >= 4) {
         if (nrows > 32) run.template operator()<4>();
         else if (nrows > 16) run.template operator()<2>();
         else run.template operator()<1>();
