@@ -709,7 +709,9 @@ hipError_t launch_permute(const int32_t* ids, int R, int T, bool with_shared, co
 // Unpermute: slot-order reduction (routed_storage_n32_consumer.cpp:176-184,
 // 296-307).
 // ---------------------------------------------------------------------------
-// Eight columns per thread; every slot's row is loaded unconditionally (rows
+// Eight columns per thread, four in each half of the row (thread j of a
+// token: columns 4j.. and 1024 + 4j.., so every load instruction of a wave
+// reads 1 KB contiguous); every slot's row is loaded unconditionally (rows
 // of slots without a live id hold stale data and are dropped by the select),
 // so all 18 row loads of a thread are in flight together.
 template <bool STREAM>
@@ -725,7 +727,7 @@ __global__ __launch_bounds__(256) void reduce_kernel(const float* __restrict__ r
     const size_t idx = size_t(blockIdx.x) * 256 + threadIdx.x;   // over T * H/8
     if (idx >= size_t(T) * kThreadsPerToken) return;
     const int t = int(idx / kThreadsPerToken);
-    const int c = int(idx % kThreadsPerToken) * kCols;
+    const int c = int(idx % kThreadsPerToken) * 4, c1 = c + kHidden / 2;
     int idv[kTop];
     float wv[kTop];
 #pragma unroll
@@ -746,17 +748,17 @@ __global__ __launch_bounds__(256) void reduce_kernel(const float* __restrict__ r
     };
 #pragma unroll
     for (int s = 0; s < kTop; ++s) {
-        const float* row = route_out + size_t(t * kTop + s) * kHidden + c;
-        rv[s][0] = stream4(row);
-        rv[s][1] = stream4(row + 4);
+        const float* row = route_out + size_t(t * kTop + s) * kHidden;
+        rv[s][0] = stream4(row + c);
+        rv[s][1] = stream4(row + c1);
     }
     const bool shared = sigmoid_table != nullptr;
     float4 sh[2] = {};
     float gate = 0.f;
     if (shared) {
-        const float* row = route_out + size_t(T * kTop + t) * kHidden + c;
-        sh[0] = stream4(row);
-        sh[1] = stream4(row + 4);
+        const float* row = route_out + size_t(T * kTop + t) * kHidden;
+        sh[0] = stream4(row + c);
+        sh[1] = stream4(row + c1);
         gate = bf16_bits_to_f32(sigmoid_table[shared_logit[t]]);
     }
     // slot-order fp32 sum (routed_storage_n32_consumer.cpp:176-184)
@@ -778,16 +780,18 @@ __global__ __launch_bounds__(256) void reduce_kernel(const float* __restrict__ r
         o[i] = f32_to_bf16_bits(sum[i]);
         if (!isfinite(sum[i]) || (o[i] & 0x7f80u) == 0x7f80u) flags |= kFlagNonfiniteOutput;
     }
-    auto pack = [](const uint16_t h[kCols]) {
-        return make_uint4(h[0] | (uint32_t(h[1]) << 16), h[2] | (uint32_t(h[3]) << 16), h[4] | (uint32_t(h[5]) << 16),
-                          h[6] | (uint32_t(h[7]) << 16));
+    // bf16 columns 0-3 to row offset c, 4-7 to c1
+    auto put = [](uint16_t* dst, const uint16_t h[kCols]) {
+        *reinterpret_cast<uint2*>(dst) = make_uint2(h[0] | (uint32_t(h[1]) << 16), h[2] | (uint32_t(h[3]) << 16));
+        *reinterpret_cast<uint2*>(dst + kHidden / 2) =
+            make_uint2(h[4] | (uint32_t(h[5]) << 16), h[6] | (uint32_t(h[7]) << 16));
     };
     const size_t base = size_t(t) * kHidden + c;
     if (final_f32) {
         *reinterpret_cast<float4*>(final_f32 + base) = make_float4(sum[0], sum[1], sum[2], sum[3]);
-        *reinterpret_cast<float4*>(final_f32 + base + 4) = make_float4(sum[4], sum[5], sum[6], sum[7]);
+        *reinterpret_cast<float4*>(final_f32 + base + kHidden / 2) = make_float4(sum[4], sum[5], sum[6], sum[7]);
     }
-    if (out) *reinterpret_cast<uint4*>(out + base) = pack(o);
+    if (out) put(out + base, o);
     if (shared) {
         const float sv[kCols] = {sh[0].x * gate, sh[0].y * gate, sh[0].z * gate, sh[0].w * gate,
                                  sh[1].x * gate, sh[1].y * gate, sh[1].z * gate, sh[1].w * gate};
@@ -798,8 +802,8 @@ __global__ __launch_bounds__(256) void reduce_kernel(const float* __restrict__ r
             so[i] = f32_to_bf16_bits(sv[i]);
             lo[i] = f32_to_bf16_bits(bf16_bits_to_f32(o[i]) + bf16_bits_to_f32(so[i]));
         }
-        if (shared_out) *reinterpret_cast<uint4*>(shared_out + base) = pack(so);
-        if (layer_out) *reinterpret_cast<uint4*>(layer_out + base) = pack(lo);
+        if (shared_out) put(shared_out + base, so);
+        if (layer_out) put(layer_out + base, lo);
     }
     flag_or(sticky, flags);
 }
