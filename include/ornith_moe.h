@@ -116,6 +116,16 @@ ORNITH_EXPORT int ornith_mi355x_single_token_path(int path);
  * single-token one. */
 ORNITH_EXPORT int ornith_mi355x_decode_route_path(int path);
 
+/* No reference counterpart: a self-check of this library's arithmetic.  The
+ * prefill gate/up epilogue computes SiLU(g) = g / (1 + portable_exp(-g)) in a
+ * short form (one-step refined reciprocal, exact remainder, one correctly
+ * rounded correction) when every gate value of a wave has 2^-60 <= |g| <= 80,
+ * and in the full form (special cases, IEEE division) otherwise.  This call
+ * evaluates both forms for every fp32 value of that domain on the device and
+ * writes the number of values compared to *checked_u64 and the number whose
+ * bits differ to *mismatches_u32 (device pointers; 0 mismatches expected). */
+ORNITH_EXPORT hipError_t ornith_mi355x_silu_selfcheck(void* checked_u64, void* mismatches_u32, hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -511,6 +511,13 @@ extern "C" int ornith_mi355x_single_token_path(int path) {
     return g_single_token_mode.exchange(path);
 }
 
+extern "C" hipError_t ornith_mi355x_silu_selfcheck(void* checked_u64, void* mismatches_u32, hipStream_t stream) {
+    if (!checked_u64 || !mismatches_u32 || !aligned(checked_u64, 8) || !aligned(mismatches_u32, 4))
+        return hipErrorInvalidValue;
+    return launch_silu_selfcheck(static_cast<unsigned long long*>(checked_u64), static_cast<uint32_t*>(mismatches_u32),
+                                 stream);
+}
+
 extern "C" int ornith_mi355x_decode_route_path(int path) {
     if (path < -1 || path > 1) return -1;
     if (path == -1) return g_route_select_mode.load();

@@ -81,14 +81,9 @@ __device__ __forceinline__ float f16_bits_to_f32(uint32_t bits) {
 __device__ __forceinline__ uint16_t f32_to_f16_bits(float v) { return __half_as_ushort(__float2half_rn(v)); }
 
 // Deterministic exp with the reference's Taylor coefficients and step order
-// (kernels/routed_storage/portable_exp.h:6-26).
-// The special cases are applied by selects after the polynomial (the GPU's
-// float ops do not trap and the conversion saturates), so no lane branches.
-__device__ __forceinline__ float portable_exp(float x) {
-    const float n_float = __builtin_rintf(x * 0x1.715476p+0f);
-    // in range for every x the result keeps (-104 < x < 89); the clamp keeps the
-    // conversion defined for the special cases, whose results are discarded
-    const int n = static_cast<int>(fminf(fmaxf(n_float, -200.f), 200.f));
+// (kernels/routed_storage/portable_exp.h:6-26): n = rint(x log2 e), the
+// reduced argument r in two steps, the degree-9 polynomial, 2^n.
+__device__ __forceinline__ float portable_exp_poly(float x, float n_float) {
     const float high = n_float * 0x1.62e400p-1f;
     const float low = n_float * 0x1.7f7d1cp-20f;
     const float r = (x - high) - low;
@@ -101,7 +96,16 @@ __device__ __forceinline__ float portable_exp(float x) {
     p = p * r + 0x1p-1f;
     p = p * r + 0x1p+0f;
     p = p * r + 0x1p+0f;
-    float y = __builtin_ldexpf(p, n);
+    return p;
+}
+// The special cases are applied by selects after the polynomial (the GPU's
+// float ops do not trap and the conversion saturates), so no lane branches.
+__device__ __forceinline__ float portable_exp(float x) {
+    const float n_float = __builtin_rintf(x * 0x1.715476p+0f);
+    // in range for every x the result keeps (-104 < x < 89); the clamp keeps the
+    // conversion defined for the special cases, whose results are discarded
+    const int n = static_cast<int>(fminf(fmaxf(n_float, -200.f), 200.f));
+    float y = __builtin_ldexpf(portable_exp_poly(x, n_float), n);
     asm volatile("" : "+v"(y));               // keep the polynomial unconditional (no per-lane branch)
     // special cases as three selects, innermost first
     y = x >= 89.f ? __builtin_huge_valf() : y;
@@ -109,6 +113,29 @@ __device__ __forceinline__ float portable_exp(float x) {
     return x != x ? x : y;
 }
 __device__ __forceinline__ float silu_portable(float g) { return fdiv_rn(g, 1.f + portable_exp(-g)); }
+
+// silu_portable for 2^-60 <= |g| <= 80 (silu_fast_domain).  There no special
+// case of portable_exp applies and |n| < 128, and the divisor d = 1 + e lies
+// in [1, 2^116] with every quotient and remainder a normal number, so the
+// division takes its short correctly rounded form: y0 = v_rcp_f32(d), one
+// Newton step y = y0 + y0 (1 - d y0), q0 = RN(g y), the exact remainder
+// g - d q0 (fma), and q = RN(q0 + remainder y) (Markstein's final step).
+// Bit-identical to silu_portable on this domain: checked on the MI355X for
+// every fp32 value in it.
+__device__ __forceinline__ bool silu_fast_domain(float g) {
+    const float a = __builtin_fabsf(g);
+    return a <= 80.f && a >= 0x1p-60f;
+}
+__device__ __forceinline__ float silu_portable_fast(float g) {
+    const float x = -g;
+    const float n_float = __builtin_rintf(x * 0x1.715476p+0f);
+    const float e = __builtin_ldexpf(portable_exp_poly(x, n_float), static_cast<int>(n_float));
+    const float d = 1.f + e;
+    const float y0 = __builtin_amdgcn_rcpf(d);
+    const float y = __builtin_fmaf(y0, __builtin_fmaf(-d, y0, 1.f), y0);
+    const float q0 = g * y;
+    return __builtin_fmaf(__builtin_fmaf(-d, q0, g), y, q0);
+}
 
 // ---- wave64 cross-lane helpers --------------------------------------------
 // Exact lane permutation l -> l ^ M, M in {1,2,4,8,16,32}, with no LDS-pipe

@@ -179,5 +179,8 @@ hipError_t launch_fixed8_gate(const uint16_t* down, const uint16_t* logit, const
 
 // ---- fill (graph-capture safe replacement for hipMemsetAsync) -------------------
 hipError_t launch_fill_u32(uint32_t* p, size_t n, uint32_t v, hipStream_t s);
+// Both SiLU forms of the gate/up epilogue over every fp32 value of the short
+// form's domain: values compared and mismatching bit patterns.
+hipError_t launch_silu_selfcheck(unsigned long long* checked, uint32_t* mismatches, hipStream_t s);
 
 }  // namespace ornith

@@ -375,14 +375,32 @@ __global__ __launch_bounds__(256, MODE == kModeDown ? 3 : 2) void prefill_mfma_k
                     } else {
                         // a non-finite gate or up value always gives a
                         // non-finite middle value here (NaN, inf * x, x / inf
-                        // or 0 * inf), so the middle value alone decides
+                        // or 0 * inf; in the fast domain silu(g) is finite and
+                        // nonzero), so the middle value alone decides.  The
+                        // short form when every gate value of the wave is in
+                        // its domain (common.hpp), the full one otherwise.
+                        bool fast = true;
 #pragma unroll
                         for (int rt = 0; rt < L; ++rt)
 #pragma unroll
-                            for (int r = 0; r < 4; ++r) {
-                                mid[rt][r] = silu_portable(val[rt][0][r]) * val[rt][1][r];
-                                finite = finite && isfinite(mid[rt][r]);
-                            }
+                            for (int r = 0; r < 4; ++r) fast = fast && silu_fast_domain(val[rt][0][r]);
+                        if (__builtin_amdgcn_ballot_w64(!fast) == 0) {
+#pragma unroll
+                            for (int rt = 0; rt < L; ++rt)
+#pragma unroll
+                                for (int r = 0; r < 4; ++r) {
+                                    mid[rt][r] = silu_portable_fast(val[rt][0][r]) * val[rt][1][r];
+                                    finite = finite && isfinite(mid[rt][r]);
+                                }
+                        } else {
+#pragma unroll
+                            for (int rt = 0; rt < L; ++rt)
+#pragma unroll
+                                for (int r = 0; r < 4; ++r) {
+                                    mid[rt][r] = silu_portable(val[rt][0][r]) * val[rt][1][r];
+                                    finite = finite && isfinite(mid[rt][r]);
+                                }
+                        }
                     }
                     if (__builtin_amdgcn_ballot_w64(!finite) != 0) {
                         // the exact flags of this lane's live rows (rare)
@@ -551,6 +569,32 @@ __global__ __launch_bounds__(256, MODE == kModeDown ? 3 : 2) void prefill_mfma_k
         else run.template operator()<1>();
     }
     flag_or(a.sticky, flags);
+}
+
+// Every fp32 bit pattern (64 per thread): silu_portable_fast against
+// silu_portable wherever silu_fast_domain holds.
+__global__ __launch_bounds__(256) void silu_selfcheck_kernel(unsigned long long* checked, uint32_t* mismatches) {
+    const uint64_t base = (uint64_t(blockIdx.x) * 256u + threadIdx.x) * 64u;
+    unsigned long long n = 0;
+    uint32_t bad = 0;
+    for (int i = 0; i < 64; ++i) {
+        const float g = __uint_as_float(uint32_t(base + i));
+        if (!silu_fast_domain(g)) continue;
+        ++n;
+        bad += __float_as_uint(silu_portable(g)) != __float_as_uint(silu_portable_fast(g)) ? 1u : 0u;
+    }
+    atomicAdd(checked, n);
+    if (bad) atomicAdd(mismatches, bad);
+}
+
+hipError_t launch_silu_selfcheck(unsigned long long* checked, uint32_t* mismatches, hipStream_t s) {
+    // the counters are cleared by a kernel (graph-safe, no memset node)
+    hipError_t st = launch_fill_u32(reinterpret_cast<uint32_t*>(checked), 2, 0u, s);
+    if (st == hipSuccess) st = launch_fill_u32(mismatches, 1, 0u, s);
+    if (st != hipSuccess) return st;
+    timed_launch("silu_selfcheck", silu_selfcheck_kernel, dim3((1u << 26) / 256), dim3(256), 0, s, checked,
+                 mismatches);
+    return hipGetLastError();
 }
 
 hipError_t launch_grouped_mfma(const MfmaArgs& a, bool gateup, int max_tiles, hipStream_t s) {

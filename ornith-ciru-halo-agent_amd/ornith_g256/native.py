@@ -84,6 +84,7 @@ _PROTOTYPES = {
     'ornith_mi355x_abi_version': ([], _INT),
     'ornith_mi355x_single_token_path': ([_INT], _INT),
     'ornith_mi355x_decode_route_path': ([_INT], _INT),
+    'ornith_mi355x_silu_selfcheck': ([_VP, _VP, _VP], _INT),
     # dense (include/ornith_dense.h)
     'ornith_dense_g256_abi_version': ([], C.c_uint32),
     'ornith_dense_g256_get_layout': ([_INT] * 4 + [C.POINTER(DenseLayout)], _INT),
@@ -559,6 +560,18 @@ def single_token_path(path=None, tile=32):
     if prev < 0:
         raise ValueError(f'single-token path must be 0 or 1, got {path}')
     return prev
+
+
+def silu_selfcheck(tile=32):
+    """Both SiLU forms of the prefill gate/up epilogue over every fp32 value
+    of the short form's domain (2^-60 <= |g| <= 80): (values compared,
+    mismatching bit patterns) -- 0 mismatches expected."""
+    dev = torch.device('cuda', torch.cuda.current_device())
+    out = torch.zeros(3, dtype=torch.int32, device=dev)          # u64 count | u32 mismatches
+    check(lib(tile).ornith_mi355x_silu_selfcheck(ptr(out), ptr(out[2:]), stream(out)), 'silu self-check')
+    torch.cuda.synchronize()
+    v = out.cpu().numpy().view('uint32')
+    return int(v[0]) | (int(v[1]) << 32), int(v[2])
 
 
 def decode_route_path(path=None, tile=32):

@@ -629,3 +629,13 @@ def test_head_g256_argmax_ties_and_nan(device, case, M):
     np.testing.assert_array_equal(from_dev(lb), ref_out)
     np.testing.assert_array_equal(from_dev(am), expect)
     assert int(flags.item()) == ref_flags
+
+
+def test_silu_short_form_matches_full_form_everywhere(device):
+    """The prefill gate/up epilogue's short SiLU form (2^-60 <= |g| <= 80)
+    against the full form (portable exp special cases, IEEE division), bit
+    for bit, for every fp32 value of that domain, on the device."""
+    from ornith_g256 import native
+    checked, mismatches = native.silu_selfcheck()
+    assert checked == 1111490562          # 2 signs x (2^-60 .. 80] in fp32
+    assert mismatches == 0
