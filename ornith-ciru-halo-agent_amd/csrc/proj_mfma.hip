@@ -599,14 +599,22 @@ hipError_t launch_silu_selfcheck(unsigned long long* checked, uint32_t* mismatch
 
 hipError_t launch_grouped_mfma(const MfmaArgs& a, bool gateup, int max_tiles, hipStream_t s) {
     if (max_tiles <= 0) return hipSuccess;
-    constexpr int kDownSub = 4;     // down: 4 column blocks (512 columns) per block
     const int tiles8 = (max_tiles + 7) / 8 * 8;   // m-tiles rounded up to the 8 XCDs
-    if (gateup)
+    if (gateup) {
         timed_launch("gateup_mfma", prefill_mfma_kernel<kModeGateUp, kHidden / kGroup, 1, 2>,
                      dim3(tiles8 * ((2 * kInter) / kNT)), dim3(256), 0, s, a);
+        return hipGetLastError();
+    }
+    // down: 4 column blocks (512 columns) per block, or 2 when that grid would
+    // fill fewer than three rounds of the chip's block slots (three blocks
+    // per CU): the second of ~1.3 rounds ran mostly empty (1120 tokens:
+    // 41.5 -> 39.3 us; 8192 tokens, 7 rounds: 195.5 with 4 against 202 with 2)
+    if (tiles8 * (kHidden / (kNT * 4)) < 3 * 3 * device_cu_count())
+        timed_launch("down_mfma", prefill_mfma_kernel<kModeDown, kInter / kGroup, 2, 1>,
+                     dim3(tiles8 * (kHidden / (kNT * 2))), dim3(256), 0, s, a);
     else
-        timed_launch("down_mfma", prefill_mfma_kernel<kModeDown, kInter / kGroup, kDownSub, 1>,
-                     dim3(tiles8 * (kHidden / (kNT * kDownSub))), dim3(256), 0, s, a);
+        timed_launch("down_mfma", prefill_mfma_kernel<kModeDown, kInter / kGroup, 4, 1>,
+                     dim3(tiles8 * (kHidden / (kNT * 4))), dim3(256), 0, s, a);
     return hipGetLastError();
 }
 
