@@ -52,12 +52,12 @@ MEASURED_TRAFFIC = {
     ('layer1', 1): 16731184, ('route1', 1): 1166652, ('gateup1', 1): 9949504, ('down1', 1): 5118494,
     ('route', 32): 2587638, ('topk', 32): 128301, ('sort', 32): 12911, ('gateup', 32): 176476796,
     ('quant_middle', 32): 804861, ('down', 32): 90919862, ('reduce', 32): 2591275,
-    ('router', 1120): 15343277, ('topk', 1120): 2186638, ('permute_scan_act', 1120): 7786599,
-    ('permute_scatter', 1120): 320474, ('gateup_mfma', 1120): 190322790, ('quant_middle', 1120): 26020252,
-    ('down_mfma', 1120): 169388429, ('reduce', 1120): 87590059,
-    ('router', 8192): 50520113, ('topk', 8192): 9599344, ('permute_scan_act', 8192): 56100543,
-    ('permute_scatter', 8192): 1531030, ('gateup_mfma', 8192): 624115093,
-    ('quant_middle', 8192): 189713614, ('down_mfma', 8192): 845719144, ('reduce', 8192): 639829122,
+    ('router', 1120): 15343263, ('topk', 1120): 2186638, ('permute_scan_act', 1120): 7786592,
+    ('permute_scatter', 1120): 320474, ('gateup_mfma', 1120): 190732263, ('quant_middle', 1120): 26020249,
+    ('down_mfma', 1120): 177260462, ('reduce', 1120): 87590525,
+    ('router', 8192): 50519818, ('topk', 8192): 9599320, ('permute_scan_act', 8192): 56100945,
+    ('permute_scatter', 8192): 1531030, ('gateup_mfma', 8192): 625504138,
+    ('quant_middle', 8192): 189713102, ('down_mfma', 8192): 845063402, ('reduce', 8192): 639829271,
 }
 
 
