@@ -49,9 +49,9 @@ DENSE_N = 6144
 # --copy-calibration); keyed by (kernel, tokens).  Commands and raw figures:
 # profiles/decode_n1_n32_hbm_traffic_pmc.md, profiles/prefill_1120_8192_hbm_traffic_pmc.md.
 MEASURED_TRAFFIC = {
-    ('layer1', 1): 16731184, ('route1', 1): 1166652, ('gateup1', 1): 9949504, ('down1', 1): 5118494,
-    ('route', 32): 2587638, ('topk', 32): 128301, ('sort', 32): 12911, ('gateup', 32): 176476796,
-    ('quant_middle', 32): 804861, ('down', 32): 90919862, ('reduce', 32): 2591275,
+    ('layer1', 1): 16738159, ('route1', 1): 1166652, ('gateup1', 1): 9949504, ('down1', 1): 5118494,
+    ('route_select', 32): 3089138, ('gateup', 32): 176469490,
+    ('quant_middle', 32): 804861, ('down', 32): 90923948, ('reduce', 32): 2596423,
     ('router', 1120): 15343263, ('topk', 1120): 2186638, ('permute_scan_act', 1120): 7786592,
     ('permute_scatter', 1120): 320474, ('gateup_mfma', 1120): 190732263, ('quant_middle', 1120): 26020249,
     ('down_mfma', 1120): 177260462, ('reduce', 1120): 87590525,
@@ -70,7 +70,7 @@ def kernel_cost(name, T, unique):
     routes = 9 * T
     if name == 'layer1':            # the whole single-token layer in one launch
         return 'hbm', banks * EXPERT_BYTES + ROUTER_BYTES + T * 2048 * 2 * 2, HBM_PEAK_GBS, 'GB/s'
-    if name in ('route1', 'route'):
+    if name in ('route1', 'route', 'route_select'):
         return 'hbm', ROUTER_BYTES + T * 2048 * 2, HBM_PEAK_GBS, 'GB/s'
     if name in ('gateup1', 'gateup'):
         return 'hbm', banks * GATEUP_BYTES + T * 2048 + routes * 512 * 4, HBM_PEAK_GBS, 'GB/s'
