@@ -136,6 +136,11 @@ __device__ __forceinline__ float silu_portable_fast(float g) {
     const float q0 = g * y;
     return __builtin_fmaf(__builtin_fmaf(-d, q0, g), y, q0);
 }
+// silu_portable of one value per lane, the short form when every active
+// lane's value is in its domain (a wave-uniform choice; same bits either way).
+__device__ __forceinline__ float silu_portable_wave(float g) {
+    return __builtin_amdgcn_ballot_w64(!silu_fast_domain(g)) == 0 ? silu_portable_fast(g) : silu_portable(g);
+}
 
 // ---- wave64 cross-lane helpers --------------------------------------------
 // Exact lane permutation l -> l ^ M, M in {1,2,4,8,16,32}, with no LDS-pipe

@@ -460,7 +460,7 @@ __global__ __launch_bounds__(512) void decode_gateup_kernel(DecodeArgs a) {
                 mid = bf16_round(a.silu_table[__float_as_uint(vg) >> 16] * vu);
             } else {
                 if (!isfinite(vg) || !isfinite(vu)) flags |= kFlagNonfiniteProjection;
-                mid = silu_portable(vg) * vu;
+                mid = silu_portable_wave(vg) * vu;
             }
             if (!isfinite(mid)) flags |= kFlagNonfiniteMiddle | kFlagNonfiniteInput;
             a.middle[size_t(lr[r0 + rr]) * kInter + p * 32 + c] = mid;

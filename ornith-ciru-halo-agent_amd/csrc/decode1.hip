@@ -218,7 +218,7 @@ __global__ __launch_bounds__(256) void decode1_gateup_kernel(DecodeArgs a) {
             mid = bf16_round(a.silu_table[__float_as_uint(vg) >> 16] * vu);
         } else {
             if (!isfinite(vg) || !isfinite(vu)) flags |= kFlagNonfiniteProjection;
-            mid = silu_portable(vg) * vu;
+            mid = silu_portable_wave(vg) * vu;
         }
         if (!isfinite(mid)) flags |= kFlagNonfiniteMiddle | kFlagNonfiniteInput;
         // the first four H128 butterflies of the down input (k bits 0..3 =
@@ -541,7 +541,7 @@ __global__ __launch_bounds__(576) void layer1_kernel(DecodeArgs a) {
             mid = bf16_round(a.silu_table[__float_as_uint(vg) >> 16] * vu);
         } else {
             if (!isfinite(vg) || !isfinite(vu)) f |= kFlagNonfiniteProjection;
-            mid = silu_portable(vg) * vu;
+            mid = silu_portable_wave(vg) * vu;
         }
         if (!isfinite(mid)) f |= kFlagNonfiniteMiddle | kFlagNonfiniteInput;
         mid = butterfly_lane<1>(mid);
