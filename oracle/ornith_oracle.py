@@ -39,6 +39,9 @@ Pinning (what checks each function, tests/test_oracle.py):
                              parity unpinned.
   * permute                - counts against numpy bincount, stable order
                              against argsort(kind='stable').
+  * head_w8_tile_layout     - every byte against the reference's scalar
+                             tile_word index, low-K byte first, with a
+                             planted transposed layout that must fail.
   * h128 order, quantize, routed_layer_shared, reduce_slots, head_w8,
     portable_exp, shared_fixed8
                            - bit for bit against scalar statement-by-statement
@@ -207,12 +210,6 @@ def pack_meta(scale_bits: np.ndarray, offset_bits: np.ndarray, tile: int) -> np.
     m = (np.asarray(scale_bits, np.uint32) | (np.asarray(offset_bits, np.uint32) << 16))
     n, groups = m.shape
     return np.ascontiguousarray(m.reshape(n // tile, tile, groups).transpose(0, 2, 1))
-
-
-def unpack_meta(meta: np.ndarray):
-    nt, groups, tile = meta.shape
-    m = meta.transpose(0, 2, 1).reshape(nt * tile, groups)
-    return (m & 0xFFFF).astype(np.uint16), (m >> 16).astype(np.uint16)
 
 
 def n16_to_n32(codes16: np.ndarray, meta16: np.ndarray):

@@ -190,7 +190,7 @@ class Runtime:
             raise RuntimeError(f'native error flags: {raised}')
         return flags
 
-    def lifecycle(self, max_inflight=2):
-        """A StepLifecycle over this runtime's flag slots."""
-        from .lifecycle import StepLifecycle
-        return StepLifecycle(self.layer_names, max_inflight, flags=self.error_flags)
+    def step_flags(self, depth=2):
+        """A StepFlags checker over this runtime's flag slots."""
+        from .lifecycle import StepFlags
+        return StepFlags(self.layer_names, depth, flags=self.error_flags)

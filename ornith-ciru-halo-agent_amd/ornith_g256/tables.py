@@ -21,14 +21,15 @@ SHA256 = '11552ec53b62b229d0ab42b4e865d0175724cd51c4eef01c05e66e930f27d2eb'
 def load_numpy():
     raw = TABLE.read_bytes()
     if hashlib.sha256(raw).hexdigest() != SHA256:
-        raise RuntimeError('Shared reference table checksum differs from its receipt')
+        raise RuntimeError(f'{TABLE.name}: sha256 is not {SHA256}; the SiLU/sigmoid tables cannot be trusted')
     n = int.from_bytes(raw[:8], 'little')
     header = json.loads(raw[8:8 + n])
     out = {}
     for name, dtype, np_dtype in (('silu_fp32', 'F32', np.float32), ('sigmoid_bf16', 'BF16', np.uint16)):
         info = header[name]
         if info['dtype'] != dtype or info['shape'] != [65536]:
-            raise RuntimeError('Invalid shared reference table geometry')
+            raise RuntimeError(f'{TABLE.name}: {name} must be {dtype} with 65536 entries, found '
+                               f"{info['dtype']} {info['shape']}")
         lo, hi = info['data_offsets']
         out[name] = np.frombuffer(raw[8 + n + lo:8 + n + hi], dtype=np_dtype).copy()
     return out['silu_fp32'], out['sigmoid_bf16']

@@ -359,26 +359,26 @@ def test_dense_method_and_flag_lifecycle(device):
         model.to(device)
         model.proj.quant_method = m
         rt = methods.Runtime(model, {'routed_storage_n32': True, 'dense_a8_max_rows': 64}, 128, device)
-        steps = rt.lifecycle()
-        tk = steps.begin('decode')
+        steps = rt.step_flags()
+        tk = steps.open('decode')
         x1 = bf16_normal(rng, (1, K))
         y1 = m.apply(model.proj, to_dev(x1, device))
         x70 = bf16_normal(rng, (70, K))
         y70 = m.apply(model.proj, to_dev(x70, device))
-        steps.snapshot(tk)
-        assert steps.complete(tk) == (0,)
+        steps.capture(tk)
+        assert steps.check_through(tk) == (0,)
         np.testing.assert_array_equal(from_dev(y1), O.dense_a8(x1, *bank.expert())[0])
         got = O.bf16_to_f32(from_dev(y70)).astype(np.float64)
         ref = (O.bf16_to_f32(O.transform_bf16(x70)).astype(np.float64)
                @ O.bf16_to_f32(O.dequantize_bf16(*bank.expert())).astype(np.float64).T)
         cos = float((got.ravel() @ ref.ravel()) / (np.linalg.norm(got) * np.linalg.norm(ref)))
         assert cos >= 0.9999 and np.abs(got - ref).max() <= 1e-2 * np.abs(ref).max()
-        tk = steps.begin('bad input')
+        tk = steps.open('bad input')
         x1[0, 5] = 0x7FC0                          # NaN
         m.apply(model.proj, to_dev(x1, device))
-        steps.snapshot(tk)
+        steps.capture(tk)
         with pytest.raises(lifecycle.OrnithWorkerFault, match="'proj': 3"):
-            steps.complete(tk)
+            steps.check_through(tk)
     finally:
         native.reset_binding()
 

@@ -1,7 +1,6 @@
 """Host-side policy of the package, on the CPU: phase plans for mixed
-batches, the per-step lifecycle of the sticky native flags (with a fake
-device transport, as the reference tests its lifecycle through an injected
-transport, lifecycle.py:76), strict checkpoint admission, the repack entry's
+batches, the per-step checks of the sticky native flags (with a list-backed
+ring standing in for the device and its pinned snapshots), strict checkpoint admission, the repack entry's
 argument checks, the quantized-layer methods before binding and the vLLM
 registration's contracts."""
 import pytest
@@ -50,112 +49,147 @@ def test_phase_context_selects_segments_per_call():
 
 
 # ---------------------------------------------------------------------------
-# Flag lifecycle (lifecycle.py:69-193)
+# Per-step flag checks (policy of lifecycle.py:69-193)
 # ---------------------------------------------------------------------------
-class FakeTransport:
-    """Device flags as a Python list; snapshots copy it."""
+class ListRing:
+    """Device flags as a Python list; ring rows are list copies."""
 
-    def __init__(self, n):
+    def __init__(self, n, depth):
         self.flags = [0] * n
+        self.slots = n
+        self.rows = [None] * depth
         self.log = []
 
-    def width(self):
-        return len(self.flags)
+    def zero(self):
+        self.log.append('zero')
+        self.flags = [0] * self.slots
 
-    def new_slot(self):
-        return {'copy': None}
+    def capture(self, row):
+        self.log.append(f'capture{row}')
+        self.rows[row] = list(self.flags)
 
-    def clear(self):
-        self.log.append('clear')
-        self.flags = [0] * len(self.flags)
-
-    def queue(self, slot):
-        self.log.append('queue')
-        slot['copy'] = list(self.flags)
-
-    def finish(self, slot):
-        self.log.append('finish')
-        return tuple(slot['copy'])
+    def read(self, row):
+        self.log.append(f'read{row}')
+        return tuple(self.rows[row])
 
 
-def _lifecycle(n=3, inflight=2):
-    t = FakeTransport(n)
-    return L.StepLifecycle([f'layers.{i}.mlp' for i in range(n)], inflight, transport=t), t
+def _steps(n=3, depth=2):
+    ring = ListRing(n, depth)
+    return L.StepFlags([f'layers.{i}.mlp' for i in range(n)], depth, ring=ring), ring
 
 
-def test_healthy_steps_clear_snapshot_and_complete():
-    lc, t = _lifecycle()
+def test_healthy_steps_zero_capture_and_check():
+    sf, ring = _steps()
     for i in range(5):
-        tk = lc.begin(f'step{i}')
-        lc.snapshot(tk)
-        assert lc.complete(tk) == (0, 0, 0)
-    assert t.log[:3] == ['clear', 'queue', 'finish']
-    assert lc.clears == lc.snapshots == lc.completed == 5
+        s = sf.open(f'step{i}')
+        assert s == i
+        sf.capture(s)
+        assert sf.check_through(s) == (0, 0, 0)
+    assert ring.log[:3] == ['zero', 'capture0', 'read0']
+    assert ring.log[3:6] == ['zero', 'capture1', 'read1']      # step 1 uses ring row 1
+    assert sf.zeroed == sf.captured == sf.read_rows == 5
 
 
 def test_a_raised_flag_poisons_the_worker():
-    lc, t = _lifecycle()
-    tk = lc.begin('decode')
-    t.flags[1] = 4                                    # invalid expert id in layer 1
-    lc.snapshot(tk)
+    sf, ring = _steps()
+    s = sf.open('decode')
+    ring.flags[1] = 4                                 # invalid expert id in layer 1
+    sf.capture(s)
     with pytest.raises(L.OrnithWorkerFault, match='layers.1.mlp'):
-        lc.complete(tk)
+        sf.check_through(s)
     with pytest.raises(L.OrnithWorkerFault):
-        lc.begin('next')                              # poisoned: no further steps
+        sf.open('next')                               # poisoned: no further steps
 
 
 def test_a_later_healthy_step_cannot_hide_an_earlier_fault():
-    lc, t = _lifecycle(inflight=3)
-    first = lc.begin('a')
-    t.flags[0] = 8
-    lc.snapshot(first)
-    second = lc.begin('b')                            # clears the device flags again
-    lc.snapshot(second)
+    sf, ring = _steps(depth=3)
+    first = sf.open('a')
+    ring.flags[0] = 8
+    sf.capture(first)
+    second = sf.open('b')                             # zeroes the device flags again
+    sf.capture(second)
     with pytest.raises(L.OrnithWorkerFault, match="step 0 \\(a\\)"):
-        lc.complete(second)
+        sf.check_through(second)
 
 
-def test_completion_requires_a_snapshot_and_the_pool_is_bounded():
-    lc, _ = _lifecycle(inflight=2)
-    a = lc.begin('a')
-    lc.begin('b')
-    with pytest.raises(RuntimeError, match='in flight'):
-        lc.begin('c')
-    with pytest.raises(RuntimeError, match='snapshot'):
-        lc.complete(a)
+def test_checking_a_later_step_keeps_the_earlier_flags():
+    sf, ring = _steps(depth=3)
+    a, b = sf.open('a'), sf.open('b')
+    sf.capture(a)
+    sf.capture(b)
+    assert sf.check_through(b) == (0, 0, 0)
+    assert sf.checked == 2
+    assert sf.check_through(a) == (0, 0, 0)           # kept for its own caller
+    with pytest.raises(RuntimeError, match='not open'):
+        sf.check_through(a)                           # taken once
 
 
-def test_abort_captures_flags_and_reraises():
-    lc, t = _lifecycle()
-    tk = lc.begin('prefill')
+def test_check_requires_a_capture_and_the_ring_is_bounded():
+    sf, _ = _steps(depth=2)
+    a = sf.open('a')
+    sf.open('b')
+    with pytest.raises(RuntimeError, match='steps are open'):
+        sf.open('c')
+    with pytest.raises(RuntimeError, match='captured'):
+        sf.check_through(a)
+    with pytest.raises(RuntimeError, match='not open'):
+        sf.capture(7)
+
+
+def test_ring_rows_are_reused_in_order():
+    sf, ring = _steps(depth=2)
+    for i in range(6):
+        s = sf.open(str(i))
+        sf.capture(s)
+        if i % 2:
+            sf.check_through(s)
+    assert [e for e in ring.log if e.startswith('capture')] == ['capture0', 'capture1'] * 3
+
+
+def test_fail_captures_flags_and_reraises():
+    sf, ring = _steps()
+    s = sf.open('prefill')
     with pytest.raises(ValueError, match='boom'):
-        lc.abort(tk, ValueError('boom'))
-    assert isinstance(lc.fault, L.OrnithWorkerFault)
-    lc2, t2 = _lifecycle()
-    tk2 = lc2.begin('prefill')
-    t2.flags[2] = 1
+        sf.fail(s, ValueError('boom'))
+    assert isinstance(sf.fault, L.OrnithWorkerFault)
+    sf2, ring2 = _steps()
+    s2 = sf2.open('prefill')
+    ring2.flags[2] = 1
     with pytest.raises(L.OrnithWorkerFault) as info:
-        lc2.abort(tk2, ValueError('boom'))
+        sf2.fail(s2, ValueError('boom'))
     assert isinstance(info.value.__cause__, ValueError)
 
 
-def test_drain_checks_every_pending_step():
-    lc, t = _lifecycle(inflight=3)
-    lc.begin('a')
-    lc.begin('b')
-    lc.drain()
-    assert lc.completed == 2
-    lc.begin('c')
-    t.flags[0] = 32
+def test_a_failing_device_copy_poisons():
+    sf, ring = _steps()
+
+    def broken(row):
+        raise OSError('copy engine gone')
+    ring.capture = broken
+    s = sf.open('x')
+    with pytest.raises(L.OrnithWorkerFault, match='copying'):
+        sf.capture(s)
     with pytest.raises(L.OrnithWorkerFault):
-        lc.drain()
+        sf.open('y')
+
+
+def test_flush_checks_every_open_step():
+    sf, ring = _steps(depth=3)
+    sf.open('a')
+    sf.open('b')
+    sf.flush()
+    assert sf.read_rows == 2 and sf.checked == 2
+    sf.open('c')
+    ring.flags[0] = 32
+    with pytest.raises(L.OrnithWorkerFault):
+        sf.flush()
 
 
 def test_bad_construction():
     with pytest.raises(ValueError):
-        L.StepLifecycle(['a'], 0, transport=FakeTransport(1))
+        L.StepFlags(['a'], 0, ring=ListRing(1, 1))
     with pytest.raises(ValueError):
-        L.StepLifecycle(['a', 'b'], 1, transport=FakeTransport(1))
+        L.StepFlags(['a', 'b'], 1, ring=ListRing(1, 1))
 
 
 # ---------------------------------------------------------------------------

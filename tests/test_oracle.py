@@ -153,6 +153,55 @@ def test_n16_to_n32_repack_equals_direct_n32():
     np.testing.assert_array_equal(m32, O.pack_meta(sb, ob, 32))
 
 
+def _w8_tile_word(n, kword, K=2048):
+    """The W8 head's physical word index, head_i8_tile_consumer.cpp:19-21:
+    words [N/16, K/16, 4, 16]; word kword of column n packs K bytes
+    4*kword..4*kword+3, the lowest K byte in the lowest byte
+    (head_i8_tile_api.h:1)."""
+    return ((n // 16 * (K // 16) + kword // 4) * 4 + (kword & 3)) * 16 + (n & 15)
+
+
+def _w8_layout_transposed(w_i8):
+    """Planted mistake: the two inner axes of the tile swapped
+    ([N/16, K/16, 16, 4] instead of [N/16, K/16, 4, 16])."""
+    good = O.head_w8_tile_layout(w_i8)
+    return np.ascontiguousarray(good.reshape(-1, 128, 4, 16).transpose(0, 1, 3, 2))
+
+
+def _w8_layout_high_first(w_i8):
+    """Planted mistake: bytes packed with the highest K byte first."""
+    good = O.head_w8_tile_layout(w_i8)
+    return good.byteswap()
+
+
+def _check_w8_layout(words, w_i8):
+    N, K = w_i8.shape
+    flat = words.reshape(-1)
+    wb = w_i8.view(np.uint8)
+    for n in range(N):
+        for kword in range(K // 4):
+            word = int(flat[_w8_tile_word(n, kword, K)])
+            for b in range(4):
+                if (word >> (8 * b)) & 0xFF != wb[n, 4 * kword + b]:
+                    return False
+    return True
+
+
+def test_w8_head_tile_layout_matches_reference_index():
+    rng = np.random.default_rng(61)
+    N, K = 48, 2048
+    w = rng.integers(-127, 128, size=(N, K), dtype=np.int8)
+    words = O.head_w8_tile_layout(w)
+    assert words.shape == (N // 16, K // 16, 4, 16) and words.dtype == np.uint32
+    assert _check_w8_layout(words, w)
+    # Every byte of the bank is covered exactly once by the reference index.
+    idx = {_w8_tile_word(n, kw, K) for n in range(N) for kw in range(K // 4)}
+    assert len(idx) == words.size and min(idx) == 0 and max(idx) == words.size - 1
+    # Planted mistakes must fail the same check.
+    assert not _check_w8_layout(_w8_layout_transposed(w), w)
+    assert not _check_w8_layout(_w8_layout_high_first(w), w)
+
+
 def test_signed_int4_maps_to_affine_exactly():
     rng = np.random.default_rng(8)
     q4 = rng.integers(-8, 8, size=(32, 256))
