@@ -104,7 +104,8 @@ ORNITH_EXPORT int ornith_mi355x_abi_version(void);
  * setting, or -1 for another value.  Results are identical either way.  The
  * one-launch kernel raises sticky flag 64 if a block gave up waiting for
  * another block's hand-off (only possible when the grid could not be
- * resident at once, e.g. CUs taken by other work for tens of ms). */
+ * resident at once, e.g. CUs taken by other work for tens of ms); see
+ * ornith_mi355x_handoff_spin_limit for what that leaves in the workspace. */
 ORNITH_EXPORT int ornith_mi355x_single_token_path(int path);
 
 /* No reference counterpart.  Which kernels run the router, top-8 and sort of
@@ -116,6 +117,22 @@ ORNITH_EXPORT int ornith_mi355x_single_token_path(int path);
  * single-token one. */
 ORNITH_EXPORT int ornith_mi355x_decode_route_path(int path);
 
+/* No reference counterpart.  Poll rounds a one-launch kernel (single-token
+ * layer, 2..32-token route) spends on one hand-off wait before it gives up
+ * and raises sticky flag 64, process-wide: default 32768; 0 makes every wait
+ * give up at once (for tests of the time-out path); -1 queries.  Returns the
+ * previous setting, or -1 for a value outside -1..16777216.
+ * A call whose arrival wait gave up (or that ran with 0) cannot confirm that
+ * every block read its sequence number, so it marks the workspace poisoned:
+ * every later one-launch call on that workspace gives up every wait at once,
+ * raises flag 64 and computes on stale hand-off words (all indices stay in
+ * range; the outputs are not meaningful) until the caller resets it. */
+ORNITH_EXPORT int ornith_mi355x_handoff_spin_limit(int spins);
+/* No reference counterpart.  Zeroes `bytes` of a workspace on `stream` (a fill
+ * kernel, no memset node), which clears the poisoned mark above; workspace
+ * NULL with bytes 0 resets the static scratch of ornith_moe_layer_launch_static
+ * on the stream's device.  Workspace 256-byte aligned, bytes a multiple of 4. */
+ORNITH_EXPORT hipError_t ornith_mi355x_workspace_reset(void* workspace, size_t bytes, hipStream_t stream);
 /* No reference counterpart: a self-check of this library's arithmetic.  The
  * prefill gate/up epilogue computes SiLU(g) = g / (1 + portable_exp(-g)) in a
  * short form (one-step refined reciprocal, exact remainder, one correctly

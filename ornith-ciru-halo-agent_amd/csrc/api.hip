@@ -453,6 +453,7 @@ extern "C" hipError_t ornith_shared_fixed8_launch(const void* input, const void*
 // code `scratch` only names the symbol: its device address comes from
 // hipGetSymbolAddress, once per device, and only that address is passed on.
 namespace {
+constexpr int kMaxHandoffSpins = 1 << 24;
 constexpr int kStaticMaxTokens = 32;
 constexpr size_t kStaticScratchBytes = size_t(5) << 20;
 constexpr int kMaxDevices = 64;
@@ -522,6 +523,22 @@ extern "C" int ornith_mi355x_decode_route_path(int path) {
     if (path < -1 || path > 1) return -1;
     if (path == -1) return g_route_select_mode.load();
     return g_route_select_mode.exchange(path);
+}
+
+extern "C" int ornith_mi355x_handoff_spin_limit(int spins) {
+    if (spins < -1 || spins > kMaxHandoffSpins) return -1;
+    if (spins == -1) return g_handoff_spins.load();
+    return g_handoff_spins.exchange(spins);
+}
+
+extern "C" hipError_t ornith_mi355x_workspace_reset(void* workspace, size_t bytes, hipStream_t stream) {
+    if (!workspace) {
+        if (bytes != 0) return hipErrorInvalidValue;
+        TRY(scratch_address(stream, &workspace));
+        bytes = kStaticScratchBytes;
+    }
+    if (!aligned(workspace, 256) || bytes % 4) return hipErrorInvalidValue;
+    return launch_fill_u32(static_cast<uint32_t*>(workspace), bytes / 4, 0u, stream);
 }
 
 // =============================================================================

@@ -277,6 +277,7 @@ __global__ __launch_bounds__(256) void decode_route_select_kernel(DecodeArgs a, 
     const int L = int(blockIdx.x), gw = L * 4 + wave;
     uint64_t* W = a.l1_words;
     const uint32_t seq = __hip_atomic_load(a.l1_seq, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const int limit = l1_limit(seq, a.handoff_spins);
     uint32_t flags = 0;
     if (gw < router_waves) {
         const int nb = (T + kTokenBatch - 1) / kTokenBatch;
@@ -322,7 +323,7 @@ __global__ __launch_bounds__(256) void decode_route_select_kernel(DecodeArgs a, 
 #pragma unroll
         for (int i = 0; i < 4; ++i) idx[i] = kDecodeRouteLogit + kDecodeMaxTokens * (lane + 64 * i) + t;
         idx[4] = SHARED ? kDecodeRouteLogit + kDecodeMaxTokens * kExperts + t : idx[3];   // the shared gate row
-        if (!l1_wait<5, 0>(W, idx, seq, got)) flags |= kFlagHandoffTimeout;
+        if (!l1_wait<5, 0>(W, idx, seq, got, limit)) flags |= kFlagHandoffTimeout;
         float v[4];
 #pragma unroll
         for (int i = 0; i < 4; ++i) v[i] = __uint_as_float(got[i]);
@@ -347,7 +348,7 @@ __global__ __launch_bounds__(256) void decode_route_select_kernel(DecodeArgs a, 
         if (wave * 64 < R) {                           // R <= 256: one id word per thread
             const int r = min(wave * 64 + lane, R - 1);
             uint32_t idx[1] = {uint32_t(kDecodeRouteIds + r)}, got[1];
-            if (!l1_wait<1, 0>(W, idx, seq, got)) flags |= kFlagHandoffTimeout;
+            if (!l1_wait<1, 0>(W, idx, seq, got, limit)) flags |= kFlagHandoffTimeout;
             if (wave * 64 + lane < R) s_ids[wave * 64 + lane] = int32_t(got[0]);
         }
         __syncthreads();
@@ -357,8 +358,12 @@ __global__ __launch_bounds__(256) void decode_route_select_kernel(DecodeArgs a, 
             uint32_t idx[5], got[5];
 #pragma unroll
             for (int i = 0; i < 5; ++i) idx[i] = kDecodeRouteArrive + 8 * min(lane + 64 * i, nblocks - 1);
-            if (!l1_wait<5, 1>(W, idx, seq, got)) flags |= kFlagHandoffTimeout;
-            if (lane == 0) __hip_atomic_store(a.l1_seq, seq + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            // advance only once every block has read `seq` (see handoff.hpp)
+            const bool arrived = l1_wait<5, 1>(W, idx, seq, got, limit);
+            if (!arrived) flags |= kFlagHandoffTimeout;
+            if (lane == 0)
+                __hip_atomic_store(a.l1_seq, arrived ? l1_next_seq(seq) : kSeqPoisoned, __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_AGENT);
         }
     }
     flag_or(a.sticky, flags);
@@ -590,20 +595,16 @@ void carve_decode(void* base, DecodeArgs& a) {
 constexpr int kDownTilesPerBlock = 2;    // 32-column down tiles per block (2048 / 32 / 2 = 32 blocks per segment)
 
 // Whether `blocks` blocks of the one-launch route kernel are resident at once
-// on the current device (occupancy checked once per device).
+// on the device that runs stream `s` (occupancy checked once per device).
 template <bool SHARED, int QMAX>
-static bool route_select_fits(int blocks) {
+static bool route_select_fits(int blocks, hipStream_t s) {
     constexpr int kMaxDevices = 64;
     static std::atomic<int> capacity[kMaxDevices];   // resident blocks; 0 unknown, -1 query failed
-    int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return false;
+    const int dev = stream_device(s);
+    if (dev < 0 || dev >= kMaxDevices) return false;
     int cap = capacity[dev].load(std::memory_order_relaxed);
     if (cap == 0) {
-        int per_cu = 0;
-        cap = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, decode_route_select_kernel<SHARED, QMAX>, 256, 0) ==
-                          hipSuccess && per_cu > 0
-                  ? per_cu * device_cu_count(0)
-                  : -1;
+        cap = resident_blocks(decode_route_select_kernel<SHARED, QMAX>, 256, dev);
         capacity[dev].store(cap, std::memory_order_relaxed);
     }
     return cap >= blocks;
@@ -621,9 +622,11 @@ static hipError_t run(const DecodeArgs& a, hipStream_t s) {
     if constexpr (ROUTER) {
         const int fused_blocks = (s1_waves + 3) / 4;
         if (fused_blocks <= kDecodeRouteMaxBlocks && g_route_select_mode.load(std::memory_order_relaxed) == 0 &&
-            route_select_fits<SHARED, QMAX>(fused_blocks)) {
+            route_select_fits<SHARED, QMAX>(fused_blocks, s)) {
+            DecodeArgs b = a;
+            b.handoff_spins = g_handoff_spins.load(std::memory_order_relaxed);
             timed_launch("route_select", decode_route_select_kernel<SHARED, QMAX>, dim3(fused_blocks), dim3(256), 0, s,
-                         a, router_waves);
+                         b, router_waves);
             st = hipGetLastError();
             if (st != hipSuccess) return st;
             fused = true;

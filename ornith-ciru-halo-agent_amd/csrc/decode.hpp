@@ -65,6 +65,7 @@ struct DecodeArgs {
     // one-launch kernels (single-token layer, 2..32-token route): call
     // sequence number and tagged hand-off words (kHandoffWords)
     uint32_t* l1_seq; uint64_t* l1_words;
+    int handoff_spins;                 // poll rounds before a hand-off wait gives up (g_handoff_spins)
     // outputs
     float* final_f32; uint16_t* out; uint16_t* shared_out; uint16_t* layer_out;
     uint32_t* sticky;
@@ -79,5 +80,8 @@ extern std::atomic<int> g_single_token_mode;
 // where the grid is resident), 1 three kernels
 extern std::atomic<int> g_route_select_mode;
 hipError_t launch_decode1(const DecodeArgs& a, bool router, bool shared, int qmax, hipStream_t s);
+// Poll rounds of the one-launch kernels' hand-off waits (default kHandoffSpins;
+// 0 makes every wait give up at once, for tests of the time-out path).
+extern std::atomic<int> g_handoff_spins;
 
 }  // namespace ornith

@@ -435,6 +435,7 @@ __global__ __launch_bounds__(576) void layer1_kernel(DecodeArgs a) {
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, L = int(blockIdx.x);
     uint64_t* W = a.l1_words;
     const uint32_t seq = __hip_atomic_load(a.l1_seq, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const int limit = l1_limit(seq, a.handoff_spins);
     const int gu = xcd_paired_block(L), s = gu >> 5, p = gu & 31;   // routed gate-up unit (slot s, pair p)
     const bool down_block = L < kLayer1DownBlocks;
     const int c = xcd_paired_block(L & (kLayer1DownBlocks - 1));   // down columns 16c..16c+15
@@ -617,7 +618,7 @@ __global__ __launch_bounds__(576) void layer1_kernel(DecodeArgs a) {
 #pragma unroll
             for (int i = 0; i < 4; ++i) idx[i] = uint32_t(kLayer1Spread * (lane + 64 * i));
             if constexpr (SHARED) idx[NW - 1] = kLayer1Spread * kExperts;
-            if (!l1_wait<NW, 0>(W, idx, seq, got)) flags |= kFlagHandoffTimeout;
+            if (!l1_wait<NW, 0>(W, idx, seq, got, limit)) flags |= kFlagHandoffTimeout;
             float lg[4];
 #pragma unroll
             for (int i = 0; i < 4; ++i) lg[i] = __uint_as_float(got[i]);
@@ -708,7 +709,7 @@ __global__ __launch_bounds__(576) void layer1_kernel(DecodeArgs a) {
         uint32_t idx[8], val[8];
 #pragma unroll
         for (int j = 0; j < 8; ++j) idx[j] = uint32_t(kLayer1Middle + wave * kInter + gm * kGroup + kb + 16 * j);
-        if (!l1_wait<8, 1>(W, idx, seq, val)) flags |= kFlagHandoffTimeout;
+        if (!l1_wait<8, 1>(W, idx, seq, val, limit)) flags |= kFlagHandoffTimeout;
         if (L == 0 && wave == 0) {
             // every block published its arrival long ago: read the words
             // now, check them at the end
@@ -802,8 +803,15 @@ __global__ __launch_bounds__(576) void layer1_kernel(DecodeArgs a) {
             idx[i] = uint32_t(kLayer1Arrive + kLayer1Spread * (lane + 64 * i));
             ok = ok && uint32_t(arrival[i] >> 32) == l1_tag(seq, idx[i]);
         }
-        if (__builtin_amdgcn_ballot_w64(!ok) != 0 && !l1_wait<4, 1>(W, idx, seq, val)) flags |= kFlagHandoffTimeout;
-        if (lane == 0) __hip_atomic_store(a.l1_seq, seq + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        // every block has read `seq` once all arrival words carry its tag;
+        // otherwise a late block could publish under the next number's tags,
+        // so the workspace is marked poisoned instead of advanced
+        const bool arrived =
+            limit > 0 && (__builtin_amdgcn_ballot_w64(!ok) == 0 || l1_wait<4, 1>(W, idx, seq, val, limit));
+        if (!arrived) flags |= kFlagHandoffTimeout;
+        if (lane == 0)
+            __hip_atomic_store(a.l1_seq, arrived ? l1_next_seq(seq) : kSeqPoisoned, __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
     }
     flag_or(a.sticky, flags);
 }
@@ -823,33 +831,31 @@ static hipError_t run1(const DecodeArgs& a, hipStream_t s) {
 }
 
 // Whether 256 blocks of the one-launch kernel are resident at once on the
-// current device (checked once per device).
+// device that runs stream `s` (checked once per device).
 template <bool ROUTER, bool SHARED, int QMAX>
-static bool layer1_fits() {
+static bool layer1_fits(hipStream_t s) {
     constexpr int kMaxDevices = 64;
     static std::atomic<int> state[kMaxDevices];   // 0 unknown, 1 fits, 2 does not
-    int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return false;
+    const int dev = stream_device(s);
+    if (dev < 0 || dev >= kMaxDevices) return false;
     int st = state[dev].load(std::memory_order_relaxed);
     if (st == 0) {
-        int per_cu = 0, cus = 0;
-        const bool ok = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, layer1_kernel<ROUTER, SHARED, QMAX>, 576,
-                                                                     0) == hipSuccess &&
-                        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess &&
-                        per_cu * cus >= kLayer1Blocks;
-        st = ok ? 1 : 2;
+        st = resident_blocks(layer1_kernel<ROUTER, SHARED, QMAX>, 576, dev) >= kLayer1Blocks ? 1 : 2;
         state[dev].store(st, std::memory_order_relaxed);
     }
     return st == 1;
 }
 
 std::atomic<int> g_single_token_mode{0};   // 0 automatic, 1 three kernels
+std::atomic<int> g_handoff_spins{kHandoffSpins};
 
 template <bool ROUTER, bool SHARED, int QMAX>
 static hipError_t run1_any(const DecodeArgs& a, hipStream_t s) {
     const int mode = g_single_token_mode.load(std::memory_order_relaxed);
-    if (mode == 1 || !layer1_fits<ROUTER, SHARED, QMAX>()) return run1<ROUTER, SHARED, QMAX>(a, s);
-    timed_launch("layer1", layer1_kernel<ROUTER, SHARED, QMAX>, dim3(kLayer1Blocks), dim3(576), 0, s, a);
+    if (mode == 1 || !layer1_fits<ROUTER, SHARED, QMAX>(s)) return run1<ROUTER, SHARED, QMAX>(a, s);
+    DecodeArgs b = a;
+    b.handoff_spins = g_handoff_spins.load(std::memory_order_relaxed);
+    timed_launch("layer1", layer1_kernel<ROUTER, SHARED, QMAX>, dim3(kLayer1Blocks), dim3(576), 0, s, b);
     return hipGetLastError();
 }
 

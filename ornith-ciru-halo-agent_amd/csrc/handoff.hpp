@@ -26,17 +26,30 @@ __device__ __forceinline__ void l1_put(uint64_t* w, uint32_t idx, uint32_t seq, 
 __device__ __forceinline__ uint64_t l1_get(uint64_t* w, uint32_t idx) {
     return __hip_atomic_load(w + idx, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
-constexpr int kHandoffSpins = 1 << 15;      // poll rounds before a wait gives up
+constexpr int kHandoffSpins = 1 << 15;      // default poll rounds before a wait gives up
+// Sequence value that marks a workspace whose last call could not confirm
+// that every block had read its sequence number (an arrival wait gave up):
+// words of that call may still be published under a tag a later call would
+// accept.  A call that reads it gives up every wait at once (raising the
+// time-out flag) and leaves the mark; zeroing the workspace clears it.  The
+// running number skips this value.
+constexpr uint32_t kSeqPoisoned = 0xFFFFFFFFu;
+__device__ __forceinline__ uint32_t l1_next_seq(uint32_t seq) { return seq + 1 == kSeqPoisoned ? 0u : seq + 1; }
+// Poll rounds of this call's waits: `spins` (the host's setting), or 0 on a
+// poisoned workspace.
+__device__ __forceinline__ int l1_limit(uint32_t seq, int spins) { return seq == kSeqPoisoned ? 0 : spins; }
 // Waits until this wave's N words idx[] carry this call's tags; val[] gets
 // their value bits.  One round of N loads at a time, all issued before any is
-// checked; PAUSE (s_sleep units of 64 clocks) between rounds.  Wave-uniform;
-// false after kHandoffSpins rounds.
+// checked; PAUSE (s_sleep units of 64 clocks) between rounds.  Wave-uniform.
+// At most `limit` rounds, then false; limit 0 reads the words once and
+// reports a time-out whatever they hold (val[] is always assigned).
 template <int N, int PAUSE>
-__device__ __forceinline__ bool l1_wait(uint64_t* w, const uint32_t (&idx)[N], uint32_t seq, uint32_t (&val)[N]) {
+__device__ __forceinline__ bool l1_wait(uint64_t* w, const uint32_t (&idx)[N], uint32_t seq, uint32_t (&val)[N],
+                                        int limit) {
     uint32_t want[N];
 #pragma unroll
     for (int i = 0; i < N; ++i) want[i] = l1_tag(seq, idx[i]);
-    for (int spin = 0; spin < kHandoffSpins; ++spin) {
+    for (int spin = 0;; ++spin) {
         uint64_t r[N];
 #pragma unroll
         for (int i = 0; i < N; ++i) r[i] = l1_get(w, idx[i]);
@@ -46,10 +59,10 @@ __device__ __forceinline__ bool l1_wait(uint64_t* w, const uint32_t (&idx)[N], u
             val[i] = uint32_t(r[i]);
             ok = ok && uint32_t(r[i] >> 32) == want[i];
         }
-        if (__builtin_amdgcn_ballot_w64(!ok) == 0) return true;
+        if (limit > 0 && __builtin_amdgcn_ballot_w64(!ok) == 0) return true;
+        if (spin + 1 >= limit) return false;
         if (PAUSE) __builtin_amdgcn_s_sleep(PAUSE);
     }
-    return false;
 }
 
 }  // namespace ornith

@@ -21,6 +21,28 @@ inline int device_cu_count(int fallback = 256) {
     return n;
 }
 
+// The device that runs stream `s` (for HIP's null stream, the current
+// device); -1 if the query fails.
+inline int stream_device(hipStream_t s) {
+    int dev = -1;
+    if (hipStreamGetDevice(s, &dev) != hipSuccess) return -1;
+    return dev;
+}
+
+// Blocks of `kernel` (`threads` threads, no dynamic LDS) that can be resident
+// at once on device `dev`, all CUs together; -1 if a query fails.  The
+// occupancy query runs with `dev` current (restored afterwards).
+template <class Kernel>
+int resident_blocks(Kernel kernel, int threads, int dev) {
+    int current = -1, per_cu = 0, cus = 0;
+    if (dev < 0 || hipGetDevice(&current) != hipSuccess) return -1;
+    if (current != dev && hipSetDevice(dev) != hipSuccess) return -1;
+    const bool ok = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, threads, 0) == hipSuccess &&
+                    hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess;
+    if (current != dev && hipSetDevice(current) != hipSuccess) return -1;
+    return ok && per_cu > 0 && cus > 0 ? per_cu * cus : -1;
+}
+
 // A run of consecutive entries of the permuted route list that all use one
 // weight bank (expert id 0..255, or kShared for the shared expert).
 struct Segment { int32_t bank, first, count, tile_base; };

@@ -85,6 +85,8 @@ _PROTOTYPES = {
     'ornith_mi355x_single_token_path': ([_INT], _INT),
     'ornith_mi355x_decode_route_path': ([_INT], _INT),
     'ornith_mi355x_silu_selfcheck': ([_VP, _VP, _VP], _INT),
+    'ornith_mi355x_handoff_spin_limit': ([_INT], _INT),
+    'ornith_mi355x_workspace_reset': ([_VP, _SZ, _VP], _INT),
     # dense (include/ornith_dense.h)
     'ornith_dense_g256_abi_version': ([], C.c_uint32),
     'ornith_dense_g256_get_layout': ([_INT] * 4 + [C.POINTER(DenseLayout)], _INT),
@@ -583,6 +585,29 @@ def decode_route_path(path=None, tile=32):
     if prev < 0:
         raise ValueError(f'decode route path must be 0 or 1, got {path}')
     return prev
+
+
+def handoff_spin_limit(spins=None, tile=32):
+    """Poll rounds of the one-launch kernels' hand-off waits, for the
+    process (default 32768; 0 gives every wait up at once, for tests of the
+    time-out path); None only queries.  Returns the previous setting."""
+    prev = lib(tile).ornith_mi355x_handoff_spin_limit(-1 if spins is None else int(spins))
+    if prev < 0:
+        raise ValueError(f'hand-off spin limit must be 0..16777216, got {spins}')
+    return prev
+
+
+def workspace_reset(workspace=None, tile=32):
+    """Zero a workspace on the current stream (clears the poisoned mark a
+    hand-off time-out leaves); None resets the static scratch of
+    moe_layer_static on the current device."""
+    if workspace is None:
+        dev = torch.device('cuda', torch.cuda.current_device())
+        check(lib(tile).ornith_mi355x_workspace_reset(None, 0, stream(torch.empty(0, device=dev))),
+              'static scratch reset')
+    else:
+        check(lib(tile).ornith_mi355x_workspace_reset(ptr(workspace), workspace.numel(), stream(workspace)),
+              'workspace reset')
 
 
 class KernelTimer:

@@ -283,3 +283,18 @@ def test_missing_library_fails_loudly(monkeypatch, tmp_path):
     monkeypatch.setattr(native, 'LIB_DIR', tmp_path)
     with pytest.raises(RuntimeError, match='missing'):
         native.lib()
+
+
+def test_handoff_spin_limit_and_workspace_reset_arguments(lib):
+    """The hand-off poll limit is a process-wide setting (-1 queries); the
+    workspace reset checks its arguments before any launch."""
+    prev = lib.ornith_mi355x_handoff_spin_limit(-1)
+    assert prev == 1 << 15
+    assert lib.ornith_mi355x_handoff_spin_limit(0) == prev
+    assert lib.ornith_mi355x_handoff_spin_limit(prev) == 0
+    assert lib.ornith_mi355x_handoff_spin_limit(-2) == -1
+    assert lib.ornith_mi355x_handoff_spin_limit((1 << 24) + 1) == -1
+    assert lib.ornith_mi355x_handoff_spin_limit(-1) == prev
+    assert lib.ornith_mi355x_workspace_reset(None, 256, None) == INVALID       # static scratch takes bytes 0
+    assert lib.ornith_mi355x_workspace_reset(C.c_void_p(0x1008), 256, None) == INVALID   # not 256-aligned
+    assert lib.ornith_mi355x_workspace_reset(C.c_void_p(0x1000), 258, None) == INVALID   # not whole words
