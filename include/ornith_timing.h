@@ -33,6 +33,19 @@ extern "C" {
 ORNITH_EXPORT hipError_t ornith_mi355x_timing_arm(const char* kernel, int capacity);
 ORNITH_EXPORT hipError_t ornith_mi355x_timing_read(const char* kernel, int* launches, double* total_ms);
 ORNITH_EXPORT int ornith_mi355x_timing_names(char* out, int capacity);
+/* Stage trace of the single-token layer kernel, for measurement.  Only a
+ * library built with -DORNITH_STAGE_TRACE (ornith_g256._build.build_stage_trace)
+ * records it; every other build returns hipErrorNotSupported.  Copies
+ * 64 calls x 256 blocks x 16 stage words (entries >= 262144) to the device
+ * buffer out_u64 on `stream`.  Call c of a run fills slot (its sequence
+ * number % 64); word = steady-clock ticks (100 MHz) in bits 0..51 | low 12
+ * bits of the sequence number << 52, 0 where the block did not reach the
+ * stage.  Stages: 0 block start, 1 router row published, 2 all logits seen,
+ * 3 experts selected, 4 routed gate-up dots done, 5 routed middle row
+ * published, 6/7/8 middle rows of slots 0/7/shared seen by the down waves,
+ * 9 down dots of slot 0 done, 10 output columns stored, 11 shared middle
+ * row published. */
+ORNITH_EXPORT hipError_t ornith_mi355x_stage_trace_read(void* out_u64, size_t entries, hipStream_t stream);
 
 #ifdef __cplusplus
 }

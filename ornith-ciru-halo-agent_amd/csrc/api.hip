@@ -10,6 +10,7 @@
 #include "../../include/ornith_routed.h"
 #include "../../include/ornith_dense.h"
 #include "../../include/ornith_moe.h"
+#include "../../include/ornith_timing.h"
 
 using namespace ornith;
 
@@ -523,6 +524,11 @@ extern "C" int ornith_mi355x_decode_route_path(int path) {
     if (path < -1 || path > 1) return -1;
     if (path == -1) return g_route_select_mode.load();
     return g_route_select_mode.exchange(path);
+}
+
+extern "C" hipError_t ornith_mi355x_stage_trace_read(void* out_u64, size_t entries, hipStream_t stream) {
+    if (!out_u64 || !aligned(out_u64, 8)) return hipErrorInvalidValue;
+    return layer1_stage_trace(static_cast<uint64_t*>(out_u64), entries, stream);
 }
 
 extern "C" int ornith_mi355x_handoff_spin_limit(int spins) {

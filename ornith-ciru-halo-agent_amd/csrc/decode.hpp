@@ -34,6 +34,10 @@ constexpr int kDecodeRouteArrive = kDecodeRouteIds + kDecodeMaxTokens * kTop;
 constexpr int kDecodeRouteMaxBlocks = 320;
 constexpr int kDecodeRouteWords = kDecodeRouteArrive + 8 * kDecodeRouteMaxBlocks;
 constexpr int kHandoffWords = kLayer1Words > kDecodeRouteWords ? kLayer1Words : kDecodeRouteWords;
+// Stage trace of the single-token layer kernel (measurement builds only):
+// kStageSlots timestamps per block for each of kStageCalls calls.
+constexpr int kStageSlots = 16;
+constexpr int kStageCalls = 64;
 // sticky flag of this library: a block of a one-launch kernel (single-token
 // layer, 2..32-token route) gave up waiting for another block's hand-off (the
 // grid was not resident at once)
@@ -80,6 +84,10 @@ extern std::atomic<int> g_single_token_mode;
 // where the grid is resident), 1 three kernels
 extern std::atomic<int> g_route_select_mode;
 hipError_t launch_decode1(const DecodeArgs& a, bool router, bool shared, int qmax, hipStream_t s);
+// Copies the single-token stage trace (kStageCalls x kLayer1Blocks x
+// kStageSlots words) to device memory `out`; hipErrorNotSupported unless the
+// library was built with ORNITH_STAGE_TRACE.
+hipError_t layer1_stage_trace(uint64_t* out, size_t entries, hipStream_t s);
 // Poll rounds of the one-launch kernels' hand-off waits (default kHandoffSpins;
 // 0 makes every wait give up at once, for tests of the time-out path).
 extern std::atomic<int> g_handoff_spins;

@@ -417,6 +417,23 @@ __device__ __forceinline__ void lds_wait(uint32_t* counter, uint32_t n) {
 constexpr int kLayer1DownBlocks = kHidden / 16;
 }  // namespace
 
+// Stage trace (measurement builds only, -DORNITH_STAGE_TRACE): lane 0 of the
+// named wave stores the steady clock (100 MHz) when a block reaches a stage,
+// into slot (call sequence number % kStageCalls) of g_layer1_stages, so the
+// calls of a captured graph land in distinct slots.  Ordinary builds compile
+// every stage point to nothing.
+#ifdef ORNITH_STAGE_TRACE
+__device__ uint64_t g_layer1_stages[kStageCalls * kLayer1Blocks * kStageSlots];
+#define L1_STAGE(i)                                                                                   \
+    do {                                                                                              \
+        if ((threadIdx.x & 63) == 0)                                                                  \
+            g_layer1_stages[(size_t(seq % kStageCalls) * kLayer1Blocks + blockIdx.x) * kStageSlots + (i)] = \
+                uint64_t(wall_clock64()) | (uint64_t(seq & 0xFFFu) << 52);                             \
+    } while (0)
+#else
+#define L1_STAGE(i) do {} while (0)
+#endif
+
 template <bool ROUTER, bool SHARED, int QMAX>
 __global__ __launch_bounds__(576) void layer1_kernel(DecodeArgs a) {
     __shared__ __align__(16) uint32_t lx[8 * 64];               // A8 words of x
@@ -436,6 +453,7 @@ __global__ __launch_bounds__(576) void layer1_kernel(DecodeArgs a) {
     uint64_t* W = a.l1_words;
     const uint32_t seq = __hip_atomic_load(a.l1_seq, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     const int limit = l1_limit(seq, a.handoff_spins);
+    if (wave == 0) L1_STAGE(0);                                  // block started
     const int gu = xcd_paired_block(L), s = gu >> 5, p = gu & 31;   // routed gate-up unit (slot s, pair p)
     const bool down_block = L < kLayer1DownBlocks;
     const int c = xcd_paired_block(L & (kLayer1DownBlocks - 1));   // down columns 16c..16c+15
@@ -497,6 +515,7 @@ __global__ __launch_bounds__(576) void layer1_kernel(DecodeArgs a) {
         float v = row(rv);
         if (a.bias) v = v + a.bias[L];
         if (lane == 0) l1_put(W, kLayer1Spread * L, seq, __float_as_uint(v));
+        L1_STAGE(1);                                                  // router row published
         if (SHARED && L == 0) {
             const float v2 = row(rv2);
             if (lane == 0) l1_put(W, kLayer1Spread * kExperts, seq, __float_as_uint(v2));
@@ -607,6 +626,7 @@ __global__ __launch_bounds__(576) void layer1_kernel(DecodeArgs a) {
         if (wave == 1) {
             lds_wait(&lsync[1], 4u);
             gate_epilogue(0, kTop, true);
+            L1_STAGE(11);                                             // shared middle published
         }
     }
     // ---- routing on wave 4 ----
@@ -619,6 +639,7 @@ __global__ __launch_bounds__(576) void layer1_kernel(DecodeArgs a) {
             for (int i = 0; i < 4; ++i) idx[i] = uint32_t(kLayer1Spread * (lane + 64 * i));
             if constexpr (SHARED) idx[NW - 1] = kLayer1Spread * kExperts;
             if (!l1_wait<NW, 0>(W, idx, seq, got, limit)) flags |= kFlagHandoffTimeout;
+            L1_STAGE(2);                                              // 257 logits seen
             float lg[4];
 #pragma unroll
             for (int i = 0; i < 4; ++i) lg[i] = __uint_as_float(got[i]);
@@ -651,6 +672,7 @@ __global__ __launch_bounds__(576) void layer1_kernel(DecodeArgs a) {
             if (lane == 0) lshared_logit = shared_logit_bits;
         }
         if (lane == kTop) lbank[kTop] = SHARED ? kShared : -1;
+        L1_STAGE(3);                                                  // experts selected
     }
     // every wave has its sequence number before the arrival word leaves
     if (lane == 0) lseq[wave] = seq;
@@ -688,6 +710,7 @@ __global__ __launch_bounds__(576) void layer1_kernel(DecodeArgs a) {
         // the routed dots always run (an empty slot's are not used), so no
         // load is left pending past this branch
         gate_dots(wr, mw, 1);
+        if (wave == 0) L1_STAGE(4);                                   // routed gate-up dots done
     }
     // down codes behind the gate-up stream (they are needed only after the
     // middle hand-off); one load site for every wave keeps them in the same
@@ -696,7 +719,10 @@ __global__ __launch_bounds__(576) void layer1_kernel(DecodeArgs a) {
     uint32_t gate_raw = 0;                  // bf16 sigmoid gate, used by the last step only
     if (SHARED && down_block && wave == 0) gate_raw = a.sigmoid_table[lshared_logit];
     __syncthreads();
-    if (wave == 0 && bank >= 0) gate_epilogue(1, s, false);
+    if (wave == 0 && bank >= 0) {
+        gate_epilogue(1, s, false);
+        L1_STAGE(5);                                                  // routed middle published
+    }
     if (!down_block) {
         flag_or(a.sticky, flags);
         return;
@@ -710,6 +736,9 @@ __global__ __launch_bounds__(576) void layer1_kernel(DecodeArgs a) {
 #pragma unroll
         for (int j = 0; j < 8; ++j) idx[j] = uint32_t(kLayer1Middle + wave * kInter + gm * kGroup + kb + 16 * j);
         if (!l1_wait<8, 1>(W, idx, seq, val, limit)) flags |= kFlagHandoffTimeout;
+        if (wave == 0) L1_STAGE(6);                                   // middle of slot 0 seen
+        if (wave == 7) L1_STAGE(7);                                   // middle of slot 7 seen
+        if (wave == 8) L1_STAGE(8);                                   // shared middle seen
         if (L == 0 && wave == 0) {
             // every block published its arrival long ago: read the words
             // now, check them at the end
@@ -763,6 +792,7 @@ __global__ __launch_bounds__(576) void layer1_kernel(DecodeArgs a) {
         if (!isfinite(v)) flags |= kFlagNonfiniteProjection;
         lro[wave][dn] = v;
     }
+    if (wave == 0) L1_STAGE(9);                                       // down dots of slot 0 done
     __syncthreads();
     if (tid < 16) {
         const int col = 16 * c + tid;
@@ -794,6 +824,7 @@ __global__ __launch_bounds__(576) void layer1_kernel(DecodeArgs a) {
             if (a.layer_out) a.layer_out[col] = f32_to_bf16_bits(bf16_bits_to_f32(o) + bf16_bits_to_f32(so));
         }
     }
+    if (wave == 0) L1_STAGE(10);                                      // output columns stored
     // ---- block 0 advances the sequence number once every block has arrived ----
     if (L == 0 && wave == 0) {
         uint32_t idx[4], val[4];
@@ -857,6 +888,18 @@ static hipError_t run1_any(const DecodeArgs& a, hipStream_t s) {
     b.handoff_spins = g_handoff_spins.load(std::memory_order_relaxed);
     timed_launch("layer1", layer1_kernel<ROUTER, SHARED, QMAX>, dim3(kLayer1Blocks), dim3(576), 0, s, b);
     return hipGetLastError();
+}
+
+hipError_t layer1_stage_trace(uint64_t* out, size_t entries, hipStream_t s) {
+#ifdef ORNITH_STAGE_TRACE
+    const size_t n = size_t(kStageCalls) * kLayer1Blocks * kStageSlots;
+    if (!out || entries < n) return hipErrorInvalidValue;
+    return hipMemcpyFromSymbolAsync(out, HIP_SYMBOL(g_layer1_stages), n * sizeof(uint64_t), 0,
+                                    hipMemcpyDeviceToDevice, s);
+#else
+    (void)out; (void)entries; (void)s;
+    return hipErrorNotSupported;
+#endif
 }
 
 hipError_t launch_decode1(const DecodeArgs& a, bool router, bool shared, int qmax, hipStream_t s) {

@@ -35,10 +35,13 @@ def library_path(tile: int = 32) -> Path:
     return LIBDIR / VARIANTS[tile]
 
 
-def _compile(name, tile, objdir):
+TRACE_DIR = LIBDIR / 'trace'
+
+
+def _compile(name, tile, objdir, extra=()):
     src = CSRC / name
     obj = objdir / (name + '.o')
-    cmd = [HIPCC, *FLAGS, f'-DORNITH_ROUTED_TILE={tile}', '-c', str(src), '-o', str(obj)]
+    cmd = [HIPCC, *FLAGS, *extra, f'-DORNITH_ROUTED_TILE={tile}', '-c', str(src), '-o', str(obj)]
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode:
         raise RuntimeError(f'hipcc failed for {name} (tile {tile}):\n{res.stderr}')
@@ -77,5 +80,20 @@ def build(verbose: bool = False, jobs: int = 8) -> list[Path]:
     return outs
 
 
+def build_stage_trace(jobs: int = 8) -> Path:
+    """The N32 build with the single-token kernel's stage trace compiled in
+    (-DORNITH_STAGE_TRACE), as lib/trace/libornith_g256_mi355x.so.  For
+    measurement only (stage_trace.py); the product builds record nothing."""
+    objdir = TRACE_DIR / 'obj'
+    objdir.mkdir(parents=True, exist_ok=True)
+    sources = [s for s in SOURCES if (CSRC / s).exists()]
+    with cf.ThreadPoolExecutor(max_workers=jobs) as pool:
+        results = list(pool.map(lambda n: _compile(n, 32, objdir, ('-DORNITH_STAGE_TRACE',)), sources))
+    out = TRACE_DIR / VARIANTS[32]
+    _link([obj for obj, _ in results], out)
+    return out
+
+
 if __name__ == '__main__':
-    print(build(verbose=True))
+    import sys
+    print(build_stage_trace() if '--stage-trace' in sys.argv[1:] else build(verbose=True))

@@ -108,6 +108,7 @@ _PROTOTYPES = {
     'ornith_mi355x_timing_arm': ([C.c_char_p, _INT], _INT),
     'ornith_mi355x_timing_read': ([C.c_char_p, C.POINTER(_INT), C.POINTER(C.c_double)], _INT),
     'ornith_mi355x_timing_names': ([C.c_char_p, _INT], _INT),
+    'ornith_mi355x_stage_trace_read': ([_VP, _SZ, _VP], _INT),
 }
 # entries that only some builds of the library export (bound when present)
 _OPTIONAL: dict = {}

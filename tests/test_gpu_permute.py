@@ -142,8 +142,8 @@ def test_routed_entry_permutation_with_edge_ids(device, banks):
     rng = np.random.default_rng(9177)
     x = to_dev(bf16_normal(rng, (T, 2048)), device)
     rw, ids = random_routing(rng, T)
-    ids[::7, 0] = 3                                    # bank 3: > 64 routes
-    ids[::5, 1] = 3
+    ids[ids == 3] = 4                                  # bank 3 only in slot 0: > 64 routes
+    ids[:, 0] = 3
     ids[2, :] = 9                                      # a token naming one expert eight times
     ids[4, 5] = -1                                     # padding
     ids[6, 2] = 300                                    # invalid: skipped, flag 4
