@@ -44,7 +44,8 @@ ORNITH_EXPORT int ornith_mi355x_timing_names(char* out, int capacity);
  * 3 experts selected, 4 routed gate-up dots done, 5 routed middle row
  * published, 6/7/8 middle rows of slots 0/7/shared seen by the down waves,
  * 9 down dots of slot 0 done, 10 output columns stored, 11 shared middle
- * row published. */
+ * row published, 12 speculative expert picks published, 13 shared gate
+ * logit seen, 14 gate-up dots of the four gate-up waves done. */
 ORNITH_EXPORT hipError_t ornith_mi355x_stage_trace_read(void* out_u64, size_t entries, hipStream_t stream);
 
 #ifdef __cplusplus

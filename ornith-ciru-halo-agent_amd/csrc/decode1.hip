@@ -415,6 +415,16 @@ __device__ __forceinline__ void lds_wait(uint32_t* counter, uint32_t n) {
     }
 }
 constexpr int kLayer1DownBlocks = kHidden / 16;
+// Waves of a block: 0-3 gate-up (wave 1 also its epilogue), 4 routing, 4-7 x
+// quantisation, 8 router row, 4-12 the down slots 0-8 (slot = wave - 4).  The
+// gate-up waves load nothing for the down part, so each down wave's poll for
+// its middle row queues behind its own down codes only, issued right after
+// the experts are known.
+constexpr int kLayer1Waves = 13, kLayer1DownWave0 = 4;
+// The routed gate-up epilogue runs on wave 1: the shared slot's down wave (12)
+// works at the same time and waves are dealt to the four SIMDs in turn
+// (wave w on SIMD w % 4), so the two do not share a SIMD.
+constexpr int kLayer1EpilogueWave = 1;
 }  // namespace
 
 // Stage trace (measurement builds only, -DORNITH_STAGE_TRACE): lane 0 of the
@@ -424,36 +434,44 @@ constexpr int kLayer1DownBlocks = kHidden / 16;
 // every stage point to nothing.
 #ifdef ORNITH_STAGE_TRACE
 __device__ uint64_t g_layer1_stages[kStageCalls * kLayer1Blocks * kStageSlots];
-#define L1_STAGE(i)                                                                                   \
+#define L1_STAGE_AT(i, t)                                                                             \
     do {                                                                                              \
         if ((threadIdx.x & 63) == 0)                                                                  \
             g_layer1_stages[(size_t(seq % kStageCalls) * kLayer1Blocks + blockIdx.x) * kStageSlots + (i)] = \
-                uint64_t(wall_clock64()) | (uint64_t(seq & 0xFFFu) << 52);                             \
+                (t) | (uint64_t(seq & 0xFFFu) << 52);                                                 \
     } while (0)
+#define L1_STAGE(i) L1_STAGE_AT(i, uint64_t(wall_clock64()))
 #else
+#define L1_STAGE_AT(i, t) do {} while (0)
 #define L1_STAGE(i) do {} while (0)
 #endif
 
 template <bool ROUTER, bool SHARED, int QMAX>
-__global__ __launch_bounds__(576) void layer1_kernel(DecodeArgs a) {
+__global__ __launch_bounds__(64 * kLayer1Waves) void layer1_kernel(DecodeArgs a) {
     __shared__ __align__(16) uint32_t lx[8 * 64];               // A8 words of x
     __shared__ float lxa[8], lxs[8];                            // group scale, scale * sum
     __shared__ float lterm[2][8][32];                           // gate-up terms: shared unit, routed unit
     __shared__ __align__(16) uint64_t s_cand[65];
-    __shared__ uint2 s_sel[kTop];
-    __shared__ int lbank[kSlots];
+    __shared__ uint2 s_sel[kTop], s_spec[kTop];
+    __shared__ int lbank[kSlots], lspec[kTop];
     __shared__ float lw8[kTop];
-    __shared__ uint32_t lshared_logit;
     __shared__ __align__(16) uint32_t lm[kSlots * 2 * 64];      // A8 words of the middle rows
     __shared__ float lma[kSlots * 2], lms[kSlots * 2];
     __shared__ float lro[kSlots][16];
-    __shared__ uint32_t lseq[kSlots];
-    __shared__ uint32_t lsync[2];   // waves done: x quantisation (4), shared-unit dots (4)
+    __shared__ uint32_t lseq[kLayer1Waves];
+    __shared__ uint32_t lgate;                                  // bf16 sigmoid gate of the shared expert
+    // waves done: x quantisation (4), shared-unit dots (4); speculative picks
+    // published (1); routed gate-up dots (4)
+    __shared__ uint32_t lsync[4];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, L = int(blockIdx.x);
     uint64_t* W = a.l1_words;
-    const uint32_t seq = __hip_atomic_load(a.l1_seq, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    const int limit = l1_limit(seq, a.handoff_spins);
-    if (wave == 0) L1_STAGE(0);                                  // block started
+    // the call's sequence number: its load is issued first and its value is
+    // used only after the independent loads below are issued (a wave's loads
+    // complete in order, so the first use waits for nothing issued later)
+    uint32_t seq_v = __hip_atomic_load(a.l1_seq, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+#ifdef ORNITH_STAGE_TRACE
+    const uint64_t t_start = uint64_t(wall_clock64());
+#endif
     const int gu = xcd_paired_block(L), s = gu >> 5, p = gu & 31;   // routed gate-up unit (slot s, pair p)
     const bool down_block = L < kLayer1DownBlocks;
     const int c = xcd_paired_block(L & (kLayer1DownBlocks - 1));   // down columns 16c..16c+15
@@ -481,6 +499,27 @@ __global__ __launch_bounds__(576) void layer1_kernel(DecodeArgs a) {
         }
     }
     uint32_t ws[32], wd[16], mws = 0, mwd = 0;
+    const int job = 2 * (wave - 4) + (lane >> 5);
+    uint4 raw{};
+    if (wave >= 4 && wave < 8) raw = *reinterpret_cast<const uint4*>(a.x + job * kGroup + lp * 8);
+    if (tid == 0) {
+        lsync[0] = 0;
+        lsync[1] = 0;
+        lsync[2] = 0;
+        lsync[3] = 0;
+    }
+    __syncthreads();
+    // The sequence number is taken only here, where every wave needs the
+    // loads it issued above anyway (without the asm the compiler converts it
+    // to a scalar right after its load and waits for it before issuing them).
+    // Each wave has it before barrier A, so before the block's arrival word.
+    asm volatile("" : "+v"(seq_v));
+    const uint32_t seq = __builtin_amdgcn_readfirstlane(seq_v);
+    const int limit = l1_limit(seq, a.handoff_spins);
+    if (lane == 0) lseq[wave] = seq;
+    if (wave == 0) L1_STAGE_AT(0, t_start);                      // block started
+    // shared-unit codes (slot-0 blocks), issued after the router rows so the
+    // two do not share the first HBM burst; the shared middle row has slack
     if (shared_unit && wave < 4) {
         const BankView bv = bank_view(true);
         const uint32_t* wp = a.s13_codes + bv.word(gcol, g, 8);
@@ -488,14 +527,6 @@ __global__ __launch_bounds__(576) void layer1_kernel(DecodeArgs a) {
         for (int j = 0; j < 32; ++j) ws[j] = wp[j * bv.stride()];
         mws = a.s13_meta[bv.meta(gcol, g, 8)];
     }
-    const int job = 2 * (wave - 4) + (lane >> 5);
-    uint4 raw{};
-    if (wave >= 4 && wave < 8) raw = *reinterpret_cast<const uint4*>(a.x + job * kGroup + lp * 8);
-    if (tid == 0) {
-        lsync[0] = 0;
-        lsync[1] = 0;
-    }
-    __syncthreads();
     // ---- router row(s) in the declared order of decode1_route_kernel, published at once ----
     if (ROUTER && wave == 8) {
         auto row = [&](const uint4 (&wv)[4]) {
@@ -523,11 +554,9 @@ __global__ __launch_bounds__(576) void layer1_kernel(DecodeArgs a) {
     }
     int id_in = -1;
     float w_in = 0.f;
-    uint32_t shared_logit_bits = 0;
     if (!ROUTER && wave == 4) {
         id_in = a.ids_in[lane & 7];
         w_in = a.reduce_w[lane & 7];
-        if (SHARED) shared_logit_bits = a.shared_logit[0];
     }
     // gate-up dots of one unit from codes in registers, into lterm[u]
     auto gate_dots = [&](const uint32_t (&wr)[32], uint32_t mw, int u) {
@@ -632,17 +661,29 @@ __global__ __launch_bounds__(576) void layer1_kernel(DecodeArgs a) {
     // ---- routing on wave 4 ----
     if (wave == 4) {
         if (ROUTER) {
-            // the 256 expert logits, and the shared gate logit when there is one
-            constexpr int NW = SHARED ? 5 : 4;
-            uint32_t idx[NW], got[NW];
+            // the 256 expert logits (the shared gate logit is read later, by
+            // the shared slot's down wave)
+            uint32_t idx[4], got[4];
 #pragma unroll
             for (int i = 0; i < 4; ++i) idx[i] = uint32_t(kLayer1Spread * (lane + 64 * i));
-            if constexpr (SHARED) idx[NW - 1] = kLayer1Spread * kExperts;
-            if (!l1_wait<NW, 0>(W, idx, seq, got, limit)) flags |= kFlagHandoffTimeout;
-            L1_STAGE(2);                                              // 257 logits seen
+            if (!l1_wait<4, 0>(W, idx, seq, got, limit)) flags |= kFlagHandoffTimeout;
+            L1_STAGE(2);                                              // 256 logits seen
             float lg[4];
 #pragma unroll
             for (int i = 0; i < 4; ++i) lg[i] = __uint_as_float(got[i]);
+            // speculative picks: the eight largest logits (ties to the lower
+            // id), published at once so waves 0-3 start loading their codes.
+            // The softmax is monotone, so these are the exact picks unless
+            // rounding makes two probabilities equal; waves 0-3 check them
+            // against the exact picks below and reload on a difference.
+            uint32_t lk[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) lk[i] = f32_order_key(lg[i] + 0.f);   // -0 -> +0
+            top8_rank_lds(lk, s_cand, s_spec);
+            if (lane < kTop) lspec[lane] = int(s_spec[lane].y);
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+            if (lane == 0) __hip_atomic_fetch_add(&lsync[2], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+            L1_STAGE(12);                                             // speculative picks published
             uint32_t k[4];
             softmax_keys(lg, k);
             top8_rank_lds(k, s_cand, s_sel);
@@ -659,28 +700,67 @@ __global__ __launch_bounds__(576) void layer1_kernel(DecodeArgs a) {
                     a.topk_ids[lane] = int(pick.y);
                 }
             }
-            if constexpr (SHARED) {
-                const uint16_t sl = f32_to_bf16_bits(__uint_as_float(got[NW - 1]));
-                if (lane == 0) lshared_logit = sl;
-                if (L == 0 && lane == 0) a.shared_logit[0] = sl;
-            }
         } else {
             if (lane < kTop) {
                 lbank[lane] = (id_in >= 0 && id_in < kExperts) ? id_in : -1;
                 lw8[lane] = w_in;
             }
-            if (lane == 0) lshared_logit = shared_logit_bits;
         }
         if (lane == kTop) lbank[kTop] = SHARED ? kShared : -1;
         L1_STAGE(3);                                                  // experts selected
     }
-    // every wave has its sequence number before the arrival word leaves
-    if (lane == 0) lseq[wave] = seq;
+    // ---- the shared slot's down wave, idle until here: the shared expert's
+    // bf16 sigmoid gate (used by the last step only) from the gate logit
+    // (block 0's second row) and the table, then the shared down codes, which
+    // need no routing, so the shared slot's down work runs as soon as its
+    // middle row (formed before the routing) arrives ----
+    uint32_t gate_bits = 0;
+    if (SHARED && down_block && wave == kLayer1DownWave0 + kTop) {
+        uint32_t sl;
+        if (ROUTER) {
+            uint32_t idx1[1] = {uint32_t(kLayer1Spread * kExperts)}, got1[1];
+            if (!l1_wait<1, 1>(W, idx1, seq, got1, limit)) flags |= kFlagHandoffTimeout;
+            sl = f32_to_bf16_bits(__uint_as_float(got1[0]));
+            if (L == 0 && lane == 0) a.shared_logit[0] = uint16_t(sl);
+            L1_STAGE(13);                                             // shared gate logit seen
+        } else {
+            sl = a.shared_logit[0];
+        }
+        gate_bits = a.sigmoid_table[sl];
+        const BankView bv = bank_view(true);
+        const uint32_t* wp = a.s2_codes + bv.word(dcol, dg, 2) + 16 * dh * bv.stride();
+#pragma unroll
+        for (int j = 0; j < 16; ++j) wd[j] = wp[j * bv.stride()];
+        mwd = a.s2_meta[bv.meta(dcol, dg, 2)];
+    }
+    // ---- routed gate-up codes (waves 0-3), loaded from the speculative pick
+    // of slot s as soon as it is published (the caller's id without the
+    // router); the exact pick is checked after the barrier ----
+    uint32_t wr[32], mw = 0;
+    int sbank = -1;
+    auto load_gate = [&](int b) {
+        const BankView bv = bank_view(false);
+        const uint32_t* wp = a.w13_codes + size_t(b) * kGateBankWords + bv.word(gcol, g, 8);
+#pragma unroll
+        for (int j = 0; j < 32; ++j) wr[j] = wp[j * bv.stride()];
+        mw = a.w13_meta[size_t(b) * kGateBankMeta + bv.meta(gcol, g, 8)];
+    };
+    if (wave < 4) {
+        if (ROUTER) {
+            lds_wait(&lsync[2], 1u);
+            sbank = lspec[s];
+        } else {
+            const int id = a.ids_in[s];
+            sbank = id >= 0 && id < kExperts ? id : -1;
+        }
+        load_gate(sbank >= 0 ? sbank : 0);
+    }
     __syncthreads();
     if (tid == 0) l1_put(W, kLayer1Arrive + kLayer1Spread * L, seq, lseq[0]);
 
-    // the down codes of slot `wave`
-    const int dbank = down_block ? lbank[wave] : -1;
+    // the down codes of slot `dslot`
+    const int dslot = wave - kLayer1DownWave0;
+    const int dbank = down_block && dslot >= 0 && dslot < kSlots ? lbank[dslot] : -1;
     auto load_down = [&]() {
         const int lb = dbank >= 0 ? dbank : 0;
         const bool sh = lb == kShared;
@@ -692,7 +772,7 @@ __global__ __launch_bounds__(576) void layer1_kernel(DecodeArgs a) {
         mwd = (sh ? a.s2_meta : a.w2_meta + size_t(lb) * kDownBankMeta)[bv.meta(dcol, dg, 2)];
     };
 
-    // ---- routed gate-up (waves 0-3); down codes right behind ----
+    // ---- routed gate-up dots (waves 0-3) ----
     int bank = -1;
     if (wave < 4) {
         bank = lbank[s];
@@ -700,51 +780,55 @@ __global__ __launch_bounds__(576) void layer1_kernel(DecodeArgs a) {
             const int id = a.ids_in[s];
             if (id != -1 && p == 0 && tid == 0) flags |= kFlagInvalidExpert;
         }
-        const int lb = bank >= 0 ? bank : 0;
-        const BankView bv = bank_view(false);
-        const uint32_t* wp = a.w13_codes + size_t(lb) * kGateBankWords + bv.word(gcol, g, 8);
-        uint32_t wr[32];
-#pragma unroll
-        for (int j = 0; j < 32; ++j) wr[j] = wp[j * bv.stride()];
-        const uint32_t mw = a.w13_meta[size_t(lb) * kGateBankMeta + bv.meta(gcol, g, 8)];
+        // the exact pick differs from the speculative one only when two
+        // softmax values tie after rounding: load the right codes
+        if (bank != sbank) load_gate(bank >= 0 ? bank : 0);
         // the routed dots always run (an empty slot's are not used), so no
         // load is left pending past this branch
         gate_dots(wr, mw, 1);
         if (wave == 0) L1_STAGE(4);                                   // routed gate-up dots done
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+        if (lane == 0) __hip_atomic_fetch_add(&lsync[3], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
     }
-    // down codes behind the gate-up stream (they are needed only after the
-    // middle hand-off); one load site for every wave keeps them in the same
-    // registers, and nothing waits for them before the dots
-    if (down_block) load_down();
-    uint32_t gate_raw = 0;                  // bf16 sigmoid gate, used by the last step only
-    if (SHARED && down_block && wave == 0) gate_raw = a.sigmoid_table[lshared_logit];
-    __syncthreads();
-    if (wave == 0 && bank >= 0) {
-        gate_epilogue(1, s, false);
-        L1_STAGE(5);                                                  // routed middle published
+    // routed down codes: issued once the block's gate-up dots are done (issued
+    // earlier they slow this CU's gate-up codes; issued after the epilogue
+    // they land after the middle rows).  No block barrier: the epilogue waits
+    // only for the four gate-up waves.  The shared slot's wave loaded its
+    // codes before barrier A.
+    if (down_block && dslot >= 0 && dslot < kTop) {
+        lds_wait(&lsync[3], 4u);
+        load_down();
+    }
+    uint64_t arrival[4] = {0, 0, 0, 0};
+    if (wave == kLayer1EpilogueWave) {
+        lds_wait(&lsync[3], 4u);
+        L1_STAGE(14);                                                 // gate-up dots of all four waves done
+        if (bank >= 0) {
+            gate_epilogue(1, s, false);
+            L1_STAGE(5);                                              // routed middle published
+        }
+    }
+    if (L == 0 && wave == 0) {
+        // every block published its arrival after barrier A: read the words
+        // now, check them at the end
+#pragma unroll
+        for (int i = 0; i < 4; ++i) arrival[i] = l1_get(W, uint32_t(kLayer1Arrive + kLayer1Spread * (lane + 64 * i)));
     }
     if (!down_block) {
         flag_or(a.sticky, flags);
         return;
     }
 
-    // ---- middle row of slot `wave`: wait, H128 tail, A8 (decode1_down_kernel) ----
+    // ---- middle row of slot `dslot`: wait, H128 tail, A8 (decode1_down_kernel) ----
     const int gm = lane >> 5, kb = strided_base(lp);
-    uint64_t arrival[4] = {0, 0, 0, 0};
     if (dbank >= 0) {
         uint32_t idx[8], val[8];
 #pragma unroll
-        for (int j = 0; j < 8; ++j) idx[j] = uint32_t(kLayer1Middle + wave * kInter + gm * kGroup + kb + 16 * j);
+        for (int j = 0; j < 8; ++j) idx[j] = uint32_t(kLayer1Middle + dslot * kInter + gm * kGroup + kb + 16 * j);
         if (!l1_wait<8, 1>(W, idx, seq, val, limit)) flags |= kFlagHandoffTimeout;
-        if (wave == 0) L1_STAGE(6);                                   // middle of slot 0 seen
-        if (wave == 7) L1_STAGE(7);                                   // middle of slot 7 seen
-        if (wave == 8) L1_STAGE(8);                                   // shared middle seen
-        if (L == 0 && wave == 0) {
-            // every block published its arrival long ago: read the words
-            // now, check them at the end
-#pragma unroll
-            for (int i = 0; i < 4; ++i) arrival[i] = l1_get(W, uint32_t(kLayer1Arrive + kLayer1Spread * (lane + 64 * i)));
-        }
+        if (dslot == 0) L1_STAGE(6);                                  // middle of slot 0 seen
+        if (dslot == 7) L1_STAGE(7);                                  // middle of slot 7 seen
+        if (dslot == 8) L1_STAGE(8);                                  // shared middle seen
         float v[8];
 #pragma unroll
         for (int j = 0; j < 8; ++j) v[j] = __uint_as_float(val[j]);
@@ -754,14 +838,14 @@ __global__ __launch_bounds__(576) void layer1_kernel(DecodeArgs a) {
         int sum;
         quantize_strided<QMAX>(v, qv, sb, sum, flags, kFlagNonfiniteInput | kFlagInvalidActivation,
                                kFlagInvalidActivation);
-        uint8_t* lb = reinterpret_cast<uint8_t*>(&lm[(2 * wave + gm) * 64]);
+        uint8_t* lb = reinterpret_cast<uint8_t*>(&lm[(2 * dslot + gm) * 64]);
 #pragma unroll
         for (int j = 0; j < 8; ++j)
             lb[4 * (2 * ((kb >> 3) + 2 * j) + (kb & 1)) + ((kb & 7) >> 1)] = uint8_t(qv[j]);
         if (lp == 0) {
             const float sc = f16_bits_to_f32(sb);
-            lma[2 * wave + gm] = sc;
-            lms[2 * wave + gm] = sc * float(sum);
+            lma[2 * dslot + gm] = sc;
+            lms[2 * dslot + gm] = sc * float(sum);
         }
     }
     // the quantised row is this wave's own: no block barrier before its dots
@@ -770,7 +854,7 @@ __global__ __launch_bounds__(576) void layer1_kernel(DecodeArgs a) {
     // ---- down dots: the two chunk halves joined exactly, then the two-group tree ----
     float term = 0.f;
     if (dbank >= 0) {
-        const uint4* ab = reinterpret_cast<const uint4*>(&lm[(2 * wave + dg) * 64 + 32 * dh]);
+        const uint4* ab = reinterpret_cast<const uint4*>(&lm[(2 * dslot + dg) * 64 + 32 * dh]);
         int dot = 0;
 #pragma unroll
         for (int c4 = 0; c4 < 8; ++c4) {
@@ -781,18 +865,19 @@ __global__ __launch_bounds__(576) void layer1_kernel(DecodeArgs a) {
             dot = dot4(code_odd(wd[2 * c4 + 1]), int(av.w), dot);
         }
         dot += xor_perm_i<16>(dot);
-        term = tree_term(dot, lma[2 * wave + dg], lms[2 * wave + dg], mwd);
+        term = tree_term(dot, lma[2 * dslot + dg], lms[2 * dslot + dg], mwd);
     }
     const float term1 = xor_perm_f<32>(term);
     if (dbank >= 0 && lane < 16) {
         float v = 0.f;
         v = v + term;
         v = v + term1;
-        if (wave == kTop) v = bf16_round(v);
+        if (dslot == kTop) v = bf16_round(v);
         if (!isfinite(v)) flags |= kFlagNonfiniteProjection;
-        lro[wave][dn] = v;
+        lro[dslot][dn] = v;
     }
-    if (wave == 0) L1_STAGE(9);                                       // down dots of slot 0 done
+    if (dslot == 0) L1_STAGE(9);                                      // down dots of slot 0 done
+    if (SHARED && dslot == kTop && lane == 0) lgate = gate_bits;
     __syncthreads();
     if (tid < 16) {
         const int col = 16 * c + tid;
@@ -815,8 +900,7 @@ __global__ __launch_bounds__(576) void layer1_kernel(DecodeArgs a) {
         if (a.final_f32) a.final_f32[col] = sum;
         if (a.out) a.out[col] = o;
         if (SHARED) {
-            asm volatile("" : "+v"(gate_raw));   // keep the gate's load unwaited until here
-            const float gate = bf16_bits_to_f32(gate_raw);
+            const float gate = bf16_bits_to_f32(lgate);
             const float sv = lro[kTop][tid] * gate;
             if (!isfinite(sv)) flags |= kFlagNonfiniteOutput;
             const uint16_t so = f32_to_bf16_bits(sv);
@@ -871,7 +955,7 @@ static bool layer1_fits(hipStream_t s) {
     if (dev < 0 || dev >= kMaxDevices) return false;
     int st = state[dev].load(std::memory_order_relaxed);
     if (st == 0) {
-        st = resident_blocks(layer1_kernel<ROUTER, SHARED, QMAX>, 576, dev) >= kLayer1Blocks ? 1 : 2;
+        st = resident_blocks(layer1_kernel<ROUTER, SHARED, QMAX>, 64 * kLayer1Waves, dev) >= kLayer1Blocks ? 1 : 2;
         state[dev].store(st, std::memory_order_relaxed);
     }
     return st == 1;
@@ -886,7 +970,8 @@ static hipError_t run1_any(const DecodeArgs& a, hipStream_t s) {
     if (mode == 1 || !layer1_fits<ROUTER, SHARED, QMAX>(s)) return run1<ROUTER, SHARED, QMAX>(a, s);
     DecodeArgs b = a;
     b.handoff_spins = g_handoff_spins.load(std::memory_order_relaxed);
-    timed_launch("layer1", layer1_kernel<ROUTER, SHARED, QMAX>, dim3(kLayer1Blocks), dim3(576), 0, s, b);
+    timed_launch("layer1", layer1_kernel<ROUTER, SHARED, QMAX>, dim3(kLayer1Blocks), dim3(64 * kLayer1Waves), 0, s,
+                 b);
     return hipGetLastError();
 }
 

@@ -70,6 +70,13 @@ __device__ __forceinline__ void router_rows_wave(const uint16_t* __restrict__ x,
     if (words && lane < nt) l1_put(words, word0 + lane, seq, __float_as_uint(pub));
 }
 
+// Order key of an fp32 value: unsigned order of keys = numeric order of the
+// values (-0 and +0 differ; NaNs sort beyond the infinities by sign).
+__device__ __forceinline__ uint32_t f32_order_key(float v) {
+    const uint32_t b = __float_as_uint(v);
+    return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+}
+
 // Softmax probabilities of one token as order keys: lane l holds experts l,
 // l+64, l+128, l+192; k[i] is the fp32 bit pattern of the probability (all
 // non-negative, so integer order is value order).

@@ -11,12 +11,17 @@ over blocks, in microseconds, plus the spacing of consecutive calls (last
 output stored -> next call's first block start).
 
     python -m ornith_g256.stage_trace [--layers 40] [--rounds 5] [--json]
+
+ORNITH_G256_TRACE_DIR names another directory holding a stage-trace build
+(to compare two builds on one machine).
 """
 from __future__ import annotations
 
 import argparse
 import json
+import os
 import sys
+from pathlib import Path
 
 import numpy as np
 import torch
@@ -26,8 +31,20 @@ from . import _build, native, synthetic
 STAGES = ['block start', 'router row published', 'all logits seen', 'experts selected',
           'routed gate-up dots done', 'routed middle published', 'middle of slot 0 seen (down)',
           'middle of slot 7 seen (down)', 'shared middle seen (down)', 'down dots of slot 0 done',
-          'output columns stored', 'shared middle published']
+          'output columns stored', 'shared middle published', 'speculative picks published',
+          'shared gate logit seen (down)', 'gate-up dots of all four waves done']
 CALLS, BLOCKS, SLOTS = 64, 256, 16
+
+
+def _slot_of_block():
+    """Routed slot of each block's gate-up unit (the kernel's XCD pairing:
+    block L = 16q + 8h + x takes unit 2(8q + x) + h, slot = unit / 32)."""
+    L = np.arange(BLOCKS)
+    x, h, q = L & 7, (L >> 3) & 1, L >> 4
+    return (2 * (8 * q + x) + h) >> 5
+
+
+SLOT_OF_BLOCK = _slot_of_block()
 TICK_US = 0.01                          # 100 MHz steady clock
 
 
@@ -52,7 +69,7 @@ def main(argv=None):
     args = ap.parse_args(argv)
     if args.layers > CALLS:
         raise SystemExit(f'at most {CALLS} calls per replay')
-    native.LIB_DIR = _build.TRACE_DIR
+    native.LIB_DIR = Path(os.environ.get('ORNITH_G256_TRACE_DIR', _build.TRACE_DIR))
     h = native.lib()
     dev = torch.device('cuda', 0)
     probe = torch.zeros(CALLS * BLOCKS * SLOTS, dtype=torch.int64, device=dev)
@@ -95,6 +112,7 @@ def main(argv=None):
     torch.cuda.synchronize()
     seq = 3 * args.layers                  # calls made so far on this workspace
     per_stage = [[] for _ in STAGES]
+    per_slot = {}
     spacing, spans, replay_ms = [], [], []
     for _ in range(args.rounds):
         start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -119,6 +137,13 @@ def main(argv=None):
                 v = v[~np.isnan(v)]
                 if v.size:
                     per_stage[k].append((np.percentile(v, 50), np.percentile(v, 90), v.max(), v.size))
+            for slot in range(8):
+                sel = SLOT_OF_BLOCK == slot
+                for k in (4, 14, 5):
+                    v = rel[sel, k]
+                    v = v[~np.isnan(v)]
+                    if v.size:
+                        per_slot.setdefault((slot, k), []).append((np.percentile(v, 50), v.max()))
             last = np.nanmax(c[:, 10])
             spans.append((last - t0) * TICK_US)
             if prev_end is not None:
@@ -132,9 +157,12 @@ def main(argv=None):
         med = np.median(a, axis=0) if len(a) else [np.nan] * 4
         rows.append({'stage': k, 'name': name, 'p50_us': float(med[0]), 'p90_us': float(med[1]),
                      'max_us': float(med[2]), 'blocks': int(med[3]) if len(a) else 0})
+    slots = {f'slot{sl}': {STAGES[k]: [float(x) for x in np.median(np.array(per_slot[(sl, k)]), axis=0)]
+                           for k in (4, 14, 5) if (sl, k) in per_slot} for sl in range(8)}
     res = {'calls': len(spans), 'us_per_call_graph': float(np.median(replay_ms)) * 1e3 / args.layers,
            'kernel_span_us_median': float(np.median(spans)),
-           'call_spacing_us_median': float(np.median(spacing)) if spacing else None, 'stages': rows}
+           'call_spacing_us_median': float(np.median(spacing)) if spacing else None, 'stages': rows,
+           'per_slot_p50_max_us': slots}
     if args.json:
         print(json.dumps(res))
         return res
@@ -145,6 +173,13 @@ def main(argv=None):
     print('|---|---:|---:|---:|---:|')
     for r in rows:
         print(f"| {r['stage']} {r['name']} | {r['p50_us']:.2f} | {r['p90_us']:.2f} | {r['max_us']:.2f} | {r['blocks']} |")
+    print()
+    print('| routed slot | gate-up dots of wave 0 p50 / max (us) | of all four waves | middle published |')
+    print('|---|---:|---:|---:|')
+    for sl in range(8):
+        d = slots[f'slot{sl}']
+        cells = [d.get(STAGES[k], [np.nan] * 2) for k in (4, 14, 5)]
+        print(f'| {sl} | ' + ' | '.join(f'{c[0]:.2f} / {c[1]:.2f}' for c in cells) + ' |')
     return res
 
 
