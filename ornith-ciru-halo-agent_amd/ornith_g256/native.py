@@ -36,7 +36,7 @@ import torch
 LIB_DIR = Path(__file__).resolve().parent / 'lib'
 BUILDS = {32: 'libornith_g256_mi355x.so', 16: 'libornith_g256_mi355x_n16.so'}
 
-HIDDEN, EXPERTS, TOP = 2048, 256, 8
+HIDDEN, EXPERTS, TOP, INTER = 2048, 256, 8, 512
 HEAD_VOCAB, HEAD_MAX_ROWS = 248320, 64
 A8_ONLY_PREFILL_ROWS = 64      # _a4_prefill entries switch to A4 above this many tokens
 
@@ -185,11 +185,11 @@ def _settings_key(settings):
     return tuple((k, str(settings.get(k))) for k in keys)
 
 
-def configure(settings, capacity, shapes):
+def configure(settings, capacity, shapes, shared_expert=False):
     """Resolve the library roles, bind the launch entries and return the
     workspace size the caller allocates once (the max over the routed
-    layout, the dense layouts plus their bf16 prefill operands, and the W8
-    head layout)."""
+    layout, the dense layouts plus their bf16 prefill operands, the W8 head
+    layout and, with `shared_expert`, the fused shared slot and fixed8)."""
     global _binding
     a8 = settings.get('routed_activation_bits', 8)
     a8_prefill = settings.get('routed_prefill_activation_bits', 8)
@@ -244,6 +244,11 @@ def configure(settings, capacity, shapes):
         sizes.append(dense_layout(capacity, n, k, tile=roles['dense']).workspace_bytes)
         sizes.append((capacity * k + n * k) * 2)       # bf16 prefill operands (transformed x, dequantised W)
     sizes.append(head_layout(HEAD_MAX_ROWS, HEAD_VOCAB, tile=roles['head']).workspace_bytes)
+    if shared_expert:
+        # the fused ninth slot (at most 16 rows, any routed build) and fixed8
+        for tile in {roles['routed'], 32}:
+            sizes.append(routed_layout(min(16, int(capacity)), 'shared', tile=tile).workspace_bytes)
+        sizes.append(shared_fixed8_bytes(capacity))
     if min(sizes) <= 0:
         raise RuntimeError('native workspace query returned an empty layout')
     _binding = binding
@@ -293,6 +298,31 @@ def phase_segments(segments):
         yield
     finally:
         _phase_plan.reset(token)
+
+
+# The phases of every row of the current model step, (start, end, is_prefill)
+# runs covering the batch, also for single-phase and small batches (the
+# plans above are only for the routed split).  The shared expert reads it to
+# know its decode rows; unset means no decode rows.
+_step_phases: contextvars.ContextVar[tuple] = contextvars.ContextVar('ornith_step_phases', default=())
+
+
+@contextmanager
+def step_phases(segments):
+    """Within this context, the rows of a model step are in the phases
+    `segments` ((start, end, is_prefill) runs from row 0); rows past the
+    last run are prefill."""
+    token = _step_phases.set(tuple((int(a), int(b), bool(p)) for a, b, p in segments))
+    try:
+        yield
+    finally:
+        _step_phases.reset(token)
+
+
+def decode_runs(rows):
+    """(start, end) runs of decode rows among the first `rows` rows of the
+    current step (empty when no step phases are set)."""
+    return tuple((a, min(b, rows)) for a, b, p in _step_phases.get() if not p and a < rows)
 
 
 def _active_plan(rows):

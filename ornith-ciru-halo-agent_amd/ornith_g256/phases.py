@@ -47,6 +47,25 @@ def plan_segments(counts: Sequence[int], prefill: Sequence[bool]) -> tuple:
     return tuple(segments)
 
 
+def step_runs(counts: Sequence[int], prefill: Sequence[bool]) -> tuple:
+    """The same runs as plan_segments without its size and mixing filter:
+    the phase of every row of the step (the shared expert's decode rows)."""
+    if len(counts) != len(prefill):
+        raise ValueError(f'{len(counts)} token counts for {len(prefill)} phases')
+    runs: list[tuple[int, int, bool]] = []
+    row = 0
+    for n, p in zip(counts, prefill):
+        n, p = int(n), bool(p)
+        if n < 0:
+            raise ValueError(f'negative token count {n}')
+        if n and runs and runs[-1][2] == p:
+            runs[-1] = (runs[-1][0], row + n, p)
+        elif n:
+            runs.append((row, row + n, p))
+        row += n
+    return tuple(runs)
+
+
 def request_phases(num_computed: Iterable[int], num_prompt: Iterable[int]) -> list[bool]:
     """A request is in prefill while fewer tokens than its prompt have been
     computed (phase_dispatch.py:15)."""
@@ -68,8 +87,10 @@ def install_vllm_hook():
         batch = self.input_batch
         n = batch.num_reqs
         phases = request_phases(batch.num_computed_tokens_cpu[:n], batch.num_prompt_tokens[:n])
-        plan = plan_segments([int(v) for v in num_scheduled_tokens], phases)
+        counts = [int(v) for v in num_scheduled_tokens]
+        plan = plan_segments(counts, phases)
         self._ornith_phase_token = native._phase_plan.set(plan)
+        self._ornith_step_token = native._step_phases.set(step_runs(counts, phases))
         return prepare_inputs(self, scheduler_output, num_scheduled_tokens)
 
     def execute(self, *args, **kwargs):
@@ -80,6 +101,10 @@ def install_vllm_hook():
             if token is not None:
                 native._phase_plan.reset(token)
                 self._ornith_phase_token = None
+            token = getattr(self, '_ornith_step_token', None)
+            if token is not None:
+                native._step_phases.reset(token)
+                self._ornith_step_token = None
 
     GPUModelRunner._prepare_inputs, GPUModelRunner.execute_model = prepare, execute
     GPUModelRunner._ornith_phase_hook = True

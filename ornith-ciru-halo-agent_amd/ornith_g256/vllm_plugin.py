@@ -11,6 +11,15 @@ unquantized.  The routing contract is the one the routed kernels implement:
 E256/top-8/H2048/I512, plain renormalised softmax top-8, one rank, no
 EP/TP/SP, int32 top-k ids (moe_base.py:12-67).
 
+Besides the quantized layers, the block's router gate (``layers.N.mlp.gate``,
+an unquantized bf16 [256, 2048] linear) runs on this library's router kernel
+(the reference routes it to its own row-dot, iu4_correctness/gates.py:113-139),
+and the block's shared expert (``layers.N.mlp.shared_expert``) is served by
+this library: for batches of at most 16 rows vLLM's shared-expert forward is
+deferred to the block's routed launch, which runs it as the fused ninth slot
+(moe_shared.py:19-77); the step's decode rows are then recomputed by fixed8
+(shared_live.py:110-147), for larger batches after vLLM's own shared forward.
+
 The methods themselves (weights, repack, apply) are those of methods.py; the
 vLLM classes here only adapt vLLM's call signatures to them.
 """
@@ -22,6 +31,7 @@ QUANT_CONFIG = dict(quant_method='ornith_g256', group_size=256, transform_block=
 DENSE_SUFFIXES = ('.linear_attn.in_proj_qkvz', '.linear_attn.out_proj', '.self_attn.qkv_proj',
                   '.self_attn.o_proj', '.mlp.shared_expert.gate_up_proj', '.mlp.shared_expert.down_proj')
 ROUTED_PREFIX = re.compile(r'layers\.[0-9]+\.mlp\.experts$')
+ROUTER_GATE = re.compile(r'layers\.[0-9]+\.mlp\.gate$')
 
 
 def check_quant_config(config: dict):
@@ -42,6 +52,38 @@ def check_routing_contract(layer):
         raise ValueError('ornith_g256 routed experts need plain renormalised softmax top-8 routing')
 
 
+def bridge_shared_experts(SharedExperts):
+    """Wrap vLLM's SharedExperts.forward (once) so a shared expert this
+    library serves (its MLP carries ``_ornith_shared``, set by
+    methods.Runtime) is computed by the library:
+      * at most 16 rows: no forward here; the output slot gets an empty
+        buffer that the block's routed launch fills (fused ninth slot);
+      * more rows: vLLM's forward, then the step's decode rows recomputed."""
+    if getattr(SharedExperts, '_ornith_bridge', False):
+        return
+    from . import methods, native
+    forward = SharedExperts.forward
+
+    def bridged(self, shared_experts_input, order):
+        shared = getattr(self._layer, '_ornith_shared', None)
+        if shared is None:
+            return forward(self, shared_experts_input, order)
+        rows = shared_experts_input.shape[0]
+        computes = order == self._determine_shared_experts_order(shared_experts_input)
+        if rows <= methods.SharedExpert.fused_max_rows:
+            if computes:
+                shared.pending = shared_experts_input.new_empty(shared_experts_input.shape)
+                self._output[self._output_idx] = shared.pending
+            return None
+        result = forward(self, shared_experts_input, order)
+        if computes and native.decode_runs(rows):
+            shared.decode_rows(shared.runtime, shared_experts_input, self._output[self._output_idx])
+        return result
+
+    SharedExperts.forward = bridged
+    SharedExperts._ornith_bridge = True
+
+
 def register():
     """Register OrnithG256Config with vLLM (raises ImportError without vLLM)."""
     import torch
@@ -50,6 +92,7 @@ def register():
     from vllm.model_executor.layers.quantization import register_quantization_config
     from vllm.model_executor.layers.quantization.base_config import QuantizationConfig
     from vllm.model_executor.layers.vocab_parallel_embedding import ParallelLMHead
+    from vllm.model_executor.layers.fused_moe.runner.shared_experts import SharedExperts
 
     from . import methods
 
@@ -69,6 +112,20 @@ def register():
 
         def process_weights_after_loading(self, layer):
             self.impl.process_weights_after_loading(layer)
+
+        def apply(self, layer, x, bias=None):
+            return self.impl.apply(layer, x, bias)
+
+    class RouterGateAdapter(UnquantizedLinearMethod):
+        """vLLM's unquantized weights; the product through the router kernel."""
+
+        def __init__(self, prefix):
+            super().__init__()
+            self.impl = methods.RouterGateMethod(prefix)
+
+        def create_weights(self, layer, *args, **kwargs):
+            super().create_weights(layer, *args, **kwargs)
+            layer.quant_method = self.impl
 
         def apply(self, layer, x, bias=None):
             return self.impl.apply(layer, x, bias)
@@ -96,7 +153,12 @@ def register():
             self.impl.process_weights_after_loading(layer)
 
         def apply(self, layer, x, topk_weights, topk_ids, shared_experts=None, shared_experts_input=None):
-            return self.impl.apply(layer, x, topk_weights, topk_ids)
+            shared = getattr(getattr(shared_experts, '_layer', None), '_ornith_shared', None)
+            if shared is None or shared.pending is None:
+                return self.impl.apply(layer, x, topk_weights, topk_ids)
+            pending, shared.pending = shared.pending, None
+            return self.impl.apply(layer, x, topk_weights, topk_ids, shared=shared, shared_out=pending,
+                                   shared_input=shared_experts_input)
 
     @register_quantization_config('ornith_g256')
     class OrnithG256Config(QuantizationConfig):
@@ -133,8 +195,11 @@ def register():
                 return MoEAdapter(layer.moe_config, prefix)
             if isinstance(layer, ParallelLMHead):
                 return LinearAdapter(prefix, head=True)
+            if isinstance(layer, LinearBase) and ROUTER_GATE.search(prefix):
+                return RouterGateAdapter(prefix)
             if isinstance(layer, LinearBase):
                 return LinearAdapter(prefix) if prefix.endswith(DENSE_SUFFIXES) else UnquantizedLinearMethod()
             return None
 
+    bridge_shared_experts(SharedExperts)
     return OrnithG256Config

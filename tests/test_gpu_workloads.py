@@ -336,6 +336,71 @@ def test_moe_method_through_runtime(device, moe, mode):
         native.reset_binding()
 
 
+def test_router_gate_and_shared_expert_through_runtime(device, moe, shared_tables):
+    """A MoE block bound to the Runtime the way the vLLM adapter binds it:
+    the router gate (RouterGateMethod) gives the fp32 logits and, in the same
+    launch, the shared expert's gate logit; the routed launch runs the shared
+    expert as the fused ninth slot (N16 routed banks through the N16 build,
+    the shared expert's dense banks repacked to N32 by the Runtime); the
+    step's decode rows of the shared output are then recomputed by fixed8.
+    Every output against the oracle, bit for bit."""
+    import torch
+    from ornith_g256 import methods, native
+    w, d = moe
+    silu, sigmoid = shared_tables
+    print('router gate + shared expert through the runtime', flush=True)
+    native.reset_binding()
+    try:
+        model = torch.nn.Module()
+        model.layers = torch.nn.ModuleList([torch.nn.Module()])
+        blk = model.layers[0].mlp = torch.nn.Module()
+        blk.experts = _moe_module(device, d)
+        blk.gate = torch.nn.Module()
+        blk.gate.weight = torch.nn.Parameter(to_dev(w['router'], device), requires_grad=False)
+        blk.gate.quant_method = methods.RouterGateMethod('layers.0.mlp.gate')
+        blk.shared_expert = torch.nn.Module()
+        for name, key, (n, k) in (('gate_up_proj', 's13', (1024, 2048)), ('down_proj', 's2', (2048, 512))):
+            lin = torch.nn.Module()
+            m = methods.G256LinearMethod(f'layers.0.mlp.shared_expert.{name}', n, k)
+            m.create_weights(lin)
+            c16, m16 = _n32_to_n16(d[key][0][None], d[key][1][None])
+            lin.load_packed('g256_codes', c16[0].cpu().view(torch.uint32))
+            lin.load_packed('g256_metadata', m16[0].cpu().view(torch.uint32))
+            m.process_weights_after_loading(lin)
+            lin.to(device)
+            lin.quant_method = m
+            setattr(blk.shared_expert, name, lin)
+        blk.shared_expert.expert_gate = torch.nn.Module()
+        blk.shared_expert.expert_gate.weight = torch.nn.Parameter(to_dev(w['gate'], device), requires_grad=False)
+        rt = methods.Runtime(model, {'routed_library': str(native.library_path(16))}, 64, device)
+        shared = rt.shared['layers.0.mlp.shared_expert']
+        assert blk.gate.quant_method.shared is shared and blk.shared_expert._ornith_shared is shared
+        rng = np.random.default_rng(2500)
+        T = 5
+        x = bf16_normal(rng, (T, 2048))
+        xd = to_dev(x, device)
+        logits = blk.gate.quant_method.apply(blk.gate, xd)
+        ref_logits = O.router_logits(x, np.concatenate([w['router'], w['gate']]))
+        np.testing.assert_array_equal(from_dev(logits).view(np.uint32), ref_logits[:, :256].view(np.uint32))
+        rw, ids, _ = O.softmax_topk(ref_logits[:, :256])
+        shared_out = torch.empty((T, 2048), dtype=torch.bfloat16, device=device)
+        with native.step_phases(((0, 2, True), (2, T, False))):
+            out = blk.experts.quant_method.apply(blk.experts, xd, to_dev(rw, device), to_dev(ids, device),
+                                                 shared=shared, shared_out=shared_out)
+        _sync()
+        ref = O.routed_layer_shared(x, rw, ids, LazyExperts(w['w13']), w['w13'].sbits, w['w13'].obits,
+                                    LazyExperts(w['w2']), w['w2'].sbits, w['w2'].obits, *w['s13'].expert(),
+                                    *w['s2'].expert(), O.f32_to_bf16(ref_logits[:, 256]), silu, sigmoid)
+        np.testing.assert_array_equal(from_dev(out), ref['out'])
+        got = from_dev(shared_out)
+        np.testing.assert_array_equal(got[:2], ref['shared_out'][:2])            # prefill rows: ninth slot
+        fixed, _ = O.shared_fixed8(x[2:], *w['s13'].expert(), *w['s2'].expert(), w['gate'][0], silu, sigmoid)
+        np.testing.assert_array_equal(got[2:], fixed)                            # decode rows: fixed8
+        assert rt.check_error_flags() == [0] * len(rt.layer_names)
+    finally:
+        native.reset_binding()
+
+
 def test_dense_method_and_flag_lifecycle(device):
     """G256LinearMethod through the runtime at one row (A8 path, bit-exact)
     and 70 rows (bf16 operands + GEMM, tolerance); then a non-finite input
