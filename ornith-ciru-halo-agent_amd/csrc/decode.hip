@@ -276,8 +276,9 @@ __global__ __launch_bounds__(256) void decode_route_select_kernel(DecodeArgs a, 
     const int T = a.T, lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int L = int(blockIdx.x), gw = L * 4 + wave;
     uint64_t* W = a.l1_words;
-    const uint32_t seq = __hip_atomic_load(a.l1_seq, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    const int limit = l1_limit(seq, a.handoff_spins);
+    // the call's sequence number: loaded first, its value taken only after
+    // each wave's own loads (router rows, x) are issued and used
+    uint32_t seq_v = __hip_atomic_load(a.l1_seq, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     uint32_t flags = 0;
     if (gw < router_waves) {
         const int nb = (T + kTokenBatch - 1) / kTokenBatch;
@@ -285,7 +286,7 @@ __global__ __launch_bounds__(256) void decode_route_select_kernel(DecodeArgs a, 
         const uint16_t* wrow = row < kExperts ? a.router_w + size_t(row) * kHidden : a.shared_gate_w;
         const bool has_bias = a.bias && row < kExperts;
         router_rows_wave(a.x, kHidden, T, t0, wrow, has_bias ? a.bias[row] : 0.f, has_bias, a.logits, kLogitStride,
-                         row, W, seq, uint32_t(kDecodeRouteLogit + kDecodeMaxTokens * row + t0));
+                         row, W, seq_v, uint32_t(kDecodeRouteLogit + kDecodeMaxTokens * row + t0));
     } else if (gw - router_waves < T * 4) {
         // quantised gate input: wave q handles groups 2(q%4), 2(q%4)+1 of token q/4
         const int q = gw - router_waves;
@@ -313,7 +314,13 @@ __global__ __launch_bounds__(256) void decode_route_select_kernel(DecodeArgs a, 
             a.x_sums[g] = sum;
         }
     }
-    __syncthreads();                                   // every wave holds seq
+    // every wave has its sequence number before the barrier, so before the
+    // block's arrival word (waves with loads have long had it: their loads
+    // were issued after it and are done)
+    asm volatile("" : "+v"(seq_v));
+    const uint32_t seq = __builtin_amdgcn_readfirstlane(seq_v);
+    const int limit = l1_limit(seq, a.handoff_spins);
+    __syncthreads();
     if (threadIdx.x == 0) l1_put(W, kDecodeRouteArrive + 8 * L, seq, 1u);
 
     // ---- selection of token 4L + wave ----

@@ -67,7 +67,14 @@ __device__ __forceinline__ void router_rows_wave(const uint16_t* __restrict__ x,
             if (lane == t) pub = v;
         }
     }
-    if (words && lane < nt) l1_put(words, word0 + lane, seq, __float_as_uint(pub));
+    if (words) {
+        // the call's sequence number is taken only now: its load was issued
+        // before the rows', and converting it earlier made the compiler wait
+        // for it before issuing them
+        asm volatile("" : "+v"(seq));
+        const uint32_t sq = __builtin_amdgcn_readfirstlane(seq);
+        if (lane < nt) l1_put(words, word0 + lane, sq, __float_as_uint(pub));
+    }
 }
 
 // Order key of an fp32 value: unsigned order of keys = numeric order of the
