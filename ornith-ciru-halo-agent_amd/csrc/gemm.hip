@@ -44,22 +44,17 @@ typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 // (r, k) at (16 * ((k % 32) / 8) + r % 16) * 8 + k % 8 - lane l's operand of a
 // 16x16x32 product (row l % 16, k chunk l / 16) is its 16 bytes at 16 l, so
 // one fragment is one contiguous 1 KiB load.
-__device__ __forceinline__ size_t frag_offset(int r, int k, int steps) {
-    return (size_t(r >> 4) * steps + (k >> 5)) * 512 + ((((k >> 3) & 3) << 4) + (r & 15)) * 8 + (k & 7);
-}
 
-// FRAG false: row-major [M, K] (the operand of a library GEMM); FRAG true:
-// fragment order over Mp rows.
-template <bool FRAG>
-__global__ __launch_bounds__(256) void transform_bf16_kernel(const uint16_t* __restrict__ x, int M, int Mp, int K,
+// Row-major [M, K] bf16(H128 x) (the activation operand of prepare_bf16):
+// a quarter-wave per (row, 256-group).
+__global__ __launch_bounds__(256) void transform_bf16_kernel(const uint16_t* __restrict__ x, int M, int K,
                                                              uint16_t* __restrict__ y, uint32_t* sticky) {
     const int G = K / kGroup, wave = blockIdx.x * 4 + (threadIdx.x >> 6);
     const int lane = threadIdx.x & 63, l = lane & 15;
-    const int g = 4 * wave + (lane >> 4);                  // (row, group) of rows 0 .. Mp - 1
-    if (4 * wave >= Mp * G) return;
-    const int gl = min(g, M * G - 1);                       // padding rows read row M - 1 and store zeros
+    const int g = 4 * wave + (lane >> 4);                  // (row, group)
+    if (4 * wave >= M * G) return;
     const bool real = g < M * G;
-    const uint16_t* src = x + size_t(gl) * kGroup + quarter_base(l);
+    const uint16_t* src = x + size_t(min(g, M * G - 1)) * kGroup + quarter_base(l);
     const uint4 r0 = *reinterpret_cast<const uint4*>(src), r1 = *reinterpret_cast<const uint4*>(src + 8);
     const uint32_t u[8] = {r0.x, r0.y, r0.z, r0.w, r1.x, r1.y, r1.z, r1.w};
     float v[16];
@@ -80,19 +75,92 @@ __global__ __launch_bounds__(256) void transform_bf16_kernel(const uint16_t* __r
         if ((a & 0x7f80u) == 0x7f80u || (b & 0x7f80u) == 0x7f80u) flags |= kDenseNonfiniteBf16;
         o[e] = real ? uint32_t(a) | (uint32_t(b) << 16) : 0u;
     }
-    if (g < Mp * G) {
-        uint16_t *d0, *d1;
-        if constexpr (FRAG) {
-            const int r = g / G, k = (g - r * G) * kGroup + quarter_base(l);   // k % 16 == 0: two 8-chunks
-            d0 = y + frag_offset(r, k, K / 32);
-            d1 = y + frag_offset(r, k + 8, K / 32);
-        } else {
-            d0 = y + size_t(g) * kGroup + quarter_base(l);
-            d1 = d0 + 8;
-        }
-        *reinterpret_cast<uint4*>(d0) = make_uint4(o[0], o[1], o[2], o[3]);
-        *reinterpret_cast<uint4*>(d1) = make_uint4(o[4], o[5], o[6], o[7]);
+    if (real) {
+        uint16_t* d = y + size_t(g) * kGroup + quarter_base(l);
+        *reinterpret_cast<uint4*>(d) = make_uint4(o[0], o[1], o[2], o[3]);
+        *reinterpret_cast<uint4*>(d + 8) = make_uint4(o[4], o[5], o[6], o[7]);
     }
+    flag_or(sticky, real ? flags : 0u);
+}
+
+// Fragment order, one wave per (16-row group rg, 128-k block kb): lane l is
+// row 16 rg + l / 4 and k chunk q = l % 4; its load i (0..3) is the 8 values
+// k = 128 kb + 32 i + 8 q + 0..7, so the four lanes of a row read 64
+// contiguous bytes per load.  Butterflies on k bits 0..2 in registers, bits 3
+// and 4 across the lanes of a quad (DPP xor 1, xor 2), bits 5 and 6 in
+// registers again: the ascending order of the reference.  Store i is all of
+// fragment 4 kb + i (lane l's 16 bytes at (16 q + l / 4) * 16), one
+// contiguous 1 KiB per store.
+__global__ __launch_bounds__(256) void transform_frag_kernel(const uint16_t* __restrict__ x, int M, int Mp, int K,
+                                                             uint16_t* __restrict__ y, uint32_t* sticky) {
+    const int KB = K / 128, S = K / 32;
+    const int wave = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+    const int rg = wave / KB, kb = wave - rg * KB;
+    if (16 * rg >= Mp) return;
+    const int r = lane >> 2, q = lane & 3, row = 16 * rg + r;
+    const bool real = row < M;
+    const uint16_t* src = x + size_t(min(row, M - 1)) * K + 128 * kb + 8 * q;
+    uint4 raw[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) raw[i] = *reinterpret_cast<const uint4*>(src + 32 * i);
+    float v[32];                                            // v[8 i + e]: k = 32 i + 8 q + e
+    uint32_t flags = 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const uint32_t u[4] = {raw[i].x, raw[i].y, raw[i].z, raw[i].w};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            v[8 * i + 2 * e] = bf16_bits_to_f32(u[e] & 0xffffu);
+            v[8 * i + 2 * e + 1] = bf16_bits_to_f32(u[e] >> 16);
+        }
+    }
+#pragma unroll
+    for (int e = 0; e < 32; ++e) if (!isfinite(v[e])) flags |= kDenseNonfiniteInput;
+#pragma unroll
+    for (int b = 1; b < 8; b <<= 1) {
+#pragma unroll
+        for (int i = 0; i < 32; ++i) {
+            if (i & b) continue;
+            const float lo = v[i], hi = v[i + b];
+            v[i] = lo + hi;
+            v[i + b] = lo - hi;
+        }
+    }
+    // k bit 3 (lane bit 0), then k bit 4 (lane bit 1): the lane with the bit
+    // set keeps partner - own, the other own + partner
+    {
+        const uint32_t flip = (lane & 1) ? 0x80000000u : 0u;
+#pragma unroll
+        for (int i = 0; i < 32; ++i) v[i] = xor_perm_f<1>(v[i]) + __uint_as_float(__float_as_uint(v[i]) ^ flip);
+    }
+    {
+        const uint32_t flip = (lane & 2) ? 0x80000000u : 0u;
+#pragma unroll
+        for (int i = 0; i < 32; ++i) v[i] = xor_perm_f<2>(v[i]) + __uint_as_float(__float_as_uint(v[i]) ^ flip);
+    }
+#pragma unroll
+    for (int b = 8; b < 32; b <<= 1) {
+#pragma unroll
+        for (int i = 0; i < 32; ++i) {
+            if (i & b) continue;
+            const float lo = v[i], hi = v[i + b];
+            v[i] = lo + hi;
+            v[i + b] = lo - hi;
+        }
+    }
+    uint32_t o[16];
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+        const float a = v[2 * e] * kInvSqrt128, b = v[2 * e + 1] * kInvSqrt128;
+        if (!isfinite(a) || !isfinite(b)) flags |= kDenseNonfiniteInput;
+        const uint16_t ha = f32_to_bf16_bits(a), hb = f32_to_bf16_bits(b);
+        if ((ha & 0x7f80u) == 0x7f80u || (hb & 0x7f80u) == 0x7f80u) flags |= kDenseNonfiniteBf16;
+        o[e] = real ? uint32_t(ha) | (uint32_t(hb) << 16) : 0u;
+    }
+    uint16_t* frag = y + (size_t(rg) * S + 4 * kb) * 512 + (16 * q + r) * 8;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+        *reinterpret_cast<uint4*>(frag + 512 * i) = make_uint4(o[4 * i], o[4 * i + 1], o[4 * i + 2], o[4 * i + 3]);
     flag_or(sticky, real ? flags : 0u);
 }
 
@@ -290,16 +358,15 @@ __global__ __launch_bounds__(256, 2) void dense_gemm_bf16_kernel(const uint16_t*
 
 hipError_t launch_transform_bf16_fast(const uint16_t* x, int M, int K, uint16_t* y, uint32_t* sticky, hipStream_t s) {
     const int waves = (M * (K / kGroup) + 3) / 4;
-    timed_launch("transform_bf16", transform_bf16_kernel<false>, dim3((waves + 3) / 4), dim3(256), 0, s, x, M, M, K, y,
-                 sticky);
+    timed_launch("transform_bf16", transform_bf16_kernel, dim3((waves + 3) / 4), dim3(256), 0, s, x, M, K, y, sticky);
     return hipGetLastError();
 }
 
 hipError_t launch_transform_bf16_frag(const uint16_t* x, int M, int K, uint16_t* y, uint32_t* sticky, hipStream_t s) {
     const int Mp = (M + 15) / 16 * 16;
-    const int waves = (Mp * (K / kGroup) + 3) / 4;
-    timed_launch("transform_bf16_frag", transform_bf16_kernel<true>, dim3((waves + 3) / 4), dim3(256), 0, s, x, M, Mp,
-                 K, y, sticky);
+    const int waves = Mp / 16 * (K / 128);
+    timed_launch("transform_bf16_frag", transform_frag_kernel, dim3((waves + 3) / 4), dim3(256), 0, s, x, M, Mp, K, y,
+                 sticky);
     return hipGetLastError();
 }
 

@@ -188,7 +188,7 @@ def _settings_key(settings):
 def configure(settings, capacity, shapes, shared_expert=False):
     """Resolve the library roles, bind the launch entries and return the
     workspace size the caller allocates once (the max over the routed
-    layout, the dense layouts plus their bf16 prefill operands, the W8 head
+    layout, the dense layouts plus the GEMM's transformed rows, the W8 head
     layout and, with `shared_expert`, the fused shared slot and fixed8)."""
     global _binding
     a8 = settings.get('routed_activation_bits', 8)
@@ -242,7 +242,7 @@ def configure(settings, capacity, shapes, shared_expert=False):
             raise ValueError('the N32 decode library must keep its parent\'s workspace layout')
     for n, k in shapes:
         sizes.append(dense_layout(capacity, n, k, tile=roles['dense']).workspace_bytes)
-        sizes.append((capacity * k + n * k) * 2)       # bf16 prefill operands (transformed x, dequantised W)
+        sizes.append((int(capacity) + 15) // 16 * 16 * k * 2)   # the GEMM's bf16(H128 x), rows padded to 16
     sizes.append(head_layout(HEAD_MAX_ROWS, HEAD_VOCAB, tile=roles['head']).workspace_bytes)
     if shared_expert:
         # the fused ninth slot (at most 16 rows, any routed build) and fixed8
@@ -371,33 +371,16 @@ def _check_banks(tile, gate, gate_meta, down, down_meta):
 # ---------------------------------------------------------------------------
 # torch ops (reference native.py:121-212)
 # ---------------------------------------------------------------------------
-def gemm_preferred(rows: int, n: int, k: int) -> bool:
-    """Which bf16 prefill route is faster for a [rows, k] x [n, k] linear,
-    as measured on MI355X over 65..8192 rows: the GEMM reading the 4-bit
-    codes for k <= 512 at every row count, and for k <= 2048 while
-    rows * n <= 8 Mi; bf16 operands + hipBLASLt otherwise (large products,
-    where the library kernel's efficiency wins, and k >= 4096)."""
-    return k <= 512 or (k <= 2048 and rows * n <= 8 << 20)
-
-
 def _dense_one(x, codes, metadata, workspace, out, flags, capacity, n, k, geometry, a8_max_rows):
     h = lib(_binding.libraries['dense'] if _binding else 32)
     _check_rows(x, out, capacity, k)
     rows = x.shape[0]
-    if rows > a8_max_rows and gemm_preferred(rows, n, k):
-        # bf16 prefill semantics on this library's GEMM: the transformed rows
-        # (padded to 16) take the arena's front, within capacity * k * 2 + n * k * 2
+    if rows > a8_max_rows:
+        # bf16 prefill semantics (dense_g256_consumer.cpp:192-246 and the
+        # reference's torch.mm) on this library's GEMM, which reads the 4-bit
+        # codes: bf16(H128 x) (rows padded to 16) takes the arena's front
         check(h.ornith_dense_g256_gemm_bf16(ptr(x), ptr(codes), ptr(metadata), ptr(workspace), workspace.numel(),
                                             ptr(out), ptr(flags), rows, n, k, stream(x)), 'dense bf16 GEMM')
-        return
-    if rows > a8_max_rows:
-        # bf16 prefill semantics: bf16(H128 x) @ bf16(dequantised W).T, both
-        # operands carved from the arena (dense_g256_consumer.cpp:192-246)
-        xt = workspace[:rows * k * 2].view(torch.bfloat16).view(rows, k)
-        wt = workspace[capacity * k * 2:(capacity * k + n * k) * 2].view(torch.bfloat16).view(n, k)
-        check(h.ornith_dense_g256_prepare_bf16(ptr(x), ptr(codes), ptr(metadata), ptr(xt), ptr(wt), ptr(flags),
-                                               rows, n, k, stream(x)), 'dense bf16 operands')
-        torch.mm(xt, wt.t(), out=out)
         return
     check(h.ornith_dense_g256_launch(ptr(x), ptr(codes), ptr(metadata), ptr(workspace), workspace.numel(), ptr(out),
                                      ptr(flags), rows, capacity, n, k, 8, 128, geometry, stream(x)), 'dense A8')
