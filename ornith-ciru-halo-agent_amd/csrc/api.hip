@@ -150,9 +150,6 @@ hipError_t run_decode(const RoutedPlan& p, void* ws, const void* input, const fl
     a.x_scales = at<uint16_t>(ws, p.l.gate_scales);
     a.x_sums = at<int32_t>(ws, p.l.gate_sums);
     a.middle = at<float>(ws, p.l.middle);
-    a.m_words = at<uint32_t>(ws, p.l.down_low);
-    a.m_scales = at<uint16_t>(ws, p.l.down_scales);
-    a.m_sums = at<int32_t>(ws, p.l.down_sums);
     a.route_out = at<float>(ws, p.l.route_out);
     carve_decode(at<void>(ws, p.decode), a);
     a.final_f32 = out ? at<float>(ws, p.l.final_f32) : nullptr;

@@ -14,9 +14,11 @@
 //                              codes stay in registers while the segment's
 //                              routes stream through four at a time; exact
 //                              int8 dots, fp32 group tree, SiLU(gate)*up.
-//   S4 quant_middle            H128 + quantisation of every middle row once.
-//   S5 decode_down_kernel      block (segment, 32 output columns), same
-//                              scheme, writing route_out.
+//   S5 decode_down_kernel      block (segment, 64 output columns), same
+//                              scheme, writing route_out; its prologue runs
+//                              H128 + quantisation of the segment's fp32
+//                              middle rows (every block of a segment, as
+//                              each needs all 512 values of its routes).
 //   S6 reduce                  slot-order combination (+ shared expert).
 //
 // Arithmetic is the reference's (routed_storage_n32_consumer.cpp:22-307); the
@@ -487,13 +489,22 @@ __global__ __launch_bounds__(512) void decode_gateup_kernel(DecodeArgs a) {
 // instruction reads two whole 128-byte rows.  The quarters' exact integer
 // partial dots meet in LDS; the two groups' terms follow in group order.  The
 // segment's routes and activations are loaded once for the block's tiles.
+// The activations are the fp32 middle rows: wave rr of a chunk takes route
+// rr, lane half = group, 8 consecutive values per lane (the half-wave layout
+// of the gate input), and runs H128 + A8/A4 quantisation itself (the
+// arithmetic of the reference's down input, routed_storage_n32_consumer.cpp:
+// 231-295) before the words go to LDS.
+// Measured alternatives (2..32 tokens): a separate quantisation kernel (4.6 us
+// at 32 tokens against +3.5 us here); quantising waves apart from the code
+// loads in 8-wave blocks (half the resident blocks: 38 us); a fixed grid of
+// 1024 blocks walking the items (items run serially per block: 29 us).
 // ---------------------------------------------------------------------------
-template <bool SHARED, int CPB>
+template <bool SHARED, int CPB, int QMAX>
 __global__ __launch_bounds__(256) void decode_down_kernel(DecodeArgs a) {
     __shared__ __align__(16) uint32_t la[kRouteChunk][128];
     __shared__ float lsa[kRouteChunk][2], lss[kRouteChunk][2];
     __shared__ int lpart[CPB][kRouteChunk][4][64];
-    __shared__ int lr[256];
+    __shared__ int lr[kSegRoutes];
     const int nseg = a.nseg[0];
     if (int(blockIdx.y) >= nseg) return;
     const Segment sg = a.segments[nseg - 1 - int(blockIdx.y)];    // shared expert's segments first
@@ -516,27 +527,31 @@ __global__ __launch_bounds__(256) void decode_down_kernel(DecodeArgs a) {
     for (int cc = 0; cc < CPB; ++cc) mw[cc] = meta[bv.meta(32 * (c0 + cc) + n, g, 2)];   // epilogue thread (g, n)
     if (tid < sg.count) lr[tid] = route_in;
     __syncthreads();
-    uint2 areg;
-    uint32_t sreg = 0;
-    int sumreg = 0;
+    float4 m0, m1;
     auto load_chunk = [&](int r0) {
-        // route rr = tid / 64 holds words 2(tid % 64), +1 of its quantised middle row
-        const int k = min(r0 + (tid >> 6), sg.count - 1);
-        areg = *reinterpret_cast<const uint2*>(a.m_words + size_t(lr[k]) * 128 + (tid & 63) * 2);
-        const int k2 = min(r0 + ((tid & 7) >> 1), sg.count - 1);
-        sreg = a.m_scales[size_t(lr[k2]) * 2 + (tid & 1)];
-        sumreg = a.m_sums[size_t(lr[k2]) * 2 + (tid & 1)];
+        // route rr = tid / 64: values 8 (lane % 32) .. + 7 of group lane / 32
+        // of its fp32 middle row (dead routes of a chunk repeat the last one)
+        const float* src = a.middle + size_t(lr[min(r0 + q, sg.count - 1)]) * kInter + 8 * lane;
+        m0 = *reinterpret_cast<const float4*>(src);
+        m1 = *reinterpret_cast<const float4*>(src + 4);
     };
     uint32_t flags = 0;
     load_chunk(0);
     for (int r0 = 0; r0 < sg.count; r0 += kRouteChunk) {
         const int nr = min(kRouteChunk, sg.count - r0);
-        __syncthreads();
-        *reinterpret_cast<uint2*>(&la[tid >> 6][(tid & 63) * 2]) = areg;
-        if (tid < 8) {
-            const float sc = f16_bits_to_f32(uint16_t(sreg));
-            lsa[tid >> 1][tid & 1] = sc;
-            lss[tid >> 1][tid & 1] = sc * float(sumreg);
+        float v[8] = {m0.x, m0.y, m0.z, m0.w, m1.x, m1.y, m1.z, m1.w};
+        h128_half(v);
+        uint32_t w2[2];
+        uint16_t sb;
+        int sum;
+        quantize_half_fast<QMAX>(v, w2, sb, sum, flags, kFlagNonfiniteInput | kFlagInvalidActivation,
+                                 kFlagInvalidActivation);
+        __syncthreads();                                   // previous chunk's readers are done
+        *reinterpret_cast<uint2*>(&la[q][2 * lane]) = make_uint2(w2[0], w2[1]);
+        if ((lane & 31) == 0) {
+            const float sc = f16_bits_to_f32(sb);
+            lsa[q][g] = sc;
+            lss[q][g] = sc * float(sum);
         }
         __syncthreads();
         if (r0 + kRouteChunk < sg.count) load_chunk(r0 + kRouteChunk);
@@ -621,7 +636,7 @@ std::atomic<int> g_route_select_mode{0};   // 0 automatic, 1 separate route / to
 
 template <bool ROUTER, bool SHARED, int QMAX>
 static hipError_t run(const DecodeArgs& a, hipStream_t s) {
-    const int T = a.T, R = T * kTop, RS = R + (SHARED ? T : 0);
+    const int T = a.T, R = T * kTop;
     const int router_waves = ROUTER ? (SHARED ? kExperts + 1 : kExperts) * ((T + kTokenBatch - 1) / kTokenBatch) : 0;
     const int s1_waves = router_waves + T * 4;
     hipError_t st;
@@ -658,10 +673,8 @@ static hipError_t run(const DecodeArgs& a, hipStream_t s) {
     timed_launch("gateup", decode_gateup_kernel<SHARED>, dim3(kInter / 32, maxseg), dim3(512), 0, s, a);
     st = hipGetLastError();
     if (st != hipSuccess) return st;
-    st = launch_quant_middle(a.middle, RS, R, a.reduce_ids, QMAX, a.m_words, a.m_scales, a.m_sums, a.sticky, s);
-    if (st != hipSuccess) return st;
-    timed_launch("down", decode_down_kernel<SHARED, kDownTilesPerBlock>, dim3(kHidden / (32 * kDownTilesPerBlock), maxseg),
-                 dim3(256), 0, s, a);
+    timed_launch("down", decode_down_kernel<SHARED, kDownTilesPerBlock, QMAX>,
+                 dim3(kHidden / (32 * kDownTilesPerBlock), maxseg), dim3(256), 0, s, a);
     st = hipGetLastError();
     if (st != hipSuccess) return st;
     return launch_reduce(a.route_out, a.reduce_w, a.reduce_ids, T, a.final_f32, a.out, a.shared_logit,

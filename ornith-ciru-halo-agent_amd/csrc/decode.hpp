@@ -63,7 +63,6 @@ struct DecodeArgs {
     // workspace
     uint32_t* x_words; uint16_t* x_scales; int32_t* x_sums;
     float* middle;                     // [RS, 512]
-    uint32_t* m_words; uint16_t* m_scales; int32_t* m_sums;   // quantised middle rows (2..32 tokens)
     float* route_out;                  // [RS, 2048]
     float* logits; Segment* segments; int32_t* routes; int32_t* nseg;
     // one-launch kernels (single-token layer, 2..32-token route): call

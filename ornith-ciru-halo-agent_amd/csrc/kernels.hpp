@@ -160,9 +160,7 @@ hipError_t launch_grouped_mfma(const MfmaArgs& a, bool gateup, int max_tiles, hi
 // Dense G256 head on the matrix cores: M <= 64 rows of A8 activations against
 // N32 codes, then the per-row argmax (numpy rule) into argmax[M].
 hipError_t launch_head_mfma(const MfmaArgs& a, int64_t* argmax, hipStream_t s);
-hipError_t launch_quant_middle(const float* middle, int RS, int R, const int32_t* ids, int qmax, uint32_t* words,
-                               uint16_t* scales, int32_t* sums, uint32_t* sticky, hipStream_t s);
-// Same over middle rows stored in permuted route order: rows 0 .. *nrows - 1
+// H128 + quantisation of middle rows stored in permuted route order: rows 0 .. *nrows - 1
 // (the permuted routes, all with a valid bank), RS rows at most.
 hipError_t launch_quant_middle_permuted(const float* middle, int RS, const int32_t* nrows, int qmax, uint32_t* words,
                                         uint16_t* scales, int32_t* sums, uint32_t* sticky, hipStream_t s);

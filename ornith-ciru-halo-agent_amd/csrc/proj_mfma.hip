@@ -851,28 +851,9 @@ hipError_t launch_head_mfma(const MfmaArgs& a, int64_t* argmax, hipStream_t s) {
     return hipGetLastError();
 }
 
-// H128 + quantisation of the middle rows [RS, 512] of every valid route.
-template <int QMAX>
-__global__ __launch_bounds__(256) void quant_middle_kernel(const float* __restrict__ middle, int RS, int R,
-                                                           const int32_t* __restrict__ ids, uint32_t* __restrict__ words,
-                                                           uint16_t* __restrict__ scales, int32_t* __restrict__ sums,
-                                                           uint32_t* sticky) {
-    const int wave = blockIdx.x * 4 + (threadIdx.x >> 6);
-    if (wave >= RS * 2) return;
-    const int lane = threadIdx.x & 63, route = wave >> 1, group = wave & 1;
-    if (route < R && (ids[route] < 0 || ids[route] >= kExperts)) return;
-    const float4 m4 = *reinterpret_cast<const float4*>(middle + size_t(route) * kInter + group * kGroup + lane * 4);
-    float v[4] = {m4.x, m4.y, m4.z, m4.w};
-    uint32_t flags = 0;
-    h128_wave(v);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) if (!isfinite(v[i])) flags |= kFlagNonfiniteInput;
-    quantize_group_wave<QMAX>(v, words + size_t(wave) * 64, scales + wave, sums + wave, flags, kFlagInvalidActivation);
-    flag_or(sticky, flags);
-}
-
-// Same over middle rows in permuted route order: rows 0 .. *nrows - 1, on
-// quarter-wave groups (common.hpp), four groups (two rows) per wave.
+// H128 + quantisation of the middle rows in permuted route order: rows 0 ..
+// *nrows - 1, on quarter-wave groups (common.hpp), four groups (two rows) per
+// wave.
 template <int QMAX>
 __global__ __launch_bounds__(256) void quant_middle_permuted_kernel(const float* __restrict__ middle, int RS,
                                                                     const int32_t* __restrict__ nrows,
@@ -914,16 +895,6 @@ hipError_t launch_quant_middle_permuted(const float* middle, int RS, const int32
         timed_launch("quant_middle", quant_middle_permuted_kernel<127>, dim3((waves + 3) / 4), dim3(256), 0, s, middle, RS, nrows, words, scales, sums, sticky);
     else
         timed_launch("quant_middle", quant_middle_permuted_kernel<7>, dim3((waves + 3) / 4), dim3(256), 0, s, middle, RS, nrows, words, scales, sums, sticky);
-    return hipGetLastError();
-}
-
-hipError_t launch_quant_middle(const float* middle, int RS, int R, const int32_t* ids, int qmax, uint32_t* words,
-                               uint16_t* scales, int32_t* sums, uint32_t* sticky, hipStream_t s) {
-    const int waves = RS * 2;
-    if (qmax == 127)
-        timed_launch("quant_middle", quant_middle_kernel<127>, dim3((waves + 3) / 4), dim3(256), 0, s, middle, RS, R, ids, words, scales, sums, sticky);
-    else
-        timed_launch("quant_middle", quant_middle_kernel<7>, dim3((waves + 3) / 4), dim3(256), 0, s, middle, RS, R, ids, words, scales, sums, sticky);
     return hipGetLastError();
 }
 
