@@ -99,9 +99,9 @@ def parse():
                    help='only run a plain 256 MiB device copy (PMC scale factor for FETCH_SIZE/WRITE_SIZE)')
     p.add_argument('--oracle-seconds', type=float, default=5.0)
     p.add_argument('--no-cpu-baseline', action='store_true')
-    p.add_argument('--part', choices=('head', 'dense', 'w8head'), default=None,
-                   help='time only the G256 LM head (32x151936) or the dense 6144x2048 prefill (1120 rows) '
-                        'and print one JSON line (for profiling those rows)')
+    p.add_argument('--part', choices=('head', 'dense', 'w8head', 'gateup-bf16-model'), default=None,
+                   help='time only the G256 LM head (32x151936), the dense 6144x2048 prefill (1120 rows), or '
+                        'the bf16 model of the grouped prefill gate-up, and print one JSON line (for profiling)')
     return p.parse_args()
 
 
@@ -213,6 +213,44 @@ def roofline(times, T, unique):
     return {'bound': bound, 'achieved': achieved, 'peak': peak, 'unit': unit, 'frac': achieved / peak,
             'traffic': traffic, 'kernel': name, 'avg_us': ms * 1e3, 'launches': launches,
             'algorithmic_per_launch': amount}
+
+
+def gateup_bf16_model_us(device, steps=10):
+    """The bf16 matrix-core design of the grouped prefill gate-up, modelled
+    by this library's code-reading bf16 GEMM (each 64-column code tile
+    dequantised into LDS once per 256-row tile, bf16 MFMA, fp32 accumulation)
+    at shapes whose (256-row tiles) x (1024-column blocks) equal the m-tiles of
+    the grouped gate-up with every tile full: 6144 x 12288 x 2048 = 288 tiles
+    (8192 tokens, 73728 routes) and 1280 x 8192 x 2048 = 40 tiles (1120
+    tokens, 10080 routes).  No row gather and no SiLU epilogue: a lower bound
+    of the grouped kernel's time."""
+    import torch
+    from ornith_g256 import native
+    res = {}
+    for M, N, live in ((6144, 12288, 73728), (1280, 8192, 10080)):
+        gen = torch.Generator(device=device)
+        gen.manual_seed(5)
+        x = torch.randn((M, 2048), generator=gen, device=device).to(torch.bfloat16)
+        codes = torch.randint(0, 2 ** 31 - 1, (N * 2048 // 8,), generator=gen, device=device, dtype=torch.int32)
+        scale = (torch.rand((N * 2048 // 256,), generator=gen, device=device) * 0.015 + 0.005).half()
+        meta = scale.view(torch.int16).to(torch.int32) & 0xffff
+        ws = torch.empty((M + 15) // 16 * 16 * 2048 * 2, dtype=torch.uint8, device=device)
+        out = torch.empty((M, N), dtype=torch.bfloat16, device=device)
+        flags = torch.zeros(1, dtype=torch.int32, device=device)
+        call = lambda: native.dense_out(x, codes, meta, ws, out, flags, M, N, 2048, 2, 128)
+        for _ in range(3):
+            call()
+        torch.cuda.synchronize()
+        with native.KernelTimer('*') as kt:
+            for _ in range(steps):
+                call()
+            torch.cuda.synchronize()
+            gemm = kt.read('dense_gemm')[1] * 1e3
+        if int(flags.item()):
+            raise RuntimeError(f'native flags raised by the bf16 gate-up model at {M}x{N}: {int(flags.item())}')
+        res[f'{M}x{N}x2048'] = {'gemm_us': gemm, 'tflops': 2 * M * N * 2048 / gemm / 1e6,
+                                'routes_modelled': live, 'tiles': M // 256 * (N // 1024)}
+    return res
 
 
 def dense_prefill_ms(T, device, steps=20):
@@ -472,6 +510,9 @@ def main():
         return
     if args.part == 'w8head':
         print(json.dumps({'w8_head_248320': w8_head_us(dev, steps=args.steps)}))
+        return
+    if args.part == 'gateup-bf16-model':
+        print(json.dumps({'gateup_bf16_model': gateup_bf16_model_us(dev, args.steps)}))
         return
     if args.part == 'dense':
         wall1, device1 = dense_prefill_ms(1, dev, 48)
