@@ -37,6 +37,10 @@ typedef struct OrnithHeadI8Layout {
 
 /* head_i8_tile_api.h:43 (returns 1) */
 ORNITH_EXPORT uint32_t ornith_head_i8_tile_abi_version(void);
+/* head_i8_tile_consumer.cpp:293 (returns 1): the build's capability marker
+ * that the launch below takes the optional per-group dots (the raw 16 group
+ * dots of every logit a shortlist re-scoring reads). */
+ORNITH_EXPORT int ornith_head_i8_tile_shortlist(void);
 /* head_i8_tile_api.h:44; head_i8_tile_consumer.cpp:248-256 */
 ORNITH_EXPORT hipError_t ornith_head_i8_tile_get_layout(int Mcap, int N, OrnithHeadI8Layout* out);
 /* head_i8_tile_api.h:45-49; head_i8_tile_consumer.cpp:257-291.  group_dots int32 [M,N,16]

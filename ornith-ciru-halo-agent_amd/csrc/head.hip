@@ -255,6 +255,7 @@ OrnithHeadI8Layout head_layout(int Mcap, int N) {
 using namespace ornith;
 
 extern "C" uint32_t ornith_head_i8_tile_abi_version(void) { return 1; }
+extern "C" int ornith_head_i8_tile_shortlist(void) { return 1; }
 
 extern "C" hipError_t ornith_head_i8_tile_get_layout(int Mcap, int N, OrnithHeadI8Layout* out) {
     if (!out || Mcap < 0 || Mcap > 64 || !head_shape(N)) return hipErrorInvalidValue;

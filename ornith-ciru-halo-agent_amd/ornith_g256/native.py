@@ -99,6 +99,7 @@ _PROTOTYPES = {
     'ornith_dense_g256_head_launch': ([_VP] * 4 + [_SZ] + [_VP] * 4 + [_INT] * 3 + [_VP], _INT),
     # W8 head (include/ornith_head.h)
     'ornith_head_i8_tile_abi_version': ([], C.c_uint32),
+    'ornith_head_i8_tile_shortlist': ([], C.c_int),
     'ornith_head_i8_tile_get_layout': ([_INT, _INT, C.POINTER(HeadLayout)], _INT),
     'ornith_head_i8_tile_launch': ([_VP] * 4 + [_SZ] + [_VP] * 2 + [_SZ] + [_VP] + [_INT] * 4 + [_VP], _INT),
     # storage conversion (include/ornith_storage.h)

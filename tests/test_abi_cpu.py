@@ -49,6 +49,7 @@ def test_markers(lib):
     assert lib.ornith_dense_g256_abi_version() == 1
     assert lib.ornith_dense_g256_n32_rows() == 16
     assert lib.ornith_head_i8_tile_abi_version() == 1
+    assert lib.ornith_head_i8_tile_shortlist() == 1
     assert lib.ornith_mi355x_abi_version() == 1
 
 
