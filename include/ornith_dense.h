@@ -66,7 +66,9 @@ ORNITH_EXPORT hipError_t ornith_dense_g256_prepare_bf16(
  * product agrees with it within fp32-accumulation tolerance.  Workspace: at
  * least round_up(M,16)*K*2 bytes (the transformed activations, in the
  * library's matrix-core fragment order), 256-byte aligned; output 16-byte
- * aligned.
+ * aligned.  Bytes beyond that (up to 32 MiB are used) let a product whose
+ * grid fills few of the chip's block slots split K: the slices' fp32 sums are
+ * kept there and added in slice order (deterministic; same tolerance).
  * Flags: 1 non-finite input/transform, 8 non-finite bf16 operand. */
 ORNITH_EXPORT hipError_t ornith_dense_g256_gemm_bf16(
     const void* input_bf16, const void* codes, const void* metadata, void* workspace, size_t workspace_bytes,

@@ -610,9 +610,13 @@ extern "C" hipError_t ornith_dense_g256_gemm_bf16(const void* input, const void*
     if (bytes < xt_bytes || !check_buffers(buffers)) return hipErrorInvalidValue;
     auto sticky = static_cast<uint32_t*>(flags);
     auto xt = static_cast<uint16_t*>(workspace);
+    // the rest of the workspace holds the fp32 slice sums of a split K
+    const size_t partial_at = align256(xt_bytes);
+    float* partial = bytes > partial_at ? at<float>(workspace, partial_at) : nullptr;
     TRY(launch_transform_bf16_frag(static_cast<const uint16_t*>(input), M, K, xt, sticky, stream));
     return launch_dense_gemm_bf16(xt, static_cast<const uint32_t*>(codes), static_cast<const uint32_t*>(metadata), M, N,
-                                  K, static_cast<uint16_t*>(output), sticky, stream);
+                                  K, static_cast<uint16_t*>(output), partial, partial ? bytes - partial_at : 0, sticky,
+                                  stream);
 }
 
 extern "C" hipError_t ornith_dense_g256_launch_n32(const void* input, const void* codes, const void* metadata,

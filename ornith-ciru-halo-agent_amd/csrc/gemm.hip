@@ -172,11 +172,16 @@ constexpr int kBM = 256, kBN = 64, kBK = 32, kRing = 4;
 // 128-byte bank line (a 16-byte access serves 8 lanes per LDS cycle)
 __device__ __forceinline__ int b_slot(int c, int chunk) { return c * 64 + ((chunk ^ ((c >> 1) & 3)) << 4); }
 
+// kslices > 1 (split K, for grids that fill few of the chip's block slots):
+// tile = (slice, row block, column block); slice ks takes 256-groups
+// [ks G / kslices, (ks + 1) G / kslices) and writes its fp32 sums to
+// partial[ks] ([M, N]); dense_slices_kernel adds the slices in order.
 __global__ __launch_bounds__(256, 2) void dense_gemm_bf16_kernel(const uint16_t* __restrict__ xt,
                                                                  const uint32_t* __restrict__ codes,
                                                                  const uint32_t* __restrict__ meta, int M, int N,
-                                                                 int K, int nblocks_m, int nblocks_n,
-                                                                 uint16_t* __restrict__ out, uint32_t* sticky) {
+                                                                 int K, int nblocks_m, int nblocks_n, int kslices,
+                                                                 uint16_t* __restrict__ out,
+                                                                 float* __restrict__ partial, uint32_t* sticky) {
     __shared__ __attribute__((aligned(16))) uint8_t sB[kRing][kBN * 64];  // bf16 [64 columns][32 k], a ring
     __shared__ __attribute__((aligned(16))) uint8_t sC[4 * 16 * 136];     // output staging, 16 rows per wave
     const int tid = threadIdx.x, lane = tid & 63;
@@ -187,12 +192,14 @@ __global__ __launch_bounds__(256, 2) void dense_gemm_bf16_kernel(const uint16_t*
     // (row block, column block) order, so its concurrent blocks share one or
     // two row blocks of A in its L2 instead of every row block.
     const int L = int(blockIdx.x), per = int(gridDim.x) / 8;
-    const int tile = (L & 7) * per + (L >> 3);
-    if (tile >= nblocks_m * nblocks_n) return;
-    const int nb = tile % nblocks_n, mb = tile / nblocks_n;
+    const int tile = (L & 7) * per + (L >> 3), mn = nblocks_m * nblocks_n;
+    if (tile >= mn * kslices) return;
+    const int ks = tile / mn, nb = tile % nblocks_n, mb = (tile - ks * mn) / nblocks_n;
     const int row0 = mb * kBM, col0 = nb * kBN;
     const bool wave_live = row0 + 64 * wm < M;
     const int G = K / kGroup, S = K / kBK;
+    const int g0 = ks * G / kslices, g1 = (ks + 1) * G / kslices;   // this slice's groups (at least one)
+    const int st0 = 8 * g0, st1 = 8 * g1;
 
     // ---- B: column c = lane, word jw = wave of the step's four (32 k) ----
     // Addresses are a wave-uniform part (scalar registers) plus one 32-bit
@@ -256,7 +263,7 @@ __global__ __launch_bounds__(256, 2) void dense_gemm_bf16_kernel(const uint16_t*
             ra[slot][rt] = *reinterpret_cast<const uint4*>(a_frag[rt] + size_t(st) * 1024 + a_lane);
     };
 
-    // Pipeline (S >= 8 steps): at step st the products of st run on B
+    // Pipeline (steps st0 .. st1 - 1 of the slice, at least 8): at step st the products of st run on B
     // fragments read from LDS during step st - 1, the fragments of st + 1 are
     // read, and the B tile of st + 2 is dequantised into LDS buffer
     // (st + 2) % kRing, then one barrier.  A buffer is rewritten two barriers
@@ -265,15 +272,15 @@ __global__ __launch_bounds__(256, 2) void dense_gemm_bf16_kernel(const uint16_t*
     // words a group before their group.
 #pragma unroll
     for (int d = 0; d < kRing; ++d) {
-        load_codes(d, d);
-        load_a(d, d);
+        load_codes(st0 + d, d);
+        load_a(st0 + d, d);
     }
-    Affine acur = affine(load_meta(0));
-    uint32_t mnext = load_meta(min(1, G - 1));
+    Affine acur = affine(load_meta(g0));
+    uint32_t mnext = load_meta(min(g0 + 1, g1 - 1));
     dequant(0, 0, acur);
-    load_codes(kRing, 0);
+    load_codes(st0 + kRing, 0);
     dequant(1, 1, acur);
-    load_codes(kRing + 1, 1);
+    load_codes(st0 + kRing + 1, 1);
     __syncthreads();
     bf16x8 fb[4];
     read_b(0, fb);
@@ -284,11 +291,11 @@ __global__ __launch_bounds__(256, 2) void dense_gemm_bf16_kernel(const uint16_t*
 #pragma unroll
         for (int ct = 0; ct < 4; ++ct) acc[rt][ct] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-    for (int g = 0; g < G; ++g) {                              // one 256-group (8 steps) per iteration
+    for (int g = g0; g < g1; ++g) {                            // one 256-group (8 steps) per iteration
         // the next group's scale and offset (for the tiles of its first two
         // steps, dequantised at steps 6 and 7), its successor's word loaded
-        const Affine anext = g + 1 < G ? affine(mnext) : acur;
-        mnext = load_meta(min(g + 2, G - 1));
+        const Affine anext = g + 1 < g1 ? affine(mnext) : acur;
+        mnext = load_meta(min(g + 2, g1 - 1));
 #pragma unroll
         for (int u = 0; u < 8; ++u) {
             const int st = 8 * g + u, slot = u % kRing, nslot = (u + 2) % kRing;
@@ -314,8 +321,8 @@ __global__ __launch_bounds__(256, 2) void dense_gemm_bf16_kernel(const uint16_t*
             // st + kRing, code slot nslot with step st + 2 + kRing (clamped:
             // unconditional loads)
             __builtin_amdgcn_sched_barrier(0);
-            load_a(min(st + kRing, S - 1), slot);
-            load_codes(min(st + 2 + kRing, S - 1), nslot);
+            load_a(min(st + kRing, st1 - 1), slot);
+            load_codes(min(st + 2 + kRing, st1 - 1), nslot);
             __builtin_amdgcn_sched_barrier(0);
             __syncthreads();
 #pragma unroll
@@ -324,6 +331,24 @@ __global__ __launch_bounds__(256, 2) void dense_gemm_bf16_kernel(const uint16_t*
         acur = anext;
     }
 
+    if (kslices > 1) {
+        // fp32 sums of this slice straight from the product layout: lane
+        // (li, q) of row tile rt and column tile ct holds row 16 rt + li,
+        // columns 16 ct + 4 q + 0..3 (N % 16 == 0: all four or none in range)
+        float* dst = partial + size_t(ks) * M * N;
+#pragma unroll
+        for (int rt = 0; rt < 4; ++rt) {
+            const int row = row0 + 64 * wm + 16 * rt + li;
+#pragma unroll
+            for (int ct = 0; ct < 4; ++ct) {
+                const int col = col0 + 16 * ct + 4 * q;
+                if (row < M && col < N)
+                    *reinterpret_cast<f32x4*>(dst + size_t(row) * N + col) = acc[rt][ct];
+            }
+        }
+        flag_or(sticky, flags);
+        return;
+    }
     // ---- epilogue: bf16 RNE of the fp32 sums, through LDS to whole-row stores ----
     // The products are (weights x activations), so lane (li, q) of row tile rt
     // and column tile ct holds row 16 rt + li, columns 16 ct + 4 q + 0..3 of its
@@ -354,6 +379,24 @@ __global__ __launch_bounds__(256, 2) void dense_gemm_bf16_kernel(const uint16_t*
     flag_or(sticky, flags);
 }
 
+// out = bf16(((partial[0] + partial[1]) + ...) + partial[kslices - 1]), four
+// columns per thread.
+__global__ __launch_bounds__(256) void dense_slices_kernel(const float* __restrict__ partial, int kslices,
+                                                           size_t count4, uint16_t* __restrict__ out) {
+    const size_t i = size_t(blockIdx.x) * 256 + threadIdx.x;
+    if (i >= count4) return;
+    const f32x4* p = reinterpret_cast<const f32x4*>(partial) + i;
+    f32x4 s = p[0];
+    for (int k = 1; k < kslices; ++k) {
+        const f32x4 v = p[size_t(k) * count4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) s[e] = s[e] + v[e];
+    }
+    const f32x2 lo = {s[0], s[1]}, hi = {s[2], s[3]};
+    reinterpret_cast<uint2*>(out)[i] = make_uint2(__builtin_bit_cast(uint32_t, __builtin_convertvector(lo, bf16x2)),
+                                                  __builtin_bit_cast(uint32_t, __builtin_convertvector(hi, bf16x2)));
+}
+
 }  // namespace
 
 hipError_t launch_transform_bf16_fast(const uint16_t* x, int M, int K, uint16_t* y, uint32_t* sticky, hipStream_t s) {
@@ -370,12 +413,31 @@ hipError_t launch_transform_bf16_frag(const uint16_t* x, int M, int K, uint16_t*
     return hipGetLastError();
 }
 
+int dense_gemm_slices(int M, int N, int K, size_t partial_bytes) {
+    // the GEMM runs two blocks per CU: a grid of fewer tiles than block slots
+    // splits K, up to kMaxDenseSlices ways with at least two 256-groups per
+    // slice (one-group slices measured slower: 1120 x 2048 x 512, 11.1 us
+    // unsplit against 16.1 + 4.6 split), as far as the partial sums fit
+    const int tiles = ((N + kBN - 1) / kBN) * ((M + kBM - 1) / kBM);
+    const int slots = 2 * device_cu_count();
+    int k = min(min(slots / max(tiles, 1), K / kGroup / 2), kMaxDenseSlices);
+    while (k > 1 && size_t(k) * M * N * 4 > partial_bytes) --k;
+    return max(k, 1);
+}
+
 hipError_t launch_dense_gemm_bf16(const uint16_t* xt, const uint32_t* codes, const uint32_t* meta, int M, int N, int K,
-                                  uint16_t* out, uint32_t* sticky, hipStream_t s) {
+                                  uint16_t* out, float* partial, size_t partial_bytes, uint32_t* sticky,
+                                  hipStream_t s) {
     const int nbn = (N + kBN - 1) / kBN, nbm = (M + kBM - 1) / kBM;
-    const int per = (nbn * nbm + 7) / 8;                 // tiles per XCD
+    const int kslices = dense_gemm_slices(M, N, K, partial ? partial_bytes : 0);
+    const int per = (nbn * nbm * kslices + 7) / 8;       // tiles per XCD
     timed_launch("dense_gemm", dense_gemm_bf16_kernel, dim3(8 * per), dim3(256), 0, s, xt, codes, meta, M, N, K, nbm,
-                 nbn, out, sticky);
+                 nbn, kslices, out, partial, sticky);
+    hipError_t st = hipGetLastError();
+    if (st != hipSuccess || kslices == 1) return st;
+    const size_t count4 = size_t(M) * N / 4;
+    timed_launch("dense_slices", dense_slices_kernel, dim3((count4 + 255) / 256), dim3(256), 0, s,
+                 static_cast<const float*>(partial), kslices, count4, out);
     return hipGetLastError();
 }
 

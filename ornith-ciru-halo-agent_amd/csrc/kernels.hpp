@@ -184,9 +184,15 @@ hipError_t launch_transform_bf16_fast(const uint16_t* x, int M, int K, uint16_t*
 // the same values in matrix-core fragment order over round_up(M, 16) rows
 // (padding rows zero): (r, k) at ((r / 16 * K / 32 + k / 32) * 64 + 16 (k % 32 / 8) + r % 16) * 8 + k % 8
 hipError_t launch_transform_bf16_frag(const uint16_t* x, int M, int K, uint16_t* y, uint32_t* sticky, hipStream_t s);
-// out bf16 [M, N] = y @ bf16(dequant(N16 codes, meta))^T, fp32 accumulation; y in fragment order
+// out bf16 [M, N] = y @ bf16(dequant(N16 codes, meta))^T, fp32 accumulation; y in fragment order.
+// A grid that fills few block slots splits K into slices (dense_gemm_slices)
+// whose fp32 sums go to `partial` (up to partial_bytes; null: no split) and
+// are added in slice order.
+constexpr int kMaxDenseSlices = 8;
+int dense_gemm_slices(int M, int N, int K, size_t partial_bytes);
 hipError_t launch_dense_gemm_bf16(const uint16_t* xt, const uint32_t* codes, const uint32_t* meta, int M, int N, int K,
-                                  uint16_t* out, uint32_t* sticky, hipStream_t s);
+                                  uint16_t* out, float* partial, size_t partial_bytes, uint32_t* sticky,
+                                  hipStream_t s);
 
 // ---- shared expert, fixed8 semantics (shared.hip) ------------------------------
 // act [M, 512] bf16 from the bf16 gate/up projection gu [M, 1024] (tabulated

@@ -38,6 +38,9 @@ BUILDS = {32: 'libornith_g256_mi355x.so', 16: 'libornith_g256_mi355x_n16.so'}
 
 HIDDEN, EXPERTS, TOP, INTER = 2048, 256, 8, 512
 HEAD_VOCAB, HEAD_MAX_ROWS = 248320, 64
+# fp32 slice sums of the dense GEMM's split K: slices x tiles stay within the
+# chip's 2 x 256 block slots and a tile has 256 x 64 outputs
+DENSE_SLICE_BYTES = 2 * 256 * 256 * 64 * 4
 A8_ONLY_PREFILL_ROWS = 64      # _a4_prefill entries switch to A4 above this many tokens
 
 _ROUTED_FIELDS = ('workspace_bytes', 'gate_x', 'gate_low', 'gate_high', 'gate_scales', 'gate_sums', 'gate_y',
@@ -243,7 +246,8 @@ def configure(settings, capacity, shapes, shared_expert=False):
             raise ValueError('the N32 decode library must keep its parent\'s workspace layout')
     for n, k in shapes:
         sizes.append(dense_layout(capacity, n, k, tile=roles['dense']).workspace_bytes)
-        sizes.append((int(capacity) + 15) // 16 * 16 * k * 2)   # the GEMM's bf16(H128 x), rows padded to 16
+        # the GEMM's bf16(H128 x), rows padded to 16, then its split-K slice sums
+        sizes.append((int(capacity) + 15) // 16 * 16 * k * 2 + DENSE_SLICE_BYTES)
     sizes.append(head_layout(HEAD_MAX_ROWS, HEAD_VOCAB, tile=roles['head']).workspace_bytes)
     if shared_expert:
         # the fused ninth slot (at most 16 rows, any routed build) and fixed8

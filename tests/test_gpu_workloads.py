@@ -170,6 +170,49 @@ def test_dense_out_prefill_tolerance(device, M, N, K):
     assert int(flags.item()) == 0
 
 
+# slices on the MI355X's 256 CUs: 8, 3, 4 and 8
+@pytest.mark.parametrize('M,N,K,slices', [(300, 512, 4096, 8), (1120, 2048, 4096, 3), (1120, 1024, 2048, 4),
+                                           (65, 96, 4096, 8)])
+def test_dense_gemm_split_k(device, M, N, K, slices):
+    """A GEMM grid that fills few of the chip's block slots splits K when the
+    workspace holds the fp32 slice sums: the slices' sums are added in slice
+    order (dense_slices ran), the result is deterministic, and it meets the
+    same tolerance against fp64 as the unsplit GEMM (cosine >= 0.9999, max
+    |err| <= 1e-2 * max |ref|)."""
+    import torch
+    from _ornith import Bank
+    native = _native()
+    print(f'dense gemm split K: {M} x {N} x {K}, {slices} slices', flush=True)
+    rng = np.random.default_rng(4000 + M + N)
+    bank = Bank(rng, 0, N, K, tile=16)
+    x = bf16_normal(rng, (M, K))
+    xt_bytes = (M + 15) // 16 * 16 * K * 2
+    ws = torch.empty(xt_bytes + native.DENSE_SLICE_BYTES + 256, dtype=torch.uint8, device=device)
+    xd, cd, md = to_dev(x, device), to_dev(bank.codes, device), to_dev(bank.meta, device)
+    outs = []
+    for bytes_ in (ws.numel(), ws.numel(), xt_bytes):      # split twice, then unsplit
+        out = torch.empty((M, N), dtype=torch.bfloat16, device=device)
+        flags = _flags(device)
+        with native.KernelTimer('*') as kt:
+            assert native.lib().ornith_dense_g256_gemm_bf16(native.ptr(xd), native.ptr(cd), native.ptr(md),
+                                                            native.ptr(ws), bytes_, native.ptr(out), native.ptr(flags),
+                                                            M, N, K, native.stream(xd)) == 0
+            _sync()
+            names = set(kt.names())
+        assert ('dense_slices' in names) == (bytes_ != xt_bytes), names
+        assert int(flags.item()) == 0
+        outs.append(from_dev(out))
+    np.testing.assert_array_equal(outs[0], outs[1])
+    ref = (O.bf16_to_f32(O.transform_bf16(x)).astype(np.float64)
+           @ O.bf16_to_f32(O.dequantize_bf16(*bank.expert())).astype(np.float64).T)
+    for got in (outs[0], outs[2]):
+        g = O.bf16_to_f32(got).astype(np.float64)
+        cos = float((g.ravel() @ ref.ravel()) / (np.linalg.norm(g) * np.linalg.norm(ref)))
+        err = float(np.abs(g - ref).max() / np.abs(ref).max())
+        print(f'  cosine {cos:.8f}  max rel err {err:.2e}', flush=True)
+        assert cos >= 0.9999 and err <= 1e-2
+
+
 # ---------------------------------------------------------------------------
 # N16-bank build (the parent routed library role, routed_direct_api.h:7)
 # ---------------------------------------------------------------------------
