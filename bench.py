@@ -65,7 +65,10 @@ def kernel_cost(name, T, unique):
     """Algorithmic work of one launch of `name` for a T-token layer that touches
     `unique` routed experts: (bound, amount, peak, unit).  hbm amounts are the
     compulsory bytes (weights of the touched banks + activations in and out);
-    mfma amounts are the int8 ops of the exact integer dots (2 per MAC)."""
+    mfma amounts are the int8 ops of the exact integer dots (2 per MAC).  The
+    grouped prefill projections report whichever roof binds at this T (the
+    larger of bytes / HBM peak and ops / int8 peak): HBM at 1120 tokens, the
+    matrix cores for the gate-up at 8192."""
     banks = unique + 1
     routes = 9 * T
     if name == 'layer1':            # the whole single-token layer in one launch
@@ -76,10 +79,14 @@ def kernel_cost(name, T, unique):
         return 'hbm', banks * GATEUP_BYTES + T * 2048 + routes * 512 * 4, HBM_PEAK_GBS, 'GB/s'
     if name in ('down1', 'down'):
         return 'hbm', banks * DOWN_BYTES + routes * 512 * 4 + T * 2048 * 2, HBM_PEAK_GBS, 'GB/s'
-    if name == 'gateup_mfma':
-        return 'mfma', 2 * routes * 1024 * 2048, INT8_PEAK_TOPS, 'TFLOP/s'
-    if name == 'down_mfma':
-        return 'mfma', 2 * routes * 2048 * 512, INT8_PEAK_TOPS, 'TFLOP/s'
+    if name in ('gateup_mfma', 'down_mfma'):
+        if name == 'gateup_mfma':       # codes + meta, A8 gate input in, fp32 middle rows out
+            nbytes, ops = banks * GATEUP_BYTES + T * 2048 + routes * 512 * 4, 2 * routes * 1024 * 2048
+        else:                           # codes + meta, A8 middle rows in, fp32 route rows out
+            nbytes, ops = banks * DOWN_BYTES + routes * 512 + routes * 2048 * 4, 2 * routes * 2048 * 512
+        if nbytes / (HBM_PEAK_GBS * 1e9) >= ops / (INT8_PEAK_TOPS * 1e12):
+            return 'hbm', nbytes, HBM_PEAK_GBS, 'GB/s'
+        return 'mfma', ops, INT8_PEAK_TOPS, 'TFLOP/s'
     if name == 'router':      # exact K=1 fp32 matrix steps (the shared-gate row on the VALU)
         return 'mfma', 2 * T * 257 * 2048, FP32_PEAK_TFLOPS, 'TFLOP/s'
     if name == 'permute_scan_act':  # the scan's block counts are noise beside the gate-input quantisation

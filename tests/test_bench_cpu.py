@@ -30,6 +30,14 @@ def test_single_token_algorithmic_bytes():
     assert unit == 'GB/s'
     assert whole == 9 * (1_081_344 + 540_672) + 256 * 2048 * 2 + 2048 * 2 + 2048 * 2 * 2 == 15_659_008
     assert whole == bench.algorithmic(1, 8)[0]
-    # prefill matrix-core work: 2 ops per MAC over 9 routes per token
-    _, ops, _, unit = bench.kernel_cost('gateup_mfma', 1120, 96)
-    assert unit == 'TFLOP/s' and ops == 2 * 9 * 1120 * 1024 * 2048
+    # prefill gate-up: at 1120 tokens the bytes bind (97 banks of codes, the
+    # A8 input, the fp32 middle rows: 129 MB = 16.1 us at 8 TB/s against
+    # 42.3 G int8 ops = 8.5 us at 5 POP/s); at 8192 the matrix cores
+    # (2 ops per MAC over 9 routes per token)
+    bound, nbytes, _, unit = bench.kernel_cost('gateup_mfma', 1120, 96)
+    assert (bound, unit) == ('hbm', 'GB/s')
+    assert nbytes == 97 * 1_081_344 + 1120 * 2048 + 9 * 1120 * 512 * 4
+    bound, ops, _, unit = bench.kernel_cost('gateup_mfma', 8192, 101)
+    assert (bound, unit) == ('mfma', 'TFLOP/s') and ops == 2 * 9 * 8192 * 1024 * 2048
+    # the down projection writes fp32 route rows: bytes bind at both sizes
+    assert bench.kernel_cost('down_mfma', 8192, 101)[0] == 'hbm'
