@@ -14,7 +14,7 @@
 //                              codes stay in registers while the segment's
 //                              routes stream through four at a time; exact
 //                              int8 dots, fp32 group tree, SiLU(gate)*up.
-//   S5 decode_down_kernel      block (segment, 64 output columns), same
+//   S5 decode_down_kernel      block (segment, 128 output columns), same
 //                              scheme, writing route_out; its prologue runs
 //                              H128 + quantisation of the segment's fp32
 //                              middle rows (every block of a segment, as
@@ -614,7 +614,7 @@ void carve_decode(void* base, DecodeArgs& a) {
     a.l1_words = static_cast<uint64_t*>(take(size_t(kHandoffWords) * 8));
 }
 
-constexpr int kDownTilesPerBlock = 2;    // 32-column down tiles per block (2048 / 32 / 2 = 32 blocks per segment)
+constexpr int kDownTilesPerBlock = 4;    // 32-column down tiles per block (2048 / 32 / 4 = 16 blocks per segment)
 
 // Whether `blocks` blocks of the one-launch route kernel are resident at once
 // on the device that runs stream `s` (occupancy checked once per device).
