@@ -37,6 +37,19 @@ constexpr int kMaxRoutes = kDecodeMaxTokens * (kTop + 1);
 constexpr int kRouteChunk = 4;
 constexpr int kTokenBatch = 8;
 
+// Router wave gw's job: the four waves of a block take four consecutive
+// router rows of one batch of 8 tokens, so they load the same token rows (L1
+// hits after the first) and different weight rows; rows run to a multiple of
+// 4 (waves past the last row have no job).
+__device__ __forceinline__ void router_wave_job(int gw, int T, int& row, int& t0) {
+    const int nb = (T + kTokenBatch - 1) / kTokenBatch, grp = gw >> 2;
+    row = 4 * (grp / nb) + (gw & 3);
+    t0 = (grp % nb) * kTokenBatch;
+}
+constexpr int router_waves_for(bool shared, int T) {
+    return ((shared ? kExperts + 1 : kExperts) + 3) / 4 * 4 * ((T + kTokenBatch - 1) / kTokenBatch);
+}
+
 // ---------------------------------------------------------------------------
 // S1
 // ---------------------------------------------------------------------------
@@ -45,8 +58,9 @@ __global__ __launch_bounds__(256) void decode_route_kernel(DecodeArgs a, int rou
     const int T = a.T, lane = threadIdx.x & 63;
     const int gw = blockIdx.x * 4 + (threadIdx.x >> 6);
     if (ROUTER && gw < router_waves) {
-        const int nb = (T + kTokenBatch - 1) / kTokenBatch;
-        const int row = gw / nb, t0 = (gw % nb) * kTokenBatch;
+        int row, t0;
+        router_wave_job(gw, T, row, t0);
+        if (row > (SHARED ? kExperts : kExperts - 1)) return;
         const uint16_t* wrow = row < kExperts ? a.router_w + size_t(row) * kHidden : a.shared_gate_w;
         const bool has_bias = a.bias && row < kExperts;
         router_rows_wave(a.x, kHidden, T, t0, wrow, has_bias ? a.bias[row] : 0.f, has_bias, a.logits, kLogitStride,
@@ -282,13 +296,15 @@ __global__ __launch_bounds__(256) void decode_route_select_kernel(DecodeArgs a, 
     // each wave's own loads (router rows, x) are issued and used
     uint32_t seq_v = __hip_atomic_load(a.l1_seq, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     uint32_t flags = 0;
-    if (gw < router_waves) {
-        const int nb = (T + kTokenBatch - 1) / kTokenBatch;
-        const int row = gw / nb, t0 = (gw % nb) * kTokenBatch;
+    int row = 0, t0 = 0;
+    if (gw < router_waves) router_wave_job(gw, T, row, t0);
+    if (gw < router_waves && row <= (SHARED ? kExperts : kExperts - 1)) {
         const uint16_t* wrow = row < kExperts ? a.router_w + size_t(row) * kHidden : a.shared_gate_w;
         const bool has_bias = a.bias && row < kExperts;
         router_rows_wave(a.x, kHidden, T, t0, wrow, has_bias ? a.bias[row] : 0.f, has_bias, a.logits, kLogitStride,
                          row, W, seq_v, uint32_t(kDecodeRouteLogit + kDecodeMaxTokens * row + t0));
+    } else if (gw < router_waves) {
+        // a padding wave of the last row group: no router row
     } else if (gw - router_waves < T * 4) {
         // quantised gate input: wave q handles groups 2(q%4), 2(q%4)+1 of token q/4
         const int q = gw - router_waves;
@@ -637,7 +653,7 @@ std::atomic<int> g_route_select_mode{0};   // 0 automatic, 1 separate route / to
 template <bool ROUTER, bool SHARED, int QMAX>
 static hipError_t run(const DecodeArgs& a, hipStream_t s) {
     const int T = a.T, R = T * kTop;
-    const int router_waves = ROUTER ? (SHARED ? kExperts + 1 : kExperts) * ((T + kTokenBatch - 1) / kTokenBatch) : 0;
+    const int router_waves = ROUTER ? router_waves_for(SHARED, T) : 0;
     const int s1_waves = router_waves + T * 4;
     hipError_t st;
     bool fused = false;
