@@ -49,8 +49,8 @@ DENSE_N = 6144
 # --copy-calibration); keyed by (kernel, tokens).  Commands and raw figures:
 # profiles/decode_n1_n32_hbm_traffic_pmc.md, profiles/prefill_1120_8192_hbm_traffic_pmc.md.
 MEASURED_TRAFFIC = {
-    ('layer1', 1): 16759322, ('route1', 1): 1166652, ('gateup1', 1): 9949504, ('down1', 1): 5118494,
-    ('route_select', 32): 3058446, ('gateup', 32): 176478845, ('down', 32): 94475882, ('reduce', 32): 2596413,
+    ('layer1', 1): 16768264, ('route1', 1): 1166652, ('gateup1', 1): 9949504, ('down1', 1): 5118494,
+    ('route_select', 32): 5329307, ('gateup', 32): 176476340, ('down', 32): 94490777, ('reduce', 32): 2596402,
     ('router', 1120): 15343263, ('topk', 1120): 2186638, ('permute_scan_act', 1120): 7786592,
     ('permute_scatter', 1120): 320474, ('gateup_mfma', 1120): 190732263, ('quant_middle', 1120): 26020249,
     ('down_mfma', 1120): 177260462, ('reduce', 1120): 87590525,
