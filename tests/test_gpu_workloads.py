@@ -213,6 +213,34 @@ def test_dense_gemm_split_k(device, M, N, K, slices):
         assert cos >= 0.9999 and err <= 1e-2
 
 
+def test_dense_out_split_k_through_the_op(device):
+    """dense_out with the workspace configure() sizes (bf16(H128 x) plus the
+    split-K slice sums) at 300 x 512 x 4096, whose 16 tiles split K: the op
+    runs the slices and their ordered sum, within the fp64 tolerance."""
+    import torch
+    from _ornith import Bank
+    native = _native()
+    M, N, K = 300, 512, 4096
+    rng = np.random.default_rng(4321)
+    bank = Bank(rng, 0, N, K, tile=16)
+    x = bf16_normal(rng, (M, K))
+    ws = torch.empty((M + 15) // 16 * 16 * K * 2 + native.DENSE_SLICE_BYTES, dtype=torch.uint8, device=device)
+    out = torch.empty((M, N), dtype=torch.bfloat16, device=device)
+    flags = _flags(device)
+    with native.KernelTimer('*') as kt:
+        native.dense_out(to_dev(x, device), to_dev(bank.codes, device), to_dev(bank.meta, device), ws, out, flags,
+                         M, N, K, 2, 64)
+        _sync()
+        assert set(kt.names()) == {'transform_bf16_frag', 'dense_gemm', 'dense_slices'}, kt.names()
+    got = O.bf16_to_f32(from_dev(out)).astype(np.float64)
+    ref = (O.bf16_to_f32(O.transform_bf16(x)).astype(np.float64)
+           @ O.bf16_to_f32(O.dequantize_bf16(*bank.expert())).astype(np.float64).T)
+    cos = float((got.ravel() @ ref.ravel()) / (np.linalg.norm(got) * np.linalg.norm(ref)))
+    err = float(np.abs(got - ref).max() / np.abs(ref).max())
+    assert cos >= 0.9999 and err <= 1e-2, (cos, err)
+    assert int(flags.item()) == 0
+
+
 # ---------------------------------------------------------------------------
 # N16-bank build (the parent routed library role, routed_direct_api.h:7)
 # ---------------------------------------------------------------------------
