@@ -259,6 +259,34 @@ def gateup_bf16_model_us(device, steps=10):
     return res
 
 
+def graph_ms(call, n, reps=3):
+    """Milliseconds per call of `call(0..n-1)` captured once into a CUDA
+    graph and replayed `reps` times (warmed up outside the capture first), so
+    host-side gaps between the calls do not count, as in a serving loop that
+    replays captured steps."""
+    import torch
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for i in range(n):
+            call(i)
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for i in range(n):
+            call(i)
+    g.replay()
+    torch.cuda.synchronize()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record()
+    for _ in range(reps):
+        g.replay()
+    b.record()
+    torch.cuda.synchronize()
+    return a.elapsed_time(b) / (reps * n)
+
+
 def dense_prefill_ms(T, device, steps=20):
     """Dense G256 linear [6144, 2048] on T rows through ornith_g256::dense_out.
     Up to 64 rows (the A8 GEMV, weight-streaming) 48 weight copies (312 MB)
@@ -293,15 +321,16 @@ def dense_prefill_ms(T, device, steps=20):
         raise RuntimeError(f'native flags raised by the dense linear at {T} rows: {int(flags.item())}')
     wall = a.elapsed_time(b) / steps
     if T > 64:
-        return wall
+        return graph_ms(call, steps)
     # Small T is bound by the host's per-call launch cost; also report the
-    # device time (sum of the library kernels' event-timed durations).
+    # device time (sum of the library kernels' event-timed durations) and the
+    # per-call time of captured calls.
     with native.KernelTimer('*') as kt:
         for i in range(steps):
             call(i)
         torch.cuda.synchronize()
         device_ms = sum(kt.read(n)[1] for n in kt.names())
-    return wall, device_ms
+    return wall, device_ms, graph_ms(call, steps)
 
 
 def head_ms(device, steps=20):
@@ -323,20 +352,16 @@ def head_ms(device, steps=20):
     for i in range(4):
         call(i)
     torch.cuda.synchronize()
-    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    a.record()
-    for i in range(steps):
-        call(i)
-    b.record()
-    torch.cuda.synchronize()
+    ms = graph_ms(call, steps)
     if int(flags.item()):
         raise RuntimeError(f'native flags raised by the G256 head: {int(flags.item())}')
-    return a.elapsed_time(b) / steps
+    return ms
 
 
 def w8_head_us(device, rows=(1, 8, 64), steps=20):
     """The reference's W8 G128 LM head [248320, 2048] (head_i8_tile_api.h:22)
-    at each row count: microseconds per call with two 520 MB weight copies
+    at each row count: microseconds per call (captured calls replayed; the
+    eager figure, host gaps included, beside it) with two 520 MB weight copies
     alternating (not MALL-resident), plus the kernel's average and its HBM
     rate over the weight and scale bytes."""
     import torch
@@ -370,8 +395,8 @@ def w8_head_us(device, rows=(1, 8, 64), steps=20):
             torch.cuda.synchronize()
             _, kms = kt.read('head_w8_mfma')
         weight_bytes = N * 2048 + N * 16 * 2
-        result[str(m)] = dict(us_per_call=a.elapsed_time(b) / steps * 1e3, kernel_us=kms * 1e3,
-                              weight_gbs=weight_bytes / (kms * 1e-3) / 1e9)
+        result[str(m)] = dict(us_per_call=graph_ms(call, steps) * 1e3, us_per_call_eager=a.elapsed_time(b) / steps * 1e3,
+                              kernel_us=kms * 1e3, weight_gbs=weight_bytes / (kms * 1e-3) / 1e9)
     if int(flags.item()):
         raise RuntimeError(f'native flags raised by the W8 head: {int(flags.item())}')
     return result
@@ -521,9 +546,10 @@ def main():
         print(json.dumps({'gateup_bf16_model': gateup_bf16_model_us(dev, args.steps)}))
         return
     if args.part == 'dense':
-        wall1, device1 = dense_prefill_ms(1, dev, 48)
+        wall1, device1, graph1 = dense_prefill_ms(1, dev, 48)
         print(json.dumps({'dense_6144x2048_1120_us': dense_prefill_ms(1120, dev, args.steps) * 1e3,
-                          'dense_6144x2048_1_us': wall1 * 1e3, 'dense_6144x2048_1_device_us': device1 * 1e3}))
+                          'dense_6144x2048_1_us': wall1 * 1e3, 'dense_6144x2048_1_device_us': device1 * 1e3,
+                          'dense_6144x2048_1_graph_us': graph1 * 1e3}))
         return
     silu, sigmoid = tables.load(dev)
     layers = [synthetic.moe_layer(10_000 + i, dev) for i in range(args.layers)]
@@ -569,9 +595,10 @@ def main():
                                         layer_roof=binding_roof(args.tokens, unique, ms),
                                         kernels_us={n: v[1] * 1e3 for n, v in times.items()})
     if args.tokens == 1:
-        wall1, device1 = dense_prefill_ms(1, dev, 48)
+        wall1, device1, graph1 = dense_prefill_ms(1, dev, 48)
         per_tokens['1']['dense_6144x2048_us'] = wall1 * 1e3
         per_tokens['1']['dense_6144x2048_device_us'] = device1 * 1e3
+        per_tokens['1']['dense_6144x2048_graph_us'] = graph1 * 1e3
 
     result = {
         'metric': 'MoE layer tokens/s',
