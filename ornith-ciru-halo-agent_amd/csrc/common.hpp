@@ -249,6 +249,14 @@ __device__ __forceinline__ void flag_or(uint32_t* sticky, uint32_t bits) {
     if (bits) atomicOr(sticky, bits);
 }
 
+// A code word of a weight stream that one launch reads once: a non-temporal
+// load, so the stream does not displace the lines other blocks still use
+// (measured on the decode paths: N=32 gate-up 33.3 -> 32.0 us and down 20.6
+// -> 19.4 us, the single-token layer 12.5 -> 12.1 us, the one-row dense
+// linear 5.9 -> 5.45 us; the W8 head at 1-8 rows got slower and keeps plain
+// loads there).
+__device__ __forceinline__ uint32_t load_once(const uint32_t* p) { return __builtin_nontemporal_load(p); }
+
 // ---- 4-bit weight unpacking -----------------------------------------------
 // A packed code word holds K values 8c..8c+7, low nibble first
 // (dense_g256_api.h:25).  Even codes (k = 8c, 8c+2, 8c+4, 8c+6) go to the

@@ -425,7 +425,7 @@ __global__ __launch_bounds__(512) void decode_gateup_kernel(DecodeArgs a) {
     const uint32_t* wp = codes + bv.word(col, g, 8);
     uint32_t wr[32];
 #pragma unroll
-    for (int j = 0; j < 32; ++j) wr[j] = wp[j * bv.stride()];
+    for (int j = 0; j < 32; ++j) wr[j] = load_once(wp + j * bv.stride());
     const uint32_t mw = meta[bv.meta(col, g, 8)];
     if (tid < sg.count) lr[tid] = route_in;
     __syncthreads();
@@ -537,7 +537,7 @@ __global__ __launch_bounds__(256) void decode_down_kernel(DecodeArgs a) {
     for (int cc = 0; cc < CPB; ++cc) {
         const uint32_t* wp = codes + bv.word(32 * (c0 + cc) + n, g, 2) + 8 * q * bv.stride();
 #pragma unroll
-        for (int j = 0; j < 8; ++j) wr[cc][j] = wp[j * bv.stride()];
+        for (int j = 0; j < 8; ++j) wr[cc][j] = load_once(wp + j * bv.stride());
     }
 #pragma unroll
     for (int cc = 0; cc < CPB; ++cc) mw[cc] = meta[bv.meta(32 * (c0 + cc) + n, g, 2)];   // epilogue thread (g, n)

@@ -179,7 +179,7 @@ __global__ __launch_bounds__(256) void decode1_gateup_kernel(DecodeArgs a) {
     const uint32_t* wp = codes + bv.word(col, g, 8);
     uint32_t wr[32];
 #pragma unroll
-    for (int j = 0; j < 32; ++j) wr[j] = wp[j * bv.stride()];
+    for (int j = 0; j < 32; ++j) wr[j] = load_once(wp + j * bv.stride());
     const uint32_t mw = meta[bv.meta(col, g, 8)];
     la[tid] = a0;
     la[tid + 256] = a1;
@@ -284,7 +284,7 @@ __global__ __launch_bounds__(576) void decode1_down_kernel(DecodeArgs a) {
     const uint32_t* wp = base + bv.word(col, g, 2) + 16 * h * bv.stride();
     uint32_t wr[16];
 #pragma unroll
-    for (int j = 0; j < 16; ++j) wr[j] = wp[j * bv.stride()];
+    for (int j = 0; j < 16; ++j) wr[j] = load_once(wp + j * bv.stride());
     const uint32_t mw = mbase[bv.meta(col, g, 2)];
     // shared-expert gate: its table load goes out behind the codes, used at the end
     const uint16_t gate_bits = SHARED ? a.sigmoid_table[shared_logit] : 0;
@@ -524,7 +524,7 @@ __global__ __launch_bounds__(64 * kLayer1Waves) void layer1_kernel(DecodeArgs a)
         const BankView bv = bank_view(true);
         const uint32_t* wp = a.s13_codes + bv.word(gcol, g, 8);
 #pragma unroll
-        for (int j = 0; j < 32; ++j) ws[j] = wp[j * bv.stride()];
+        for (int j = 0; j < 32; ++j) ws[j] = load_once(wp + j * bv.stride());
         mws = a.s13_meta[bv.meta(gcol, g, 8)];
     }
     // ---- router row(s) in the declared order of decode1_route_kernel, published at once ----
@@ -730,7 +730,7 @@ __global__ __launch_bounds__(64 * kLayer1Waves) void layer1_kernel(DecodeArgs a)
         const BankView bv = bank_view(true);
         const uint32_t* wp = a.s2_codes + bv.word(dcol, dg, 2) + 16 * dh * bv.stride();
 #pragma unroll
-        for (int j = 0; j < 16; ++j) wd[j] = wp[j * bv.stride()];
+        for (int j = 0; j < 16; ++j) wd[j] = load_once(wp + j * bv.stride());
         mwd = a.s2_meta[bv.meta(dcol, dg, 2)];
     }
     // ---- routed gate-up codes (waves 0-3), loaded from the speculative pick
@@ -742,7 +742,7 @@ __global__ __launch_bounds__(64 * kLayer1Waves) void layer1_kernel(DecodeArgs a)
         const BankView bv = bank_view(false);
         const uint32_t* wp = a.w13_codes + size_t(b) * kGateBankWords + bv.word(gcol, g, 8);
 #pragma unroll
-        for (int j = 0; j < 32; ++j) wr[j] = wp[j * bv.stride()];
+        for (int j = 0; j < 32; ++j) wr[j] = load_once(wp + j * bv.stride());
         mw = a.w13_meta[size_t(b) * kGateBankMeta + bv.meta(gcol, g, 8)];
     };
     if (wave < 4) {
@@ -768,7 +768,7 @@ __global__ __launch_bounds__(64 * kLayer1Waves) void layer1_kernel(DecodeArgs a)
         const uint32_t* wp = (sh ? a.s2_codes : a.w2_codes + size_t(lb) * kDownBankWords) + bv.word(dcol, dg, 2) +
                              16 * dh * bv.stride();
 #pragma unroll
-        for (int j = 0; j < 16; ++j) wd[j] = wp[j * bv.stride()];
+        for (int j = 0; j < 16; ++j) wd[j] = load_once(wp + j * bv.stride());
         mwd = (sh ? a.s2_meta : a.w2_meta + size_t(lb) * kDownBankMeta)[bv.meta(dcol, dg, 2)];
     };
 

@@ -129,7 +129,10 @@ __global__ __launch_bounds__(64 * kW8Waves, 1) void head_w8_mfma_kernel(
     auto load_b = [&](int st, int slot) {
         const uint32_t* src = wbase + size_t(st) * 512;
 #pragma unroll
-        for (int u = 0; u < 8; ++u) bw[slot][u] = src[256 * (u >> 2) + 16 * (u & 3)];
+        for (int u = 0; u < 8; ++u) {
+            const uint32_t* pu = src + 256 * (u >> 2) + 16 * (u & 3);
+            bw[slot][u] = MT >= 4 ? load_once(pu) : *pu;   // non-temporal only for the 64-row tiles (measured)
+        }
         bs[slot] = sbase[size_t(st >> 4) * (16 * kHeadGroups) + (st & 15)];
     };
 #pragma unroll

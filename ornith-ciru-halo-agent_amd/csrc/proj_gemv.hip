@@ -196,7 +196,7 @@ __global__ __launch_bounds__(256) void dense_stream_kernel(ProjArgs a) {
         if (TILE == 32) {
             const uint32_t* wp = a.codes + (size_t(blockIdx.x) * GS + gq) * 1024 + L;
 #pragma unroll
-            for (int j = 0; j < 32; ++j) wr[j] = wp[j * 32];
+            for (int j = 0; j < 32; ++j) wr[j] = load_once(wp + j * 32);
             mw = a.meta[(size_t(blockIdx.x) * GS + gq) * 32 + L];
         } else {
             const int tA = 2 * blockIdx.x;
@@ -205,8 +205,8 @@ __global__ __launch_bounds__(256) void dense_stream_kernel(ProjArgs a) {
             const uint32_t* pb = a.codes + (size_t(tB) * GS + gq) * 512 + jp * 16 + n16;
 #pragma unroll
             for (int i = 0; i < 16; ++i) {
-                wr[i] = pa[i * 32];
-                wr[16 + i] = pb[i * 32];
+                wr[i] = load_once(pa + i * 32);
+                wr[16 + i] = load_once(pb + i * 32);
             }
             const int cq = min(col, a.N - 1);
             mw = a.meta[(size_t(cq >> 4) * GS + gq) * 16 + (cq & 15)];

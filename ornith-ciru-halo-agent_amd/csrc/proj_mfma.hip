@@ -701,7 +701,7 @@ __global__ __launch_bounds__(64 * WPB, 1) void head_tile_kernel(MfmaArgs a, int 
     auto load_b = [&](int st, int slot) {
         const uint32_t* src = cbase + size_t(st) * 1024;
 #pragma unroll
-        for (int u = 0; u < 16; ++u) bw[slot][u] = src[128 * (u >> 1) + 32 * (u & 1)];
+        for (int u = 0; u < 16; ++u) bw[slot][u] = load_once(src + 128 * (u >> 1) + 32 * (u & 1));
         bm[slot] = mbase[size_t(st) * 32];
     };
 #pragma unroll
