@@ -252,10 +252,14 @@ __device__ __forceinline__ void flag_or(uint32_t* sticky, uint32_t bits) {
 // A code word of a weight stream that one launch reads once: a non-temporal
 // load, so the stream does not displace the lines other blocks still use
 // (measured on the decode paths: N=32 gate-up 33.3 -> 32.0 us and down 20.6
-// -> 19.4 us, the single-token layer 12.5 -> 12.1 us, the one-row dense
-// linear 5.9 -> 5.45 us; the W8 head at 1-8 rows got slower and keeps plain
-// loads there).
+// -> 19.4 us, the single-token layer 12.5 -> 12.1 us and its router rows
+// (load_once4) 11.85 -> 11.55 us more, the one-row dense linear 5.9 -> 5.45
+// us; the W8 head at 1-8 rows got slower and keeps plain loads there).
 __device__ __forceinline__ uint32_t load_once(const uint32_t* p) { return __builtin_nontemporal_load(p); }
+__device__ __forceinline__ uint4 load_once4(const void* p) {
+    const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+    return make_uint4(v[0], v[1], v[2], v[3]);
+}
 
 // ---- 4-bit weight unpacking -----------------------------------------------
 // A packed code word holds K values 8c..8c+7, low nibble first

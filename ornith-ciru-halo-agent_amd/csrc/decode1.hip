@@ -490,12 +490,12 @@ __global__ __launch_bounds__(64 * kLayer1Waves) void layer1_kernel(DecodeArgs a)
         const uint16_t* wrow = a.router_w + size_t(L) * kHidden;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            rv[i] = *reinterpret_cast<const uint4*>(wrow + (i * 64 + lane) * 8);
+            rv[i] = load_once4(wrow + (i * 64 + lane) * 8);
             xv[i] = *reinterpret_cast<const uint4*>(a.x + (i * 64 + lane) * 8);
         }
         if (SHARED && L == 0) {
 #pragma unroll
-            for (int i = 0; i < 4; ++i) rv2[i] = *reinterpret_cast<const uint4*>(a.shared_gate_w + (i * 64 + lane) * 8);
+            for (int i = 0; i < 4; ++i) rv2[i] = load_once4(a.shared_gate_w + (i * 64 + lane) * 8);
         }
     }
     uint32_t ws[32], wd[16], mws = 0, mwd = 0;
