@@ -109,7 +109,8 @@ hipError_t run_routed(const RoutedPlan& p, void* ws, const void* input, const fl
     a.bank_meta_words = kDownBankMeta;
     a.act_words = dw; a.act_scales = dsc; a.act_sums = dsum;
     a.K = kInter;
-    a.tile_xcd = 0;
+    // down: an XCD's m-tiles contiguous up to 2048 tokens (block orders: proj_mfma.hip)
+    a.tile_xcd = T > 2048 ? 0 : 2;
     a.out = at<float>(ws, p.l.route_out);
     TRY(launch_grouped_mfma(a, false, max_tiles, s));
     return launch_reduce(at<float>(ws, p.l.route_out), weights, ids, T, out ? at<float>(ws, p.l.final_f32) : nullptr,

@@ -154,7 +154,7 @@ struct MfmaArgs {
     uint16_t* out_bf16;
     float* arg_val; int32_t* arg_idx;
     uint32_t flag_projection, flag_bf16;
-    int tile_xcd;                                // prefill block order: 0 column-block major, 1 tile per XCD
+    int tile_xcd;                                // prefill block order: 0 column-block major, 1 tile per XCD, 2 tile ranges per XCD
 };
 hipError_t launch_grouped_mfma(const MfmaArgs& a, bool gateup, int max_tiles, hipStream_t s);
 // Dense G256 head on the matrix cores: M <= 64 rows of A8 activations against

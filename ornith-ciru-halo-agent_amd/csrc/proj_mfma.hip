@@ -140,7 +140,7 @@ __global__ __launch_bounds__(256, MODE == kModeDown ? 3 : 2) void prefill_mfma_k
     __shared__ int s_bi[HEAD ? 4 : 1][kMT];
 
     // Workgroups go to the 8 XCDs round-robin (linear block L runs on XCD
-    // L % 8).  Two block orders:
+    // L % 8).  Three block orders:
     //  - column-block major (a.tile_xcd == 0): nt = L % NCB.  Every XCD runs
     //    one column slice of every tile (even load; each XCD streams all the
     //    tiles' activation rows);
@@ -148,6 +148,11 @@ __global__ __launch_bounds__(256, MODE == kModeDown ? 3 : 2) void prefill_mfma_k
     //    m-tile 8q + x, so all column blocks of a tile share one L2 (its
     //    activation rows are fetched once) and each XCD walks every 8th tile.
     //    At large T (full tiles, heavy experts) this cuts the L2 misses ~3x.
+    //  - tile ranges per XCD (a.tile_xcd == 2): the same L, XCD x runs the
+    //    contiguous m-tiles [x per, (x + 1) per), per = ceil(ntiles / 8), so
+    //    an expert's consecutive m-tiles also share its weights in one L2.
+    //    Measured: down at 1120 tokens 38.7 -> 36.8 us; at 8192 tokens down
+    //    200.7 -> 204.6 and gate-up 352 -> 368 us, which keep orders 0 and 1.
     // Head: one m-tile of the a.R input rows, block L = column block L.
     const int L = int(blockIdx.x);
     int nt, mtile;
@@ -158,8 +163,15 @@ __global__ __launch_bounds__(256, MODE == kModeDown ? 3 : 2) void prefill_mfma_k
         td = Segment{0, 0, a.R, 0};
     } else {
         const int ntiles = a.ntiles[0];
-        nt = a.tile_xcd ? (L >> 3) % NCB : L % NCB;
-        mtile = a.tile_xcd ? 8 * (L / (8 * NCB)) + (L & 7) : L / NCB;
+        if (a.tile_xcd == 2) {
+            const int per = (ntiles + 7) >> 3, q = L / (8 * NCB);
+            nt = (L >> 3) % NCB;
+            mtile = (L & 7) * per + q;
+            if (q >= per) return;
+        } else {
+            nt = a.tile_xcd ? (L >> 3) % NCB : L % NCB;
+            mtile = a.tile_xcd ? 8 * (L / (8 * NCB)) + (L & 7) : L / NCB;
+        }
         if (mtile >= ntiles) return;
         td = a.tiles[mtile];
     }
