@@ -139,7 +139,8 @@ __global__ __launch_bounds__(256) void project_gemv_kernel(ProjArgs a, int NT, i
 }
 
 // Dense weight-streaming projection for up to kStreamRows rows (decode and
-// small batches).  One block of 4 waves owns 32 consecutive output columns;
+// small batches).  One block of 4 waves owns COLS (32, or 16 on tile-16
+// banks above kDenseNarrowRows rows) consecutive output columns;
 // half-wave h of the block owns group g0 + h of the current 8-group pass.
 // Each lane keeps its 32 code words of that group in registers (every load of
 // the block is issued before the first dot), so one pass over the bank moves
@@ -148,7 +149,8 @@ __global__ __launch_bounds__(256) void project_gemv_kernel(ProjArgs a, int NT, i
 //   tile 16: lane L = 16*jp + n holds words (2i+jp)*16 + n (i < 16) of the two
 //            16-column blocks of the 32-column unit; the two half-dots of a
 //            column meet across lanes L and L^16, after which lane L keeps
-//            column L of the unit.
+//            column L of the unit.  With 16 columns a lane holds the words
+//            of its one block and lanes L, L^16 both end with column n.
 // FUSED (a.dense_x set, up to kDenseFusedRows rows): the block also prepares
 // its activations from the bf16 input: the H128 +
 // group-256 int8 recipe of act_bf16_block, 16 lanes per (row, group), written
@@ -161,9 +163,16 @@ __global__ __launch_bounds__(256) void project_gemv_kernel(ProjArgs a, int NT, i
 // project_gemv_kernel's bit for bit.
 constexpr int kStreamRows = kDenseStreamRows;   // rows whose running sums stay in LDS
 constexpr int kStreamChunk = 8;     // rows per term pass (8 rows x 32 columns = 256 threads)
+// Tile-16 banks above this many rows (the activations read from the
+// workspace) run 16-column blocks: twice the blocks, each lane streaming one
+// 16-column tile.  One-row-per-block latency favours 32 columns below it
+// (graph-timed per call, 16 against 32 columns: 1 row 6.0 / 5.55 us, 8 rows
+// 15.8 / 12.6, 16 rows 15.8 / 16.1, 32 rows 24.5 / 25.6, 64 rows 40.9 / 44.1).
+constexpr int kDenseNarrowRows = 16;
 
-template <int TILE, bool FUSED>
+template <int TILE, bool FUSED, int COLS = 32>
 __global__ __launch_bounds__(256) void dense_stream_kernel(ProjArgs a) {
+    static_assert(COLS == 32 || TILE == 16, "16-column blocks read the N16 layout");
     __shared__ uint32_t la[kStreamChunk][8 * 64];
     __shared__ float lsa[kStreamChunk][8], lss[kStreamChunk][8];
     __shared__ float lterm[kStreamChunk][8][32];
@@ -171,7 +180,7 @@ __global__ __launch_bounds__(256) void dense_stream_kernel(ProjArgs a) {
 
     const int tid = threadIdx.x, hw = tid >> 5, L = tid & 31, jp = L >> 4, n16 = L & 15;
     const int GS = a.K / kGroup, M = a.dense_rows;
-    const int col0 = blockIdx.x * 32, col = col0 + L;
+    const int col0 = blockIdx.x * COLS, col = col0 + (COLS == 16 ? n16 : L);
     for (int g0 = 0; g0 < GS; g0 += 8) {
         const int g = g0 + hw, gc = min(8, GS - g0);
         const bool gv = g < GS;
@@ -199,14 +208,14 @@ __global__ __launch_bounds__(256) void dense_stream_kernel(ProjArgs a) {
             for (int j = 0; j < 32; ++j) wr[j] = load_once(wp + j * 32);
             mw = a.meta[(size_t(blockIdx.x) * GS + gq) * 32 + L];
         } else {
-            const int tA = 2 * blockIdx.x;
+            const int tA = COLS == 16 ? int(blockIdx.x) : 2 * int(blockIdx.x);
             const int tB = (tA + 1) * 16 < a.N ? tA + 1 : tA;
             const uint32_t* pa = a.codes + (size_t(tA) * GS + gq) * 512 + jp * 16 + n16;
             const uint32_t* pb = a.codes + (size_t(tB) * GS + gq) * 512 + jp * 16 + n16;
 #pragma unroll
             for (int i = 0; i < 16; ++i) {
                 wr[i] = load_once(pa + i * 32);
-                wr[16 + i] = load_once(pb + i * 32);
+                if (COLS == 32) wr[16 + i] = load_once(pb + i * 32);
             }
             const int cq = min(col, a.N - 1);
             mw = a.meta[(size_t(cq >> 4) * GS + gq) * 16 + (cq & 15)];
@@ -290,17 +299,20 @@ __global__ __launch_bounds__(256) void dense_stream_kernel(ProjArgs a) {
                         const uint2 av = *reinterpret_cast<const uint2*>(&ab[4 * i + 2 * jp]);
                         d0 = dot4(code_even(wr[i]), int(av.x), d0);
                         d0 = dot4(code_odd(wr[i]), int(av.y), d0);
-                        d1 = dot4(code_even(wr[16 + i]), int(av.x), d1);
-                        d1 = dot4(code_odd(wr[16 + i]), int(av.y), d1);
+                        if (COLS == 32) {
+                            d1 = dot4(code_even(wr[16 + i]), int(av.x), d1);
+                            d1 = dot4(code_odd(wr[16 + i]), int(av.y), d1);
+                        }
                     }
-                    const int sA = d0 + xor_perm_i<16>(d0), sB = d1 + xor_perm_i<16>(d1);
+                    const int sA = d0 + xor_perm_i<16>(d0), sB = COLS == 32 ? d1 + xor_perm_i<16>(d1) : sA;
                     dot = jp ? sB : sA;
                 }
-                if (gv) lterm[r][hw][L] = tree_term(dot, lsa[r][hw], lss[r][hw], mw);
+                // 16-column blocks: lanes L and L ^ 16 hold the same column
+                if (gv && (COLS == 32 || jp == 0)) lterm[r][hw][L] = tree_term(dot, lsa[r][hw], lss[r][hw], mw);
             }
             __syncthreads();
             const int r = tid >> 5;
-            if (r < nr) {
+            if (r < nr && (COLS == 32 || L < 16)) {
                 float v = g0 == 0 ? 0.f : lrun[r0 + r][L];
                 for (int gl = 0; gl < gc; ++gl) v = v + lterm[r][gl][L];
                 lrun[r0 + r][L] = v;
@@ -308,10 +320,10 @@ __global__ __launch_bounds__(256) void dense_stream_kernel(ProjArgs a) {
         }
     }
     __syncthreads();
-    for (int q = tid; q < M * 32; q += 256) {
-        const int r = q >> 5, c = col0 + (q & 31);
+    for (int q = tid; q < M * COLS; q += 256) {
+        const int r = q / COLS, c = col0 + q % COLS;
         if (c >= a.N) continue;
-        const float v = lrun[r][q & 31];
+        const float v = lrun[r][q % COLS];
         const size_t o = size_t(r) * a.N + c;
         const uint16_t b = f32_to_bf16_bits(v);
         uint32_t f = 0;
@@ -337,6 +349,9 @@ hipError_t launch_project_gemv(const ProjArgs& a, int max_segments, Out mode, hi
             else timed_launch("dense_stream", dense_stream_kernel<16, true>, g, dim3(256), 0, s, a);
         } else {
             if (a.tile == 32) timed_launch("dense_stream", dense_stream_kernel<32, false>, g, dim3(256), 0, s, a);
+            else if (a.dense_rows > kDenseNarrowRows)
+                timed_launch("dense_stream", dense_stream_kernel<16, false, 16>, dim3((a.N + 15) / 16), dim3(256), 0, s,
+                             a);
             else timed_launch("dense_stream", dense_stream_kernel<16, false>, g, dim3(256), 0, s, a);
         }
         return hipGetLastError();

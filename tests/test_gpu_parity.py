@@ -47,7 +47,7 @@ def moe(device):
                                         (16, 2048, 512, 32), (3, 48, 768, 16), (64, 1024, 4096, 16),
                                         (9, 2080, 2048, 32), (2, 128, 8192, 16), (65, 96, 512, 16),
                                         (8, 6144, 2048, 32), (8, 2080, 2048, 16), (7, 48, 768, 16),
-                                        (6, 1024, 2048, 32)])
+                                        (6, 1024, 2048, 32), (33, 2080, 2048, 16)])
 def test_dense_a8_bit_exact(device, M, N, K, tile):
     import torch
     native = _native()
