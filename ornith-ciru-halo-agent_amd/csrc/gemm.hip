@@ -10,11 +10,11 @@
 // by tolerance.
 //
 // Two kernels:
-//  - transform: bf16(H128 x) of every 256-group, quarter-wave groups (16
-//    lanes x 16 values, the butterflies in registers and by DPP), written in
-//    matrix-core fragment order so that every A operand is one contiguous
-//    1 KiB load (a row-major operand puts the 16 rows of a fragment in 16
-//    cache lines per instruction, and the L1 tag lookups become the limit);
+//  - transform: bf16(H128 x) of every 128-block, one wave per (8 rows, 128
+//    k), the butterflies in registers and by DPP, written in matrix-core
+//    fragment order so that every A operand is one contiguous 1 KiB load (a
+//    row-major operand puts the 16 rows of a fragment in 16 cache lines per
+//    instruction, and the L1 tag lookups become the limit);
 //  - gemm: block tile 256 rows x 64 columns, 4 waves of 64 x 64 rows, two
 //    blocks per CU (one block's barrier wait is covered by the other's
 //    products), v_mfma_f32_16x16x32_bf16 on 32-k steps.  Per step every
@@ -83,30 +83,31 @@ __global__ __launch_bounds__(256) void transform_bf16_kernel(const uint16_t* __r
     flag_or(sticky, real ? flags : 0u);
 }
 
-// Fragment order, one wave per (16-row group rg, 128-k block kb): lane l is
-// row 16 rg + l / 4 and k chunk q = l % 4; its load i (0..3) is the 8 values
-// k = 128 kb + 32 i + 8 q + 0..7, so the four lanes of a row read 64
-// contiguous bytes per load.  Butterflies on k bits 0..2 in registers, bits 3
-// and 4 across the lanes of a quad (DPP xor 1, xor 2), bits 5 and 6 in
-// registers again: the ascending order of the reference.  Store i is all of
-// fragment 4 kb + i (lane l's 16 bytes at (16 q + l / 4) * 16), one
-// contiguous 1 KiB per store.
+// Fragment order, one wave per (8-row half rg8 of a 16-row group, 128-k
+// block kb): lane l is row 8 rg8 + l / 8 and k chunks c = q + 8 i (q = l % 8,
+// i = 0, 1), i.e. k = 128 kb + 64 i + 8 q + 0..7, so the eight lanes of a row
+// read 128 contiguous bytes per load.  Butterflies on k bits 0..2 in
+// registers, bits 3, 4 and 5 across the lanes of a row (xor 1, 2, 4), bit 6
+// in registers again: the ascending order of the reference.  Chunk c lands
+// in fragment 4 kb + c / 4 at rows (16 (c % 4) + 8 (rg8 % 2) + l / 8) * 8:
+// two 16-byte stores per lane.  Two waves per 16-row group keep two or more
+// waves on a SIMD (one wave alone issues its vector work at half rate).
 __global__ __launch_bounds__(256) void transform_frag_kernel(const uint16_t* __restrict__ x, int M, int Mp, int K,
                                                              uint16_t* __restrict__ y, uint32_t* sticky) {
     const int KB = K / 128, S = K / 32;
     const int wave = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
-    const int rg = wave / KB, kb = wave - rg * KB;
-    if (16 * rg >= Mp) return;
-    const int r = lane >> 2, q = lane & 3, row = 16 * rg + r;
+    const int rg8 = wave / KB, kb = wave - rg8 * KB;
+    if (8 * rg8 >= Mp) return;
+    const int r = lane >> 3, q = lane & 7, row = 8 * rg8 + r;
     const bool real = row < M;
     const uint16_t* src = x + size_t(min(row, M - 1)) * K + 128 * kb + 8 * q;
-    uint4 raw[4];
+    uint4 raw[2];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) raw[i] = *reinterpret_cast<const uint4*>(src + 32 * i);
-    float v[32];                                            // v[8 i + e]: k = 32 i + 8 q + e
+    for (int i = 0; i < 2; ++i) raw[i] = *reinterpret_cast<const uint4*>(src + 64 * i);
+    float v[16];                                            // v[8 i + e]: k = 64 i + 8 q + e
     uint32_t flags = 0;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
+    for (int i = 0; i < 2; ++i) {
         const uint32_t u[4] = {raw[i].x, raw[i].y, raw[i].z, raw[i].w};
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
@@ -115,52 +116,56 @@ __global__ __launch_bounds__(256) void transform_frag_kernel(const uint16_t* __r
         }
     }
 #pragma unroll
-    for (int e = 0; e < 32; ++e) if (!isfinite(v[e])) flags |= kDenseNonfiniteInput;
+    for (int e = 0; e < 16; ++e) if (!isfinite(v[e])) flags |= kDenseNonfiniteInput;
 #pragma unroll
     for (int b = 1; b < 8; b <<= 1) {
 #pragma unroll
-        for (int i = 0; i < 32; ++i) {
+        for (int i = 0; i < 16; ++i) {
             if (i & b) continue;
             const float lo = v[i], hi = v[i + b];
             v[i] = lo + hi;
             v[i + b] = lo - hi;
         }
     }
-    // k bit 3 (lane bit 0), then k bit 4 (lane bit 1): the lane with the bit
-    // set keeps partner - own, the other own + partner
+    // k bits 3, 4, 5 (lane bits 0, 1, 2): the lane with the bit set keeps
+    // partner - own, the other own + partner
     {
         const uint32_t flip = (lane & 1) ? 0x80000000u : 0u;
 #pragma unroll
-        for (int i = 0; i < 32; ++i) v[i] = xor_perm_f<1>(v[i]) + __uint_as_float(__float_as_uint(v[i]) ^ flip);
+        for (int i = 0; i < 16; ++i) v[i] = xor_perm_f<1>(v[i]) + __uint_as_float(__float_as_uint(v[i]) ^ flip);
     }
     {
         const uint32_t flip = (lane & 2) ? 0x80000000u : 0u;
 #pragma unroll
-        for (int i = 0; i < 32; ++i) v[i] = xor_perm_f<2>(v[i]) + __uint_as_float(__float_as_uint(v[i]) ^ flip);
+        for (int i = 0; i < 16; ++i) v[i] = xor_perm_f<2>(v[i]) + __uint_as_float(__float_as_uint(v[i]) ^ flip);
+    }
+    {
+        const uint32_t flip = (lane & 4) ? 0x80000000u : 0u;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) v[i] = xor_perm_f<4>(v[i]) + __uint_as_float(__float_as_uint(v[i]) ^ flip);
     }
 #pragma unroll
-    for (int b = 8; b < 32; b <<= 1) {
-#pragma unroll
-        for (int i = 0; i < 32; ++i) {
-            if (i & b) continue;
-            const float lo = v[i], hi = v[i + b];
-            v[i] = lo + hi;
-            v[i + b] = lo - hi;
-        }
+    for (int i = 0; i < 8; ++i) {
+        const float lo = v[i], hi = v[i + 8];
+        v[i] = lo + hi;
+        v[i + 8] = lo - hi;
     }
-    uint32_t o[16];
+    uint32_t o[8];
 #pragma unroll
-    for (int e = 0; e < 16; ++e) {
+    for (int e = 0; e < 8; ++e) {
         const float a = v[2 * e] * kInvSqrt128, b = v[2 * e + 1] * kInvSqrt128;
         if (!isfinite(a) || !isfinite(b)) flags |= kDenseNonfiniteInput;
         const uint16_t ha = f32_to_bf16_bits(a), hb = f32_to_bf16_bits(b);
         if ((ha & 0x7f80u) == 0x7f80u || (hb & 0x7f80u) == 0x7f80u) flags |= kDenseNonfiniteBf16;
         o[e] = real ? uint32_t(ha) | (uint32_t(hb) << 16) : 0u;
     }
-    uint16_t* frag = y + (size_t(rg) * S + 4 * kb) * 512 + (16 * q + r) * 8;
+    const int rg = rg8 >> 1, r16 = 8 * (rg8 & 1) + r;
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
-        *reinterpret_cast<uint4*>(frag + 512 * i) = make_uint4(o[4 * i], o[4 * i + 1], o[4 * i + 2], o[4 * i + 3]);
+    for (int i = 0; i < 2; ++i) {
+        const int c = q + 8 * i;
+        uint16_t* frag = y + (size_t(rg) * S + 4 * kb + c / 4) * 512 + (16 * (c % 4) + r16) * 8;
+        *reinterpret_cast<uint4*>(frag) = make_uint4(o[4 * i], o[4 * i + 1], o[4 * i + 2], o[4 * i + 3]);
+    }
     flag_or(sticky, real ? flags : 0u);
 }
 
@@ -407,7 +412,7 @@ hipError_t launch_transform_bf16_fast(const uint16_t* x, int M, int K, uint16_t*
 
 hipError_t launch_transform_bf16_frag(const uint16_t* x, int M, int K, uint16_t* y, uint32_t* sticky, hipStream_t s) {
     const int Mp = (M + 15) / 16 * 16;
-    const int waves = Mp / 16 * (K / 128);
+    const int waves = Mp / 8 * (K / 128);
     timed_launch("transform_bf16_frag", transform_frag_kernel, dim3((waves + 3) / 4), dim3(256), 0, s, x, M, Mp, K, y,
                  sticky);
     return hipGetLastError();
