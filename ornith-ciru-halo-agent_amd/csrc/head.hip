@@ -74,8 +74,13 @@ __global__ __launch_bounds__(256) void head_encode_kernel(const uint16_t* __rest
 // flight, the ring running across tiles.
 //  - Weights of one (tile, group) are 2 KiB: words [kq 0..7][kr 0..3][n 0..15],
 //    word (kq, kr, n) = the four K bytes 16 kq + 4 kr .. +3 of column n.  For
-//    k-step s (64 K) lane n + 16q loads words (4s + q, 0..3, n): the 16
-//    contiguous K bytes 64 s + 16 q .. +15 of column n, its B operand.
+//    k-step s (64 K) lane n + 16q needs words (4s + q, 0..3, n): the 16
+//    contiguous K bytes 64 s + 16 q .. +15 of column n, its B operand.  Those
+//    words lie 64 bytes apart, so (LB, the path without group dots) each lane
+//    loads 16 contiguous bytes instead (two loads per block, a quarter of the
+//    address work of dword loads: the 64-row head 154 -> 142 us) and the
+//    wave passes the block through 2 KiB of LDS to regroup it per column;
+//    the group-dot path keeps the dword loads into registers.
 //  - A: lane r + 16q reads row r's same 16 bytes from LDS; 16-byte piece p of
 //    row r sits at slot (p & ~15) | ((p ^ r) & 15).
 //  - C: register k of lane n + 16q is row 4q + k, column n.  Dots start from
@@ -88,7 +93,7 @@ constexpr int kW8DotBiasBits = 0x4B400000;
 constexpr int kW8Waves = 8;
 typedef int w8_i32x4 __attribute__((ext_vector_type(4)));
 
-template <int MT, int D, bool DOTS>
+template <int MT, int D, bool DOTS, bool LB = false>
 __global__ __launch_bounds__(64 * kW8Waves, 1) void head_w8_mfma_kernel(
     const uint32_t* __restrict__ w, const uint16_t* __restrict__ wscale, const uint32_t* __restrict__ act,
     const uint16_t* __restrict__ ascale, int M, int N, int nwaves, float* __restrict__ diag,
@@ -98,6 +103,11 @@ __global__ __launch_bounds__(64 * kW8Waves, 1) void head_w8_mfma_kernel(
     __shared__ __attribute__((aligned(16))) uint32_t sA[ROWS * RW];
     __shared__ __attribute__((aligned(16))) float s_sa[kHeadGroups][ROWS];
     __shared__ __attribute__((aligned(16))) float s_nb[kHeadGroups][ROWS];
+    // LB: each wave's (tile, group) block passes through 2 KiB of LDS: 16-byte
+    // loads in (chunk c of a 1 KiB half from lane c), chunk c stored at
+    // position c ^ 4 ((c >> 4) & 3), B words read back per column
+    // (conflict-free both ways)
+    __shared__ __attribute__((aligned(16))) uint32_t sB[LB ? kW8Waves * 512 : 4];
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, li = lane & 15, q = lane >> 4;
 
     for (int i = tid; i < ROWS * (RW / 4); i += NT) {
@@ -126,12 +136,27 @@ __global__ __launch_bounds__(64 * kW8Waves, 1) void head_w8_mfma_kernel(
     const uint16_t* sbase = wscale + size_t(16 * t0 + li) * kHeadGroups;
     uint32_t bw[D][8];
     uint16_t bs[D];
+    uint32_t* stg = sB + (LB ? wv * 512 : 0);
+    const int pos = lane ^ (((lane >> 4) & 3) << 2);
+    const uint32_t* wx = w + size_t(t0) * (kHeadGroups * 512) + 4 * lane;
     auto load_b = [&](int st, int slot) {
-        const uint32_t* src = wbase + size_t(st) * 512;
+        if constexpr (LB) {
+            const uint32_t* src = wx + size_t(st) * 512;
 #pragma unroll
-        for (int u = 0; u < 8; ++u) {
-            const uint32_t* pu = src + 256 * (u >> 2) + 16 * (u & 3);
-            bw[slot][u] = MT >= 4 ? load_once(pu) : *pu;   // non-temporal only for the 64-row tiles (measured)
+            for (int h = 0; h < 2; ++h) {
+                const uint4 v = MT >= 4 ? load_once4(src + 256 * h) : *reinterpret_cast<const uint4*>(src + 256 * h);
+                bw[slot][4 * h] = v.x;
+                bw[slot][4 * h + 1] = v.y;
+                bw[slot][4 * h + 2] = v.z;
+                bw[slot][4 * h + 3] = v.w;
+            }
+        } else {
+            const uint32_t* src = wbase + size_t(st) * 512;
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                const uint32_t* pu = src + 256 * (u >> 2) + 16 * (u & 3);
+                bw[slot][u] = MT >= 4 ? load_once(pu) : *pu;   // non-temporal only for the 64-row tiles (measured)
+            }
         }
         bs[slot] = sbase[size_t(st >> 4) * (16 * kHeadGroups) + (st & 15)];
     };
@@ -156,10 +181,21 @@ __global__ __launch_bounds__(64 * kW8Waves, 1) void head_w8_mfma_kernel(
             for (int slot = 0; slot < D; ++slot) {
                 const int g = g0 + slot;
                 w8_i32x4 acc[MT];
+                uint32_t bl[8];
+                if constexpr (LB) {
+#pragma unroll
+                    for (int h = 0; h < 2; ++h)
+                        *reinterpret_cast<uint4*>(&stg[256 * h + 4 * pos]) =
+                            make_uint4(bw[slot][4 * h], bw[slot][4 * h + 1], bw[slot][4 * h + 2], bw[slot][4 * h + 3]);
+#pragma unroll
+                    for (int u = 0; u < 8; ++u) bl[u] = stg[256 * (u >> 2) + 64 * q + 16 * ((u & 3) ^ q) + li];
+                } else {
+#pragma unroll
+                    for (int u = 0; u < 8; ++u) bl[u] = bw[slot][u];
+                }
 #pragma unroll
                 for (int s = 0; s < 2; ++s) {
-                    const w8_i32x4 fb = {int(bw[slot][4 * s]), int(bw[slot][4 * s + 1]), int(bw[slot][4 * s + 2]),
-                                         int(bw[slot][4 * s + 3])};
+                    const w8_i32x4 fb = {int(bl[4 * s]), int(bl[4 * s + 1]), int(bl[4 * s + 2]), int(bl[4 * s + 3])};
 #pragma unroll
                     for (int rt = 0; rt < MT; ++rt) {
                         const int r = 16 * rt + li, p = 8 * g + 4 * s + q;
@@ -169,7 +205,12 @@ __global__ __launch_bounds__(64 * kW8Waves, 1) void head_w8_mfma_kernel(
                         acc[rt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(fa, fb, s ? acc[rt] : kInit, 0, 0, 0);
                     }
                 }
-                const float sw = f16_bits_to_f32(bs[slot]);
+                // the scale is taken at its use: converted early, every slot's
+                // scale (the last load of its refill) was waited for at the top
+                // of a pass, which emptied the ring
+                uint32_t sbits = bs[slot];
+                asm volatile("" : "+v"(sbits));
+                const float sw = f16_bits_to_f32(uint16_t(sbits));
                 // always refill (the wave's last steps reload the current one:
                 // a predicated load would make every later wait drain the queue)
                 load_b(g + D < kHeadGroups || refill ? 16 * t + g + D : 16 * t + g, slot);
@@ -315,10 +356,10 @@ extern "C" hipError_t ornith_head_i8_tile_launch(const void* input, const void* 
         else if (mt == 3) go(head_w8_mfma_kernel<3, 2, true>);
         else go(head_w8_mfma_kernel<4, 2, true>);
     } else {
-        if (mt == 1) go(head_w8_mfma_kernel<1, 4, false>);
-        else if (mt == 2) go(head_w8_mfma_kernel<2, 4, false>);
-        else if (mt == 3) go(head_w8_mfma_kernel<3, 2, false>);
-        else go(head_w8_mfma_kernel<4, 2, false>);
+        if (mt == 1) go(head_w8_mfma_kernel<1, 4, false, true>);
+        else if (mt == 2) go(head_w8_mfma_kernel<2, 4, false, true>);
+        else if (mt == 3) go(head_w8_mfma_kernel<3, 4, false, true>);
+        else go(head_w8_mfma_kernel<4, 4, false, true>);
     }
     return hipGetLastError();
 }
