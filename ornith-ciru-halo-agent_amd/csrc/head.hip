@@ -77,8 +77,8 @@ __global__ __launch_bounds__(256) void head_encode_kernel(const uint16_t* __rest
 //    k-step s (64 K) lane n + 16q needs words (4s + q, 0..3, n): the 16
 //    contiguous K bytes 64 s + 16 q .. +15 of column n, its B operand.  Those
 //    words lie 64 bytes apart, so (LB, the path without group dots) each lane
-//    loads 16 contiguous bytes instead (two loads per block, a quarter of the
-//    address work of dword loads: the 64-row head 154 -> 142 us) and the
+//    loads 16 contiguous bytes instead (two non-temporal loads per block:
+//    1 row 96 -> 81 us, 64 rows 154 -> 141 us against dword loads) and the
 //    wave passes the block through 2 KiB of LDS to regroup it per column;
 //    the group-dot path keeps the dword loads into registers.
 //  - A: lane r + 16q reads row r's same 16 bytes from LDS; 16-byte piece p of
@@ -144,7 +144,8 @@ __global__ __launch_bounds__(64 * kW8Waves, 1) void head_w8_mfma_kernel(
             const uint32_t* src = wx + size_t(st) * 512;
 #pragma unroll
             for (int h = 0; h < 2; ++h) {
-                const uint4 v = MT >= 4 ? load_once4(src + 256 * h) : *reinterpret_cast<const uint4*>(src + 256 * h);
+                // non-temporal at every row count (1 row 95 -> 81 us, 8 rows 110 -> 99)
+                const uint4 v = load_once4(src + 256 * h);
                 bw[slot][4 * h] = v.x;
                 bw[slot][4 * h + 1] = v.y;
                 bw[slot][4 * h + 2] = v.z;
