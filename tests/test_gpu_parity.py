@@ -494,12 +494,14 @@ def test_moe_layer_single_token_ties(device, moe, shared_tables, case):
 # Heads
 # ---------------------------------------------------------------------------
 # Rows run in tiles of 16 on the matrix cores: 1..64 rows cover one to four
-# row tiles (40, 33, 24 and 56 leave partial tiles); 65536 and 248320 are the
+# row tiles (40, 33, 24, 56, 13 and 30 leave partial tiles; 13 and 30 also
+# partial 4-row store groups); 65536 and 248320 are the
 # reference's full head widths (head_i8_tile_api.h:22), where every wave
 # streams two (65536) or seven to eight (248320) column tiles.
 @pytest.mark.parametrize('M,N,dots', [(1, 256, False), (3, 1024, True), (40, 4096, False), (64, 4096, True),
                                       (33, 1024, False), (17, 256, True), (1, 65536, False), (64, 248320, False),
-                                      (24, 65536, False), (56, 65536, False)])
+                                      (24, 65536, False), (56, 65536, False), (13, 4096, False),
+                                      (30, 1024, False)])
 def test_head_w8_bit_exact(device, M, N, dots):
     import torch
     native = _native()
