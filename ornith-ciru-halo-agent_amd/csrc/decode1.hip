@@ -790,15 +790,13 @@ __global__ __launch_bounds__(64 * kLayer1Waves) void layer1_kernel(DecodeArgs a)
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
         if (lane == 0) __hip_atomic_fetch_add(&lsync[3], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
     }
-    // routed down codes: issued once the block's gate-up dots are done (issued
-    // earlier they slow this CU's gate-up codes; issued after the epilogue
-    // they land after the middle rows).  No block barrier: the epilogue waits
-    // only for the four gate-up waves.  The shared slot's wave loaded its
-    // codes before barrier A.
-    if (down_block && dslot >= 0 && dslot < kTop) {
-        lds_wait(&lsync[3], 4u);
-        load_down();
-    }
+    // routed down codes: issued as soon as the experts are known (barrier A),
+    // behind the block's gate-up codes.  With both streams non-temporal this
+    // measured 0.12 us per layer faster than issuing them after the block's
+    // gate-up dots (without the hint, the early issue slowed the gate-up
+    // codes); issued after the epilogue they land after the middle rows.
+    // The shared slot's wave loaded its codes before barrier A.
+    if (down_block && dslot >= 0 && dslot < kTop) load_down();
     uint64_t arrival[4] = {0, 0, 0, 0};
     if (wave == kLayer1EpilogueWave) {
         lds_wait(&lsync[3], 4u);
