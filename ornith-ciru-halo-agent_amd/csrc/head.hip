@@ -108,6 +108,7 @@ __global__ __launch_bounds__(64 * kW8Waves, 1) void head_w8_mfma_kernel(
     // position c ^ 4 ((c >> 4) & 3), B words read back per column
     // (conflict-free both ways)
     __shared__ __attribute__((aligned(16))) uint32_t sB[LB ? kW8Waves * 512 : 4];
+    // LB up to 32 rows: each wave's logits of a four-tile group (rows of 68 floats)
     __shared__ __attribute__((aligned(16))) float sO[LB && MT <= 2 ? kW8Waves * ROWS * 68 : 4];
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, li = lane & 15, q = lane >> 4;
 
